@@ -1,0 +1,233 @@
+#!/usr/bin/env python3
+"""Headline benchmark: FlashAttention-2 forward on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
+
+Workload (the reference's headline,
+``benchmarks/benchmark_throughput.py:205-222``): B=2 H=8 N=4096 D=64 fp16,
+sm_scale=1/8, seeded synthetic inputs resident in HBM.  A "step" is one
+``forward_flash2`` call; the non-causal pass is the timed step whose
+throughput is ``value``, and the causal pass is timed the same way and
+reported beside it.  TFLOP/s use the reference's formula 4.B.H.N^2.D (halved
+for causal, ``benchmark_throughput.py:23-31``).
+
+Prints ONE JSON line.  ``roofline`` prices the FA2 kernel against the
+MI355X dense-fp16 MFMA peak (2.5 PFLOP/s) using HIP events recorded on the
+stream the kernel runs on; ``traffic`` comes from the committed rocprofv3
+FETCH_SIZE/WRITE_SIZE summary (``profiles/``) when present.  The
+``cpu_baseline`` leg times PyTorch-CPU ``scaled_dot_product_attention`` in
+float32 on the same inputs on this host (the reference tests' comparator)
+and doubles as the correctness gate of the numbers printed.
+"""
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+MFMA_PEAK_TFLOPS = 2500.0  # MI355X dense fp16 MFMA, published
+HBM_PEAK_GBS = 8000.0
+METRIC = "attn fwd TFLOP/s + % MFMA peak, B2 H8 N4096 D64 fp16 causal/non-causal"
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "fa2_C2_traffic.json")
+
+
+def parse():
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[1])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=25)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--cpu-runs", type=int, default=3)
+    return ap.parse_args()
+
+
+def time_steps(fn, steps, warmup):
+    """Warm up, then time exactly `steps` calls: wall clock between two
+    synchronisations, plus one HIP event pair around the whole region on the
+    current stream (the stream the kernel is launched on)."""
+    import torch
+
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    start.record()
+    for _ in range(steps):
+        fn()
+    end.record()
+    torch.cuda.synchronize()
+    wall_ms = (time.perf_counter() - t0) * 1e3
+    return wall_ms / steps, start.elapsed_time(end) / steps
+
+
+def median_event_latency(fn, runs=100):
+    """The reference's method (benchmark_throughput.py:34-54): one event
+    pair per call, median of `runs`."""
+    import torch
+
+    pairs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+             for _ in range(runs)]
+    for s, e in pairs:
+        s.record()
+        fn()
+        e.record()
+    torch.cuda.synchronize()
+    lat = sorted(s.elapsed_time(e) for s, e in pairs)
+    return lat[len(lat) // 2], lat[0], sum(lat) / len(lat)
+
+
+def cpu_baseline_leg(q16, k16, v16, gpu_out, sm_scale, runs):
+    """PyTorch-CPU SDPA in fp32 on the same inputs (timed), and the parity
+    of the GPU outputs against it."""
+    import numpy as np
+    import torch
+
+    from oracle import error_stats
+    from oracle.cpu_sdpa import sdpa_cpu_f32, to_cpu_f32
+
+    tq, tk, tv = to_cpu_f32(q16, k16, v16)  # upcast once, outside the timed region
+    res = {}
+    for causal in (False, True):
+        sdpa_cpu_f32(tq, tk, tv, sm_scale, causal)  # warm-up
+        times = []
+        for _ in range(runs):
+            t0 = time.perf_counter()
+            ref = sdpa_cpu_f32(tq, tk, tv, sm_scale, causal)
+            times.append(time.perf_counter() - t0)
+        mx, mean = error_stats(gpu_out[causal], ref.numpy().astype(np.float64))
+        res[causal] = (statistics.median(times), mx, mean)
+    cpu_model = ""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    cpu_model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return res, torch.get_num_threads(), os.cpu_count(), cpu_model
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU only (got --gpus {args.gpus}); the "
+              "path shards over (batch, head) with no communication, see DESIGN.md.",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import numpy as np
+    import torch
+
+    import flashlite_amd
+    from flashlite_amd import capi
+    from flashlite_amd.workloads import HEADLINE, WORKLOADS, workload_inputs
+
+    if not torch.cuda.is_available():
+        print("bench.py: no GPU visible", file=sys.stderr)
+        sys.exit(1)
+    dev = torch.device("cuda:0")
+    w = WORKLOADS[HEADLINE]
+    q16, k16, v16 = workload_inputs(w)
+    q, k, v = (torch.from_numpy(x).to(dev) for x in (q16, k16, v16))
+    out = torch.empty_like(q)
+    fwd = flashlite_amd.forward_flash2
+
+    results = {}
+    gpu_out = {}
+    for causal in (False, True):
+        fn = lambda c=causal: fwd(q, k, v, w.sm_scale, c, out=out)  # noqa: E731
+        wall_ms, kern_ms = time_steps(fn, args.steps, args.warmup)
+        med, mn, mean = median_event_latency(fn)
+        flops = (2.0 if causal else 4.0) * w.batch * w.heads * w.seq ** 2 * w.head_dim
+        results[causal] = dict(wall_ms=wall_ms, kern_ms=kern_ms, med=med, mn=mn, mean=mean,
+                               flops=flops)
+        fn()
+        torch.cuda.synchronize()
+        gpu_out[causal] = out.float().cpu().numpy().astype(np.float64)
+
+    p = capi.tensor_params(q, k, v, out, w.sm_scale, False)
+    cfg = capi.select_config(p)
+    nc, ca = results[False], results[True]
+    value = nc["flops"] / (nc["wall_ms"] * 1e-3) / 1e12
+    achieved = nc["flops"] / (nc["kern_ms"] * 1e-3) / 1e12
+    io_bytes = 4 * w.batch * w.heads * w.seq * w.head_dim * 2
+
+    traffic = None
+    if os.path.exists(TRAFFIC_FILE):
+        with open(TRAFFIC_FILE) as f:
+            traffic = json.load(f).get("noncausal_bytes_per_launch")
+
+    line = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(nc["wall_ms"], 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp16",
+        "data": "synthetic (numpy RandomState seed %d, N(0,1) -> fp32 -> fp16), resident in HBM"
+                % w.seed,
+        "config": {"workload": HEADLINE, "batch": w.batch, "heads": w.heads, "seq_len": w.seq,
+                   "head_dim": w.head_dim, "causal": False, "sm_scale": w.sm_scale,
+                   "tile_config": capi.config_name(cfg)},
+        "frac_mfma_peak": round(value / MFMA_PEAK_TFLOPS, 4),
+        "latency_ms": {"noncausal_median": round(nc["med"], 5), "noncausal_min": round(nc["mn"], 5),
+                       "causal_median": round(ca["med"], 5), "causal_min": round(ca["mn"], 5)},
+        "causal": {
+            "value": round(ca["flops"] / (ca["wall_ms"] * 1e-3) / 1e12, 2),
+            "ms_per_step": round(ca["wall_ms"], 5),
+            "kernel_tflops": round(ca["flops"] / (ca["kern_ms"] * 1e-3) / 1e12, 2),
+            "frac_mfma_peak": round(ca["flops"] / (ca["kern_ms"] * 1e-3) / 1e12 / MFMA_PEAK_TFLOPS,
+                                    4),
+        },
+        "roofline": {
+            "bound": "mfma",
+            "achieved": round(achieved, 2),
+            "peak": MFMA_PEAK_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": round(achieved / MFMA_PEAK_TFLOPS, 4),
+            "traffic": traffic,
+            "kernel_avg_us": round(nc["kern_ms"] * 1e3, 3),
+            "algorithmic_flops_per_launch": nc["flops"],
+            "algorithmic_bytes_per_launch": io_bytes,
+        },
+        "cpu_baseline": None,
+    }
+
+    if not args.no_cpu:
+        res, threads, ncpu, model = cpu_baseline_leg(q16, k16, v16, gpu_out, w.sm_scale,
+                                                     args.cpu_runs)
+        t_nc, mx_nc, mean_nc = res[False]
+        t_c, mx_c, mean_c = res[True]
+        line["cpu_baseline"] = {
+            "value": round(nc["flops"] / t_nc / 1e12, 5),
+            "unit": "TFLOP/s",
+            "cores": threads,
+            "kind": "port",
+            "sample": (f"full {HEADLINE} non-causal call, torch-CPU scaled_dot_product_attention "
+                       f"fp32, median of {args.cpu_runs} after 1 warm-up; host {model} "
+                       f"({ncpu} logical CPUs)"),
+            "latency_s": round(t_nc, 4),
+            "causal_latency_s": round(t_c, 4),
+        }
+        line["parity_vs_cpu"] = {"noncausal_max_abs": mx_nc, "noncausal_mean_abs": mean_nc,
+                                 "causal_max_abs": mx_c, "causal_mean_abs": mean_c,
+                                 "pass": bool(mx_nc <= 2e-3 and mean_nc <= 2e-4 and
+                                              mx_c <= 2e-3 and mean_c <= 2e-4)}
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,34 @@
+"""flashlite_amd -- FlashAttention-2 forward for AMD Instinct MI355X (gfx950).
+
+Drop-in for the ``flash_attn_wmma`` extension of thebigblender/FlashLite:
+
+    from flashlite_amd import forward_flash2, forward_naive
+    out = forward_flash2(q, k, v, sm_scale=0.0, is_causal=False, out=None)
+
+(``import flash_attn_wmma`` works too, from the repository root.)  The
+functions are the torch binding built from ``csrc/flash_attn.cpp``; the
+kernels are hand-written HIP for gfx950 in ``csrc/*.hip`` behind the C ABI
+declared in ``include/flashlite_attn.h``.  There is no fallback: if the
+extension is not built, importing raises ImportError.
+"""
+
+from __future__ import annotations
+
+import os
+
+import torch  # noqa: F401  (loads libtorch/libc10 before the extension)
+
+_PKG_DIR = os.path.dirname(os.path.abspath(__file__))
+
+try:
+    from . import flash_attn_wmma as _ext
+except ImportError as exc:  # pragma: no cover - exercised only without a build
+    raise ImportError(
+        "flashlite_amd: the HIP extension is not built. Run `python -m flashlite_amd.build` "
+        "(or `python -c 'import __graft_entry__ as g; g.build()'`) from the repository root."
+    ) from exc
+
+forward_flash2 = _ext.forward_flash2
+forward_naive = _ext.forward_naive
+
+__all__ = ["forward_flash2", "forward_naive"]

@@ -1,0 +1,113 @@
+"""In-tree build of the HIP library and the torch binding.
+
+    python -m flashlite_amd.build
+
+1. ``hipcc --offload-arch=gfx950`` compiles the kernels and the C ABI
+   (``csrc/*.hip``) into ``flashlite_amd/libflashlite_attn.so``.
+2. The host C++ compiler compiles the binding (``csrc/flash_attn.cpp``)
+   against the torch headers into
+   ``flashlite_amd/flash_attn_wmma<EXT_SUFFIX>``, linked to the library
+   with an ``$ORIGIN`` rpath.
+
+No hipify step, no JIT cache: both files are written next to this script so
+they travel with the source tree.  Every call rebuilds.
+"""
+
+from __future__ import annotations
+
+import os
+import shutil
+import subprocess
+import sys
+import sysconfig
+
+PKG_DIR = os.path.dirname(os.path.abspath(__file__))
+REPO_DIR = os.path.dirname(PKG_DIR)
+CSRC = os.path.join(PKG_DIR, "csrc")
+INCLUDE = os.path.join(REPO_DIR, "include")
+ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
+ARCH = "gfx950"
+
+LIB_NAME = "libflashlite_attn.so"
+EXT_NAME = "flash_attn_wmma"
+
+HIP_SOURCES = ["fa2_fwd.hip", "naive_fwd.hip", "capi.hip"]
+
+# -packed-fp32-ops: keep the compiler from emitting v_pk_{add,mul,fma}_f32.
+HIP_FLAGS = [
+    f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-shared",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-Wall", "-Wno-unused-command-line-argument",
+]
+
+
+def _run(cmd):
+    proc = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
+    # hipcc's host pass does not know the packed-fp32 target feature; that
+    # warning is expected and dropped from the log.
+    out = "\n".join(line for line in proc.stdout.splitlines()
+                    if "is not a recognized feature for this target" not in line)
+    if proc.returncode != 0:
+        raise RuntimeError(f"build step failed ({proc.returncode}): {' '.join(cmd)}\n{out}")
+    return out
+
+
+def lib_path() -> str:
+    return os.path.join(PKG_DIR, LIB_NAME)
+
+
+def ext_path() -> str:
+    return os.path.join(PKG_DIR, EXT_NAME + sysconfig.get_config_var("EXT_SUFFIX"))
+
+
+def build_library(verbose: bool = False) -> str:
+    hipcc = os.path.join(ROCM, "bin", "hipcc")
+    out = lib_path()
+    tmp = out + ".tmp"
+    cmd = [hipcc, *HIP_FLAGS, f"-I{INCLUDE}", f"-I{CSRC}",
+           *[os.path.join(CSRC, s) for s in HIP_SOURCES], "-o", tmp]
+    log = _run(cmd)
+    if verbose and log.strip():
+        print(log)
+    os.replace(tmp, out)
+    return out
+
+
+def build_extension(verbose: bool = False) -> str:
+    import torch.utils.cpp_extension as ce
+
+    cxx = shutil.which(os.environ.get("CXX", "g++")) or "g++"
+    torch_inc = ce.include_paths(device_type="cuda")
+    torch_lib = ce.library_paths(device_type="cuda")
+    py_inc = sysconfig.get_paths()["include"]
+    abi = int(__import__("torch")._C._GLIBCXX_USE_CXX11_ABI)
+    out = ext_path()
+    tmp = out + ".tmp"
+    cmd = [cxx, "-O2", "-std=c++17", "-fPIC", "-shared", "-fvisibility=hidden",
+           "-D__HIP_PLATFORM_AMD__=1", "-DUSE_ROCM=1", "-DHIPBLAS_V2",
+           f"-D_GLIBCXX_USE_CXX11_ABI={abi}", f"-DTORCH_EXTENSION_NAME={EXT_NAME}",
+           "-DTORCH_API_INCLUDE_EXTENSION_H",
+           *[f"-I{p}" for p in torch_inc], f"-I{py_inc}", f"-I{INCLUDE}",
+           os.path.join(CSRC, "flash_attn.cpp"),
+           f"-L{PKG_DIR}", "-lflashlite_attn",
+           *[f"-L{p}" for p in torch_lib],
+           "-lc10", "-ltorch", "-ltorch_cpu", "-ltorch_python", "-lc10_hip", "-ltorch_hip",
+           f"-L{ROCM}/lib", "-lamdhip64",
+           "-Wl,-rpath,$ORIGIN", *[f"-Wl,-rpath,{p}" for p in torch_lib], f"-Wl,-rpath,{ROCM}/lib",
+           "-o", tmp]
+    log = _run(cmd)
+    if verbose and log.strip():
+        print(log)
+    os.replace(tmp, out)
+    return out
+
+
+def build(verbose: bool = False):
+    lib = build_library(verbose)
+    ext = build_extension(verbose)
+    return lib, ext
+
+
+if __name__ == "__main__":
+    for path in build(verbose="-v" in sys.argv):
+        print("built", os.path.relpath(path, REPO_DIR))

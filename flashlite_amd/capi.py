@@ -1,0 +1,134 @@
+"""ctypes view of the C ABI in ``include/flashlite_attn.h``.
+
+This is the binding a non-torch host (or a test) uses to reach the HIP
+library directly: raw device pointers, sizes, an opaque ``hipStream_t``.
+Loading the library does not touch the GPU.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+
+_PKG_DIR = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_PKG_DIR, "libflashlite_attn.so")
+
+FL_OK = 0
+FL_ERR_INVALID_ARGUMENT = 1
+FL_ERR_UNSUPPORTED = 2
+FL_ERR_MISALIGNED = 3
+FL_ERR_LAUNCH = 4
+FL_ERR_BAD_CONFIG = 5
+
+# Every symbol the header declares.
+EXPORTED = (
+    "fl_attn_fwd_f16",
+    "fl_attn_fwd_f16_cfg",
+    "fl_attn_naive_f16",
+    "fl_attn_last_error",
+    "fl_attn_num_configs",
+    "fl_attn_config_name",
+    "fl_attn_select_config",
+)
+
+
+class FlAttnParams(ctypes.Structure):
+    """Mirror of ``fl_attn_params``."""
+
+    _fields_ = [
+        ("q", ctypes.c_void_p),
+        ("k", ctypes.c_void_p),
+        ("v", ctypes.c_void_p),
+        ("o", ctypes.c_void_p),
+        ("batch", ctypes.c_int64),
+        ("heads", ctypes.c_int64),
+        ("seq_q", ctypes.c_int64),
+        ("seq_k", ctypes.c_int64),
+        ("head_dim", ctypes.c_int64),
+        ("sm_scale", ctypes.c_double),
+        ("causal", ctypes.c_int32),
+    ]
+
+
+class FlashLiteError(RuntimeError):
+    def __init__(self, code: int, message: str):
+        super().__init__(f"[{code}] {message}")
+        self.code = code
+
+
+_lib = None
+
+
+def load(path: str = LIB_PATH) -> ctypes.CDLL:
+    """Load ``libflashlite_attn.so`` (once) and declare its signatures."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(path):
+        raise FileNotFoundError(f"{path} is not built; run `python -m flashlite_amd.build`")
+    lib = ctypes.CDLL(path)
+    P = ctypes.POINTER(FlAttnParams)
+    lib.fl_attn_fwd_f16.argtypes = [P, ctypes.c_void_p]
+    lib.fl_attn_fwd_f16.restype = ctypes.c_int
+    lib.fl_attn_fwd_f16_cfg.argtypes = [P, ctypes.c_int32, ctypes.c_void_p]
+    lib.fl_attn_fwd_f16_cfg.restype = ctypes.c_int
+    lib.fl_attn_naive_f16.argtypes = [P, ctypes.c_void_p]
+    lib.fl_attn_naive_f16.restype = ctypes.c_int
+    lib.fl_attn_last_error.argtypes = []
+    lib.fl_attn_last_error.restype = ctypes.c_char_p
+    lib.fl_attn_num_configs.argtypes = []
+    lib.fl_attn_num_configs.restype = ctypes.c_int
+    lib.fl_attn_config_name.argtypes = [ctypes.c_int32]
+    lib.fl_attn_config_name.restype = ctypes.c_char_p
+    lib.fl_attn_select_config.argtypes = [P]
+    lib.fl_attn_select_config.restype = ctypes.c_int
+    _lib = lib
+    return lib
+
+
+def make_params(q=0, k=0, v=0, o=0, batch=1, heads=1, seq_q=1, seq_k=None, head_dim=64,
+                sm_scale=0.0, causal=False) -> FlAttnParams:
+    """Build a params struct from raw addresses (ints) and sizes."""
+    return FlAttnParams(q or None, k or None, v or None, o or None, batch, heads, seq_q,
+                        seq_q if seq_k is None else seq_k, head_dim, float(sm_scale),
+                        1 if causal else 0)
+
+
+def last_error() -> str:
+    msg = load().fl_attn_last_error()
+    return msg.decode() if msg else ""
+
+
+def check(rc: int) -> None:
+    if rc != FL_OK:
+        raise FlashLiteError(rc, last_error())
+
+
+def fwd(params: FlAttnParams, stream: int = 0, config: int = -1) -> int:
+    """``fl_attn_fwd_f16_cfg``; returns the status code."""
+    return load().fl_attn_fwd_f16_cfg(ctypes.byref(params), config, stream or None)
+
+
+def naive(params: FlAttnParams, stream: int = 0) -> int:
+    """``fl_attn_naive_f16``; returns the status code."""
+    return load().fl_attn_naive_f16(ctypes.byref(params), stream or None)
+
+
+def num_configs() -> int:
+    return load().fl_attn_num_configs()
+
+
+def config_name(cfg: int) -> str | None:
+    n = load().fl_attn_config_name(cfg)
+    return n.decode() if n else None
+
+
+def select_config(params: FlAttnParams) -> int:
+    return load().fl_attn_select_config(ctypes.byref(params))
+
+
+def tensor_params(q, k, v, o, sm_scale=0.0, causal=False) -> FlAttnParams:
+    """Params for torch tensors q, k, v, o of shape [B, H, N, D] (device memory)."""
+    b, h, n, d = q.shape
+    return make_params(q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), b, h, n,
+                       k.shape[2], d, sm_scale, causal)

@@ -1,0 +1,174 @@
+// C-ABI entry points: argument checks, the sm_scale sentinel and prescale,
+// the adaptive tile dispatcher, and the launch.
+//
+// Reference host entries: csrc/kernel_flash2.cu:732-839 (flash2) and
+// csrc/kernel_naive.cu:242-323 (naive).  The torch-tensor checks live in the
+// binding (flash_attn.cpp); here are the checks a raw-pointer caller needs,
+// plus the ones the reference skipped (N_k != N_q, 64-bit sizes, alignment).
+
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstdint>
+
+#include "fl_internal.h"
+#include "flashlite_attn.h"
+
+namespace {
+
+thread_local char g_err[512] = "";
+
+int fail(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+// float(log2 e) widened to double, as the reference multiplies a double
+// sm_scale by its float LOG2_E constant (kernel_flash2.cu:16, :772).
+constexpr double kLog2eF = (double)1.44269504088896340736f;
+
+// sm_scale == 0.0 -> 1/sqrt(D) computed in float (kernel_flash2.cu:769-771).
+double resolve_scale(double s, int64_t d) {
+  if (s == 0.0) return (double)(1.0f / std::sqrt((float)d));
+  return s;
+}
+
+// Shared argument checks; fills `a` on success.
+int check_common(const fl_attn_params* p, fl::FwdArgs* a, const char* who) {
+  if (p == nullptr) return fail(FL_ERR_INVALID_ARGUMENT, "%s: params is NULL", who);
+  if (p->batch < 0 || p->heads < 0 || p->seq_q < 0 || p->seq_k < 0 || p->head_dim < 1)
+    return fail(FL_ERR_INVALID_ARGUMENT,
+                "%s: sizes must be non-negative and head_dim >= 1 (got B=%lld H=%lld N_q=%lld "
+                "N_k=%lld D=%lld)",
+                who, (long long)p->batch, (long long)p->heads, (long long)p->seq_q,
+                (long long)p->seq_k, (long long)p->head_dim);
+  if (p->seq_k != p->seq_q)
+    return fail(FL_ERR_UNSUPPORTED, "%s: N_k (%lld) must equal N_q (%lld)", who,
+                (long long)p->seq_k, (long long)p->seq_q);
+  const double scale = resolve_scale(p->sm_scale, p->head_dim);
+  const float c = (float)(std::fabs(scale) * kLog2eF);
+  if (!std::isfinite(scale) || !std::isfinite(c) || c == 0.0f)
+    return fail(FL_ERR_INVALID_ARGUMENT, "%s: sm_scale*log2(e) must be finite and non-zero (sm_scale=%g)",
+                who, scale);
+  const int64_t bh = p->batch * p->heads;
+  if (p->batch != 0 && bh / p->batch != p->heads)
+    return fail(FL_ERR_UNSUPPORTED, "%s: B*H overflows", who);
+  if (bh > INT32_MAX || p->seq_q > INT32_MAX || p->head_dim > INT32_MAX)
+    return fail(FL_ERR_UNSUPPORTED, "%s: B*H, N and D must each fit in int32", who);
+  a->q = p->q;
+  a->k = p->k;
+  a->v = p->v;
+  a->o = p->o;
+  a->batch_heads = (int)bh;
+  a->seq = (int)p->seq_q;
+  a->head_dim = (int)p->head_dim;
+  a->scale_log2 = c;
+  a->negate = scale < 0.0 ? 1 : 0;
+  a->causal = p->causal ? 1 : 0;
+  return FL_OK;
+}
+
+bool empty_problem(const fl::FwdArgs& a) { return a.batch_heads == 0 || a.seq == 0; }
+
+int check_pointers(const fl_attn_params* p, const char* who, uintptr_t align) {
+  if (!p->q || !p->k || !p->v || !p->o)
+    return fail(FL_ERR_INVALID_ARGUMENT, "%s: q, k, v and o must be non-NULL", who);
+  const uintptr_t m = align - 1;
+  if (((uintptr_t)p->q | (uintptr_t)p->k | (uintptr_t)p->v | (uintptr_t)p->o) & m)
+    return fail(FL_ERR_MISALIGNED, "%s: q, k, v and o must be %u-byte aligned", who, (unsigned)align);
+  return FL_OK;
+}
+
+// Tile-configuration choice for 256 CUs.  Every configuration computes the
+// same result; this only picks the work-group height (32 * waves query rows)
+// so that there are at least two work-groups per CU when the problem allows,
+// and otherwise the smallest height (most work-groups).  It replaces the
+// reference's `seq_len >= 2048 -> Br=128` rule (kernel_flash2.cu:786-789),
+// which was sized for 20 SMs.
+int select_fa2(const fl::FwdArgs& a) {
+  constexpr int64_t kTargetWgs = 2 * 256;
+  for (int cfg = fl::kNumFa2Configs - 1; cfg >= 0; --cfg) {
+    const int64_t br = 32 * fl::kFa2Configs[cfg].waves;
+    const int64_t wgs = (a.seq + br - 1) / br * (int64_t)a.batch_heads;
+    if (wgs >= kTargetWgs) return cfg;
+  }
+  return 0;
+}
+
+int check_fa2(const fl_attn_params* p, fl::FwdArgs* a) {
+  const char* who = "fl_attn_fwd_f16";
+  int rc = check_common(p, a, who);
+  if (rc != FL_OK) return rc;
+  if (p->head_dim != 64)
+    return fail(FL_ERR_UNSUPPORTED, "FlashLite WMMA kernel currently requires head_dim == 64");
+  // Grid = ceil(N/32) * B*H work-groups at the smallest tile; per-head
+  // offsets are 64-bit in the kernel.
+  if (((int64_t)a->seq + 31) / 32 * (int64_t)a->batch_heads > INT32_MAX)
+    return fail(FL_ERR_UNSUPPORTED, "%s: too many work-groups (B*H*ceil(N/32) > 2^31-1)", who);
+  return FL_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* fl_attn_last_error(void) { return g_err; }
+
+int fl_attn_num_configs(void) { return fl::kNumFa2Configs; }
+
+const char* fl_attn_config_name(int32_t config) {
+  if (config < 0 || config >= fl::kNumFa2Configs) return nullptr;
+  return fl::kFa2Configs[config].name;
+}
+
+int fl_attn_select_config(const fl_attn_params* p) {
+  fl::FwdArgs a;
+  if (check_fa2(p, &a) != FL_OK) return -1;
+  return select_fa2(a);
+}
+
+int fl_attn_fwd_f16_cfg(const fl_attn_params* p, int32_t config, void* stream) {
+  fl::FwdArgs a;
+  int rc = check_fa2(p, &a);
+  if (rc != FL_OK) return rc;
+  if (config < -1 || config >= fl::kNumFa2Configs)
+    return fail(FL_ERR_BAD_CONFIG, "fl_attn_fwd_f16: config %d out of range [-1, %d)", (int)config,
+                fl::kNumFa2Configs);
+  if (empty_problem(a)) return FL_OK;
+  rc = check_pointers(p, "fl_attn_fwd_f16", 16);
+  if (rc != FL_OK) return rc;
+  const int cfg = config < 0 ? select_fa2(a) : config;
+  const hipError_t e = fl::launch_fa2(a, cfg, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess)
+    return fail(FL_ERR_LAUNCH, "fl_attn_fwd_f16: launch failed: %s", hipGetErrorString(e));
+  return FL_OK;
+}
+
+int fl_attn_fwd_f16(const fl_attn_params* p, void* stream) {
+  return fl_attn_fwd_f16_cfg(p, -1, stream);
+}
+
+int fl_attn_naive_f16(const fl_attn_params* p, void* stream) {
+  const char* who = "fl_attn_naive_f16";
+  fl::FwdArgs a;
+  int rc = check_common(p, &a, who);
+  if (rc != FL_OK) return rc;
+  if (empty_problem(a)) return FL_OK;
+  if (a.seq > fl::naive_max_seq(a.head_dim))
+    return fail(FL_ERR_UNSUPPORTED, "%s: N=%d exceeds the LDS capacity of the naive kernel (max %lld at D=%d)",
+                who, a.seq, (long long)fl::naive_max_seq(a.head_dim), a.head_dim);
+  if (a.batch_heads > 65535)
+    return fail(FL_ERR_UNSUPPORTED, "%s: B*H=%d exceeds the grid limit 65535", who, a.batch_heads);
+  rc = check_pointers(p, who, 2);
+  if (rc != FL_OK) return rc;
+  const hipError_t e = fl::launch_naive(a, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return fail(FL_ERR_LAUNCH, "%s: launch failed: %s", who, hipGetErrorString(e));
+  return FL_OK;
+}
+
+}  // extern "C"

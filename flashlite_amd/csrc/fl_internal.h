@@ -1,0 +1,42 @@
+// Internal interface between the C-ABI layer (capi.hip) and the gfx950
+// kernels (fa2_fwd.hip, naive_fwd.hip).  Host-side only types.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace fl {
+
+// Arguments shared by every forward launch.  Sizes are validated by the
+// C-ABI layer before a launch function sees them.
+struct FwdArgs {
+  const void* q;
+  const void* k;
+  const void* v;
+  void* o;
+  int batch_heads;   // B*H
+  int seq;           // N (== N_k)
+  int head_dim;      // D
+  float scale_log2;  // |sm_scale| * log2(e), always > 0
+  int negate;        // 1 when sm_scale < 0: the kernel flips the sign of Q
+  int causal;
+};
+
+// One FA2 tile configuration: `waves` waves of 64 lanes, each owning 32
+// query rows, so a work-group covers 32*waves queries; KV tiles of 64 keys.
+struct Fa2Config {
+  int waves;
+  const char* name;
+};
+
+constexpr int kNumFa2Configs = 4;
+extern const Fa2Config kFa2Configs[kNumFa2Configs];
+
+// Launches the FA2 kernel for configuration `cfg` on `stream`.
+hipError_t launch_fa2(const FwdArgs& a, int cfg, hipStream_t stream);
+
+// Largest seq the naive kernel can stage in LDS for this head_dim.
+int64_t naive_max_seq(int64_t head_dim);
+hipError_t launch_naive(const FwdArgs& a, hipStream_t stream);
+
+}  // namespace fl

@@ -1,0 +1,146 @@
+// PyTorch-ROCm binding of the `flash_attn_wmma` module: the drop-in
+// replacement of the reference's csrc/flash_attn.cpp:4-29 (same module name,
+// function names, argument names, defaults and return values).
+//
+// The torch-side half of the reference host entries lives here, with the
+// reference's checks in the reference's order and with its messages:
+//   forward_flash2: csrc/kernel_flash2.cu:741-767,
+//   forward_naive:  csrc/kernel_naive.cu:252-276, 285.
+// Then the call goes through the C ABI (include/flashlite_attn.h) on the
+// current HIP stream of the tensors' device.  A non-zero status becomes a
+// RuntimeError carrying the library's message (the reference's CUDA_CHECK,
+// csrc/includes/flash_attn.h:15-22).  Plain C++: compiled by the host
+// compiler, no hipify.
+
+#include <torch/extension.h>
+
+// ROCm PyTorch reports HIP devices as device type `cuda`; its HIP guard and
+// stream accessors for that case are the "MasqueradingAsCUDA" variants.
+#include <ATen/hip/impl/HIPGuardImplMasqueradingAsCUDA.h>
+#include <ATen/hip/impl/HIPStreamMasqueradingAsCUDA.h>
+
+#include <optional>
+
+#include "flashlite_attn.h"
+
+namespace flash_attn {
+
+namespace {
+
+void* current_stream(const torch::Tensor& t) {
+  return static_cast<void*>(
+      c10::hip::getCurrentHIPStreamMasqueradingAsCUDA(t.device().index()).stream());
+}
+
+fl_attn_params make_params(const torch::Tensor& q, const torch::Tensor& k, const torch::Tensor& v,
+                           torch::Tensor& o, double sm_scale, bool is_causal) {
+  fl_attn_params p;
+  p.q = q.data_ptr();
+  p.k = k.data_ptr();
+  p.v = v.data_ptr();
+  p.o = o.data_ptr();
+  p.batch = q.size(0);
+  p.heads = q.size(1);
+  p.seq_q = q.size(2);
+  p.seq_k = k.size(2);
+  p.head_dim = q.size(3);
+  p.sm_scale = sm_scale;
+  p.causal = is_causal ? 1 : 0;
+  return p;
+}
+
+void check_same_device(const torch::Tensor& q, const torch::Tensor& k, const torch::Tensor& v) {
+  TORCH_CHECK(k.device() == q.device() && v.device() == q.device(),
+              "All tensors must be on the same device");
+}
+
+}  // namespace
+
+torch::Tensor flash_attn_forward_naive(torch::Tensor q, torch::Tensor k, torch::Tensor v,
+                                       double sm_scale, bool is_causal) {
+  TORCH_CHECK(q.is_cuda(), "Query tensor must be on CUDA");
+  TORCH_CHECK(k.is_cuda(), "Key tensor must be on CUDA");
+  TORCH_CHECK(v.is_cuda(), "Value tensor must be on CUDA");
+
+  TORCH_CHECK(q.is_contiguous(), "Query tensor must be contiguous");
+  TORCH_CHECK(k.is_contiguous(), "Key tensor must be contiguous");
+  TORCH_CHECK(v.is_contiguous(), "Value tensor must be contiguous");
+
+  TORCH_CHECK(q.dtype() == torch::kHalf, "Query tensor must be FP16 (Half)");
+  TORCH_CHECK(k.dtype() == torch::kHalf, "Key tensor must be FP16 (Half)");
+  TORCH_CHECK(v.dtype() == torch::kHalf, "Value tensor must be FP16 (Half)");
+
+  TORCH_CHECK(q.dim() == 4, "Query tensor must have 4 dimensions [B, H, N, D]");
+  TORCH_CHECK(k.dim() == 4, "Key tensor must have 4 dimensions [B, H, N, D]");
+  TORCH_CHECK(v.dim() == 4, "Value tensor must have 4 dimensions [B, H, N, D]");
+
+  TORCH_CHECK(k.size(0) == q.size(0) && k.size(1) == q.size(1) && k.size(3) == q.size(3),
+              "Key dimensions must match Query dimensions [B, H, N_k, D]");
+  TORCH_CHECK(v.size(0) == q.size(0) && v.size(1) == q.size(1) && v.size(2) == k.size(2) &&
+                  v.size(3) == q.size(3),
+              "Value dimensions must match Key dimensions [B, H, N_k, D]");
+  check_same_device(q, k, v);
+
+  auto out = torch::empty_like(q);
+
+  const c10::hip::HIPGuardMasqueradingAsCUDA guard(q.device());
+  fl_attn_params p = make_params(q, k, v, out, sm_scale, is_causal);
+  const int rc = fl_attn_naive_f16(&p, current_stream(q));
+  TORCH_CHECK(rc == FL_OK, "FlashLite HIP error: ", fl_attn_last_error());
+  return out;
+}
+
+torch::Tensor flash_attn_forward_flash2(torch::Tensor q, torch::Tensor k, torch::Tensor v,
+                                        double sm_scale, bool is_causal,
+                                        std::optional<torch::Tensor> out) {
+  TORCH_CHECK(q.is_cuda() && k.is_cuda() && v.is_cuda(), "All tensors must be on CUDA");
+  TORCH_CHECK(q.is_contiguous() && k.is_contiguous() && v.is_contiguous(),
+              "All tensors must be contiguous");
+  TORCH_CHECK(q.dtype() == torch::kHalf && k.dtype() == torch::kHalf && v.dtype() == torch::kHalf,
+              "All tensors must be FP16 (Half)");
+  TORCH_CHECK(q.dim() == 4 && k.dim() == 4 && v.dim() == 4, "Tensors must be 4D [B, H, N, D]");
+
+  const int64_t batch_size = q.size(0);
+  const int64_t num_heads = q.size(1);
+  const int64_t head_dim = q.size(3);
+
+  TORCH_CHECK(k.size(0) == batch_size && k.size(1) == num_heads && k.size(3) == head_dim,
+              "Key dimensions must match Query dimensions [B, H, N_k, D]");
+  TORCH_CHECK(v.size(0) == batch_size && v.size(1) == num_heads && v.size(2) == k.size(2) &&
+                  v.size(3) == head_dim,
+              "Value dimensions must match Key dimensions [B, H, N_k, D]");
+  TORCH_CHECK(head_dim == 64, "FlashLite WMMA kernel currently requires head_dim == 64");
+  check_same_device(q, k, v);
+
+  torch::Tensor out_tensor;
+  if (out.has_value() && out.value().defined()) {
+    out_tensor = out.value();
+    TORCH_CHECK(out_tensor.is_cuda() && out_tensor.is_contiguous(),
+                "out tensor must be contiguous CUDA tensor");
+    TORCH_CHECK(out_tensor.sizes() == q.sizes(), "out tensor shape must match q");
+    TORCH_CHECK(out_tensor.dtype() == torch::kHalf, "out tensor dtype must be FP16");
+    TORCH_CHECK(out_tensor.device() == q.device(), "out tensor must be on the same device as q");
+  } else {
+    out_tensor = torch::empty_like(q);
+  }
+
+  const c10::hip::HIPGuardMasqueradingAsCUDA guard(q.device());
+  fl_attn_params p = make_params(q, k, v, out_tensor, sm_scale, is_causal);
+  const int rc = fl_attn_fwd_f16(&p, current_stream(q));
+  TORCH_CHECK(rc == FL_OK, "FlashLite HIP error: ", fl_attn_last_error());
+  return out_tensor;
+}
+
+}  // namespace flash_attn
+
+PYBIND11_MODULE(flash_attn_wmma, m) {
+  m.doc() = "FlashAttention-2 forward for AMD Instinct MI355X (gfx950): MFMA + LDS HIP kernels";
+
+  m.def("forward_naive", &flash_attn::flash_attn_forward_naive,
+        "Naive attention forward (HIP baseline, one work-group per query row)", py::arg("q"),
+        py::arg("k"), py::arg("v"), py::arg("sm_scale") = 0.0, py::arg("is_causal") = false);
+
+  m.def("forward_flash2", &flash_attn::flash_attn_forward_flash2,
+        "FlashAttention-2 forward (gfx950 MFMA)", py::arg("q"), py::arg("k"), py::arg("v"),
+        py::arg("sm_scale") = 0.0, py::arg("is_causal") = false, py::arg("out") = py::none());
+}

@@ -1,0 +1,99 @@
+/*
+ * flashlite_attn.h -- C ABI of the MI355X (gfx950) FlashAttention-2 forward
+ * engine.  Plain pointers and sizes only: no torch, no HIP types.  The
+ * stream is passed as an opaque `void*` holding a `hipStream_t` (NULL = the
+ * legacy default stream).
+ *
+ * Reference surface replaced (thebigblender/FlashLite):
+ *   - the host entry of `flash_attn_wmma.forward_flash2`,
+ *     csrc/kernel_flash2.cu:732-839 (declared csrc/includes/flash_attn.h:117-124,
+ *     bound at csrc/flash_attn.cpp:18-28);
+ *   - the host entry of `flash_attn_wmma.forward_naive`,
+ *     csrc/kernel_naive.cu:242-323 (declared csrc/includes/flash_attn.h:100-106,
+ *     bound at csrc/flash_attn.cpp:7-16).
+ * The torch-side checks (device, contiguity, dtype, rank, shapes, `out=`) stay
+ * in the binding (flashlite_amd/csrc/flash_attn.cpp) with the reference's
+ * messages; the checks below are the ones a raw-pointer caller needs.
+ *
+ * Layout: q, k, v, o are fp16 [batch, heads, seq, head_dim], contiguous.
+ * The library allocates nothing, never synchronises, keeps no mutable global
+ * state and may be called from several host threads at once.  Launches are
+ * asynchronous on `stream`; results are visible after the stream reaches
+ * them.  `o` may alias `q` (each work-group reads its own query rows before
+ * it writes them); it must not alias `k` or `v`.
+ */
+#ifndef FLASHLITE_ATTN_H
+#define FLASHLITE_ATTN_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Status codes returned by every entry point. */
+enum fl_status {
+  FL_OK = 0,
+  FL_ERR_INVALID_ARGUMENT = 1, /* NULL pointer, negative size, non-finite scale */
+  FL_ERR_UNSUPPORTED = 2,      /* head_dim != 64 (flash2), seq_k != seq_q, sizes past limits */
+  FL_ERR_MISALIGNED = 3,       /* flash2 needs 16-byte aligned q/k/v/o */
+  FL_ERR_LAUNCH = 4,           /* the HIP launch itself failed */
+  FL_ERR_BAD_CONFIG = 5        /* forced tile configuration out of range */
+};
+
+typedef struct fl_attn_params {
+  const void* q;      /* fp16 [B, H, N, D] */
+  const void* k;      /* fp16 [B, H, N, D] */
+  const void* v;      /* fp16 [B, H, N, D] */
+  void* o;            /* fp16 [B, H, N, D], written for rows < N */
+  int64_t batch;      /* B */
+  int64_t heads;      /* H */
+  int64_t seq_q;      /* N (query rows) */
+  int64_t seq_k;      /* key/value rows; must equal seq_q */
+  int64_t head_dim;   /* D */
+  double sm_scale;    /* 0.0 means 1/sqrt(D) (kernel_flash2.cu:769-771) */
+  int32_t causal;     /* non-zero: key j visible to query i iff j <= i */
+} fl_attn_params;
+
+/*
+ * FlashAttention-2 forward, fp16 in/out, fp32 accumulation, D == 64.
+ * Replaces flash_attn_forward_flash2's validation tail, scale handling,
+ * adaptive dispatcher and launch (csrc/kernel_flash2.cu:756-757, 769-772,
+ * 786-837).  The tile configuration comes from the built-in dispatcher.
+ */
+int fl_attn_fwd_f16(const fl_attn_params* p, void* stream);
+
+/*
+ * Same as fl_attn_fwd_f16 with the tile configuration forced (`config` in
+ * [0, fl_attn_num_configs()), or -1 for the dispatcher's choice).  Replaces
+ * the reference's two hard-wired launch branches (Br=64 / Br=128,
+ * csrc/kernel_flash2.cu:789-835); used by sweeps and by tests that check
+ * every configuration against the oracle.
+ */
+int fl_attn_fwd_f16_cfg(const fl_attn_params* p, int32_t config, void* stream);
+
+/*
+ * Un-fused baseline: one work-group per query row, scores staged in LDS.
+ * Any head_dim >= 1; seq limited by LDS (about 40k keys at D=64).
+ * Replaces flash_attn_forward_naive's scale handling and launch
+ * (csrc/kernel_naive.cu:278-320), without the reference's shared-memory
+ * write-after-read race between its two block reductions (:66 vs :81-83).
+ */
+int fl_attn_naive_f16(const fl_attn_params* p, void* stream);
+
+/* Detail message of the last non-OK status on the calling thread. */
+const char* fl_attn_last_error(void);
+
+/* Dispatcher introspection (no counterpart in the reference, whose dispatch
+ * rule is the fixed `seq_len >= 2048` test at csrc/kernel_flash2.cu:789). */
+int fl_attn_num_configs(void);
+const char* fl_attn_config_name(int32_t config);
+/* Returns the configuration fl_attn_fwd_f16 would launch for `p`, or -1 if
+ * `p` is rejected (the reason is in fl_attn_last_error()). */
+int fl_attn_select_config(const fl_attn_params* p);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FLASHLITE_ATTN_H */

@@ -1,0 +1,54 @@
+"""Helpers shared by the GPU tests: run the HIP library through its C ABI on
+torch-allocated device memory and compare with the CPU oracle."""
+
+import numpy as np
+
+from flashlite_amd import capi
+from oracle import attention_fp32, error_stats
+
+# north_star tolerance for fp16 outputs against the fp32 oracle
+MAX_ABS = 2e-3
+MEAN_ABS = 2e-4
+
+
+def to_dev(x, dev):
+    import torch
+
+    return torch.from_numpy(np.ascontiguousarray(x)).to(dev)
+
+
+def run_capi(q16, k16, v16, sm_scale, causal, dev, config=-1, naive=False, out_fill=float("nan")):
+    """Launch through the C ABI; unwritten outputs stay NaN and fail later."""
+    import torch
+
+    tq, tk, tv = (to_dev(x, dev) for x in (q16, k16, v16))
+    o = torch.full_like(tq, out_fill)
+    p = capi.tensor_params(tq, tk, tv, o, sm_scale, causal)
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    rc = capi.naive(p, stream) if naive else capi.fwd(p, stream, config)
+    capi.check(rc)
+    torch.cuda.synchronize(dev)
+    return o.cpu().numpy()
+
+
+def sample_rows(n, count=256, seed=0):
+    """Query rows to check on big shapes: both ends, block edges, random."""
+    rs = np.random.RandomState(seed)
+    rows = set(range(min(n, 40))) | set(range(max(0, n - 40), n))
+    for edge in range(0, n, 128):
+        for r in (edge - 1, edge, edge + 31, edge + 32, edge + 63, edge + 64):
+            if 0 <= r < n:
+                rows.add(r)
+    rows |= set(rs.randint(0, n, size=min(count, n)).tolist())
+    return np.array(sorted(rows), dtype=np.int64)
+
+
+def assert_close_oracle(out, q16, k16, v16, sm_scale, causal, rows=None, max_abs=MAX_ABS,
+                        mean_abs=MEAN_ABS, ref=None):
+    if ref is None:
+        ref = attention_fp32(q16, k16, v16, sm_scale, causal, rows=rows)
+    got = out if rows is None else out[:, :, rows]
+    assert np.isfinite(got).all(), "non-finite (or unwritten) outputs"
+    mx, mean = error_stats(got, ref)
+    assert mx <= max_abs and mean <= mean_abs, f"max-abs {mx:.3e} mean-abs {mean:.3e}"
+    return mx, mean

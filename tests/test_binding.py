@@ -1,0 +1,177 @@
+"""The torch binding `flash_attn_wmma`: same surface as the reference module
+(csrc/flash_attn.cpp:4-29) and the reference host checks in order with their
+messages (csrc/kernel_flash2.cu:741-764, csrc/kernel_naive.cu:252-276)."""
+
+import inspect  # noqa: F401
+import math
+
+import numpy as np
+import pytest
+import torch
+
+import flash_attn_wmma
+import flashlite_amd
+
+
+def test_import_names():
+    assert flash_attn_wmma.forward_flash2 is flashlite_amd.forward_flash2
+    assert flash_attn_wmma.forward_naive is flashlite_amd.forward_naive
+    # the binding lives in-tree, next to the HIP library it links
+    mod = flashlite_amd._ext
+    assert mod.__name__ == "flashlite_amd.flash_attn_wmma"
+
+
+def test_signatures_and_defaults():
+    doc = flash_attn_wmma.forward_flash2.__doc__
+    assert doc.startswith("forward_flash2(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, "
+                          "sm_scale: typing.SupportsFloat = 0.0, is_causal: bool = False, "
+                          "out: torch.Tensor | None = None) -> torch.Tensor")
+    doc = flash_attn_wmma.forward_naive.__doc__
+    assert doc.startswith("forward_naive(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, "
+                          "sm_scale: typing.SupportsFloat = 0.0, is_causal: bool = False) "
+                          "-> torch.Tensor")
+
+
+def _cpu(shape=(1, 2, 8, 64), dtype=torch.float16):
+    return torch.zeros(shape, dtype=dtype)
+
+
+def test_cpu_tensors_rejected_first():
+    q = _cpu()
+    with pytest.raises(RuntimeError, match="All tensors must be on CUDA"):
+        flash_attn_wmma.forward_flash2(q, q, q)
+    with pytest.raises(RuntimeError, match="Query tensor must be on CUDA"):
+        flash_attn_wmma.forward_naive(q, q, q)
+    # the device check precedes every other check, as in the reference
+    with pytest.raises(RuntimeError, match="All tensors must be on CUDA"):
+        flash_attn_wmma.forward_flash2(_cpu((2, 3), torch.float32), q, q)
+
+
+# --- on the GPU: the rest of the validation chain and the call forms --------
+
+def _g(shape=(1, 2, 8, 64), dtype=torch.float16, dev="cuda"):
+    return torch.randn(shape, device=dev).to(dtype)
+
+
+@pytest.mark.gpu
+def test_flash2_validation_order(cuda):
+    f = flash_attn_wmma.forward_flash2
+    q = _g()
+    nc = _g((1, 2, 64, 8)).transpose(2, 3)
+    cases = [
+        ((q, q.cpu(), q), "All tensors must be on CUDA"),
+        ((q, nc, q), "All tensors must be contiguous"),
+        ((q, q.float(), q), "All tensors must be FP16"),
+        ((q, q, _g((2, 8, 64))), "Tensors must be 4D"),
+        ((q, _g((1, 3, 8, 64)), q), "Key dimensions must match"),
+        ((q, q, _g((1, 2, 9, 64))), "Value dimensions must match"),
+        ((_g((1, 2, 8, 32)),) * 3, "requires head_dim == 64"),
+    ]
+    for args, msg in cases:
+        with pytest.raises(RuntimeError, match=msg):
+            f(*args)
+    # N_k != N_q passes the reference checks but is rejected by the library
+    k = _g((1, 2, 16, 64))
+    with pytest.raises(RuntimeError, match="N_k"):
+        f(q, k, k)
+
+
+@pytest.mark.gpu
+def test_flash2_out_validation(cuda):
+    f = flash_attn_wmma.forward_flash2
+    q = _g()
+    with pytest.raises(RuntimeError, match="out tensor must be contiguous CUDA tensor"):
+        f(q, q, q, out=torch.empty_like(q).cpu())
+    with pytest.raises(RuntimeError, match="out tensor shape must match q"):
+        f(q, q, q, out=_g((1, 2, 9, 64)))
+    with pytest.raises(RuntimeError, match="out tensor dtype must be FP16"):
+        f(q, q, q, out=torch.empty_like(q, dtype=torch.float32))
+
+
+@pytest.mark.gpu
+def test_naive_validation_order(cuda):
+    f = flash_attn_wmma.forward_naive
+    q = _g()
+    nc = _g((1, 2, 64, 8)).transpose(2, 3)
+    cases = [
+        ((q, q.cpu(), q), "Key tensor must be on CUDA"),
+        ((q, q, nc), "Value tensor must be contiguous"),
+        ((q.float(), q, q), "Query tensor must be FP16"),
+        ((q, _g((2, 8, 64)), q), "Key tensor must have 4 dimensions"),
+        ((q, _g((2, 2, 8, 64)), q), "Key dimensions must match"),
+        ((q, q, _g((1, 2, 8, 63))), "Value dimensions must match"),
+    ]
+    for args, msg in cases:
+        with pytest.raises(RuntimeError, match=msg):
+            f(*args)
+
+
+@pytest.mark.gpu
+def test_flash2_call_forms_and_out_buffer(cuda):
+    from oracle import attention_fp32, error_stats
+    from flashlite_amd.workloads import make_qkv
+
+    q16, k16, v16 = make_qkv(2, 4, 256, 64, seed=91)
+    q, k, v = (torch.from_numpy(x).to(cuda) for x in (q16, k16, v16))
+    sm = 1.0 / math.sqrt(64)
+    a = flash_attn_wmma.forward_flash2(q, k, v, sm, True)              # positional
+    b = flash_attn_wmma.forward_flash2(q, k, v, sm_scale=sm, is_causal=True)
+    c = flash_attn_wmma.forward_flash2(q, k, v, is_causal=True)        # sentinel default
+    buf = torch.empty_like(q)
+    d = flash_attn_wmma.forward_flash2(q, k, v, sm, True, out=buf)
+    assert d.data_ptr() == buf.data_ptr()
+    for x in (b, c, d):
+        assert torch.equal(a, x)
+    assert a.shape == q.shape and a.dtype == torch.float16
+    ref = attention_fp32(q16, k16, v16, sm, True)
+    mx, mean = error_stats(a.cpu().numpy(), ref)
+    assert mx <= 2e-3 and mean <= 2e-4
+    # default is non-causal
+    nc = flash_attn_wmma.forward_flash2(q, k, v)
+    mx, mean = error_stats(nc.cpu().numpy(), attention_fp32(q16, k16, v16, 0.0, False))
+    assert mx <= 2e-3 and mean <= 2e-4
+
+
+@pytest.mark.gpu
+def test_flash2_out_reused_many_times(cuda):
+    # the C4 usage pattern: one preallocated buffer, many calls
+    from flashlite_amd.workloads import make_qkv
+
+    q16, k16, v16 = make_qkv(4, 4, 256, 64, seed=92)
+    q, k, v = (torch.from_numpy(x).to(cuda) for x in (q16, k16, v16))
+    buf = torch.empty_like(q)
+    first = flash_attn_wmma.forward_flash2(q, k, v, 0.125, True, out=buf).clone()
+    for _ in range(20):
+        flash_attn_wmma.forward_flash2(q, k, v, 0.125, True, out=buf)
+    assert torch.equal(buf, first)
+
+
+@pytest.mark.gpu
+def test_naive_via_binding(cuda):
+    from oracle import attention_fp32, error_stats
+    from flashlite_amd.workloads import make_qkv
+
+    q16, k16, v16 = make_qkv(1, 4, 300, 64, seed=93)
+    q, k, v = (torch.from_numpy(x).to(cuda) for x in (q16, k16, v16))
+    for causal in (False, True):
+        o = flash_attn_wmma.forward_naive(q, k, v, 0.125, causal)
+        mx, mean = error_stats(o.cpu().numpy(), attention_fp32(q16, k16, v16, 0.125, causal))
+        assert mx <= 2e-3 and mean <= 2e-4
+
+
+@pytest.mark.gpu
+def test_current_stream_is_used(cuda):
+    from flashlite_amd.workloads import make_qkv
+
+    q16, k16, v16 = make_qkv(2, 8, 1024, 64, seed=94)
+    q, k, v = (torch.from_numpy(x).to(cuda) for x in (q16, k16, v16))
+    ref = flash_attn_wmma.forward_flash2(q, k, v, 0.125, False)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        out = torch.empty_like(q)
+        for _ in range(3):
+            flash_attn_wmma.forward_flash2(q, k, v, 0.125, False, out=out)
+    torch.cuda.current_stream().wait_stream(s)
+    assert torch.equal(out, ref)
+    assert np.isfinite(out.float().cpu().numpy()).all()

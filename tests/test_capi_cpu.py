@@ -1,0 +1,127 @@
+"""The C-ABI library on a machine without a GPU: it loads, exports every
+symbol the header declares, and rejects bad arguments before any launch.
+No call here reaches the GPU (each returns from validation)."""
+
+import ctypes
+import os
+import re
+
+import pytest
+
+from flashlite_amd import capi
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "flashlite_attn.h")
+
+# Fake, 256-byte aligned device addresses: never dereferenced by these tests.
+A = 0x7F0000000000
+
+
+def test_library_loads_and_exports_header_symbols():
+    lib = capi.load()
+    with open(HEADER) as f:
+        text = f.read()
+    declared = set(re.findall(r"^\s*(?:int|const char\*)\s+(fl_\w+)\s*\(", text, re.M))
+    assert declared == set(capi.EXPORTED)
+    for name in declared:
+        assert isinstance(getattr(lib, name), ctypes._CFuncPtr)
+
+
+def test_config_table():
+    assert capi.num_configs() == 4
+    names = [capi.config_name(i) for i in range(4)]
+    assert names == ["br32_bc64_w1", "br64_bc64_w2", "br128_bc64_w4", "br256_bc64_w8"]
+    assert capi.config_name(4) is None and capi.config_name(-1) is None
+
+
+def _p(**kw):
+    base = dict(q=A, k=A + 0x100000, v=A + 0x200000, o=A + 0x300000, batch=2, heads=8,
+                seq_q=4096, head_dim=64, sm_scale=0.125, causal=False)
+    base.update(kw)
+    return capi.make_params(**base)
+
+
+def test_null_params():
+    lib = capi.load()
+    assert lib.fl_attn_fwd_f16(None, None) == capi.FL_ERR_INVALID_ARGUMENT
+    assert "NULL" in capi.last_error()
+    assert lib.fl_attn_naive_f16(None, None) == capi.FL_ERR_INVALID_ARGUMENT
+
+
+def test_head_dim_must_be_64_for_flash2():
+    assert capi.fwd(_p(head_dim=128)) == capi.FL_ERR_UNSUPPORTED
+    assert capi.last_error() == "FlashLite WMMA kernel currently requires head_dim == 64"
+
+
+def test_seq_k_must_equal_seq_q():
+    assert capi.fwd(_p(seq_k=100)) == capi.FL_ERR_UNSUPPORTED
+    assert "N_k" in capi.last_error()
+    assert capi.naive(_p(seq_k=100)) == capi.FL_ERR_UNSUPPORTED
+
+
+def test_negative_sizes():
+    assert capi.fwd(_p(batch=-1)) == capi.FL_ERR_INVALID_ARGUMENT
+    assert capi.naive(_p(head_dim=0)) == capi.FL_ERR_INVALID_ARGUMENT
+
+
+def test_null_pointers_and_alignment():
+    assert capi.fwd(_p(o=0)) == capi.FL_ERR_INVALID_ARGUMENT
+    assert capi.fwd(_p(k=A + 8)) == capi.FL_ERR_MISALIGNED
+    assert "16-byte" in capi.last_error()
+    # the naive kernel reads fp16 scalars: 2-byte alignment suffices, 1 does not
+    assert capi.naive(_p(k=A + 1, seq_q=16)) == capi.FL_ERR_MISALIGNED
+
+
+def test_non_finite_scale():
+    assert capi.fwd(_p(sm_scale=float("inf"))) == capi.FL_ERR_INVALID_ARGUMENT
+    assert capi.fwd(_p(sm_scale=float("nan"))) == capi.FL_ERR_INVALID_ARGUMENT
+    assert capi.fwd(_p(sm_scale=1e-300)) == capi.FL_ERR_INVALID_ARGUMENT  # underflows to 0
+
+
+def test_bad_config():
+    assert capi.fwd(_p(), config=4) == capi.FL_ERR_BAD_CONFIG
+    assert capi.fwd(_p(), config=-2) == capi.FL_ERR_BAD_CONFIG
+
+
+def test_empty_problems_are_noops():
+    # zero-size work returns OK without touching pointers or the device
+    for kw in (dict(seq_q=0), dict(batch=0), dict(heads=0)):
+        p = _p(q=0, k=0, v=0, o=0, **kw)
+        assert capi.fwd(p) == capi.FL_OK
+        assert capi.naive(p) == capi.FL_OK
+
+
+def test_naive_limits():
+    assert capi.naive(_p(seq_q=1 << 20)) == capi.FL_ERR_UNSUPPORTED
+    assert "LDS" in capi.last_error()
+    assert capi.naive(_p(batch=256, heads=512, seq_q=16)) == capi.FL_ERR_UNSUPPORTED
+
+
+def test_dispatcher_choices():
+    # At least two work-groups per CU (512) when the problem allows, else the
+    # smallest tile height.
+    sel = lambda **kw: capi.select_config(_p(**kw))  # noqa: E731
+    assert sel(batch=2, heads=8, seq_q=4096) == 2     # 512 WGs of 128 rows
+    assert sel(batch=1, heads=16, seq_q=16384) == 3   # 1024 WGs of 256 rows
+    assert sel(batch=32, heads=32, seq_q=256) == 3    # 1024 WGs of 256 rows
+    assert sel(batch=2, heads=8, seq_q=512) == 0      # 256 WGs of 32 rows
+    assert sel(batch=1, heads=1, seq_q=128) == 0
+    assert sel(head_dim=80) == -1
+
+
+@pytest.mark.parametrize("fn", ["fwd", "naive"])
+def test_error_message_is_thread_local(fn):
+    import threading
+
+    seen = {}
+
+    def worker():
+        getattr(capi, fn)(_p(seq_k=3))
+        seen["msg"] = capi.last_error()
+
+    capi.fwd(_p(head_dim=128))
+    t = threading.Thread(target=worker)
+    t.start()
+    t.join()
+    assert "N_k" in seen["msg"]
+    assert capi.last_error() == "FlashLite WMMA kernel currently requires head_dim == 64"
