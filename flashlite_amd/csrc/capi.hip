@@ -92,7 +92,7 @@ int check_pointers(const fl_attn_params* p, const char* who, uintptr_t align) {
 // which was sized for 20 SMs.
 int select_fa2(const fl::FwdArgs& a) {
   constexpr int64_t kTargetWgs = 2 * 256;
-  for (int cfg = fl::kNumFa2Configs - 1; cfg >= 0; --cfg) {
+  for (int cfg = 3; cfg >= 0; --cfg) {
     const int64_t br = 32 * fl::kFa2Configs[cfg].waves;
     const int64_t wgs = (a.seq + br - 1) / br * (int64_t)a.batch_heads;
     if (wgs >= kTargetWgs) return cfg;

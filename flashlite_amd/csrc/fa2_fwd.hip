@@ -10,18 +10,19 @@
 //   keys >= N masked, query rows >= N never written (:373, :380),
 //   P rounded to fp16 before the PV product (:278-285), fp32 row sums.
 //
-// Work decomposition.  A work-group of W waves owns 32*W consecutive query
-// rows of one (batch, head); wave w owns 32 of them.  The KV sequence is
-// walked in tiles of 64 keys staged in LDS (double-buffered, one barrier per
-// tile) and shared by the W waves.
+// Work decomposition.  A work-group owns 32*W consecutive query rows of one
+// (batch, head); each of its W waves owns 32 of them (struct Rows below).
+// The KV sequence is walked in tiles of 64 keys staged in LDS and shared by
+// the W waves.
 //
 // MFMA formulation (v_mfma_f32_32x32x16_f16, 64 lanes, lane l: column l%32,
 // k-group g = l/32):
-//   GEMM1  S^T[key][query] = K . Q^T   A = K rows from LDS (ds_read_b128),
-//                                      B = the wave's Q rows, held in VGPRs.
+//   GEMM1  S^T[key][query] = K . Q'^T - m   A = K rows from LDS
+//                                           (ds_read_b128), B = the wave's
+//                                           prescaled Q rows in VGPRs, C = -m.
 //     Each lane then owns ONE query (column l%32) and 16 of a 32-key block
 //     (rows 8*(r/4) + 4*g + r%4 of accumulator r); the other 16 sit in lane
-//     l^32.  A row max/sum is 16 in-lane ops plus one v_permlane32_swap.
+//     l^32.  A row max is 16 in-lane ops plus one v_permlane32_swap.
 //   GEMM2  O^T[d][query] += V^T . P^T  B = P^T straight from the GEMM1
 //                                      accumulators (packed to fp16),
 //                                      A = V^T read with ds_read_b64_tr_b16,
@@ -31,26 +32,52 @@
 // swapped via the tr-read addresses) so each lane ends with 8 contiguous
 // head-dim values per accumulator half: the epilogue stores 16-byte vectors.
 //
-// Softmax.  Scores stay raw (unscaled) in fp32; the running max m is kept in
-// raw units and p = exp2(s*c - m*c) is one FMA plus v_exp_f32, with
-// c = |sm_scale| * log2(e) (the reference's prescale, kernel_flash2.cu:772).
-// The max is only moved when some lane's new tile max exceeds it by more
-// than 8 in the log2 domain, so p <= 2^8 (exact in fp16 range); this skips
-// the O rescale on almost every tile and is exact math (softmax is shift
-// invariant).  Each lane accumulates the row sum of its own 32 keys; the two
-// halves of a row are added once, in the epilogue.
+// Softmax, at one exp per score.  Q is prescaled by c = |sm_scale| * log2 e
+// (the reference's prescale, kernel_flash2.cu:772) when c <= 1, so GEMM1
+// returns base-2 logits; the running stabiliser m enters as the MFMA
+// accumulator's initial value, so GEMM1 returns logit - m and p = v_exp_f32
+// of the accumulator.  m is the exact row max of the first tile and is then
+// only moved when a later tile's row max exceeds it by more than 8 (so
+// p <= 2^8, exact in fp16; a stale m is exact math since softmax is shift
+// invariant, and m never exceeds the running max, so the row sum stays
+// >= 1).  The decision is made before the exponentials, which then depend on
+// nothing else and interleave with the iteration's MFMAs.  Row sums are taken
+// from the fp16-rounded p with v_dot2_f32_f16, the same p GEMM2 multiplies;
+// each lane sums its own keys and the two halves of a row meet once, in the
+// epilogue.  When c > 1 (SCALED) Q keeps its scale and the logits are
+// multiplied by c instead, so |Q'| never exceeds |Q|.
 //
-// Causal.  Key blocks entirely above a wave's diagonal are skipped (never
-// multiplied); blocks on the diagonal and the ragged tail are masked to -inf;
-// every other block runs unmasked.  Work-groups are issued heaviest-first.
+// K/V staging.  Tiles are fetched straight into LDS with buffer_load ... lds
+// (no VGPRs, no LDS-store instructions; rows past N read as zeros through
+// the buffer resource's bound) D tiles ahead, into rings of D+1 slots per
+// tensor.  Each slot is its own LDS object and the loops are unrolled by the
+// ring length, so every slot address is static.  One explicit
+// "s_waitcnt vmcnt(n); s_barrier" per step makes a tile visible.
+//
+// Two schedules:
+//   fa2_fwd_kernel (any W): iteration j runs the softmax of tile j alongside
+//     GEMM1 of tile j+1 (independent work the compiler interleaves) and then
+//     GEMM2 of tile j; one barrier per tile.
+//   fa2_fwd_pp_kernel (W = 8, "ping-pong"): waves w and w+4 of a 512-lane
+//     work-group share a SIMD (gfx950 dispatch), so the work-group splits
+//     into group A = waves 0-3 and group B = waves 4-7, and every step one
+//     group runs its MFMA phase (GEMM2 of tile j-1 + GEMM1 of tile j, 16
+//     MFMAs) while the other runs its softmax phase (exp / cvt / dot2) on the
+//     same SIMD; a barrier ends each step and the groups swap.  The matrix
+//     core and the VALU of each SIMD are then busy at the same time.
+//
+// Causal.  Keys after a lane's query and keys >= N are masked to -inf on the
+// diagonal and tail tiles only; work-groups are issued heaviest-first.
 //
 // LDS.  Rows of 128 B (64 halfs).  16-byte chunks are XOR-swizzled per row:
 // K with (row&7)^((row>>3)&1), V with 2*(row&3), which makes the GEMM1
 // ds_read_b128 pattern, the GEMM2 ds_read_b64_tr_b16 pattern and the
-// row-contiguous tile stores conflict-free for 32- or 64-bank LDS.
+// row-contiguous tile writes conflict-free for 32- or 64-bank LDS.
 
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+
+#include <utility>
 
 #include "fl_internal.h"
 
@@ -60,23 +87,25 @@ namespace {
 
 typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
 typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
 typedef short short4_t __attribute__((ext_vector_type(4)));
 typedef float float16_t __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+typedef int i32x4_t __attribute__((ext_vector_type(4)));
 
-constexpr int kD = 64;                 // head dim
-constexpr int kBc = 64;                // keys per KV tile
-constexpr int kRowBytes = kD * 2;      // 128
+constexpr int kD = 64;                       // head dim
+constexpr int kBc = 64;                      // keys per KV tile
+constexpr int kRowBytes = kD * 2;            // 128
 constexpr int kTileBytes = kBc * kRowBytes;  // 8 KiB
-constexpr float kTau = 8.0f;           // max lag of the running max, log2 units
+constexpr float kLag = 8.0f;                 // max lag of m behind a row max, log2 units
 
 __device__ __forceinline__ int k_swz(int row) { return (row & 7) ^ ((row >> 3) & 1); }
 __device__ __forceinline__ int v_swz(int row) { return (row & 3) << 1; }
 
 __device__ __forceinline__ float ninf() { return -__builtin_huge_valf(); }
 
-// Value of x in lane l^32, combined with the own value: returns
-// {x[l], x[l^32]} in some order for every lane.
+// v_permlane32_swap of x with itself yields {x[l], x[l^32]} in some order
+// in every lane l, so max/sum of the pair combine the two halves of a row.
 __device__ __forceinline__ float pair_max(float x) {
   auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
   return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
@@ -86,270 +115,723 @@ __device__ __forceinline__ float pair_sum(float x) {
   return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
+// Raw buffer resource (gfx9 layout): 48-bit base, stride 0, num_records
+// bytes, dword 3 = 0x00020000 (32-bit data format, no swizzle).  Loads at
+// offsets >= num_records return zeros.
+__device__ __forceinline__ i32x4_t buffer_rsrc(const void* base, int bytes) {
+  const uint64_t a = (uint64_t)(uintptr_t)base;
+  i32x4_t r;
+  r[0] = __builtin_amdgcn_readfirstlane((int)(uint32_t)a);
+  r[1] = __builtin_amdgcn_readfirstlane((int)(uint32_t)(a >> 32) & 0xFFFF);
+  r[2] = __builtin_amdgcn_readfirstlane(bytes);
+  r[3] = 0x00020000;
+  return r;
+}
+
 __device__ __forceinline__ half4_t lds_read_tr(const uint8_t* p) {
   short4_t s = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
       (short4_t __attribute__((address_space(3)))*)(p));
   return __builtin_bit_cast(half4_t, s);
 }
 
-template <int W, bool CAUSAL>
-__global__ void __launch_bounds__(64 * W)
-fa2_fwd_kernel(const _Float16* Q, const _Float16* __restrict__ K,
-               const _Float16* __restrict__ V, _Float16* O, int seq, int nqb,
-               float c, int negate) {
-  constexpr int kThreads = 64 * W;
-  constexpr int kBr = 32 * W;
-  constexpr int kChunksPerThread = (kTileBytes / 16) / kThreads;  // per tensor
-  static_assert(kChunksPerThread * kThreads * 16 == kTileBytes, "tile split");
+// End of a step: this wave's LDS fetches older than its newest `pending`
+// ones have landed, its own LDS reads have completed, then the work-group
+// barrier.  The asm is a compiler memory barrier, and the sched_barriers
+// keep the scheduler from moving any instruction (MFMAs included) across
+// it, so each step's work stays in its step.
+template <int kPending>
+__device__ __forceinline__ void sync_ring() {
+  static_assert(kPending >= 0 && kPending < 64, "vmcnt range");
+  __builtin_amdgcn_sched_barrier(0);
+  asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" : : "n"(kPending) : "memory");
+  __builtin_amdgcn_sched_barrier(0);
+}
 
-  __shared__ __attribute__((aligned(16))) uint8_t lds[2][2][kTileBytes];  // [buf][K,V]
+template <int N>
+struct Ic {
+  static constexpr int value = N;
+};
 
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int g = lane >> 5;
-  const int col = lane & 31;
+template <int... I, class F>
+__device__ __forceinline__ void static_for(std::integer_sequence<int, I...>, F&& f) {
+  (f(Ic<I>{}), ...);
+}
 
-  // Work-group -> (batch*head, query block).  Work-groups are dealt to the
-  // 8 XCDs round-robin; remap so that consecutive query blocks of one head
-  // land on the same XCD (shared K/V in its L2).  Causal: heaviest first.
+// Work-group -> (batch*head, query block).  Work-groups are dealt to the 8
+// XCDs round-robin; remap so that consecutive query blocks of one head land
+// on the same XCD (shared K/V in its L2).  Causal: heaviest first.
+template <bool CAUSAL>
+__device__ __forceinline__ void wg_coords(int nqb, int& bh, int& qb) {
   const int total = gridDim.x;
   int lin = blockIdx.x;
   if ((total & 7) == 0) lin = (lin & 7) * (total >> 3) + (lin >> 3);
-  const int bh = lin / nqb;
-  int qb = lin - bh * nqb;
+  bh = lin / nqb;
+  qb = lin - bh * nqb;
   if (CAUSAL) qb = nqb - 1 - qb;
+}
 
-  const size_t head_off = (size_t)bh * (size_t)seq * kD;
-  const _Float16* Qh = Q + head_off;
-  const _Float16* Kh = K + head_off;
-  const _Float16* Vh = V + head_off;
-  _Float16* Oh = O + head_off;
-
-  const int q0 = qb * kBr;
-  const int qw = q0 + 32 * wave;   // first query of this wave (32-aligned)
-  const int my_q = qw + col;
-
-  // Q^T B-operand: lane holds Q[my_q][16s + 8g .. +7] for s = 0..3.
-  half8_t qf[4];
-#pragma unroll
-  for (int s = 0; s < 4; ++s) {
-    if (my_q < seq) {
-      u32x4_t raw = *reinterpret_cast<const u32x4_t*>(Qh + (size_t)my_q * kD + 16 * s + 8 * g);
-      if (negate) raw ^= (u32x4_t){0x80008000u, 0x80008000u, 0x80008000u, 0x80008000u};
-      qf[s] = __builtin_bit_cast(half8_t, raw);
-    } else {
-      qf[s] = (half8_t){0, 0, 0, 0, 0, 0, 0, 0};
-    }
+// K/V rings: kSlots LDS objects per tensor, selected by a static index
+// (negative indices wrap).
+template <int kSlots>
+struct Rings {
+  static_assert(kSlots >= 2 && kSlots <= 4, "ring depth");
+  uint8_t* k[4];
+  uint8_t* v[4];
+  template <int I>
+  __device__ __forceinline__ uint8_t* kslot(Ic<I>) const {
+    return k[((I % kSlots) + kSlots) % kSlots];
   }
-
-  int ntiles = (seq + kBc - 1) / kBc;
-  if (CAUSAL) {
-    const int q_last = min(q0 + kBr, seq) - 1;
-    ntiles = min(ntiles, q_last / kBc + 1);
+  template <int I>
+  __device__ __forceinline__ uint8_t* vslot(Ic<I>) const {
+    return v[((I % kSlots) + kSlots) % kSlots];
   }
+};
 
-  // Tile staging: thread t moves 16-byte chunks t + i*kThreads of each of
-  // the K and V tiles (chunk id -> row id/8, chunk id%8).
-  u32x4_t kreg[kChunksPerThread], vreg[kChunksPerThread];
-  auto load_tile = [&](int j) {
-    const int k0 = j * kBc;
+// Asynchronous fetch of tile t (clamped to the last tile the work-group
+// needs) straight into LDS with buffer_load_dwordx4 ... lds: each wave moves
+// `kSegs` 1 KiB segments (8 rows); lane i of a segment lands at byte 16*i,
+// i.e. row i/8, physical chunk i%8, which holds logical chunk
+// (i%8) ^ swz(row).  Issued from inline assembly so the compiler does not
+// guard LDS reads of other slots with waits on it; sync_ring<> tracks it.
+template <int kSegs, bool IS_V>
+__device__ __forceinline__ void fetch_tile(const i32x4_t& rs, const uint8_t* slot, int t,
+                                           int last_tile, int wave, int lane) {
+  t = min(t, last_tile);
 #pragma unroll
-    for (int i = 0; i < kChunksPerThread; ++i) {
-      const int id = tid + i * kThreads;
-      const int row = id >> 3, ch = id & 7;
-      const int key = k0 + row;
-      if (key < seq) {
-        kreg[i] = *reinterpret_cast<const u32x4_t*>(Kh + (size_t)key * kD + 8 * ch);
-        vreg[i] = *reinterpret_cast<const u32x4_t*>(Vh + (size_t)key * kD + 8 * ch);
+  for (int i = 0; i < kSegs; ++i) {
+    const int seg = wave * kSegs + i;
+    const int row = 8 * seg + (lane >> 3);
+    const int phys = lane & 7;
+    const int logical = phys ^ (IS_V ? v_swz(row) : k_swz(row));
+    const int voff = (t * kBc + row) * kRowBytes + 16 * logical;
+    const uint32_t lds_base = (uint32_t)(uintptr_t)(slot + 1024 * seg);
+    asm volatile("buffer_load_dwordx4 %0, %1, 0 offen lds" : : "v"(voff), "s"(rs), "{m0}"(lds_base));
+  }
+}
+
+// The 32 query rows one wave owns: prescaled Q, running max, row sums and
+// O accumulator, plus the tile-level building blocks.
+template <bool CAUSAL, bool SCALED>
+struct Rows {
+  int g, col, qw, my_q, seq;
+  int tr_row, tr_col;
+  float cr;
+  half8_t qf[4];    // Q'^T B-operand
+  float16_t o[2];   // O^T accumulator, d-blocks 0 / 1
+  float16_t bias;   // -m broadcast, GEMM1's accumulator input
+  float m;          // running stabiliser, units of t = q'.k
+  float l;          // this lane's share of the row sum
+  half8_t p[2][2];  // fp16 P^T B-operands of the last softmaxed tile
+
+  __device__ __forceinline__ void init(const _Float16* Qh, int lane, int qw_, int seq_, float cq,
+                                       float cr_) {
+    g = lane >> 5;
+    col = lane & 31;
+    qw = qw_;
+    my_q = qw + col;
+    seq = seq_;
+    cr = cr_;
+    // GEMM2 tr-read address pieces: lane l is lane j = l%16 of 16-lane group
+    // G = l/16; it points at key row 4*(G/2) + j/4 (+16t, +8 for the second
+    // read) and head-dim column 16*(G%2) + 4*swap2(j%4) (+32 per d-block).
+    const int trG = lane >> 4, trj = lane & 15;
+    tr_row = 4 * (trG >> 1) + (trj >> 2);
+    const int tr_x = trj & 3;
+    tr_col = 16 * (trG & 1) + 4 * (((tr_x & 1) << 1) | (tr_x >> 1));
+    // Q'^T: lane holds cq * Q[my_q][16s + 8g .. +7] for s = 0..3, in fp16.
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      if (my_q < seq) {
+        const half8_t raw =
+            *reinterpret_cast<const half8_t*>(Qh + (size_t)my_q * kD + 16 * s + 8 * g);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) qf[s][e] = (_Float16)((float)raw[e] * cq);
       } else {
-        kreg[i] = (u32x4_t){0, 0, 0, 0};
-        vreg[i] = (u32x4_t){0, 0, 0, 0};
+        qf[s] = (half8_t){0, 0, 0, 0, 0, 0, 0, 0};
       }
     }
-  };
-  auto store_tile = [&](int buf) {
 #pragma unroll
-    for (int i = 0; i < kChunksPerThread; ++i) {
-      const int id = tid + i * kThreads;
-      const int row = id >> 3, ch = id & 7;
-      *reinterpret_cast<u32x4_t*>(&lds[buf][0][row * kRowBytes + 16 * (ch ^ k_swz(row))]) = kreg[i];
-      *reinterpret_cast<u32x4_t*>(&lds[buf][1][row * kRowBytes + 16 * (ch ^ v_swz(row))]) = vreg[i];
+    for (int r = 0; r < 16; ++r) {
+      o[0][r] = 0.0f;
+      o[1][r] = 0.0f;
+      bias[r] = 0.0f;
     }
-  };
+    m = 0.0f;
+    l = 0.0f;
+  }
 
-  // Per-lane GEMM2 tr-read address pieces (see header comment): lane l is
-  // lane j = l%16 of 16-lane group G = l/16; it points at key row
-  // 4*(G/2) + j/4 (+16t, +8 for the second read) and head-dim column
-  // 16*(G%2) + 4*swap2(j%4) (+32 per d-block).
-  const int trG = lane >> 4, trj = lane & 15;
-  const int tr_row = 4 * (trG >> 1) + (trj >> 2);
-  const int tr_x = trj & 3;
-  const int tr_col = 16 * (trG & 1) + 4 * (((tr_x & 1) << 1) | (tr_x >> 1));
-
-  float16_t o_acc[2];
+  // K operands of GEMM1 (both 32-key blocks, 4 head-dim steps each).
+  __device__ __forceinline__ void read_k(const uint8_t* kt, half8_t (&ka)[2][4]) const {
 #pragma unroll
-  for (int db = 0; db < 2; ++db)
+    for (int kb = 0; kb < 2; ++kb) {
+      const int row = 32 * kb + col;
 #pragma unroll
-    for (int r = 0; r < 16; ++r) o_acc[db][r] = 0.0f;
-  float m_used = ninf();   // running max, raw score units
-  float mc = ninf();       // m_used * c
-  float l_part = 0.0f;     // this lane's share of the row sum
-
-  load_tile(0);
-  store_tile(0);
-  __syncthreads();
-
-  for (int j = 0; j < ntiles; ++j) {
-    const int buf = j & 1;
-    if (j + 1 < ntiles) load_tile(j + 1);
-
-    const int k0 = j * kBc;
-    // Key blocks (32 keys) this wave needs: block kb starts at k0 + 32kb.
-    int nkb = (k0 + 32 < seq) ? 2 : 1;
-    if (CAUSAL) {
-      if (k0 > qw) nkb = 0;
-      else if (k0 + 32 > qw) nkb = min(nkb, 1);
+      for (int st = 0; st < 4; ++st) {
+        const int ch = 2 * st + g;
+        ka[kb][st] =
+            *reinterpret_cast<const half8_t*>(kt + row * kRowBytes + 16 * (ch ^ k_swz(row)));
+      }
     }
-    if (nkb > 0) {
-      const uint8_t* Ks = lds[buf][0];
-      const uint8_t* Vs = lds[buf][1];
-
-      // ---- GEMM1: S^T = K . Q^T
-      float16_t s_acc[2];
+  }
+  // V^T operands of GEMM2 (2 d-blocks x 4 16-key steps).
+  __device__ __forceinline__ void read_v(const uint8_t* vt, half8_t (&va)[2][4]) const {
 #pragma unroll
-      for (int kb = 0; kb < 2; ++kb) {
-        if (kb < nkb) {
+    for (int db = 0; db < 2; ++db)
 #pragma unroll
-          for (int r = 0; r < 16; ++r) s_acc[kb][r] = 0.0f;
-          const int row = 32 * kb + col;
-#pragma unroll
-          for (int s = 0; s < 4; ++s) {
-            const int ch = 2 * s + g;
-            half8_t a = *reinterpret_cast<const half8_t*>(Ks + row * kRowBytes + 16 * (ch ^ k_swz(row)));
-            s_acc[kb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, qf[s], s_acc[kb], 0, 0, 0);
-          }
-        } else {
-#pragma unroll
-          for (int r = 0; r < 16; ++r) s_acc[kb][r] = ninf();
-        }
+      for (int t = 0; t < 4; ++t) {
+        const int r1 = 16 * t + tr_row;
+        const int r2 = r1 + 8;
+        const int dcol = 32 * db + tr_col;
+        const int ch = dcol >> 3, hb = ((dcol >> 2) & 1) * 8;
+        const half4_t lo = lds_read_tr(vt + r1 * kRowBytes + 16 * (ch ^ v_swz(r1)) + hb);
+        const half4_t hi = lds_read_tr(vt + r2 * kRowBytes + 16 * (ch ^ v_swz(r2)) + hb);
+        va[db][t] = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
       }
-
-      // ---- mask: ragged tail (keys >= seq) and the causal diagonal block
+  }
+  // GEMM1: s[kb] = K[32kb + row] . Q'^T - m.
+  __device__ __forceinline__ void gemm1(const half8_t (&ka)[2][4], float16_t (&s)[2]) const {
 #pragma unroll
-      for (int kb = 0; kb < 2; ++kb) {
-        const int kstart = k0 + 32 * kb;
-        const bool tail = kstart + 32 > seq;
-        const bool diag = CAUSAL && (kstart == qw);
-        if (kb < nkb && (tail || diag)) {
+    for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const int key = kstart + 8 * (r >> 2) + 4 * g + (r & 3);
-            const bool ok = key < seq && (!CAUSAL || key <= my_q);
-            s_acc[kb][r] = ok ? s_acc[kb][r] : ninf();
-          }
-        }
-      }
-
-      // ---- running max (lazy: moved only when it lags by > kTau)
-      float mx = ninf();
+      for (int st = 0; st < 4; ++st)
+        s[kb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka[kb][st], qf[st], st == 0 ? bias : s[kb],
+                                                       0, 0, 0);
+  }
+  // GEMM2: O^T += V^T . P^T
+  __device__ __forceinline__ void gemm2(const half8_t (&va)[2][4]) {
+#pragma unroll
+    for (int db = 0; db < 2; ++db)
+#pragma unroll
+      for (int t = 0; t < 4; ++t)
+        o[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va[db][t], p[t >> 1][t & 1], o[db], 0, 0, 0);
+  }
+  // Masks keys >= seq and, when causal, keys after the lane's query (tile t).
+  __device__ __forceinline__ void mask(int t, float16_t (&s)[2]) const {
+    const int k0 = t * kBc;
+    if (k0 + kBc > seq || (CAUSAL && k0 + kBc - 1 > qw)) {
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s_acc[kb][r]);
-      mx = pair_max(mx);
-      const bool need = (mx - m_used) * c > kTau;
-      if (__builtin_amdgcn_ballot_w64(need) != 0) {
-        const float m_new = fmaxf(m_used, mx);
-        const float alpha = __builtin_amdgcn_exp2f((m_used - m_new) * c);
-        l_part *= alpha;
-#pragma unroll
-        for (int db = 0; db < 2; ++db)
-#pragma unroll
-          for (int r = 0; r < 16; ++r) o_acc[db][r] *= alpha;
-        m_used = m_new;
-        mc = m_used * c;
-      }
-
-      // ---- P = exp2(s*c - m*c), row-sum share, pack to fp16 B-operands
-      half8_t pf[2][2];
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb) {
-        if (kb >= nkb) continue;
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-#pragma unroll
-          for (int e = 0; e < 8; ++e) {
-            const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(s_acc[kb][8 * h + e], c, -mc));
-            l_part += p;
-            pf[kb][h][e] = (_Float16)p;
-          }
+        for (int r = 0; r < 16; ++r) {
+          const int key = k0 + 32 * kb + 8 * (r >> 2) + 4 * g + (r & 3);
+          const bool ok = key < seq && (!CAUSAL || key <= my_q);
+          s[kb][r] = ok ? s[kb][r] : ninf();
         }
-      }
-
-      // ---- GEMM2: O^T += V^T . P^T
-#pragma unroll
-      for (int db = 0; db < 2; ++db) {
-#pragma unroll
-        for (int kb = 0; kb < 2; ++kb) {
-          if (kb < nkb) {
-#pragma unroll
-            for (int h = 0; h < 2; ++h) {
-              const int t = 2 * kb + h;
-              const int r1 = 16 * t + tr_row;
-              const int r2 = r1 + 8;
-              const int dcol = 32 * db + tr_col;
-              const int ch = dcol >> 3, hb = ((dcol >> 2) & 1) * 8;
-              half4_t lo = lds_read_tr(Vs + r1 * kRowBytes + 16 * (ch ^ v_swz(r1)) + hb);
-              half4_t hi = lds_read_tr(Vs + r2 * kRowBytes + 16 * (ch ^ v_swz(r2)) + hb);
-              half8_t a = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
-              o_acc[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, pf[kb][h], o_acc[db], 0, 0, 0);
-            }
-          }
-        }
-      }
-    }
-
-    if (j + 1 < ntiles) store_tile(buf ^ 1);
-    __syncthreads();
-  }
-
-  // ---- epilogue: O = O^T / l, 16-byte stores of 8 contiguous head dims
-  const float l_tot = pair_sum(l_part);
-  const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
-  if (my_q < seq) {
-    _Float16* orow = Oh + (size_t)my_q * kD;
-#pragma unroll
-    for (int db = 0; db < 2; ++db) {
-#pragma unroll
-      for (int hh = 0; hh < 2; ++hh) {
-        half8_t out;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) out[e] = (_Float16)(o_acc[db][8 * hh + e] * inv);
-        *reinterpret_cast<half8_t*>(orow + 32 * db + 16 * hh + 8 * g) = out;
-      }
     }
   }
+  // Row max of a tile (both halves of the row).
+  __device__ __forceinline__ float tile_max(const float16_t (&s)[2]) const {
+    float mx = ninf();
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[kb][r]);
+    return pair_max(mx);
+  }
+  __device__ __forceinline__ static void sub(float16_t (&s)[2], float d) {
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) s[kb][r] -= d;
+  }
+  __device__ __forceinline__ void set_m(float mm) {
+    m = mm;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) bias[r] = -mm;
+  }
+  // First tile: m = the exact row max (every row sees key 0, so it is finite).
+  __device__ __forceinline__ void first_tile(float16_t (&s)[2]) {
+    const float m0 = tile_max(s);
+    sub(s, m0);
+    set_m(m0);
+  }
+  // p = 2^(t - m) (times cr when SCALED) packed to fp16 B-operands; returns
+  // this lane's sum of the fp16-rounded p (v_dot2_f32_f16 against (1, 1)),
+  // in two partial sums for instruction-level parallelism.
+  __device__ __forceinline__ float exponentiate(const float16_t (&s)[2]) {
+    const half2_t one = {(_Float16)1.0f, (_Float16)1.0f};
+    float sum0 = 0.0f, sum1 = 0.0f;
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int e = 0; e < 8; e += 2) {
+          float x0 = s[kb][8 * h + e], x1 = s[kb][8 * h + e + 1];
+          if (SCALED) {
+            x0 *= cr;
+            x1 *= cr;
+          }
+          const half2_t ph = {(_Float16)__builtin_amdgcn_exp2f(x0),
+                              (_Float16)__builtin_amdgcn_exp2f(x1)};
+          p[kb][h][e] = ph[0];
+          p[kb][h][e + 1] = ph[1];
+          if (kb == 0)
+            sum0 = __builtin_amdgcn_fdot2(ph, one, sum0, false);
+          else
+            sum1 = __builtin_amdgcn_fdot2(ph, one, sum1, false);
+        }
+    return sum0 + sum1;
+  }
+  // Lazy stabiliser, decided before any exponential: scores are t - m and
+  // while every row's tile max stays within kLag (log2 units) of m, p stays
+  // <= 2^kLag (exact in fp16) and nothing is rescaled.  Otherwise (rare) m
+  // moves up to the new row max and what was accumulated is rescaled;
+  // `on_shift(d)` lets the caller shift scores computed against the old m.
+  // Deciding first keeps the exponentials free of any later dependency, so
+  // they interleave with the MFMAs of the same iteration.
+  template <class F>
+  __device__ __forceinline__ void restabilise(float16_t (&s)[2], F&& on_shift) {
+    const float mx = tile_max(s);
+    const float lag = SCALED ? mx * cr : mx;
+    if (__builtin_amdgcn_ballot_w64(lag > kLag) != 0) {
+      const float d = fmaxf(mx, 0.0f);
+      const float alpha = __builtin_amdgcn_exp2f(-(SCALED ? cr : 1.0f) * d);
+      l *= alpha;
+#pragma unroll
+      for (int db = 0; db < 2; ++db)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) o[db][r] *= alpha;
+      sub(s, d);
+      on_shift(d);
+      set_m(m + d);
+    }
+  }
+  // Softmax of one tile into p (restabilise, then exponentiate) and the row
+  // sum update.
+  template <class F>
+  __device__ __forceinline__ void softmax(float16_t (&s)[2], F&& on_shift) {
+    restabilise(s, on_shift);
+    l += exponentiate(s);
+  }
+  // O = O^T / l, 16-byte stores of 8 contiguous head dims; rows >= N skipped.
+  __device__ __forceinline__ void store(_Float16* Oh) const {
+    const float l_tot = pair_sum(l);
+    const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
+    if (my_q < seq) {
+      _Float16* orow = Oh + (size_t)my_q * kD;
+#pragma unroll
+      for (int db = 0; db < 2; ++db)
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh) {
+          half8_t out;
+#pragma unroll
+          for (int e = 0; e < 8; ++e) out[e] = (_Float16)(o[db][8 * hh + e] * inv);
+          *reinterpret_cast<half8_t*>(orow + 32 * db + 16 * hh + 8 * g) = out;
+        }
+    }
+  }
+};
+
+// Zeroes every V slot once: a tail tile's rows past N then hold zeros (or
+// earlier finite data), never uninitialised bits, under p == 0.
+template <int kSlots, int kThreads>
+__device__ __forceinline__ void zero_v_slots(const Rings<kSlots>& rings) {
+  const u32x4_t z = {0, 0, 0, 0};
+  static_for(std::make_integer_sequence<int, kSlots>{}, [&](auto i) __attribute__((always_inline)) {
+    for (int off = 16 * (int)threadIdx.x; off < kTileBytes; off += 16 * kThreads)
+      *reinterpret_cast<u32x4_t*>(rings.vslot(i) + off) = z;
+  });
+  __syncthreads();
 }
 
-template <int W>
-hipError_t launch_w(const FwdArgs& a, hipStream_t stream) {
-  const int br = 32 * W;
+#define FL_DECLARE_RINGS(R)                                                          \
+  __shared__ __attribute__((aligned(16))) uint8_t kr0[kTileBytes], kr1[kTileBytes], \
+      kr2[kTileBytes], kr3[kTileBytes];                                              \
+  __shared__ __attribute__((aligned(16))) uint8_t vr0[kTileBytes], vr1[kTileBytes], \
+      vr2[kTileBytes], vr3[kTileBytes];                                              \
+  const Rings<R> rings = {{kr0, kr1, kr2, kr3}, {vr0, vr1, vr2, vr3}}
+
+// ---------------------------------------------------------------------------
+// Pipelined schedule, W waves.  D = fetch distance in tiles.
+template <int W, int D, bool CAUSAL, bool SCALED>
+__global__ void __launch_bounds__(64 * W, 2)
+fa2_fwd_kernel(const _Float16* Q, const _Float16* __restrict__ K,
+               const _Float16* __restrict__ V, _Float16* O, int seq, int nqb,
+               float cq, float cr) {
+  constexpr int kSlots = D + 1;
+  constexpr int kUnroll = (kSlots % 2 == 0) ? kSlots : 2 * kSlots;
+  constexpr int kBr = 32 * W;
+  constexpr int kSegs = 8 / W;            // 1 KiB DMA segments per wave per tile
+  constexpr int kDmaPerIter = 2 * kSegs;  // K + V loads a wave issues per iteration
+  static_assert(kSegs * W == 8, "tile split");
+  FL_DECLARE_RINGS(kSlots);
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  int bh, qb;
+  wg_coords<CAUSAL>(nqb, bh, qb);
+  const size_t head_off = (size_t)bh * (size_t)seq * kD;
+  const i32x4_t rk = buffer_rsrc(K + head_off, seq * kRowBytes);
+  const i32x4_t rv = buffer_rsrc(V + head_off, seq * kRowBytes);
+  const int q0 = qb * kBr;
+
+  Rows<CAUSAL, SCALED> rows;
+  rows.init(Q + head_off, lane, q0 + 32 * wave, seq, cq, cr);
+
+  int ntiles = (seq + kBc - 1) / kBc;
+  if (CAUSAL) ntiles = min(ntiles, (min(q0 + kBr, seq) - 1) / kBc + 1);
+  const int last = ntiles - 1;
+
+  // One iteration for tile j (position I of the unrolled loop): fetch
+  // K(j+D+1), V(j+D) into the slots K(j) and V(j-1) vacated before the
+  // previous barrier; read the K(j+1) and V(j) operands; softmax(j)
+  // alongside GEMM1(j+1); GEMM2(j); wait for this wave's part of K(j+2) and
+  // V(j+1), barrier.
+  auto iteration = [&](auto i, int j, float16_t (&S)[2], float16_t (&Sn)[2]) __attribute__((always_inline)) {
+    constexpr int I = decltype(i)::value;
+    fetch_tile<kSegs, false>(rk, rings.kslot(Ic<I + D + 1>{}), j + D + 1, last, wave, lane);
+    fetch_tile<kSegs, true>(rv, rings.vslot(Ic<I + D>{}), j + D, last, wave, lane);
+    half8_t ka[2][4], va[2][4];
+    rows.read_k(rings.kslot(Ic<I + 1>{}), ka);
+    rows.read_v(rings.vslot(Ic<I>{}), va);
+    // GEMM1 of a tile past the end reads a stale slot; its result is unused.
+    rows.gemm1(ka, Sn);
+    rows.softmax(S, [&](float d) __attribute__((always_inline)) { Rows<CAUSAL, SCALED>::sub(Sn, d); });
+    rows.gemm2(va);
+    rows.mask(j + 1, Sn);
+    sync_ring<(D - 1) * kDmaPerIter>();
+  };
+
+  // ---- prologue: K(0), V(0), K(1) landed; fetch groups of iterations
+  // 1-D .. -1 in flight; S(0) with the exact row max.
+  zero_v_slots<kSlots, 64 * W>(rings);
+  fetch_tile<kSegs, false>(rk, rings.kslot(Ic<0>{}), 0, last, wave, lane);
+  fetch_tile<kSegs, true>(rv, rings.vslot(Ic<0>{}), 0, last, wave, lane);
+  fetch_tile<kSegs, false>(rk, rings.kslot(Ic<1>{}), 1, last, wave, lane);
+  sync_ring<0>();
+  static_for(std::make_integer_sequence<int, D - 1>{}, [&](auto i) __attribute__((always_inline)) {
+    constexpr int G = decltype(i)::value + 1 - D;  // iteration 1-D+i
+    fetch_tile<kSegs, false>(rk, rings.kslot(Ic<G + D + 1>{}), G + D + 1, last, wave, lane);
+    fetch_tile<kSegs, true>(rv, rings.vslot(Ic<G + D>{}), G + D, last, wave, lane);
+  });
+  float16_t S0[2], S1[2];
+  {
+    half8_t ka[2][4];
+    rows.read_k(rings.kslot(Ic<0>{}), ka);
+    rows.gemm1(ka, S0);
+  }
+  rows.mask(0, S0);
+  rows.first_tile(S0);
+
+  // ---- main loop, unrolled so ring slots and S / S_next roles are static ----
+  for (int j0 = 0; j0 < ntiles; j0 += kUnroll) {
+    static_for(std::make_integer_sequence<int, kUnroll>{}, [&](auto i) __attribute__((always_inline)) {
+      constexpr int I = decltype(i)::value;
+      const int j = j0 + I;
+      if (j < ntiles) {
+        if constexpr (I % 2 == 0)
+          iteration(i, j, S0, S1);
+        else
+          iteration(i, j, S1, S0);
+      }
+    });
+  }
+
+  // No fetch may still be writing LDS when the work-group retires.
+  __builtin_amdgcn_s_waitcnt(0);
+  rows.store(O + head_off);
+}
+
+// ---------------------------------------------------------------------------
+// Ping-pong schedule, 8 waves: group A (waves 0-3) and group B (waves 4-7)
+// alternate MFMA and softmax phases on shared SIMDs.  Step s ends with a
+// barrier; the MFMA phase M(j) is GEMM2(j-1) + GEMM1(j), the softmax phase
+// V(j) turns S(j) into P(j):
+//     step   0     1     2     3    ...  2j     2j+1  ...  2n     2n+1
+//     A     M(0)  V(0)  M(1)  V(1)  ...  M(j)   V(j)  ...  M(n)    -
+//     B      -    M(0)  V(0)  M(1)  ...  V(j-1) M(j)  ...  V(n-1) M(n)
+// K(t) is read in steps 2t, 2t+1 and V(t) in 2t+2, 2t+3; step 2u (even)
+// fetches K(u+D) and V(u+D-1) into rings of D+1 slots, and every odd step
+// ends by waiting for the fetch group issued D-1 groups earlier.
+template <int D, bool CAUSAL, bool SCALED>
+__global__ void __launch_bounds__(512, 1)
+fa2_fwd_pp_kernel(const _Float16* Q, const _Float16* __restrict__ K,
+                  const _Float16* __restrict__ V, _Float16* O, int seq, int nqb,
+                  float cq, float cr) {
+  constexpr int kSlots = D + 1;
+  constexpr int kBr = 256;
+  constexpr int kPending = (D - 1) * 2;  // one K and one V segment per wave per group
+  FL_DECLARE_RINGS(kSlots);
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const bool group_b = wave >= 4;
+  int bh, qb;
+  wg_coords<CAUSAL>(nqb, bh, qb);
+  const size_t head_off = (size_t)bh * (size_t)seq * kD;
+  const i32x4_t rk = buffer_rsrc(K + head_off, seq * kRowBytes);
+  const i32x4_t rv = buffer_rsrc(V + head_off, seq * kRowBytes);
+  const int q0 = qb * kBr;
+
+  Rows<CAUSAL, SCALED> rows;
+  rows.init(Q + head_off, lane, q0 + 32 * wave, seq, cq, cr);
+
+  int ntiles = (seq + kBc - 1) / kBc;
+  if (CAUSAL) ntiles = min(ntiles, (min(q0 + kBr, seq) - 1) / kBc + 1);
+  const int n = ntiles;
+  const int last = n - 1;
+
+  // Fetch group u (ring position U = u mod kSlots, static): K(u+D), V(u+D-1).
+  auto fetch_group = [&](auto upos, int u) __attribute__((always_inline)) {
+    constexpr int U = decltype(upos)::value;
+    fetch_tile<1, false>(rk, rings.kslot(Ic<U + D>{}), u + D, last, wave, lane);
+    fetch_tile<1, true>(rv, rings.vslot(Ic<U + D - 1>{}), max(u + D - 1, 0), last, wave, lane);
+  };
+  float16_t S[2];
+  // MFMA phase M(j) at ring position J = j mod kSlots: GEMM2(j-1), GEMM1(j).
+  auto mfma_phase = [&](auto jpos, auto has_v, auto has_k) __attribute__((always_inline)) {
+    constexpr int J = decltype(jpos)::value;
+    half8_t ka[2][4], va[2][4];
+    if constexpr (decltype(has_v)::value) rows.read_v(rings.vslot(Ic<J - 1>{}), va);
+    if constexpr (decltype(has_k)::value) rows.read_k(rings.kslot(Ic<J>{}), ka);
+    if constexpr (decltype(has_v)::value) rows.gemm2(va);
+    if constexpr (decltype(has_k)::value) rows.gemm1(ka, S);
+  };
+  // Softmax phase V(j).
+  auto softmax_phase = [&](int j) __attribute__((always_inline)) {
+    rows.mask(j, S);
+    if (j == 0) rows.first_tile(S);
+    rows.softmax(S, [](float) {});
+  };
+
+  // ---- prologue: zero V slots, fetch groups -D .. -1, wait for group -D.
+  zero_v_slots<kSlots, 512>(rings);
+  static_for(std::make_integer_sequence<int, D>{}, [&](auto i) __attribute__((always_inline)) {
+    constexpr int u = decltype(i)::value - D;
+    fetch_group(Ic<u>{}, u);
+  });
+  sync_ring<kPending>();
+
+  if (!group_b) {
+    // step 0: M(0) (GEMM1 only); step 1: V(0)
+    fetch_group(Ic<0>{}, 0);
+    mfma_phase(Ic<0>{}, Ic<0>{}, Ic<1>{});
+    sync_ring<63>();
+    softmax_phase(0);
+    sync_ring<kPending>();
+    // steps 2j, 2j+1 for j = 1 .. n-1
+    for (int j0 = 1; j0 < n; j0 += kSlots) {
+      static_for(std::make_integer_sequence<int, kSlots>{}, [&](auto i) __attribute__((always_inline)) {
+        constexpr int J = 1 + decltype(i)::value;  // position of j0 + i (j0 = 1 mod kSlots)
+        const int j = j0 + decltype(i)::value;
+        if (j < n) {
+          fetch_group(Ic<J>{}, j);
+          mfma_phase(Ic<J>{}, Ic<1>{}, Ic<1>{});
+          sync_ring<63>();
+          softmax_phase(j);
+          sync_ring<kPending>();
+        }
+      });
+    }
+    // step 2n: M(n) (GEMM2 only) at position n mod kSlots
+    static_for(std::make_integer_sequence<int, kSlots>{}, [&](auto i) __attribute__((always_inline)) {
+      constexpr int J = decltype(i)::value;
+      if (n % kSlots == J) {
+        fetch_group(Ic<J>{}, n);
+        mfma_phase(Ic<J>{}, Ic<1>{}, Ic<0>{});
+      }
+    });
+    sync_ring<63>();
+    // step 2n+1: idle
+    sync_ring<kPending>();
+  } else {
+    // step 0: idle; step 1: M(0); step 2: V(0)
+    fetch_group(Ic<0>{}, 0);
+    sync_ring<63>();
+    mfma_phase(Ic<0>{}, Ic<0>{}, Ic<1>{});
+    sync_ring<kPending>();
+    fetch_group(Ic<1>{}, 1);
+    softmax_phase(0);
+    sync_ring<63>();
+    // steps 2j+1, 2j+2 for j = 1 .. n-1
+    for (int j0 = 1; j0 < n; j0 += kSlots) {
+      static_for(std::make_integer_sequence<int, kSlots>{}, [&](auto i) __attribute__((always_inline)) {
+        constexpr int J = 1 + decltype(i)::value;
+        const int j = j0 + decltype(i)::value;
+        if (j < n) {
+          mfma_phase(Ic<J>{}, Ic<1>{}, Ic<1>{});
+          sync_ring<kPending>();
+          fetch_group(Ic<J + 1>{}, j + 1);
+          softmax_phase(j);
+          sync_ring<63>();
+        }
+      });
+    }
+    // step 2n+1: M(n) (GEMM2 only)
+    static_for(std::make_integer_sequence<int, kSlots>{}, [&](auto i) __attribute__((always_inline)) {
+      constexpr int J = decltype(i)::value;
+      if (n % kSlots == J) mfma_phase(Ic<J>{}, Ic<1>{}, Ic<0>{});
+    });
+    sync_ring<kPending>();
+  }
+
+  __builtin_amdgcn_s_waitcnt(0);
+  rows.store(O + head_off);
+}
+
+// ---------------------------------------------------------------------------
+// Two blocks per wave, 4 waves: each wave owns 64 query rows as blocks A and
+// B of 32, so every K and V operand read from LDS feeds both blocks' MFMAs
+// (half the LDS traffic per flop of the 32-row schedules), and block B runs
+// half a tile behind block A so one block's softmax overlaps the other
+// block's MFMAs inside the wave:
+//     iteration t, step 1:  softmax_A(t)   with  GEMM2_B(t-1), GEMM1_B(t)
+//     iteration t, step 2:  softmax_B(t)   with  GEMM2_A(t),   GEMM1_A(t+1)
+// K(t) operands are read from LDS in step 2 of iteration t-1 and kept in
+// VGPRs for GEMM1_B(t); V(t) operands likewise for GEMM2_B(t).  So
+// iteration t reads exactly K(t+1) and V(t) from LDS, as fa2_fwd_kernel
+// does, with the same fetch ring.
+template <int D, bool CAUSAL, bool SCALED>
+__global__ void __launch_bounds__(256, 1)
+fa2_fwd_x2_kernel(const _Float16* Q, const _Float16* __restrict__ K,
+                  const _Float16* __restrict__ V, _Float16* O, int seq, int nqb,
+                  float cq, float cr) {
+  constexpr int W = 4;
+  constexpr int kSlots = D + 1;
+  constexpr int kUnroll = kSlots;
+  constexpr int kBr = 64 * W;
+  constexpr int kSegs = 8 / W;            // 1 KiB DMA segments per wave per tile
+  constexpr int kDmaPerIter = 2 * kSegs;  // K + V loads a wave issues per iteration
+  FL_DECLARE_RINGS(kSlots);
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  int bh, qb;
+  wg_coords<CAUSAL>(nqb, bh, qb);
+  const size_t head_off = (size_t)bh * (size_t)seq * kD;
+  const i32x4_t rk = buffer_rsrc(K + head_off, seq * kRowBytes);
+  const i32x4_t rv = buffer_rsrc(V + head_off, seq * kRowBytes);
+  const int q0 = qb * kBr;
+
+  Rows<CAUSAL, SCALED> ra, rb;
+  ra.init(Q + head_off, lane, q0 + 64 * wave, seq, cq, cr);
+  rb.init(Q + head_off, lane, q0 + 64 * wave + 32, seq, cq, cr);
+
+  int ntiles = (seq + kBc - 1) / kBc;
+  if (CAUSAL) ntiles = min(ntiles, (min(q0 + kBr, seq) - 1) / kBc + 1);
+  const int last = ntiles - 1;
+
+  half8_t kops[2][4], vops[2][4];  // K(t) / V(t) operands, shared by both blocks
+  float16_t sa[2], sb[2];
+
+  auto iteration = [&](auto i, int t) __attribute__((always_inline)) {
+    constexpr int I = decltype(i)::value;
+    fetch_tile<kSegs, false>(rk, rings.kslot(Ic<I + D + 1>{}), t + D + 1, last, wave, lane);
+    fetch_tile<kSegs, true>(rv, rings.vslot(Ic<I + D>{}), t + D, last, wave, lane);
+    // step 1: softmax_A(t) with GEMM2_B(t-1) and GEMM1_B(t)
+    if (t > 0) rb.gemm2(vops);
+    rb.gemm1(kops, sb);
+    ra.mask(t, sa);
+    if (t == 0) ra.first_tile(sa);
+    ra.softmax(sa, [](float) __attribute__((always_inline)) {});
+    // step 2: softmax_B(t) with GEMM2_A(t) and GEMM1_A(t+1); reads V(t), K(t+1)
+    ra.read_v(rings.vslot(Ic<I>{}), vops);
+    ra.read_k(rings.kslot(Ic<I + 1>{}), kops);
+    ra.gemm2(vops);
+    // GEMM1 of a tile past the end reads a stale slot; its result is unused.
+    ra.gemm1(kops, sa);
+    rb.mask(t, sb);
+    if (t == 0) rb.first_tile(sb);
+    rb.softmax(sb, [](float) __attribute__((always_inline)) {});
+    sync_ring<(D - 1) * kDmaPerIter>();
+  };
+
+  // ---- prologue: K(0), V(0), K(1) landed; fetch groups of iterations
+  // 1-D .. -1 in flight; K(0) operands and S_A(0).
+  zero_v_slots<kSlots, 64 * W>(rings);
+  fetch_tile<kSegs, false>(rk, rings.kslot(Ic<0>{}), 0, last, wave, lane);
+  fetch_tile<kSegs, true>(rv, rings.vslot(Ic<0>{}), 0, last, wave, lane);
+  fetch_tile<kSegs, false>(rk, rings.kslot(Ic<1>{}), 1, last, wave, lane);
+  sync_ring<0>();
+  static_for(std::make_integer_sequence<int, D - 1>{}, [&](auto i) __attribute__((always_inline)) {
+    constexpr int G = decltype(i)::value + 1 - D;  // iteration 1-D+i
+    fetch_tile<kSegs, false>(rk, rings.kslot(Ic<G + D + 1>{}), G + D + 1, last, wave, lane);
+    fetch_tile<kSegs, true>(rv, rings.vslot(Ic<G + D>{}), G + D, last, wave, lane);
+  });
+  ra.read_k(rings.kslot(Ic<0>{}), kops);
+  ra.gemm1(kops, sa);
+
+  for (int t0 = 0; t0 < ntiles; t0 += kUnroll) {
+    static_for(std::make_integer_sequence<int, kUnroll>{}, [&](auto i) __attribute__((always_inline)) {
+      const int t = t0 + decltype(i)::value;
+      if (t < ntiles) iteration(i, t);
+    });
+  }
+  // GEMM2_B of the last tile (its V operands and P_B are in registers).
+  rb.gemm2(vops);
+
+  __builtin_amdgcn_s_waitcnt(0);
+  ra.store(O + head_off);
+  rb.store(O + head_off);
+}
+
+// Q is prescaled by cq = +-min(c, 1) in the kernel; the remaining factor
+// cr = c / |cq| (1 unless c > 1) is applied to the scores.
+struct Scales {
+  float cq, cr;
+  bool scaled;
+  explicit Scales(const FwdArgs& a) {
+    const float c = a.scale_log2;
+    cq = (c <= 1.0f ? c : 1.0f) * (a.negate ? -1.0f : 1.0f);
+    cr = c <= 1.0f ? 1.0f : c;
+    scaled = cr != 1.0f;
+  }
+};
+
+template <template <bool, bool> class Launcher>
+hipError_t dispatch(const FwdArgs& a, hipStream_t stream, int br) {
   const int nqb = (a.seq + br - 1) / br;
   const dim3 grid((unsigned)(nqb * a.batch_heads));
-  const dim3 block(64 * W);
-  const auto* q = static_cast<const _Float16*>(a.q);
-  const auto* k = static_cast<const _Float16*>(a.k);
-  const auto* v = static_cast<const _Float16*>(a.v);
-  auto* o = static_cast<_Float16*>(a.o);
-  if (a.causal)
-    hipLaunchKernelGGL((fa2_fwd_kernel<W, true>), grid, block, 0, stream, q, k, v, o, a.seq, nqb,
-                       a.scale_log2, a.negate);
-  else
-    hipLaunchKernelGGL((fa2_fwd_kernel<W, false>), grid, block, 0, stream, q, k, v, o, a.seq, nqb,
-                       a.scale_log2, a.negate);
+  const Scales sc(a);
+  if (a.causal) {
+    if (sc.scaled) Launcher<true, true>::run(a, grid, nqb, sc.cq, sc.cr, stream);
+    else Launcher<true, false>::run(a, grid, nqb, sc.cq, sc.cr, stream);
+  } else {
+    if (sc.scaled) Launcher<false, true>::run(a, grid, nqb, sc.cq, sc.cr, stream);
+    else Launcher<false, false>::run(a, grid, nqb, sc.cq, sc.cr, stream);
+  }
   return hipGetLastError();
 }
+
+template <int W, int D>
+struct PipelinedLaunch {
+  template <bool C, bool S>
+  struct L {
+    static void run(const FwdArgs& a, dim3 grid, int nqb, float cq, float cr, hipStream_t st) {
+      hipLaunchKernelGGL((fa2_fwd_kernel<W, D, C, S>), grid, dim3(64 * W), 0, st,
+                         static_cast<const _Float16*>(a.q), static_cast<const _Float16*>(a.k),
+                         static_cast<const _Float16*>(a.v), static_cast<_Float16*>(a.o), a.seq,
+                         nqb, cq, cr);
+    }
+  };
+};
+
+template <int D>
+struct TwoBlockLaunch {
+  template <bool C, bool S>
+  struct L {
+    static void run(const FwdArgs& a, dim3 grid, int nqb, float cq, float cr, hipStream_t st) {
+      hipLaunchKernelGGL((fa2_fwd_x2_kernel<D, C, S>), grid, dim3(256), 0, st,
+                         static_cast<const _Float16*>(a.q), static_cast<const _Float16*>(a.k),
+                         static_cast<const _Float16*>(a.v), static_cast<_Float16*>(a.o), a.seq,
+                         nqb, cq, cr);
+    }
+  };
+};
+
+template <int D>
+struct PingPongLaunch {
+  template <bool C, bool S>
+  struct L {
+    static void run(const FwdArgs& a, dim3 grid, int nqb, float cq, float cr, hipStream_t st) {
+      hipLaunchKernelGGL((fa2_fwd_pp_kernel<D, C, S>), grid, dim3(512), 0, st,
+                         static_cast<const _Float16*>(a.q), static_cast<const _Float16*>(a.k),
+                         static_cast<const _Float16*>(a.v), static_cast<_Float16*>(a.o), a.seq,
+                         nqb, cq, cr);
+    }
+  };
+};
 
 }  // namespace
 
@@ -358,14 +840,20 @@ const Fa2Config kFa2Configs[kNumFa2Configs] = {
     {2, "br64_bc64_w2"},
     {4, "br128_bc64_w4"},
     {8, "br256_bc64_w8"},
+    {8, "br256_bc64_w8_pingpong"},
+    {8, "br256_bc64_w4x2"},
 };
 
+// Fetch distance: three tiles ahead where LDS allows (64 KiB of rings per
+// work-group), one tile for single-wave groups.
 hipError_t launch_fa2(const FwdArgs& a, int cfg, hipStream_t stream) {
-  switch (kFa2Configs[cfg].waves) {
-    case 1: return launch_w<1>(a, stream);
-    case 2: return launch_w<2>(a, stream);
-    case 4: return launch_w<4>(a, stream);
-    case 8: return launch_w<8>(a, stream);
+  switch (cfg) {
+    case 0: return dispatch<PipelinedLaunch<1, 1>::L>(a, stream, 32);
+    case 1: return dispatch<PipelinedLaunch<2, 3>::L>(a, stream, 64);
+    case 2: return dispatch<PipelinedLaunch<4, 3>::L>(a, stream, 128);
+    case 3: return dispatch<PipelinedLaunch<8, 3>::L>(a, stream, 256);
+    case 4: return dispatch<PingPongLaunch<3>::L>(a, stream, 256);
+    case 5: return dispatch<TwoBlockLaunch<3>::L>(a, stream, 256);
     default: return hipErrorInvalidValue;
   }
 }

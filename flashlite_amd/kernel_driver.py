@@ -1,0 +1,62 @@
+"""Runs one forward configuration a fixed number of times, for profilers.
+
+    python -m flashlite_amd.kernel_driver --workload C2_headline_B2H8N4096 \
+        --causal 0 --config -1 --iters 20
+
+Inputs are the workload's seeded synthetic tensors, resident on the GPU
+before the first launch; each launch goes through the C ABI
+(``fl_attn_fwd_f16_cfg``, or ``fl_attn_naive_f16`` with ``--naive``) on the
+current stream.  Under ``rocprofv3 --kernel-trace --stats`` or ``--pmc`` the
+kernel's dispatches are the only ones besides the input uploads.  Prints the
+mean launch time measured with HIP events on that stream.
+"""
+
+from __future__ import annotations
+
+import argparse
+import sys
+
+
+def main(argv=None):
+    ap = argparse.ArgumentParser(description="run one forward configuration repeatedly")
+    ap.add_argument("--workload", default="C2_headline_B2H8N4096")
+    ap.add_argument("--causal", type=int, default=0)
+    ap.add_argument("--config", type=int, default=-1, help="tile configuration (-1 = dispatcher)")
+    ap.add_argument("--iters", type=int, default=20)
+    ap.add_argument("--naive", action="store_true")
+    args = ap.parse_args(argv)
+
+    import torch
+
+    from flashlite_amd import capi
+    from flashlite_amd.workloads import WORKLOADS, workload_inputs
+
+    w = WORKLOADS[args.workload]
+    dev = torch.device("cuda:0")
+    q, k, v = (torch.from_numpy(x).to(dev) for x in workload_inputs(w))
+    o = torch.empty_like(q)
+    p = capi.tensor_params(q, k, v, o, w.sm_scale, bool(args.causal))
+    stream = torch.cuda.current_stream().cuda_stream
+    cfg = capi.select_config(p) if args.config < 0 else args.config
+
+    def launch():
+        rc = capi.naive(p, stream) if args.naive else capi.fwd(p, stream, cfg)
+        capi.check(rc)
+
+    launch()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(args.iters):
+        launch()
+    end.record()
+    torch.cuda.synchronize()
+    us = start.elapsed_time(end) * 1e3 / args.iters
+    flops = (2.0 if args.causal else 4.0) * w.batch * w.heads * w.seq ** 2 * w.head_dim
+    name = "naive" if args.naive else capi.config_name(cfg)
+    print(f"{args.workload} causal={args.causal} {name}: {us:.2f} us/launch, "
+          f"{flops / us / 1e6:.1f} TFLOP/s", flush=True)
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -28,10 +28,11 @@ def test_library_loads_and_exports_header_symbols():
 
 
 def test_config_table():
-    assert capi.num_configs() == 4
-    names = [capi.config_name(i) for i in range(4)]
-    assert names == ["br32_bc64_w1", "br64_bc64_w2", "br128_bc64_w4", "br256_bc64_w8"]
-    assert capi.config_name(4) is None and capi.config_name(-1) is None
+    assert capi.num_configs() == 6
+    names = [capi.config_name(i) for i in range(6)]
+    assert names == ["br32_bc64_w1", "br64_bc64_w2", "br128_bc64_w4", "br256_bc64_w8",
+                     "br256_bc64_w8_pingpong", "br256_bc64_w4x2"]
+    assert capi.config_name(6) is None and capi.config_name(-1) is None
 
 
 def _p(**kw):
@@ -79,7 +80,7 @@ def test_non_finite_scale():
 
 
 def test_bad_config():
-    assert capi.fwd(_p(), config=4) == capi.FL_ERR_BAD_CONFIG
+    assert capi.fwd(_p(), config=6) == capi.FL_ERR_BAD_CONFIG
     assert capi.fwd(_p(), config=-2) == capi.FL_ERR_BAD_CONFIG
 
 

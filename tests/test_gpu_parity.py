@@ -18,13 +18,14 @@ from oracle import error_stats
 pytestmark = pytest.mark.gpu
 
 GOLDEN = os.path.join(os.path.dirname(__file__), "golden")
-NCFG = 4  # tile configurations exported by the library
+NCFG = 6  # tile configurations exported by the library
 
 
 def test_num_configs():
     assert capi.num_configs() == NCFG
     assert [capi.config_name(i) for i in range(NCFG)] == [
-        "br32_bc64_w1", "br64_bc64_w2", "br128_bc64_w4", "br256_bc64_w8"]
+        "br32_bc64_w1", "br64_bc64_w2", "br128_bc64_w4", "br256_bc64_w8", "br256_bc64_w8_pingpong",
+        "br256_bc64_w4x2"]
 
 
 @pytest.mark.parametrize("config", list(range(NCFG)))
