@@ -84,20 +84,23 @@ int check_pointers(const fl_attn_params* p, const char* who, uintptr_t align) {
   return FL_OK;
 }
 
-// Tile-configuration choice for 256 CUs.  Every configuration computes the
-// same result; this only picks the work-group height (32 * waves query rows)
-// so that there are at least two work-groups per CU when the problem allows,
-// and otherwise the smallest height (most work-groups).  It replaces the
-// reference's `seq_len >= 2048 -> Br=128` rule (kernel_flash2.cu:786-789),
-// which was sized for 20 SMs.
+// Tile-configuration choice for 256 CUs (measured on MI355X; every
+// configuration computes the same result).  Non-causal work-groups are all
+// equally long: one 256-row group of 8 waves per CU when there are enough of
+// them, else the key-range-split 128-row group (8 waves, two key halves)
+// while there are fewer than two 128-row groups per CU.  Causal groups differ
+// in length and are balanced by dispatch order, which needs many of them:
+// 128-row groups of 4 waves, two per CU.  Smaller problems fall back to
+// smaller groups.  Replaces the reference's `seq_len >= 2048 -> Br=128` rule
+// (kernel_flash2.cu:786-789), which was sized for 20 SMs.
 int select_fa2(const fl::FwdArgs& a) {
-  constexpr int64_t kTargetWgs = 2 * 256;
-  for (int cfg = 3; cfg >= 0; --cfg) {
-    const int64_t br = 32 * fl::kFa2Configs[cfg].waves;
-    const int64_t wgs = (a.seq + br - 1) / br * (int64_t)a.batch_heads;
-    if (wgs >= kTargetWgs) return cfg;
-  }
-  return 0;
+  constexpr int64_t kCus = 256;
+  auto wgs = [&](int64_t br) { return (a.seq + br - 1) / br * (int64_t)a.batch_heads; };
+  if (!a.causal && wgs(256) >= kCus) return 3;                       // br256_bc64_w8
+  if (!a.causal && a.seq >= 2048 && wgs(128) < 2 * kCus) return 6;  // br128_bc64_w4_split2
+  if (wgs(128) >= kCus / 4) return 2;                                // br128_bc64_w4
+  if (wgs(64) >= kCus / 4) return 1;                                 // br64_bc64_w2
+  return 0;                                                          // br32_bc64_w1
 }
 
 int check_fa2(const fl_attn_params* p, fl::FwdArgs* a) {
@@ -106,6 +109,11 @@ int check_fa2(const fl_attn_params* p, fl::FwdArgs* a) {
   if (rc != FL_OK) return rc;
   if (p->head_dim != 64)
     return fail(FL_ERR_UNSUPPORTED, "FlashLite WMMA kernel currently requires head_dim == 64");
+  // K/V tiles are fetched through 32-bit buffer offsets within one head
+  // (N * 128 bytes, plus one tile of slack).
+  if (a->seq > (INT32_MAX / 128) - 128)
+    return fail(FL_ERR_UNSUPPORTED, "%s: N=%d exceeds the per-head addressing limit (%d)", who, a->seq,
+                (INT32_MAX / 128) - 128);
   // Grid = ceil(N/32) * B*H work-groups at the smallest tile; per-head
   // offsets are 64-bit in the kernel.
   if (((int64_t)a->seq + 31) / 32 * (int64_t)a->batch_heads > INT32_MAX)

@@ -98,6 +98,7 @@ constexpr int kBc = 64;                      // keys per KV tile
 constexpr int kRowBytes = kD * 2;            // 128
 constexpr int kTileBytes = kBc * kRowBytes;  // 8 KiB
 constexpr float kLag = 8.0f;                 // max lag of m behind a row max, log2 units
+constexpr float kSumLimit = 32768.0f;        // lane tile-sum bound that keeps p in fp16 range
 
 __device__ __forceinline__ int k_swz(int row) { return (row & 7) ^ ((row >> 3) & 1); }
 __device__ __forceinline__ int v_swz(int row) { return (row & 3) << 1; }
@@ -158,15 +159,35 @@ __device__ __forceinline__ void static_for(std::integer_sequence<int, I...>, F&&
 }
 
 // Work-group -> (batch*head, query block).  Work-groups are dealt to the 8
-// XCDs round-robin; remap so that consecutive query blocks of one head land
-// on the same XCD (shared K/V in its L2).  Causal: heaviest first.
-template <bool CAUSAL>
+// XCDs round-robin; remap so that the query blocks of a head land on the
+// same XCD (shared K/V in its L2).  Causal work-groups differ in length, so
+// each XCD is fed heaviest first (longest-processing-time order, heads
+// interleaved); with kSlotsPerCu == 2 co-resident work-groups the first 64
+// of an XCD (one per slot of its 32 CUs, dealt CU by CU) are arranged so
+// that each CU pairs the j-th heaviest block with the j-th lightest.
+template <bool CAUSAL, int kSlotsPerCu>
 __device__ __forceinline__ void wg_coords(int nqb, int& bh, int& qb) {
+  constexpr int kCusPerXcd = 32;
   const int total = gridDim.x;
-  int lin = blockIdx.x;
-  if ((total & 7) == 0) lin = (lin & 7) * (total >> 3) + (lin >> 3);
-  bh = lin / nqb;
-  qb = lin - bh * nqb;
+  const int i = blockIdx.x;
+  const int per = total >> 3;
+  if ((total & 7) != 0) {
+    bh = i / nqb;
+    qb = i - bh * nqb;
+  } else if (!CAUSAL || per % nqb != 0) {
+    const int lin = (i & 7) * per + (i >> 3);
+    bh = lin / nqb;
+    qb = lin - bh * nqb;
+  } else {
+    const int hx = per / nqb;  // whole heads per XCD
+    const int k = i >> 3;      // dispatch position within the XCD
+    constexpr int first = kCusPerXcd * kSlotsPerCu;
+    int r = k;                 // work rank, 0 = heaviest
+    if (kSlotsPerCu == 2 && per >= first && k >= kCusPerXcd && k < first)
+      r = first - 1 - (k - kCusPerXcd);
+    bh = (i & 7) * hx + r % hx;
+    qb = r / hx;
+  }
   if (CAUSAL) qb = nqb - 1 - qb;
 }
 
@@ -174,9 +195,9 @@ __device__ __forceinline__ void wg_coords(int nqb, int& bh, int& qb) {
 // (negative indices wrap).
 template <int kSlots>
 struct Rings {
-  static_assert(kSlots >= 2 && kSlots <= 4, "ring depth");
-  uint8_t* k[4];
-  uint8_t* v[4];
+  static_assert(kSlots >= 2 && kSlots <= 8, "ring depth");
+  uint8_t* k[8];
+  uint8_t* v[8];
   template <int I>
   __device__ __forceinline__ uint8_t* kslot(Ic<I>) const {
     return k[((I % kSlots) + kSlots) % kSlots];
@@ -214,6 +235,7 @@ __device__ __forceinline__ void fetch_tile(const i32x4_t& rs, const uint8_t* slo
 template <bool CAUSAL, bool SCALED>
 struct Rows {
   int g, col, qw, my_q, seq;
+  int kv_lim;       // keys >= kv_lim are masked (seq, or the end of a split range)
   int tr_row, tr_col;
   float cr;
   half8_t qf[4];    // Q'^T B-operand
@@ -230,6 +252,7 @@ struct Rows {
     qw = qw_;
     my_q = qw + col;
     seq = seq_;
+    kv_lim = seq_;
     cr = cr_;
     // GEMM2 tr-read address pieces: lane l is lane j = l%16 of 16-lane group
     // G = l/16; it points at key row 4*(G/2) + j/4 (+16t, +8 for the second
@@ -298,23 +321,39 @@ struct Rows {
                                                        0, 0, 0);
   }
   // GEMM2: O^T += V^T . P^T
-  __device__ __forceinline__ void gemm2(const half8_t (&va)[2][4]) {
+  __device__ __forceinline__ void gemm2(const half8_t (&va)[2][4], const half8_t (&pp)[2][2]) {
 #pragma unroll
     for (int db = 0; db < 2; ++db)
 #pragma unroll
       for (int t = 0; t < 4; ++t)
-        o[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va[db][t], p[t >> 1][t & 1], o[db], 0, 0, 0);
+        o[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va[db][t], pp[t >> 1][t & 1], o[db], 0, 0, 0);
   }
-  // Masks keys >= seq and, when causal, keys after the lane's query (tile t).
+  __device__ __forceinline__ void gemm2(const half8_t (&va)[2][4]) { gemm2(va, p); }
+  // GEMM1 of one tile and GEMM2 of another, issued as four interleaved
+  // accumulation chains (s[0], o[0], s[1], o[1]) so consecutive MFMAs never
+  // depend on each other.
+  __device__ __forceinline__ void gemm12(const half8_t (&ka)[2][4], float16_t (&s)[2],
+                                         const half8_t (&va)[2][4], const half8_t (&pp)[2][2]) {
+#pragma unroll
+    for (int st = 0; st < 4; ++st) {
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        s[h] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka[h][st], qf[st], st == 0 ? bias : s[h], 0, 0, 0);
+        o[h] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va[h][st], pp[st >> 1][st & 1], o[h], 0, 0, 0);
+      }
+    }
+  }
+  // Masks keys >= kv_lim and, when causal, keys after the lane's query
+  // (tile t).
   __device__ __forceinline__ void mask(int t, float16_t (&s)[2]) const {
     const int k0 = t * kBc;
-    if (k0 + kBc > seq || (CAUSAL && k0 + kBc - 1 > qw)) {
+    if (k0 + kBc > kv_lim || (CAUSAL && k0 + kBc - 1 > qw)) {
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
           const int key = k0 + 32 * kb + 8 * (r >> 2) + 4 * g + (r & 3);
-          const bool ok = key < seq && (!CAUSAL || key <= my_q);
+          const bool ok = key < kv_lim && (!CAUSAL || key <= my_q);
           s[kb][r] = ok ? s[kb][r] : ninf();
         }
     }
@@ -339,18 +378,21 @@ struct Rows {
 #pragma unroll
     for (int r = 0; r < 16; ++r) bias[r] = -mm;
   }
-  // First tile: m = the exact row max (every row sees key 0, so it is finite).
+  // First tile: m = the exact row max.  A row with no key in the tile (only
+  // possible for the second range of a split, where such a row then has no
+  // key in the whole range) gets m = 0 and p = 0 throughout.
   __device__ __forceinline__ void first_tile(float16_t (&s)[2]) {
-    const float m0 = tile_max(s);
+    float m0 = tile_max(s);
+    m0 = m0 == ninf() ? 0.0f : m0;
     sub(s, m0);
     set_m(m0);
   }
   // p = 2^(t - m) (times cr when SCALED) packed to fp16 B-operands; returns
-  // this lane's sum of the fp16-rounded p (v_dot2_f32_f16 against (1, 1)),
-  // in two partial sums for instruction-level parallelism.
-  __device__ __forceinline__ float exponentiate(const float16_t (&s)[2]) {
-    const half2_t one = {(_Float16)1.0f, (_Float16)1.0f};
-    float sum0 = 0.0f, sum1 = 0.0f;
+  // this lane's sum of p, taken in fp32 over four chains.  (The row sum uses
+  // v_add_f32 rather than v_dot2_f32_f16 on the packed p: on gfx950 the dot2
+  // instructions do not issue alongside MFMA work, adds and conversions do.)
+  __device__ __forceinline__ float exponentiate(const float16_t (&s)[2], half8_t (&pn)[2][2]) const {
+    float sum[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
@@ -362,16 +404,43 @@ struct Rows {
             x0 *= cr;
             x1 *= cr;
           }
-          const half2_t ph = {(_Float16)__builtin_amdgcn_exp2f(x0),
-                              (_Float16)__builtin_amdgcn_exp2f(x1)};
-          p[kb][h][e] = ph[0];
-          p[kb][h][e + 1] = ph[1];
-          if (kb == 0)
-            sum0 = __builtin_amdgcn_fdot2(ph, one, sum0, false);
-          else
-            sum1 = __builtin_amdgcn_fdot2(ph, one, sum1, false);
+          const float e0 = __builtin_amdgcn_exp2f(x0), e1 = __builtin_amdgcn_exp2f(x1);
+          pn[kb][h][e] = (_Float16)e0;
+          pn[kb][h][e + 1] = (_Float16)e1;
+          sum[2 * kb + h] += e0 + e1;
         }
-    return sum0 + sum1;
+    return (sum[0] + sum[1]) + (sum[2] + sum[3]);
+  }
+  __device__ __forceinline__ float exponentiate(const float16_t (&s)[2]) { return exponentiate(s, p); }
+  // Softmax of tile j into pn with the stabiliser checked after the fact,
+  // for schedules where GEMM2 trails by one tile: at this point O holds tiles
+  // < j and S_next (tile j+1) was computed against the current m.  When a
+  // lane's partial row sum exceeds 2^15 (rare: a row max rose well above m;
+  // also catches inf/NaN), m moves up to the tile's row max, O, l and
+  // S_next are rescaled / shifted and the tile is exponentiated again.
+  // Nothing in the common path depends on a comparison, so the exponentials
+  // are free to interleave with both GEMMs.
+  template <class F>
+  __device__ __forceinline__ void softmax_trailing(float16_t (&s)[2], half8_t (&pn)[2][2],
+                                                   F&& on_shift) {
+    float sum = exponentiate(s, pn);
+    // Keep the fp16 packing ahead of the branch (it would otherwise be sunk
+    // past it, out of reach of the MFMAs it can overlap).
+    asm volatile("" : : "v"(pn[0][0]), "v"(pn[0][1]), "v"(pn[1][0]), "v"(pn[1][1]));
+    if (__builtin_amdgcn_ballot_w64(!(sum <= kSumLimit)) != 0) {
+      const float d = fmaxf(tile_max(s), 0.0f);
+      const float alpha = __builtin_amdgcn_exp2f(-(SCALED ? cr : 1.0f) * d);
+      l *= alpha;
+#pragma unroll
+      for (int db = 0; db < 2; ++db)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) o[db][r] *= alpha;
+      sub(s, d);
+      on_shift(d);
+      set_m(m + d);
+      sum = exponentiate(s, pn);
+    }
+    l += sum;
   }
   // Lazy stabiliser, decided before any exponential: scores are t - m and
   // while every row's tile max stays within kLag (log2 units) of m, p stays
@@ -403,6 +472,31 @@ struct Rows {
   __device__ __forceinline__ void softmax(float16_t (&s)[2], F&& on_shift) {
     restabilise(s, on_shift);
     l += exponentiate(s);
+  }
+  // Split key range: the partner wave holds the same rows over a disjoint
+  // key range.  Its O, m and l go through LDS as part[k * 64 + lane]
+  // (k < 32: O, 32: m, 33: l) and are combined at the larger m.
+  __device__ __forceinline__ void save_partial(float* part, int lane) const {
+#pragma unroll
+    for (int db = 0; db < 2; ++db)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) part[(16 * db + r) * 64 + lane] = o[db][r];
+    part[32 * 64 + lane] = m;
+    part[33 * 64 + lane] = l;
+  }
+  __device__ __forceinline__ void merge_partial(const float* part, int lane) {
+    const float m1 = part[32 * 64 + lane], l1 = part[33 * 64 + lane];
+    const bool has1 = pair_sum(l1) > 0.0f;  // rows with no key in the other range
+    const float mm = has1 ? fmaxf(m, m1) : m;
+    const float k = SCALED ? cr : 1.0f;
+    const float a0 = __builtin_amdgcn_exp2f(k * (m - mm));
+    const float a1 = has1 ? __builtin_amdgcn_exp2f(k * (m1 - mm)) : 0.0f;
+    l = a0 * l + a1 * l1;
+#pragma unroll
+    for (int db = 0; db < 2; ++db)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) o[db][r] = a0 * o[db][r] + a1 * part[(16 * db + r) * 64 + lane];
+    m = mm;
   }
   // O = O^T / l, 16-byte stores of 8 contiguous head dims; rows >= N skipped.
   __device__ __forceinline__ void store(_Float16* Oh) const {
@@ -437,15 +531,39 @@ __device__ __forceinline__ void zero_v_slots(const Rings<kSlots>& rings) {
 
 #define FL_DECLARE_RINGS(R)                                                          \
   __shared__ __attribute__((aligned(16))) uint8_t kr0[kTileBytes], kr1[kTileBytes], \
-      kr2[kTileBytes], kr3[kTileBytes];                                              \
+      kr2[kTileBytes], kr3[kTileBytes], kr4[kTileBytes], kr5[kTileBytes],           \
+      kr6[kTileBytes], kr7[kTileBytes];                                              \
   __shared__ __attribute__((aligned(16))) uint8_t vr0[kTileBytes], vr1[kTileBytes], \
-      vr2[kTileBytes], vr3[kTileBytes];                                              \
-  const Rings<R> rings = {{kr0, kr1, kr2, kr3}, {vr0, vr1, vr2, vr3}}
+      vr2[kTileBytes], vr3[kTileBytes], vr4[kTileBytes], vr5[kTileBytes],           \
+      vr6[kTileBytes], vr7[kTileBytes];                                              \
+  const Rings<R> rings = {{kr0, kr1, kr2, kr3, kr4, kr5, kr6, kr7},                \
+                          {vr0, vr1, vr2, vr3, vr4, vr5, vr6, vr7}}
+
+// K/V rings of one key-range stream: kSlots consecutive tiles per tensor,
+// slot I selected by a static index (negative indices wrap), so every slot
+// address is the stream base plus a constant.
+template <int kSlots>
+struct StreamRings {
+  uint8_t* k;
+  uint8_t* v;
+  template <int I>
+  __device__ __forceinline__ uint8_t* kslot(Ic<I>) const {
+    return k + kTileBytes * (((I % kSlots) + kSlots) % kSlots);
+  }
+  template <int I>
+  __device__ __forceinline__ uint8_t* vslot(Ic<I>) const {
+    return v + kTileBytes * (((I % kSlots) + kSlots) % kSlots);
+  }
+};
 
 // ---------------------------------------------------------------------------
-// Pipelined schedule, W waves.  D = fetch distance in tiles.
-template <int W, int D, bool CAUSAL, bool SCALED>
-__global__ void __launch_bounds__(64 * W, 2)
+// Pipelined schedule: W waves of 32 query rows, D = fetch distance in tiles.
+// SPLIT = 2 adds a second set of W waves for the same rows that walks the
+// second half of the key range with its own rings (waves w and w + W share
+// a SIMD); the halves are merged through LDS at the end.  That halves the
+// longest key walk, the critical path of causal attention's last q-blocks.
+template <int W, int D, int SPLIT, bool CAUSAL, bool SCALED>
+__global__ void __launch_bounds__(64 * W * SPLIT, SPLIT == 1 ? 2 : 1)
 fa2_fwd_kernel(const _Float16* Q, const _Float16* __restrict__ K,
                const _Float16* __restrict__ V, _Float16* O, int seq, int nqb,
                float cq, float cr) {
@@ -454,82 +572,121 @@ fa2_fwd_kernel(const _Float16* Q, const _Float16* __restrict__ K,
   constexpr int kBr = 32 * W;
   constexpr int kSegs = 8 / W;            // 1 KiB DMA segments per wave per tile
   constexpr int kDmaPerIter = 2 * kSegs;  // K + V loads a wave issues per iteration
+  constexpr int kRingBytes = SPLIT * kSlots * kTileBytes;
   static_assert(kSegs * W == 8, "tile split");
-  FL_DECLARE_RINGS(kSlots);
+  static_assert(SPLIT == 1 || SPLIT == 2, "key-range split");
+  static_assert(SPLIT == 1 || kRingBytes >= W * 34 * 64 * 4, "merge buffer");
+  __shared__ __attribute__((aligned(16))) uint8_t kring[kRingBytes];
+  __shared__ __attribute__((aligned(16))) uint8_t vring[kRingBytes];
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int stream = wave / W;       // key-range half
+  const int rw = wave - stream * W;  // 32-row block within the work-group
   int bh, qb;
-  wg_coords<CAUSAL>(nqb, bh, qb);
+  wg_coords<CAUSAL, (W == 4 && SPLIT == 1) ? 2 : 1>(nqb, bh, qb);
   const size_t head_off = (size_t)bh * (size_t)seq * kD;
   const i32x4_t rk = buffer_rsrc(K + head_off, seq * kRowBytes);
   const i32x4_t rv = buffer_rsrc(V + head_off, seq * kRowBytes);
   const int q0 = qb * kBr;
+  const StreamRings<kSlots> rings = {kring + stream * (kSlots * kTileBytes),
+                                     vring + stream * (kSlots * kTileBytes)};
 
   Rows<CAUSAL, SCALED> rows;
-  rows.init(Q + head_off, lane, q0 + 32 * wave, seq, cq, cr);
+  rows.init(Q + head_off, lane, q0 + 32 * rw, seq, cq, cr);
 
   int ntiles = (seq + kBc - 1) / kBc;
   if (CAUSAL) ntiles = min(ntiles, (min(q0 + kBr, seq) - 1) / kBc + 1);
-  const int last = ntiles - 1;
+  // Key tiles [tbeg, tend) of this stream; both streams run t0 + 1
+  // iterations (the same barriers), the shorter one on masked tiles.
+  const int t0 = SPLIT == 1 ? ntiles : (ntiles + 1) / 2;
+  const int tbeg = stream == 0 ? 0 : t0;
+  const int tend = stream == 0 ? t0 : ntiles;
+  const int last = max(tend - 1, tbeg);  // fetch clamp
+  if (SPLIT == 2 && stream == 0) rows.kv_lim = min(seq, t0 * kBc);
 
-  // One iteration for tile j (position I of the unrolled loop): fetch
-  // K(j+D+1), V(j+D) into the slots K(j) and V(j-1) vacated before the
-  // previous barrier; read the K(j+1) and V(j) operands; softmax(j)
-  // alongside GEMM1(j+1); GEMM2(j); wait for this wave's part of K(j+2) and
-  // V(j+1), barrier.
-  auto iteration = [&](auto i, int j, float16_t (&S)[2], float16_t (&Sn)[2]) __attribute__((always_inline)) {
+  // Iteration j (position I of the unrolled loop), for j = 0 .. t0, on key
+  // tile t = tbeg + j: fetch K(t+D+1) and V(t+D-1) into the slots of K(t)
+  // and V(t-2), vacated before the previous barrier; read the K(t+1) and
+  // V(t-1) operands; then three independent pieces of work the compiler
+  // interleaves: GEMM1(t+1), GEMM2(t-1) with P(t-1), and the softmax of S(t)
+  // into P(t).  Finally mask S(t+1), wait for this wave's part of K(t+2) and
+  // V(t), barrier.  Iteration 0 multiplies a zeroed V slot by P = 0, and
+  // iteration t0 exponentiates a fully masked S (p = 0); both only fill the
+  // pipeline.
+  auto iteration = [&](auto i, int j, float16_t (&S)[2], float16_t (&Sn)[2], half8_t (&P)[2][2],
+                       const half8_t (&Pp)[2][2]) __attribute__((always_inline)) {
     constexpr int I = decltype(i)::value;
-    fetch_tile<kSegs, false>(rk, rings.kslot(Ic<I + D + 1>{}), j + D + 1, last, wave, lane);
-    fetch_tile<kSegs, true>(rv, rings.vslot(Ic<I + D>{}), j + D, last, wave, lane);
+    const int t = tbeg + j;
+    fetch_tile<kSegs, false>(rk, rings.kslot(Ic<I + D + 1>{}), t + D + 1, last, rw, lane);
+    fetch_tile<kSegs, true>(rv, rings.vslot(Ic<I + D - 1>{}), t + D - 1, last, rw, lane);
     half8_t ka[2][4], va[2][4];
     rows.read_k(rings.kslot(Ic<I + 1>{}), ka);
-    rows.read_v(rings.vslot(Ic<I>{}), va);
-    // GEMM1 of a tile past the end reads a stale slot; its result is unused.
-    rows.gemm1(ka, Sn);
-    rows.softmax(S, [&](float d) __attribute__((always_inline)) { Rows<CAUSAL, SCALED>::sub(Sn, d); });
-    rows.gemm2(va);
-    rows.mask(j + 1, Sn);
+    rows.read_v(rings.vslot(Ic<I - 1>{}), va);
+    // GEMM1 of a tile past the range reads a stale slot; its result is masked.
+    rows.gemm12(ka, Sn, va, Pp);
+    rows.softmax_trailing(S, P, [&](float d) __attribute__((always_inline)) {
+      Rows<CAUSAL, SCALED>::sub(Sn, d);
+    });
+    rows.mask(t + 1, Sn);
     sync_ring<(D - 1) * kDmaPerIter>();
   };
 
-  // ---- prologue: K(0), V(0), K(1) landed; fetch groups of iterations
-  // 1-D .. -1 in flight; S(0) with the exact row max.
-  zero_v_slots<kSlots, 64 * W>(rings);
-  fetch_tile<kSegs, false>(rk, rings.kslot(Ic<0>{}), 0, last, wave, lane);
-  fetch_tile<kSegs, true>(rv, rings.vslot(Ic<0>{}), 0, last, wave, lane);
-  fetch_tile<kSegs, false>(rk, rings.kslot(Ic<1>{}), 1, last, wave, lane);
+  // ---- prologue: K(tbeg), K(tbeg+1) landed; fetch groups of iterations
+  // 1-D .. -1 in flight; S(tbeg) with the exact row max.
+  {
+    const u32x4_t z = {0, 0, 0, 0};
+    for (int off = 16 * (int)threadIdx.x; off < kRingBytes; off += 16 * 64 * W * SPLIT)
+      *reinterpret_cast<u32x4_t*>(vring + off) = z;
+    __syncthreads();
+  }
+  fetch_tile<kSegs, false>(rk, rings.kslot(Ic<0>{}), tbeg, last, rw, lane);
+  fetch_tile<kSegs, false>(rk, rings.kslot(Ic<1>{}), tbeg + 1, last, rw, lane);
   sync_ring<0>();
   static_for(std::make_integer_sequence<int, D - 1>{}, [&](auto i) __attribute__((always_inline)) {
     constexpr int G = decltype(i)::value + 1 - D;  // iteration 1-D+i
-    fetch_tile<kSegs, false>(rk, rings.kslot(Ic<G + D + 1>{}), G + D + 1, last, wave, lane);
-    fetch_tile<kSegs, true>(rv, rings.vslot(Ic<G + D>{}), G + D, last, wave, lane);
+    fetch_tile<kSegs, false>(rk, rings.kslot(Ic<G + D + 1>{}), tbeg + G + D + 1, last, rw, lane);
+    fetch_tile<kSegs, true>(rv, rings.vslot(Ic<G + D - 1>{}), tbeg + G + D - 1, last, rw, lane);
   });
   float16_t S0[2], S1[2];
+  half8_t P0[2][2], P1[2][2];
+#pragma unroll
+  for (int a = 0; a < 2; ++a)
+#pragma unroll
+    for (int b = 0; b < 2; ++b) P1[a][b] = (half8_t){0, 0, 0, 0, 0, 0, 0, 0};
   {
     half8_t ka[2][4];
     rows.read_k(rings.kslot(Ic<0>{}), ka);
     rows.gemm1(ka, S0);
   }
-  rows.mask(0, S0);
+  rows.mask(tbeg, S0);
   rows.first_tile(S0);
 
-  // ---- main loop, unrolled so ring slots and S / S_next roles are static ----
-  for (int j0 = 0; j0 < ntiles; j0 += kUnroll) {
+  // ---- main loop, unrolled so ring slots and S / P roles are static ----
+  for (int j0 = 0; j0 <= t0; j0 += kUnroll) {
     static_for(std::make_integer_sequence<int, kUnroll>{}, [&](auto i) __attribute__((always_inline)) {
       constexpr int I = decltype(i)::value;
       const int j = j0 + I;
-      if (j < ntiles) {
+      if (j <= t0) {
         if constexpr (I % 2 == 0)
-          iteration(i, j, S0, S1);
+          iteration(i, j, S0, S1, P0, P1);
         else
-          iteration(i, j, S1, S0);
+          iteration(i, j, S1, S0, P1, P0);
       }
     });
   }
 
-  // No fetch may still be writing LDS when the work-group retires.
+  // No fetch may still be writing LDS when the work-group retires or the
+  // rings are reused for the merge.
   __builtin_amdgcn_s_waitcnt(0);
+  if constexpr (SPLIT == 2) {
+    __syncthreads();
+    float* part = reinterpret_cast<float*>(kring) + rw * (34 * 64);
+    if (stream == 1) rows.save_partial(part, lane);
+    __syncthreads();
+    if (stream == 1) return;
+    rows.merge_partial(part, lane);
+  }
   rows.store(O + head_off);
 }
 
@@ -558,7 +715,7 @@ fa2_fwd_pp_kernel(const _Float16* Q, const _Float16* __restrict__ K,
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const bool group_b = wave >= 4;
   int bh, qb;
-  wg_coords<CAUSAL>(nqb, bh, qb);
+  wg_coords<CAUSAL, 1>(nqb, bh, qb);
   const size_t head_off = (size_t)bh * (size_t)seq * kD;
   const i32x4_t rk = buffer_rsrc(K + head_off, seq * kRowBytes);
   const i32x4_t rv = buffer_rsrc(V + head_off, seq * kRowBytes);
@@ -698,7 +855,7 @@ fa2_fwd_x2_kernel(const _Float16* Q, const _Float16* __restrict__ K,
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   int bh, qb;
-  wg_coords<CAUSAL>(nqb, bh, qb);
+  wg_coords<CAUSAL, 1>(nqb, bh, qb);
   const size_t head_off = (size_t)bh * (size_t)seq * kD;
   const i32x4_t rk = buffer_rsrc(K + head_off, seq * kRowBytes);
   const i32x4_t rv = buffer_rsrc(V + head_off, seq * kRowBytes);
@@ -794,12 +951,12 @@ hipError_t dispatch(const FwdArgs& a, hipStream_t stream, int br) {
   return hipGetLastError();
 }
 
-template <int W, int D>
+template <int W, int D, int SPLIT>
 struct PipelinedLaunch {
   template <bool C, bool S>
   struct L {
     static void run(const FwdArgs& a, dim3 grid, int nqb, float cq, float cr, hipStream_t st) {
-      hipLaunchKernelGGL((fa2_fwd_kernel<W, D, C, S>), grid, dim3(64 * W), 0, st,
+      hipLaunchKernelGGL((fa2_fwd_kernel<W, D, SPLIT, C, S>), grid, dim3(64 * W * SPLIT), 0, st,
                          static_cast<const _Float16*>(a.q), static_cast<const _Float16*>(a.k),
                          static_cast<const _Float16*>(a.v), static_cast<_Float16*>(a.o), a.seq,
                          nqb, cq, cr);
@@ -842,18 +999,20 @@ const Fa2Config kFa2Configs[kNumFa2Configs] = {
     {8, "br256_bc64_w8"},
     {8, "br256_bc64_w8_pingpong"},
     {8, "br256_bc64_w4x2"},
+    {8, "br128_bc64_w4_split2"},
 };
 
 // Fetch distance: three tiles ahead where LDS allows (64 KiB of rings per
 // work-group), one tile for single-wave groups.
 hipError_t launch_fa2(const FwdArgs& a, int cfg, hipStream_t stream) {
   switch (cfg) {
-    case 0: return dispatch<PipelinedLaunch<1, 1>::L>(a, stream, 32);
-    case 1: return dispatch<PipelinedLaunch<2, 3>::L>(a, stream, 64);
-    case 2: return dispatch<PipelinedLaunch<4, 3>::L>(a, stream, 128);
-    case 3: return dispatch<PipelinedLaunch<8, 3>::L>(a, stream, 256);
+    case 0: return dispatch<PipelinedLaunch<1, 1, 1>::L>(a, stream, 32);
+    case 1: return dispatch<PipelinedLaunch<2, 3, 1>::L>(a, stream, 64);
+    case 2: return dispatch<PipelinedLaunch<4, 3, 1>::L>(a, stream, 128);
+    case 3: return dispatch<PipelinedLaunch<8, 3, 1>::L>(a, stream, 256);
     case 4: return dispatch<PingPongLaunch<3>::L>(a, stream, 256);
     case 5: return dispatch<TwoBlockLaunch<3>::L>(a, stream, 256);
+    case 6: return dispatch<PipelinedLaunch<4, 3, 2>::L>(a, stream, 128);
     default: return hipErrorInvalidValue;
   }
 }

@@ -28,11 +28,11 @@ def test_library_loads_and_exports_header_symbols():
 
 
 def test_config_table():
-    assert capi.num_configs() == 6
-    names = [capi.config_name(i) for i in range(6)]
+    assert capi.num_configs() == 7
+    names = [capi.config_name(i) for i in range(7)]
     assert names == ["br32_bc64_w1", "br64_bc64_w2", "br128_bc64_w4", "br256_bc64_w8",
-                     "br256_bc64_w8_pingpong", "br256_bc64_w4x2"]
-    assert capi.config_name(6) is None and capi.config_name(-1) is None
+                     "br256_bc64_w8_pingpong", "br256_bc64_w4x2", "br128_bc64_w4_split2"]
+    assert capi.config_name(7) is None and capi.config_name(-1) is None
 
 
 def _p(**kw):
@@ -60,6 +60,12 @@ def test_seq_k_must_equal_seq_q():
     assert capi.naive(_p(seq_k=100)) == capi.FL_ERR_UNSUPPORTED
 
 
+def test_sequence_addressing_limit():
+    # K/V tiles are addressed with 32-bit offsets inside one head
+    assert capi.fwd(_p(batch=1, heads=1, seq_q=1 << 24)) == capi.FL_ERR_UNSUPPORTED
+    assert "addressing limit" in capi.last_error()
+
+
 def test_negative_sizes():
     assert capi.fwd(_p(batch=-1)) == capi.FL_ERR_INVALID_ARGUMENT
     assert capi.naive(_p(head_dim=0)) == capi.FL_ERR_INVALID_ARGUMENT
@@ -80,7 +86,7 @@ def test_non_finite_scale():
 
 
 def test_bad_config():
-    assert capi.fwd(_p(), config=6) == capi.FL_ERR_BAD_CONFIG
+    assert capi.fwd(_p(), config=7) == capi.FL_ERR_BAD_CONFIG
     assert capi.fwd(_p(), config=-2) == capi.FL_ERR_BAD_CONFIG
 
 
@@ -99,13 +105,21 @@ def test_naive_limits():
 
 
 def test_dispatcher_choices():
-    # At least two work-groups per CU (512) when the problem allows, else the
-    # smallest tile height.
     sel = lambda **kw: capi.select_config(_p(**kw))  # noqa: E731
-    assert sel(batch=2, heads=8, seq_q=4096) == 2     # 512 WGs of 128 rows
-    assert sel(batch=1, heads=16, seq_q=16384) == 3   # 1024 WGs of 256 rows
-    assert sel(batch=32, heads=32, seq_q=256) == 3    # 1024 WGs of 256 rows
-    assert sel(batch=2, heads=8, seq_q=512) == 0      # 256 WGs of 32 rows
+    # non-causal: 8-wave 256-row groups when there is one per CU
+    assert sel(batch=2, heads=8, seq_q=4096) == 3      # 256 groups
+    assert sel(batch=1, heads=16, seq_q=16384) == 3
+    assert sel(batch=32, heads=32, seq_q=256) == 3
+    # fewer than two 128-row groups per CU at N >= 2048: split key range
+    assert sel(batch=2, heads=8, seq_q=2048) == 6      # 256 groups of 128 rows
+    assert sel(batch=1, heads=1, seq_q=4096) == 6
+    # causal: 128-row groups balanced by dispatch order
+    assert sel(batch=2, heads=8, seq_q=4096, causal=True) == 2
+    assert sel(batch=1, heads=16, seq_q=16384, causal=True) == 2
+    assert sel(batch=32, heads=32, seq_q=256, causal=True) == 2
+    # small problems: smaller groups
+    assert sel(batch=2, heads=8, seq_q=512) == 2       # 64 groups of 128 rows
+    assert sel(batch=2, heads=4, seq_q=512) == 1       # 64 groups of 64 rows
     assert sel(batch=1, heads=1, seq_q=128) == 0
     assert sel(head_dim=80) == -1
 

@@ -18,14 +18,15 @@ from oracle import error_stats
 pytestmark = pytest.mark.gpu
 
 GOLDEN = os.path.join(os.path.dirname(__file__), "golden")
-NCFG = 6  # tile configurations exported by the library
+NCFG = 7  # tile configurations exported by the library
+SPLIT_CFG = 6  # the key-range-split configuration
 
 
 def test_num_configs():
     assert capi.num_configs() == NCFG
     assert [capi.config_name(i) for i in range(NCFG)] == [
         "br32_bc64_w1", "br64_bc64_w2", "br128_bc64_w4", "br256_bc64_w8", "br256_bc64_w8_pingpong",
-        "br256_bc64_w4x2"]
+        "br256_bc64_w4x2", "br128_bc64_w4_split2"]
 
 
 @pytest.mark.parametrize("config", list(range(NCFG)))
@@ -47,6 +48,24 @@ def test_benchmark_configs(cuda, name, causal):
     rows = None if w.seq <= 1024 else sample_rows(w.seq, seed=w.seed)
     mx, mean = assert_close_oracle(out, q, k, v, w.sm_scale, causal, rows=rows)
     print(f"{name} causal={causal}: max-abs {mx:.2e} mean-abs {mean:.2e}")
+
+
+@pytest.mark.parametrize("config", [2, 3, SPLIT_CFG])
+@pytest.mark.parametrize("causal", [False, True])
+def test_headline_each_config(cuda, config, causal):
+    w = WORKLOADS["C2_headline_B2H8N4096"]
+    q, k, v = workload_inputs(w)
+    out = run_capi(q, k, v, w.sm_scale, causal, cuda, config=config)
+    assert_close_oracle(out, q, k, v, w.sm_scale, causal, rows=sample_rows(w.seq, seed=w.seed))
+
+
+@pytest.mark.parametrize("scale", [-0.2, 1.0, 3.0])
+@pytest.mark.parametrize("causal", [False, True])
+def test_split_scales(cuda, scale, causal):
+    # peaked softmax: the stabiliser moves in both key ranges before the merge
+    q, k, v = make_qkv(1, 4, 700, 64, seed=43)
+    out = run_capi(q, k, v, scale, causal, cuda, config=SPLIT_CFG)
+    assert_close_oracle(out, q, k, v, scale, causal, max_abs=2e-3 if scale < 1 else 4e-3)
 
 
 def test_c3_long_causal(cuda):
