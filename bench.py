@@ -42,7 +42,8 @@ def parse():
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=25)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    ap.add_argument("--cpu-runs", type=int, default=3)
+    ap.add_argument("--cpu-seconds", type=float, default=10.0,
+                    help="CPU work per mask in the baseline leg (repeats full calls)")
     return ap.parse_args()
 
 
@@ -83,8 +84,9 @@ def median_event_latency(fn, runs=100):
     return lat[len(lat) // 2], lat[0], sum(lat) / len(lat)
 
 
-def cpu_baseline_leg(q16, k16, v16, gpu_out, sm_scale, runs):
-    """PyTorch-CPU SDPA in fp32 on the same inputs (timed), and the parity
+def cpu_baseline_leg(q16, k16, v16, gpu_out, sm_scale, seconds):
+    """PyTorch-CPU SDPA in fp32 on the same inputs: full calls repeated for
+    about `seconds` of CPU work per mask (median call time), and the parity
     of the GPU outputs against it."""
     import numpy as np
     import torch
@@ -97,12 +99,12 @@ def cpu_baseline_leg(q16, k16, v16, gpu_out, sm_scale, runs):
     for causal in (False, True):
         sdpa_cpu_f32(tq, tk, tv, sm_scale, causal)  # warm-up
         times = []
-        for _ in range(runs):
+        while len(times) < 3 or sum(times) < seconds:
             t0 = time.perf_counter()
             ref = sdpa_cpu_f32(tq, tk, tv, sm_scale, causal)
             times.append(time.perf_counter() - t0)
         mx, mean = error_stats(gpu_out[causal], ref.numpy().astype(np.float64))
-        res[causal] = (statistics.median(times), mx, mean)
+        res[causal] = (statistics.median(times), mx, mean, len(times))
     cpu_model = ""
     try:
         with open("/proc/cpuinfo") as f:
@@ -208,17 +210,17 @@ def main():
 
     if not args.no_cpu:
         res, threads, ncpu, model = cpu_baseline_leg(q16, k16, v16, gpu_out, w.sm_scale,
-                                                     args.cpu_runs)
-        t_nc, mx_nc, mean_nc = res[False]
-        t_c, mx_c, mean_c = res[True]
+                                                     args.cpu_seconds)
+        t_nc, mx_nc, mean_nc, n_nc = res[False]
+        t_c, mx_c, mean_c, n_c = res[True]
         line["cpu_baseline"] = {
             "value": round(nc["flops"] / t_nc / 1e12, 5),
             "unit": "TFLOP/s",
             "cores": threads,
             "kind": "port",
-            "sample": (f"full {HEADLINE} non-causal call, torch-CPU scaled_dot_product_attention "
-                       f"fp32, median of {args.cpu_runs} after 1 warm-up; host {model} "
-                       f"({ncpu} logical CPUs)"),
+            "sample": (f"full {HEADLINE} calls, torch-CPU scaled_dot_product_attention fp32, "
+                       f"median of {n_nc} non-causal ({n_c} causal) calls (~{args.cpu_seconds:.0f} s "
+                       f"of CPU work per mask) after 1 warm-up; host {model} ({ncpu} logical CPUs)"),
             "latency_s": round(t_nc, 4),
             "causal_latency_s": round(t_c, 4),
         }

@@ -36,38 +36,42 @@
 // (the reference's prescale, kernel_flash2.cu:772) when c <= 1, so GEMM1
 // returns base-2 logits; the running stabiliser m enters as the MFMA
 // accumulator's initial value, so GEMM1 returns logit - m and p = v_exp_f32
-// of the accumulator.  m is the exact row max of the first tile and is then
-// only moved when a later tile's row max exceeds it by more than 8 (so
-// p <= 2^8, exact in fp16; a stale m is exact math since softmax is shift
-// invariant, and m never exceeds the running max, so the row sum stays
-// >= 1).  The decision is made before the exponentials, which then depend on
-// nothing else and interleave with the iteration's MFMAs.  Row sums are taken
-// from the fp16-rounded p with v_dot2_f32_f16, the same p GEMM2 multiplies;
-// each lane sums its own keys and the two halves of a row meet once, in the
+// of the accumulator.  m is the exact row max of the first tile and later
+// only moves when a tile would push p out of range (a stale m is exact math
+// since softmax is shift invariant; m never exceeds the running max, so the
+// row sum stays >= 1).  p is packed to fp16 for GEMM2; row sums add the fp32
+// p with v_add_f32 (the reference also sums fp32 p, :339) -- on gfx950
+// v_dot2_f32_f16 would stall the matrix core, plain VALU ops do not.  Each
+// lane sums its own keys and the two halves of a row meet once, in the
 // epilogue.  When c > 1 (SCALED) Q keeps its scale and the logits are
 // multiplied by c instead, so |Q'| never exceeds |Q|.
 //
 // K/V staging.  Tiles are fetched straight into LDS with buffer_load ... lds
 // (no VGPRs, no LDS-store instructions; rows past N read as zeros through
 // the buffer resource's bound) D tiles ahead, into rings of D+1 slots per
-// tensor.  Each slot is its own LDS object and the loops are unrolled by the
-// ring length, so every slot address is static.  One explicit
-// "s_waitcnt vmcnt(n); s_barrier" per step makes a tile visible.
+// tensor.  Loops are unrolled by the ring length, so every slot address is
+// a constant offset.  One explicit "s_waitcnt vmcnt(n); s_barrier" per step
+// makes a tile visible.
 //
-// Two schedules:
-//   fa2_fwd_kernel (any W): iteration j runs the softmax of tile j alongside
-//     GEMM1 of tile j+1 (independent work the compiler interleaves) and then
-//     GEMM2 of tile j; one barrier per tile.
+// Schedules:
+//   fa2_fwd_kernel (any W; SPLIT = 1 or 2): iteration j runs GEMM1 of tile
+//     j+1, GEMM2 of tile j-1 and the softmax of tile j -- three independent
+//     pieces of work the compiler interleaves -- and checks the stabiliser
+//     after the exponentials (Rows::softmax_trailing); one barrier per tile.
+//     SPLIT = 2 doubles the waves: the second set walks the second half of
+//     the key range with its own rings, and the halves merge through LDS.
 //   fa2_fwd_pp_kernel (W = 8, "ping-pong"): waves w and w+4 of a 512-lane
-//     work-group share a SIMD (gfx950 dispatch), so the work-group splits
-//     into group A = waves 0-3 and group B = waves 4-7, and every step one
-//     group runs its MFMA phase (GEMM2 of tile j-1 + GEMM1 of tile j, 16
-//     MFMAs) while the other runs its softmax phase (exp / cvt / dot2) on the
-//     same SIMD; a barrier ends each step and the groups swap.  The matrix
-//     core and the VALU of each SIMD are then busy at the same time.
+//     work-group share a SIMD, so group A = waves 0-3 and group B = waves
+//     4-7 alternate an MFMA phase (GEMM2 of tile j-1 + GEMM1 of tile j) and
+//     a softmax phase, with a barrier per phase.
+//   fa2_fwd_x2_kernel (4 waves of 64 rows): each wave owns two 32-row blocks
+//     that share every K/V operand read.
+//   The last two decide the stabiliser before the exponentials
+//   (Rows::restabilise); they are kept as selectable, tested alternatives.
 //
 // Causal.  Keys after a lane's query and keys >= N are masked to -inf on the
-// diagonal and tail tiles only; work-groups are issued heaviest-first.
+// diagonal and tail tiles only; work-groups are fed to each XCD heaviest
+// first, with heavy and light blocks paired on a CU (wg_coords).
 //
 // LDS.  Rows of 128 B (64 halfs).  16-byte chunks are XOR-swizzled per row:
 // K with (row&7)^((row>>3)&1), V with 2*(row&3), which makes the GEMM1

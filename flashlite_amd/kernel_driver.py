@@ -9,6 +9,10 @@ before the first launch; each launch goes through the C ABI
 current stream.  Under ``rocprofv3 --kernel-trace --stats`` or ``--pmc`` the
 kernel's dispatches are the only ones besides the input uploads.  Prints the
 mean launch time measured with HIP events on that stream.
+
+``--copy-mib M`` instead runs an elementwise fp16 kernel that reads M MiB and
+writes M MiB (``torch.mul(src, 1, out=dst)``): the reference point that
+scales the HBM byte counters (FETCH_SIZE / WRITE_SIZE) of a profile.
 """
 
 from __future__ import annotations
@@ -24,9 +28,27 @@ def main(argv=None):
     ap.add_argument("--config", type=int, default=-1, help="tile configuration (-1 = dispatcher)")
     ap.add_argument("--iters", type=int, default=20)
     ap.add_argument("--naive", action="store_true")
+    ap.add_argument("--copy-mib", type=int, default=0, help="run the calibration copy instead")
     args = ap.parse_args(argv)
 
     import torch
+
+    if args.copy_mib:
+        n = args.copy_mib * (1 << 20) // 2
+        src = torch.ones(n, dtype=torch.float16, device="cuda:0")
+        dst = torch.empty_like(src)
+        torch.mul(src, 1, out=dst)
+        torch.cuda.synchronize()
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
+        for _ in range(args.iters):
+            torch.mul(src, 1, out=dst)
+        end.record()
+        torch.cuda.synchronize()
+        us = start.elapsed_time(end) * 1e3 / args.iters
+        print(f"copy {args.copy_mib} MiB read + {args.copy_mib} MiB write: {us:.2f} us/launch, "
+              f"{2 * args.copy_mib * (1 << 20) / us / 1e3:.1f} GB/s", flush=True)
+        return 0
 
     from flashlite_amd import capi
     from flashlite_amd.workloads import WORKLOADS, workload_inputs
