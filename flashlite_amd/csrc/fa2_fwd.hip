@@ -81,6 +81,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <map>
+#include <mutex>
 #include <utility>
 
 #include "fl_internal.h"
@@ -192,6 +194,41 @@ __device__ __forceinline__ void wg_coords(int nqb, int& bh, int& qb) {
     bh = (i & 7) * hx + r % hx;
     qb = r / hx;
   }
+  if (CAUSAL) qb = nqb - 1 - qb;
+}
+
+// Work-group -> (batch*head, query block, key half) for the cross-work-group
+// split: the two halves of a query block are adjacent in dispatch order on
+// one XCD.  Causal: heaviest first as in wg_coords, in units of halves.
+template <bool CAUSAL, int kSlotsPerCu>
+__device__ __forceinline__ void wg_coords_split(int nqb, int& bh, int& qb, int& half) {
+  constexpr int kCusPerXcd = 32;
+  const int total = gridDim.x;
+  const int i = blockIdx.x;
+  const int per = total >> 3;
+  const int items = 2 * nqb;  // work-groups per head
+  int lin;
+  if ((total & 7) != 0) {
+    lin = i;
+  } else if (!CAUSAL || per % items != 0) {
+    lin = (i & 7) * per + (i >> 3);
+  } else {
+    const int hx = per / items;
+    const int k = i >> 3;
+    constexpr int first = kCusPerXcd * kSlotsPerCu;
+    int r = k;
+    if (kSlotsPerCu == 2 && per >= first && k >= kCusPerXcd && k < first)
+      r = first - 1 - (k - kCusPerXcd);
+    // rank r: query-block rank r / (2 hx), head (r / 2) % hx, half r % 2
+    bh = (i & 7) * hx + (r >> 1) % hx;
+    qb = nqb - 1 - r / (2 * hx);
+    half = r & 1;
+    return;
+  }
+  bh = lin / items;
+  const int rem = lin - bh * items;
+  qb = rem >> 1;
+  half = rem & 1;
   if (CAUSAL) qb = nqb - 1 - qb;
 }
 
@@ -488,12 +525,15 @@ struct Rows {
     part[32 * 64 + lane] = m;
     part[33 * 64 + lane] = l;
   }
+  // Symmetric in the two ranges: a row with no key in one range (l == 0
+  // across the lane pair) takes the other's values.
   __device__ __forceinline__ void merge_partial(const float* part, int lane) {
     const float m1 = part[32 * 64 + lane], l1 = part[33 * 64 + lane];
-    const bool has1 = pair_sum(l1) > 0.0f;  // rows with no key in the other range
-    const float mm = has1 ? fmaxf(m, m1) : m;
+    const bool has0 = pair_sum(l) > 0.0f;
+    const bool has1 = pair_sum(l1) > 0.0f;
+    const float mm = has0 ? (has1 ? fmaxf(m, m1) : m) : m1;
     const float k = SCALED ? cr : 1.0f;
-    const float a0 = __builtin_amdgcn_exp2f(k * (m - mm));
+    const float a0 = has0 ? __builtin_amdgcn_exp2f(k * (m - mm)) : 0.0f;
     const float a1 = has1 ? __builtin_amdgcn_exp2f(k * (m1 - mm)) : 0.0f;
     l = a0 * l + a1 * l1;
 #pragma unroll
@@ -566,11 +606,17 @@ struct StreamRings {
 // second half of the key range with its own rings (waves w and w + W share
 // a SIMD); the halves are merged through LDS at the end.  That halves the
 // longest key walk, the critical path of causal attention's last q-blocks.
-template <int W, int D, int SPLIT, bool CAUSAL, bool SCALED>
-__global__ void __launch_bounds__(64 * W * SPLIT, SPLIT == 1 ? 2 : 1)
+//
+// XSPLIT (with SPLIT = 1) splits the key range across two work-groups
+// instead, so each CU keeps two independent 4-wave groups: both halves
+// write their partial state to `ws` (per query block: two slots of
+// W * 34 * 64 floats) and bump `cnt[query block]`; the second to arrive
+// merges, writes O and resets the counter for the next launch.
+template <int W, int D, int SPLIT, bool XSPLIT, bool CAUSAL, bool SCALED>
+__global__ void __launch_bounds__(64 * W * SPLIT, 2)  // 2 waves per SIMD: <= 256 VGPRs
 fa2_fwd_kernel(const _Float16* Q, const _Float16* __restrict__ K,
                const _Float16* __restrict__ V, _Float16* O, int seq, int nqb,
-               float cq, float cr) {
+               float cq, float cr, float* ws, unsigned* cnt) {
   constexpr int kSlots = D + 1;
   constexpr int kUnroll = (kSlots % 2 == 0) ? kSlots : 2 * kSlots;
   constexpr int kBr = 32 * W;
@@ -583,18 +629,24 @@ fa2_fwd_kernel(const _Float16* Q, const _Float16* __restrict__ K,
   __shared__ __attribute__((aligned(16))) uint8_t kring[kRingBytes];
   __shared__ __attribute__((aligned(16))) uint8_t vring[kRingBytes];
 
+  static_assert(!XSPLIT || SPLIT == 1, "one split kind at a time");
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int stream = wave / W;       // key-range half
-  const int rw = wave - stream * W;  // 32-row block within the work-group
-  int bh, qb;
-  wg_coords<CAUSAL, (W == 4 && SPLIT == 1) ? 2 : 1>(nqb, bh, qb);
+  int bh, qb, stream;  // stream: key-range half
+  if constexpr (XSPLIT) {
+    wg_coords_split<CAUSAL, W == 4 ? 2 : 1>(nqb, bh, qb, stream);
+  } else {
+    wg_coords<CAUSAL, (W == 4 && SPLIT == 1) ? 2 : 1>(nqb, bh, qb);
+    stream = wave / W;
+  }
+  const int rw = XSPLIT ? wave : wave - stream * W;  // 32-row block within the work-group
   const size_t head_off = (size_t)bh * (size_t)seq * kD;
   const i32x4_t rk = buffer_rsrc(K + head_off, seq * kRowBytes);
   const i32x4_t rv = buffer_rsrc(V + head_off, seq * kRowBytes);
   const int q0 = qb * kBr;
-  const StreamRings<kSlots> rings = {kring + stream * (kSlots * kTileBytes),
-                                     vring + stream * (kSlots * kTileBytes)};
+  const int ring = XSPLIT ? 0 : stream;
+  const StreamRings<kSlots> rings = {kring + ring * (kSlots * kTileBytes),
+                                     vring + ring * (kSlots * kTileBytes)};
 
   Rows<CAUSAL, SCALED> rows;
   rows.init(Q + head_off, lane, q0 + 32 * rw, seq, cq, cr);
@@ -603,11 +655,12 @@ fa2_fwd_kernel(const _Float16* Q, const _Float16* __restrict__ K,
   if (CAUSAL) ntiles = min(ntiles, (min(q0 + kBr, seq) - 1) / kBc + 1);
   // Key tiles [tbeg, tend) of this stream; both streams run t0 + 1
   // iterations (the same barriers), the shorter one on masked tiles.
-  const int t0 = SPLIT == 1 ? ntiles : (ntiles + 1) / 2;
+  constexpr bool kSplit = SPLIT == 2 || XSPLIT;
+  const int t0 = kSplit ? (ntiles + 1) / 2 : ntiles;
   const int tbeg = stream == 0 ? 0 : t0;
   const int tend = stream == 0 ? t0 : ntiles;
   const int last = max(tend - 1, tbeg);  // fetch clamp
-  if (SPLIT == 2 && stream == 0) rows.kv_lim = min(seq, t0 * kBc);
+  if (kSplit && stream == 0) rows.kv_lim = min(seq, t0 * kBc);
 
   // Iteration j (position I of the unrolled loop), for j = 0 .. t0, on key
   // tile t = tbeg + j: fetch K(t+D+1) and V(t+D-1) into the slots of K(t)
@@ -663,6 +716,8 @@ fa2_fwd_kernel(const _Float16* Q, const _Float16* __restrict__ K,
     rows.read_k(rings.kslot(Ic<0>{}), ka);
     rows.gemm1(ka, S0);
   }
+  // Iteration 0 refills K(tbeg)'s slot: every wave's reads of it must be done.
+  sync_ring<(D - 1) * kDmaPerIter>();
   rows.mask(tbeg, S0);
   rows.first_tile(S0);
 
@@ -690,6 +745,24 @@ fa2_fwd_kernel(const _Float16* Q, const _Float16* __restrict__ K,
     __syncthreads();
     if (stream == 1) return;
     rows.merge_partial(part, lane);
+  }
+  if constexpr (XSPLIT) {
+    // Publish this half, then count arrivals; the later half merges.
+    const size_t blk = (size_t)bh * nqb + qb;
+    float* mine = ws + (blk * 2 + stream) * (size_t)(W * 34 * 64) + rw * (34 * 64);
+    float* other = ws + (blk * 2 + (stream ^ 1)) * (size_t)(W * 34 * 64) + rw * (34 * 64);
+    rows.save_partial(mine, lane);
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+    __syncthreads();
+    __shared__ unsigned arrived;
+    if (threadIdx.x == 0)
+      arrived = __hip_atomic_fetch_add(cnt + blk, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __syncthreads();
+    if (arrived == 0) return;
+    if (threadIdx.x == 0)
+      __hip_atomic_store(cnt + blk, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    rows.merge_partial(other, lane);
   }
   rows.store(O + head_off);
 }
@@ -911,6 +984,8 @@ fa2_fwd_x2_kernel(const _Float16* Q, const _Float16* __restrict__ K,
     fetch_tile<kSegs, true>(rv, rings.vslot(Ic<G + D>{}), G + D, last, wave, lane);
   });
   ra.read_k(rings.kslot(Ic<0>{}), kops);
+  // Iteration 0 refills K(0)'s slot: every wave's reads of it must be done.
+  sync_ring<(D - 1) * kDmaPerIter>();
   ra.gemm1(kops, sa);
 
   for (int t0 = 0; t0 < ntiles; t0 += kUnroll) {
@@ -945,25 +1020,36 @@ hipError_t dispatch(const FwdArgs& a, hipStream_t stream, int br) {
   const int nqb = (a.seq + br - 1) / br;
   const dim3 grid((unsigned)(nqb * a.batch_heads));
   const Scales sc(a);
+  hipError_t e;
   if (a.causal) {
-    if (sc.scaled) Launcher<true, true>::run(a, grid, nqb, sc.cq, sc.cr, stream);
-    else Launcher<true, false>::run(a, grid, nqb, sc.cq, sc.cr, stream);
+    if (sc.scaled) e = Launcher<true, true>::run(a, grid, nqb, sc.cq, sc.cr, stream);
+    else e = Launcher<true, false>::run(a, grid, nqb, sc.cq, sc.cr, stream);
   } else {
-    if (sc.scaled) Launcher<false, true>::run(a, grid, nqb, sc.cq, sc.cr, stream);
-    else Launcher<false, false>::run(a, grid, nqb, sc.cq, sc.cr, stream);
+    if (sc.scaled) e = Launcher<false, true>::run(a, grid, nqb, sc.cq, sc.cr, stream);
+    else e = Launcher<false, false>::run(a, grid, nqb, sc.cq, sc.cr, stream);
   }
-  return hipGetLastError();
+  return e != hipSuccess ? e : hipGetLastError();
 }
 
-template <int W, int D, int SPLIT>
+template <int W, int D, int SPLIT, bool XSPLIT = false>
 struct PipelinedLaunch {
   template <bool C, bool S>
   struct L {
-    static void run(const FwdArgs& a, dim3 grid, int nqb, float cq, float cr, hipStream_t st) {
-      hipLaunchKernelGGL((fa2_fwd_kernel<W, D, SPLIT, C, S>), grid, dim3(64 * W * SPLIT), 0, st,
-                         static_cast<const _Float16*>(a.q), static_cast<const _Float16*>(a.k),
-                         static_cast<const _Float16*>(a.v), static_cast<_Float16*>(a.o), a.seq,
-                         nqb, cq, cr);
+    static hipError_t run(const FwdArgs& a, dim3 grid, int nqb, float cq, float cr, hipStream_t st) {
+      float* ws = nullptr;
+      unsigned* cnt = nullptr;
+      if (XSPLIT) {
+        const size_t blocks = grid.x;  // query blocks
+        const hipError_t e =
+            split_workspace(st, blocks * 2 * W * 34 * 64 * sizeof(float), blocks, &ws, &cnt);
+        if (e != hipSuccess) return e;
+        grid.x *= 2;
+      }
+      hipLaunchKernelGGL((fa2_fwd_kernel<W, D, SPLIT, XSPLIT, C, S>), grid, dim3(64 * W * SPLIT),
+                         0, st, static_cast<const _Float16*>(a.q),
+                         static_cast<const _Float16*>(a.k), static_cast<const _Float16*>(a.v),
+                         static_cast<_Float16*>(a.o), a.seq, nqb, cq, cr, ws, cnt);
+      return hipSuccess;
     }
   };
 };
@@ -972,11 +1058,12 @@ template <int D>
 struct TwoBlockLaunch {
   template <bool C, bool S>
   struct L {
-    static void run(const FwdArgs& a, dim3 grid, int nqb, float cq, float cr, hipStream_t st) {
+    static hipError_t run(const FwdArgs& a, dim3 grid, int nqb, float cq, float cr, hipStream_t st) {
       hipLaunchKernelGGL((fa2_fwd_x2_kernel<D, C, S>), grid, dim3(256), 0, st,
                          static_cast<const _Float16*>(a.q), static_cast<const _Float16*>(a.k),
                          static_cast<const _Float16*>(a.v), static_cast<_Float16*>(a.o), a.seq,
                          nqb, cq, cr);
+      return hipSuccess;
     }
   };
 };
@@ -985,16 +1072,57 @@ template <int D>
 struct PingPongLaunch {
   template <bool C, bool S>
   struct L {
-    static void run(const FwdArgs& a, dim3 grid, int nqb, float cq, float cr, hipStream_t st) {
+    static hipError_t run(const FwdArgs& a, dim3 grid, int nqb, float cq, float cr, hipStream_t st) {
       hipLaunchKernelGGL((fa2_fwd_pp_kernel<D, C, S>), grid, dim3(512), 0, st,
                          static_cast<const _Float16*>(a.q), static_cast<const _Float16*>(a.k),
                          static_cast<const _Float16*>(a.v), static_cast<_Float16*>(a.o), a.seq,
                          nqb, cq, cr);
+      return hipSuccess;
     }
   };
 };
 
 }  // namespace
+
+// Workspace of the cross-work-group split, one per (device, stream): the
+// partial states of every query block plus one arrival counter each.
+// Counters start at zero and each launch leaves them at zero.  Grown on
+// demand (a growth waits for the device before freeing the old buffer).
+hipError_t split_workspace(hipStream_t stream, size_t part_bytes, size_t counters, float** part,
+                           unsigned** cnt) {
+  struct Buf {
+    void* base = nullptr;
+    size_t part = 0, counters = 0;
+  };
+  static std::mutex mu;
+  static std::map<std::pair<int, hipStream_t>, Buf> bufs;
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  std::lock_guard<std::mutex> lock(mu);
+  Buf& b = bufs[{dev, stream}];
+  if (b.part < part_bytes || b.counters < counters) {
+    if (b.base) {
+      e = hipDeviceSynchronize();
+      if (e != hipSuccess) return e;
+      e = hipFree(b.base);
+      if (e != hipSuccess) return e;
+      b = Buf{};
+    }
+    const size_t pb = (part_bytes + 255) & ~(size_t)255;
+    e = hipMalloc(&b.base, pb + counters * sizeof(unsigned));
+    if (e != hipSuccess) return e;
+    e = hipMemset(static_cast<char*>(b.base) + pb, 0, counters * sizeof(unsigned));
+    if (e != hipSuccess) return e;
+    e = hipDeviceSynchronize();
+    if (e != hipSuccess) return e;
+    b.part = pb;
+    b.counters = counters;
+  }
+  *part = static_cast<float*>(b.base);
+  *cnt = reinterpret_cast<unsigned*>(static_cast<char*>(b.base) + b.part);
+  return hipSuccess;
+}
 
 const Fa2Config kFa2Configs[kNumFa2Configs] = {
     {1, "br32_bc64_w1"},
@@ -1004,6 +1132,7 @@ const Fa2Config kFa2Configs[kNumFa2Configs] = {
     {8, "br256_bc64_w8_pingpong"},
     {8, "br256_bc64_w4x2"},
     {8, "br128_bc64_w4_split2"},
+    {4, "br128_bc64_w4_xsplit2"},
 };
 
 // Fetch distance: three tiles ahead where LDS allows (64 KiB of rings per
@@ -1017,6 +1146,7 @@ hipError_t launch_fa2(const FwdArgs& a, int cfg, hipStream_t stream) {
     case 4: return dispatch<PingPongLaunch<3>::L>(a, stream, 256);
     case 5: return dispatch<TwoBlockLaunch<3>::L>(a, stream, 256);
     case 6: return dispatch<PipelinedLaunch<4, 3, 2>::L>(a, stream, 128);
+    case 7: return dispatch<PipelinedLaunch<4, 3, 1, true>::L>(a, stream, 128);
     default: return hipErrorInvalidValue;
   }
 }

@@ -28,11 +28,12 @@ def test_library_loads_and_exports_header_symbols():
 
 
 def test_config_table():
-    assert capi.num_configs() == 7
-    names = [capi.config_name(i) for i in range(7)]
+    assert capi.num_configs() == 8
+    names = [capi.config_name(i) for i in range(8)]
     assert names == ["br32_bc64_w1", "br64_bc64_w2", "br128_bc64_w4", "br256_bc64_w8",
-                     "br256_bc64_w8_pingpong", "br256_bc64_w4x2", "br128_bc64_w4_split2"]
-    assert capi.config_name(7) is None and capi.config_name(-1) is None
+                     "br256_bc64_w8_pingpong", "br256_bc64_w4x2", "br128_bc64_w4_split2",
+                     "br128_bc64_w4_xsplit2"]
+    assert capi.config_name(8) is None and capi.config_name(-1) is None
 
 
 def _p(**kw):
@@ -86,7 +87,7 @@ def test_non_finite_scale():
 
 
 def test_bad_config():
-    assert capi.fwd(_p(), config=7) == capi.FL_ERR_BAD_CONFIG
+    assert capi.fwd(_p(), config=8) == capi.FL_ERR_BAD_CONFIG
     assert capi.fwd(_p(), config=-2) == capi.FL_ERR_BAD_CONFIG
 
 

@@ -18,15 +18,15 @@ from oracle import error_stats
 pytestmark = pytest.mark.gpu
 
 GOLDEN = os.path.join(os.path.dirname(__file__), "golden")
-NCFG = 7  # tile configurations exported by the library
-SPLIT_CFG = 6  # the key-range-split configuration
+NCFG = 8  # tile configurations exported by the library
+SPLIT_CFGS = [6, 7]  # the key-range-split configurations (in-group, across groups)
 
 
 def test_num_configs():
     assert capi.num_configs() == NCFG
     assert [capi.config_name(i) for i in range(NCFG)] == [
         "br32_bc64_w1", "br64_bc64_w2", "br128_bc64_w4", "br256_bc64_w8", "br256_bc64_w8_pingpong",
-        "br256_bc64_w4x2", "br128_bc64_w4_split2"]
+        "br256_bc64_w4x2", "br128_bc64_w4_split2", "br128_bc64_w4_xsplit2"]
 
 
 @pytest.mark.parametrize("config", list(range(NCFG)))
@@ -50,7 +50,7 @@ def test_benchmark_configs(cuda, name, causal):
     print(f"{name} causal={causal}: max-abs {mx:.2e} mean-abs {mean:.2e}")
 
 
-@pytest.mark.parametrize("config", [2, 3, SPLIT_CFG])
+@pytest.mark.parametrize("config", [2, 3] + SPLIT_CFGS)
 @pytest.mark.parametrize("causal", [False, True])
 def test_headline_each_config(cuda, config, causal):
     w = WORKLOADS["C2_headline_B2H8N4096"]
@@ -59,13 +59,26 @@ def test_headline_each_config(cuda, config, causal):
     assert_close_oracle(out, q, k, v, w.sm_scale, causal, rows=sample_rows(w.seq, seed=w.seed))
 
 
+@pytest.mark.parametrize("config", SPLIT_CFGS)
 @pytest.mark.parametrize("scale", [-0.2, 1.0, 3.0])
 @pytest.mark.parametrize("causal", [False, True])
-def test_split_scales(cuda, scale, causal):
+def test_split_scales(cuda, config, scale, causal):
     # peaked softmax: the stabiliser moves in both key ranges before the merge
     q, k, v = make_qkv(1, 4, 700, 64, seed=43)
-    out = run_capi(q, k, v, scale, causal, cuda, config=SPLIT_CFG)
+    out = run_capi(q, k, v, scale, causal, cuda, config=config)
     assert_close_oracle(out, q, k, v, scale, causal, max_abs=2e-3 if scale < 1 else 4e-3)
+
+
+def test_xsplit_repeated_and_resized(cuda):
+    # The cross-group split keeps per-query-block arrival counters in a
+    # workspace that every launch must leave at zero: repeat launches, grow
+    # the problem (new workspace), shrink it again, and compare each result.
+    cfg = SPLIT_CFGS[1]
+    for n, causal in ((300, True), (300, True), (1500, False), (300, True), (1500, True)):
+        q, k, v = make_qkv(2, 3, n, 64, seed=2000 + n)
+        for _ in range(2):
+            out = run_capi(q, k, v, 0.125, causal, cuda, config=cfg)
+            assert_close_oracle(out, q, k, v, 0.125, causal)
 
 
 def test_c3_long_causal(cuda):
