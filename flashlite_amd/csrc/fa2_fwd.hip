@@ -64,10 +64,8 @@
 //     work-group share a SIMD, so group A = waves 0-3 and group B = waves
 //     4-7 alternate an MFMA phase (GEMM2 of tile j-1 + GEMM1 of tile j) and
 //     a softmax phase, with a barrier per phase.
-//   fa2_fwd_x2_kernel (4 waves of 64 rows): each wave owns two 32-row blocks
-//     that share every K/V operand read.
-//   The last two decide the stabiliser before the exponentials
-//   (Rows::restabilise); they are kept as selectable, tested alternatives.
+//   The ping-pong kernel decides the stabiliser before the exponentials
+//   (Rows::restabilise); it is kept as a selectable, tested alternative.
 //
 // Causal.  Keys after a lane's query and keys >= N are masked to -inf on the
 // diagonal and tail tiles only; work-groups are fed to each XCD heaviest
@@ -81,8 +79,6 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
-#include <map>
-#include <mutex>
 #include <utility>
 
 #include "fl_internal.h"
@@ -194,41 +190,6 @@ __device__ __forceinline__ void wg_coords(int nqb, int& bh, int& qb) {
     bh = (i & 7) * hx + r % hx;
     qb = r / hx;
   }
-  if (CAUSAL) qb = nqb - 1 - qb;
-}
-
-// Work-group -> (batch*head, query block, key half) for the cross-work-group
-// split: the two halves of a query block are adjacent in dispatch order on
-// one XCD.  Causal: heaviest first as in wg_coords, in units of halves.
-template <bool CAUSAL, int kSlotsPerCu>
-__device__ __forceinline__ void wg_coords_split(int nqb, int& bh, int& qb, int& half) {
-  constexpr int kCusPerXcd = 32;
-  const int total = gridDim.x;
-  const int i = blockIdx.x;
-  const int per = total >> 3;
-  const int items = 2 * nqb;  // work-groups per head
-  int lin;
-  if ((total & 7) != 0) {
-    lin = i;
-  } else if (!CAUSAL || per % items != 0) {
-    lin = (i & 7) * per + (i >> 3);
-  } else {
-    const int hx = per / items;
-    const int k = i >> 3;
-    constexpr int first = kCusPerXcd * kSlotsPerCu;
-    int r = k;
-    if (kSlotsPerCu == 2 && per >= first && k >= kCusPerXcd && k < first)
-      r = first - 1 - (k - kCusPerXcd);
-    // rank r: query-block rank r / (2 hx), head (r / 2) % hx, half r % 2
-    bh = (i & 7) * hx + (r >> 1) % hx;
-    qb = nqb - 1 - r / (2 * hx);
-    half = r & 1;
-    return;
-  }
-  bh = lin / items;
-  const int rem = lin - bh * items;
-  qb = rem >> 1;
-  half = rem & 1;
   if (CAUSAL) qb = nqb - 1 - qb;
 }
 
@@ -606,17 +567,11 @@ struct StreamRings {
 // second half of the key range with its own rings (waves w and w + W share
 // a SIMD); the halves are merged through LDS at the end.  That halves the
 // longest key walk, the critical path of causal attention's last q-blocks.
-//
-// XSPLIT (with SPLIT = 1) splits the key range across two work-groups
-// instead, so each CU keeps two independent 4-wave groups: both halves
-// write their partial state to `ws` (per query block: two slots of
-// W * 34 * 64 floats) and bump `cnt[query block]`; the second to arrive
-// merges, writes O and resets the counter for the next launch.
-template <int W, int D, int SPLIT, bool XSPLIT, bool CAUSAL, bool SCALED>
+template <int W, int D, int SPLIT, bool CAUSAL, bool SCALED>
 __global__ void __launch_bounds__(64 * W * SPLIT, 2)  // 2 waves per SIMD: <= 256 VGPRs
 fa2_fwd_kernel(const _Float16* Q, const _Float16* __restrict__ K,
                const _Float16* __restrict__ V, _Float16* O, int seq, int nqb,
-               float cq, float cr, float* ws, unsigned* cnt) {
+               float cq, float cr) {
   constexpr int kSlots = D + 1;
   constexpr int kUnroll = (kSlots % 2 == 0) ? kSlots : 2 * kSlots;
   constexpr int kBr = 32 * W;
@@ -629,24 +584,18 @@ fa2_fwd_kernel(const _Float16* Q, const _Float16* __restrict__ K,
   __shared__ __attribute__((aligned(16))) uint8_t kring[kRingBytes];
   __shared__ __attribute__((aligned(16))) uint8_t vring[kRingBytes];
 
-  static_assert(!XSPLIT || SPLIT == 1, "one split kind at a time");
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  int bh, qb, stream;  // stream: key-range half
-  if constexpr (XSPLIT) {
-    wg_coords_split<CAUSAL, W == 4 ? 2 : 1>(nqb, bh, qb, stream);
-  } else {
-    wg_coords<CAUSAL, (W == 4 && SPLIT == 1) ? 2 : 1>(nqb, bh, qb);
-    stream = wave / W;
-  }
-  const int rw = XSPLIT ? wave : wave - stream * W;  // 32-row block within the work-group
+  const int stream = wave / W;       // key-range half
+  const int rw = wave - stream * W;  // 32-row block within the work-group
+  int bh, qb;
+  wg_coords<CAUSAL, (W == 4 && SPLIT == 1) ? 2 : 1>(nqb, bh, qb);
   const size_t head_off = (size_t)bh * (size_t)seq * kD;
   const i32x4_t rk = buffer_rsrc(K + head_off, seq * kRowBytes);
   const i32x4_t rv = buffer_rsrc(V + head_off, seq * kRowBytes);
   const int q0 = qb * kBr;
-  const int ring = XSPLIT ? 0 : stream;
-  const StreamRings<kSlots> rings = {kring + ring * (kSlots * kTileBytes),
-                                     vring + ring * (kSlots * kTileBytes)};
+  const StreamRings<kSlots> rings = {kring + stream * (kSlots * kTileBytes),
+                                     vring + stream * (kSlots * kTileBytes)};
 
   Rows<CAUSAL, SCALED> rows;
   rows.init(Q + head_off, lane, q0 + 32 * rw, seq, cq, cr);
@@ -655,7 +604,7 @@ fa2_fwd_kernel(const _Float16* Q, const _Float16* __restrict__ K,
   if (CAUSAL) ntiles = min(ntiles, (min(q0 + kBr, seq) - 1) / kBc + 1);
   // Key tiles [tbeg, tend) of this stream; both streams run t0 + 1
   // iterations (the same barriers), the shorter one on masked tiles.
-  constexpr bool kSplit = SPLIT == 2 || XSPLIT;
+  constexpr bool kSplit = SPLIT == 2;
   const int t0 = kSplit ? (ntiles + 1) / 2 : ntiles;
   const int tbeg = stream == 0 ? 0 : t0;
   const int tend = stream == 0 ? t0 : ntiles;
@@ -745,24 +694,6 @@ fa2_fwd_kernel(const _Float16* Q, const _Float16* __restrict__ K,
     __syncthreads();
     if (stream == 1) return;
     rows.merge_partial(part, lane);
-  }
-  if constexpr (XSPLIT) {
-    // Publish this half, then count arrivals; the later half merges.
-    const size_t blk = (size_t)bh * nqb + qb;
-    float* mine = ws + (blk * 2 + stream) * (size_t)(W * 34 * 64) + rw * (34 * 64);
-    float* other = ws + (blk * 2 + (stream ^ 1)) * (size_t)(W * 34 * 64) + rw * (34 * 64);
-    rows.save_partial(mine, lane);
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
-    __syncthreads();
-    __shared__ unsigned arrived;
-    if (threadIdx.x == 0)
-      arrived = __hip_atomic_fetch_add(cnt + blk, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __syncthreads();
-    if (arrived == 0) return;
-    if (threadIdx.x == 0)
-      __hip_atomic_store(cnt + blk, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-    rows.merge_partial(other, lane);
   }
   rows.store(O + head_off);
 }
@@ -904,104 +835,6 @@ fa2_fwd_pp_kernel(const _Float16* Q, const _Float16* __restrict__ K,
   rows.store(O + head_off);
 }
 
-// ---------------------------------------------------------------------------
-// Two blocks per wave, 4 waves: each wave owns 64 query rows as blocks A and
-// B of 32, so every K and V operand read from LDS feeds both blocks' MFMAs
-// (half the LDS traffic per flop of the 32-row schedules), and block B runs
-// half a tile behind block A so one block's softmax overlaps the other
-// block's MFMAs inside the wave:
-//     iteration t, step 1:  softmax_A(t)   with  GEMM2_B(t-1), GEMM1_B(t)
-//     iteration t, step 2:  softmax_B(t)   with  GEMM2_A(t),   GEMM1_A(t+1)
-// K(t) operands are read from LDS in step 2 of iteration t-1 and kept in
-// VGPRs for GEMM1_B(t); V(t) operands likewise for GEMM2_B(t).  So
-// iteration t reads exactly K(t+1) and V(t) from LDS, as fa2_fwd_kernel
-// does, with the same fetch ring.
-template <int D, bool CAUSAL, bool SCALED>
-__global__ void __launch_bounds__(256, 1)
-fa2_fwd_x2_kernel(const _Float16* Q, const _Float16* __restrict__ K,
-                  const _Float16* __restrict__ V, _Float16* O, int seq, int nqb,
-                  float cq, float cr) {
-  constexpr int W = 4;
-  constexpr int kSlots = D + 1;
-  constexpr int kUnroll = kSlots;
-  constexpr int kBr = 64 * W;
-  constexpr int kSegs = 8 / W;            // 1 KiB DMA segments per wave per tile
-  constexpr int kDmaPerIter = 2 * kSegs;  // K + V loads a wave issues per iteration
-  FL_DECLARE_RINGS(kSlots);
-
-  const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  int bh, qb;
-  wg_coords<CAUSAL, 1>(nqb, bh, qb);
-  const size_t head_off = (size_t)bh * (size_t)seq * kD;
-  const i32x4_t rk = buffer_rsrc(K + head_off, seq * kRowBytes);
-  const i32x4_t rv = buffer_rsrc(V + head_off, seq * kRowBytes);
-  const int q0 = qb * kBr;
-
-  Rows<CAUSAL, SCALED> ra, rb;
-  ra.init(Q + head_off, lane, q0 + 64 * wave, seq, cq, cr);
-  rb.init(Q + head_off, lane, q0 + 64 * wave + 32, seq, cq, cr);
-
-  int ntiles = (seq + kBc - 1) / kBc;
-  if (CAUSAL) ntiles = min(ntiles, (min(q0 + kBr, seq) - 1) / kBc + 1);
-  const int last = ntiles - 1;
-
-  half8_t kops[2][4], vops[2][4];  // K(t) / V(t) operands, shared by both blocks
-  float16_t sa[2], sb[2];
-
-  auto iteration = [&](auto i, int t) __attribute__((always_inline)) {
-    constexpr int I = decltype(i)::value;
-    fetch_tile<kSegs, false>(rk, rings.kslot(Ic<I + D + 1>{}), t + D + 1, last, wave, lane);
-    fetch_tile<kSegs, true>(rv, rings.vslot(Ic<I + D>{}), t + D, last, wave, lane);
-    // step 1: softmax_A(t) with GEMM2_B(t-1) and GEMM1_B(t)
-    if (t > 0) rb.gemm2(vops);
-    rb.gemm1(kops, sb);
-    ra.mask(t, sa);
-    if (t == 0) ra.first_tile(sa);
-    ra.softmax(sa, [](float) __attribute__((always_inline)) {});
-    // step 2: softmax_B(t) with GEMM2_A(t) and GEMM1_A(t+1); reads V(t), K(t+1)
-    ra.read_v(rings.vslot(Ic<I>{}), vops);
-    ra.read_k(rings.kslot(Ic<I + 1>{}), kops);
-    ra.gemm2(vops);
-    // GEMM1 of a tile past the end reads a stale slot; its result is unused.
-    ra.gemm1(kops, sa);
-    rb.mask(t, sb);
-    if (t == 0) rb.first_tile(sb);
-    rb.softmax(sb, [](float) __attribute__((always_inline)) {});
-    sync_ring<(D - 1) * kDmaPerIter>();
-  };
-
-  // ---- prologue: K(0), V(0), K(1) landed; fetch groups of iterations
-  // 1-D .. -1 in flight; K(0) operands and S_A(0).
-  zero_v_slots<kSlots, 64 * W>(rings);
-  fetch_tile<kSegs, false>(rk, rings.kslot(Ic<0>{}), 0, last, wave, lane);
-  fetch_tile<kSegs, true>(rv, rings.vslot(Ic<0>{}), 0, last, wave, lane);
-  fetch_tile<kSegs, false>(rk, rings.kslot(Ic<1>{}), 1, last, wave, lane);
-  sync_ring<0>();
-  static_for(std::make_integer_sequence<int, D - 1>{}, [&](auto i) __attribute__((always_inline)) {
-    constexpr int G = decltype(i)::value + 1 - D;  // iteration 1-D+i
-    fetch_tile<kSegs, false>(rk, rings.kslot(Ic<G + D + 1>{}), G + D + 1, last, wave, lane);
-    fetch_tile<kSegs, true>(rv, rings.vslot(Ic<G + D>{}), G + D, last, wave, lane);
-  });
-  ra.read_k(rings.kslot(Ic<0>{}), kops);
-  // Iteration 0 refills K(0)'s slot: every wave's reads of it must be done.
-  sync_ring<(D - 1) * kDmaPerIter>();
-  ra.gemm1(kops, sa);
-
-  for (int t0 = 0; t0 < ntiles; t0 += kUnroll) {
-    static_for(std::make_integer_sequence<int, kUnroll>{}, [&](auto i) __attribute__((always_inline)) {
-      const int t = t0 + decltype(i)::value;
-      if (t < ntiles) iteration(i, t);
-    });
-  }
-  // GEMM2_B of the last tile (its V operands and P_B are in registers).
-  rb.gemm2(vops);
-
-  __builtin_amdgcn_s_waitcnt(0);
-  ra.store(O + head_off);
-  rb.store(O + head_off);
-}
-
 // Q is prescaled by cq = +-min(c, 1) in the kernel; the remaining factor
 // cr = c / |cq| (1 unless c > 1) is applied to the scores.
 struct Scales {
@@ -1031,35 +864,12 @@ hipError_t dispatch(const FwdArgs& a, hipStream_t stream, int br) {
   return e != hipSuccess ? e : hipGetLastError();
 }
 
-template <int W, int D, int SPLIT, bool XSPLIT = false>
+template <int W, int D, int SPLIT>
 struct PipelinedLaunch {
   template <bool C, bool S>
   struct L {
     static hipError_t run(const FwdArgs& a, dim3 grid, int nqb, float cq, float cr, hipStream_t st) {
-      float* ws = nullptr;
-      unsigned* cnt = nullptr;
-      if (XSPLIT) {
-        const size_t blocks = grid.x;  // query blocks
-        const hipError_t e =
-            split_workspace(st, blocks * 2 * W * 34 * 64 * sizeof(float), blocks, &ws, &cnt);
-        if (e != hipSuccess) return e;
-        grid.x *= 2;
-      }
-      hipLaunchKernelGGL((fa2_fwd_kernel<W, D, SPLIT, XSPLIT, C, S>), grid, dim3(64 * W * SPLIT),
-                         0, st, static_cast<const _Float16*>(a.q),
-                         static_cast<const _Float16*>(a.k), static_cast<const _Float16*>(a.v),
-                         static_cast<_Float16*>(a.o), a.seq, nqb, cq, cr, ws, cnt);
-      return hipSuccess;
-    }
-  };
-};
-
-template <int D>
-struct TwoBlockLaunch {
-  template <bool C, bool S>
-  struct L {
-    static hipError_t run(const FwdArgs& a, dim3 grid, int nqb, float cq, float cr, hipStream_t st) {
-      hipLaunchKernelGGL((fa2_fwd_x2_kernel<D, C, S>), grid, dim3(256), 0, st,
+      hipLaunchKernelGGL((fa2_fwd_kernel<W, D, SPLIT, C, S>), grid, dim3(64 * W * SPLIT), 0, st,
                          static_cast<const _Float16*>(a.q), static_cast<const _Float16*>(a.k),
                          static_cast<const _Float16*>(a.v), static_cast<_Float16*>(a.o), a.seq,
                          nqb, cq, cr);
@@ -1084,55 +894,13 @@ struct PingPongLaunch {
 
 }  // namespace
 
-// Workspace of the cross-work-group split, one per (device, stream): the
-// partial states of every query block plus one arrival counter each.
-// Counters start at zero and each launch leaves them at zero.  Grown on
-// demand (a growth waits for the device before freeing the old buffer).
-hipError_t split_workspace(hipStream_t stream, size_t part_bytes, size_t counters, float** part,
-                           unsigned** cnt) {
-  struct Buf {
-    void* base = nullptr;
-    size_t part = 0, counters = 0;
-  };
-  static std::mutex mu;
-  static std::map<std::pair<int, hipStream_t>, Buf> bufs;
-  int dev = 0;
-  hipError_t e = hipGetDevice(&dev);
-  if (e != hipSuccess) return e;
-  std::lock_guard<std::mutex> lock(mu);
-  Buf& b = bufs[{dev, stream}];
-  if (b.part < part_bytes || b.counters < counters) {
-    if (b.base) {
-      e = hipDeviceSynchronize();
-      if (e != hipSuccess) return e;
-      e = hipFree(b.base);
-      if (e != hipSuccess) return e;
-      b = Buf{};
-    }
-    const size_t pb = (part_bytes + 255) & ~(size_t)255;
-    e = hipMalloc(&b.base, pb + counters * sizeof(unsigned));
-    if (e != hipSuccess) return e;
-    e = hipMemset(static_cast<char*>(b.base) + pb, 0, counters * sizeof(unsigned));
-    if (e != hipSuccess) return e;
-    e = hipDeviceSynchronize();
-    if (e != hipSuccess) return e;
-    b.part = pb;
-    b.counters = counters;
-  }
-  *part = static_cast<float*>(b.base);
-  *cnt = reinterpret_cast<unsigned*>(static_cast<char*>(b.base) + b.part);
-  return hipSuccess;
-}
-
 const Fa2Config kFa2Configs[kNumFa2Configs] = {
     {1, "br32_bc64_w1"},
     {2, "br64_bc64_w2"},
     {4, "br128_bc64_w4"},
     {8, "br256_bc64_w8"},
     {8, "br256_bc64_w8_pingpong"},
-    {8, "br256_bc64_w4x2"},
     {8, "br128_bc64_w4_split2"},
-    {4, "br128_bc64_w4_xsplit2"},
 };
 
 // Fetch distance: three tiles ahead where LDS allows (64 KiB of rings per
@@ -1144,9 +912,7 @@ hipError_t launch_fa2(const FwdArgs& a, int cfg, hipStream_t stream) {
     case 2: return dispatch<PipelinedLaunch<4, 3, 1>::L>(a, stream, 128);
     case 3: return dispatch<PipelinedLaunch<8, 3, 1>::L>(a, stream, 256);
     case 4: return dispatch<PingPongLaunch<3>::L>(a, stream, 256);
-    case 5: return dispatch<TwoBlockLaunch<3>::L>(a, stream, 256);
-    case 6: return dispatch<PipelinedLaunch<4, 3, 2>::L>(a, stream, 128);
-    case 7: return dispatch<PipelinedLaunch<4, 3, 1, true>::L>(a, stream, 128);
+    case 5: return dispatch<PipelinedLaunch<4, 3, 2>::L>(a, stream, 128);
     default: return hipErrorInvalidValue;
   }
 }

@@ -29,12 +29,8 @@ struct Fa2Config {
   const char* name;
 };
 
-constexpr int kNumFa2Configs = 8;
+constexpr int kNumFa2Configs = 6;
 extern const Fa2Config kFa2Configs[kNumFa2Configs];
-
-// Workspace of the cross-work-group key split (fa2_fwd.hip).
-hipError_t split_workspace(hipStream_t stream, size_t part_bytes, size_t counters, float** part,
-                           unsigned** cnt);
 
 // Launches the FA2 kernel for configuration `cfg` on `stream`.
 hipError_t launch_fa2(const FwdArgs& a, int cfg, hipStream_t stream);

@@ -28,12 +28,11 @@ def test_library_loads_and_exports_header_symbols():
 
 
 def test_config_table():
-    assert capi.num_configs() == 8
-    names = [capi.config_name(i) for i in range(8)]
+    assert capi.num_configs() == 6
+    names = [capi.config_name(i) for i in range(6)]
     assert names == ["br32_bc64_w1", "br64_bc64_w2", "br128_bc64_w4", "br256_bc64_w8",
-                     "br256_bc64_w8_pingpong", "br256_bc64_w4x2", "br128_bc64_w4_split2",
-                     "br128_bc64_w4_xsplit2"]
-    assert capi.config_name(8) is None and capi.config_name(-1) is None
+                     "br256_bc64_w8_pingpong", "br128_bc64_w4_split2"]
+    assert capi.config_name(6) is None and capi.config_name(-1) is None
 
 
 def _p(**kw):
@@ -87,7 +86,7 @@ def test_non_finite_scale():
 
 
 def test_bad_config():
-    assert capi.fwd(_p(), config=8) == capi.FL_ERR_BAD_CONFIG
+    assert capi.fwd(_p(), config=6) == capi.FL_ERR_BAD_CONFIG
     assert capi.fwd(_p(), config=-2) == capi.FL_ERR_BAD_CONFIG
 
 
@@ -112,8 +111,8 @@ def test_dispatcher_choices():
     assert sel(batch=1, heads=16, seq_q=16384) == 3
     assert sel(batch=32, heads=32, seq_q=256) == 3
     # fewer than two 128-row groups per CU at N >= 2048: split key range
-    assert sel(batch=2, heads=8, seq_q=2048) == 6      # 256 groups of 128 rows
-    assert sel(batch=1, heads=1, seq_q=4096) == 6
+    assert sel(batch=2, heads=8, seq_q=2048) == 5      # 256 groups of 128 rows
+    assert sel(batch=1, heads=1, seq_q=4096) == 5
     # causal: 128-row groups balanced by dispatch order
     assert sel(batch=2, heads=8, seq_q=4096, causal=True) == 2
     assert sel(batch=1, heads=16, seq_q=16384, causal=True) == 2
