@@ -163,10 +163,14 @@ __device__ __forceinline__ void static_for(std::integer_sequence<int, I...>, F&&
 // Work-group -> (batch*head, query block).  Work-groups are dealt to the 8
 // XCDs round-robin; remap so that the query blocks of a head land on the
 // same XCD (shared K/V in its L2).  Causal work-groups differ in length, so
-// each XCD is fed heaviest first (longest-processing-time order, heads
-// interleaved); with kSlotsPerCu == 2 co-resident work-groups the first 64
-// of an XCD (one per slot of its 32 CUs, dealt CU by CU) are arranged so
-// that each CU pairs the j-th heaviest block with the j-th lightest.
+// each XCD is fed heaviest first (heads interleaved).  Measured dispatch on
+// gfx950: an XCD fills its 32 CUs in a fixed order with its first 32
+// work-groups; with two co-resident work-groups per CU its next 32 fill the
+// second slots of the same CUs in the same order; after that each goes to
+// whichever CU frees first.  So with kSlotsPerCu == 2 the second 32 are
+// taken in reverse (CU j pairs the j-th heaviest block with the j-th
+// lightest of the first 64), and every later position keeps the
+// longest-processing-time order.
 template <bool CAUSAL, int kSlotsPerCu>
 __device__ __forceinline__ void wg_coords(int nqb, int& bh, int& qb) {
   constexpr int kCusPerXcd = 32;
