@@ -418,6 +418,24 @@ struct Rows {
     return (sum[0] + sum[1]) + (sum[2] + sum[3]);
   }
   __device__ __forceinline__ float exponentiate(const float16_t (&s)[2]) { return exponentiate(s, p); }
+  // Softmax of tile j into pn at the current m, no rescaling: returns the
+  // lanes whose tile sum left the range where every p is a finite fp16
+  // (also catches inf / NaN); the caller then recomputes with rescaling.
+  __device__ __forceinline__ uint64_t softmax_fast(const float16_t (&s)[2], half8_t (&pn)[2][2]) {
+    const float sum = exponentiate(s, pn);
+    l += sum;
+    return __builtin_amdgcn_ballot_w64(!(sum <= kSumLimit));
+  }
+  // Back to the state after init (Q stays loaded).
+  __device__ __forceinline__ void reset() {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      o[0][r] = 0.0f;
+      o[1][r] = 0.0f;
+    }
+    set_m(0.0f);
+    l = 0.0f;
+  }
   // Softmax of tile j into pn with the stabiliser checked after the fact,
   // for schedules where GEMM2 trails by one tile: at this point O holds tiles
   // < j and S_next (tile j+1) was computed against the current m.  When a
@@ -620,12 +638,22 @@ fa2_fwd_kernel(const _Float16* Q, const _Float16* __restrict__ K,
   // and V(t-2), vacated before the previous barrier; read the K(t+1) and
   // V(t-1) operands; then three independent pieces of work the compiler
   // interleaves: GEMM1(t+1), GEMM2(t-1) with P(t-1), and the softmax of S(t)
-  // into P(t).  Finally mask S(t+1), wait for this wave's part of K(t+2) and
-  // V(t), barrier.  Iteration 0 multiplies a zeroed V slot by P = 0, and
-  // iteration t0 exponentiates a fully masked S (p = 0); both only fill the
-  // pipeline.
+  // into P(t).  Finally mask S(t+1) (MASKED iterations only), wait for this
+  // wave's part of K(t+2) and V(t), barrier.  Iteration 0 multiplies a
+  // zeroed V slot by P = 0, and iteration t0 exponentiates a fully masked S
+  // (p = 0); both only fill the pipeline.
+  //
+  // Two passes.  The first never moves the stabiliser m (the exact row max
+  // of the first tile): it only records, branch-free, whether any tile's p
+  // left the fp16-safe range (Rows::softmax_fast).  If one did anywhere in
+  // the work-group (rare: a later key scores far above the first tile's
+  // best), the whole query block is recomputed by the CHECKED pass, which
+  // rescales when needed (Rows::softmax_trailing).  Without per-tile
+  // branches the first pass's iterations are single basic blocks.
+  uint64_t out_of_range = 0;
   auto iteration = [&](auto i, int j, float16_t (&S)[2], float16_t (&Sn)[2], half8_t (&P)[2][2],
-                       const half8_t (&Pp)[2][2]) __attribute__((always_inline)) {
+                       const half8_t (&Pp)[2][2], auto masked, auto checked)
+                       __attribute__((always_inline)) {
     constexpr int I = decltype(i)::value;
     const int t = tbeg + j;
     fetch_tile<kSegs, false>(rk, rings.kslot(Ic<I + D + 1>{}), t + D + 1, last, rw, lane);
@@ -635,57 +663,90 @@ fa2_fwd_kernel(const _Float16* Q, const _Float16* __restrict__ K,
     rows.read_v(rings.vslot(Ic<I - 1>{}), va);
     // GEMM1 of a tile past the range reads a stale slot; its result is masked.
     rows.gemm12(ka, Sn, va, Pp);
-    rows.softmax_trailing(S, P, [&](float d) __attribute__((always_inline)) {
-      Rows<CAUSAL, SCALED>::sub(Sn, d);
-    });
-    rows.mask(t + 1, Sn);
+    if constexpr (decltype(checked)::value) {
+      rows.softmax_trailing(S, P, [&](float d) __attribute__((always_inline)) {
+        Rows<CAUSAL, SCALED>::sub(Sn, d);
+      });
+    } else {
+      out_of_range |= rows.softmax_fast(S, P);
+    }
+    if constexpr (decltype(masked)::value) rows.mask(t + 1, Sn);
     sync_ring<(D - 1) * kDmaPerIter>();
   };
 
-  // ---- prologue: K(tbeg), K(tbeg+1) landed; fetch groups of iterations
-  // 1-D .. -1 in flight; S(tbeg) with the exact row max.
-  {
-    const u32x4_t z = {0, 0, 0, 0};
-    for (int off = 16 * (int)threadIdx.x; off < kRingBytes; off += 16 * 64 * W * SPLIT)
-      *reinterpret_cast<u32x4_t*>(vring + off) = z;
-    __syncthreads();
-  }
-  fetch_tile<kSegs, false>(rk, rings.kslot(Ic<0>{}), tbeg, last, rw, lane);
-  fetch_tile<kSegs, false>(rk, rings.kslot(Ic<1>{}), tbeg + 1, last, rw, lane);
-  sync_ring<0>();
-  static_for(std::make_integer_sequence<int, D - 1>{}, [&](auto i) __attribute__((always_inline)) {
-    constexpr int G = decltype(i)::value + 1 - D;  // iteration 1-D+i
-    fetch_tile<kSegs, false>(rk, rings.kslot(Ic<G + D + 1>{}), tbeg + G + D + 1, last, rw, lane);
-    fetch_tile<kSegs, true>(rv, rings.vslot(Ic<G + D - 1>{}), tbeg + G + D - 1, last, rw, lane);
-  });
-  float16_t S0[2], S1[2];
-  half8_t P0[2][2], P1[2][2];
-#pragma unroll
-  for (int a = 0; a < 2; ++a)
-#pragma unroll
-    for (int b = 0; b < 2; ++b) P1[a][b] = (half8_t){0, 0, 0, 0, 0, 0, 0, 0};
-  {
-    half8_t ka[2][4];
-    rows.read_k(rings.kslot(Ic<0>{}), ka);
-    rows.gemm1(ka, S0);
-  }
-  // Iteration 0 refills K(tbeg)'s slot: every wave's reads of it must be done.
-  sync_ring<(D - 1) * kDmaPerIter>();
-  rows.mask(tbeg, S0);
-  rows.first_tile(S0);
+  // Iterations j < jm need no mask (tile tbeg + j + 1 lies below both the
+  // key limit and, causal, this wave's first query row).  The split point
+  // may differ between waves: every iteration has exactly one barrier.
+  int tm = rows.kv_lim >> 6;
+  if (CAUSAL) tm = min(tm, (q0 + 32 * rw + 1) >> 6);
+  const int jm = max(0, tm - tbeg - 1);
 
-  // ---- main loop, unrolled so ring slots and S / P roles are static ----
-  for (int j0 = 0; j0 <= t0; j0 += kUnroll) {
-    static_for(std::make_integer_sequence<int, kUnroll>{}, [&](auto i) __attribute__((always_inline)) {
-      constexpr int I = decltype(i)::value;
-      const int j = j0 + I;
-      if (j <= t0) {
-        if constexpr (I % 2 == 0)
-          iteration(i, j, S0, S1, P0, P1);
-        else
-          iteration(i, j, S1, S0, P1, P0);
-      }
+  auto run_pass = [&](auto checked) __attribute__((always_inline)) {
+    // ---- prologue: K(tbeg), K(tbeg+1) landed; fetch groups of iterations
+    // 1-D .. -1 in flight; S(tbeg) with the exact row max.
+    {
+      const u32x4_t z = {0, 0, 0, 0};
+      for (int off = 16 * (int)threadIdx.x; off < kRingBytes; off += 16 * 64 * W * SPLIT)
+        *reinterpret_cast<u32x4_t*>(vring + off) = z;
+      __syncthreads();
+    }
+    fetch_tile<kSegs, false>(rk, rings.kslot(Ic<0>{}), tbeg, last, rw, lane);
+    fetch_tile<kSegs, false>(rk, rings.kslot(Ic<1>{}), tbeg + 1, last, rw, lane);
+    sync_ring<0>();
+    static_for(std::make_integer_sequence<int, D - 1>{}, [&](auto i) __attribute__((always_inline)) {
+      constexpr int G = decltype(i)::value + 1 - D;  // iteration 1-D+i
+      fetch_tile<kSegs, false>(rk, rings.kslot(Ic<G + D + 1>{}), tbeg + G + D + 1, last, rw, lane);
+      fetch_tile<kSegs, true>(rv, rings.vslot(Ic<G + D - 1>{}), tbeg + G + D - 1, last, rw, lane);
     });
+    float16_t S0[2], S1[2];
+    half8_t P0[2][2], P1[2][2];
+#pragma unroll
+    for (int a = 0; a < 2; ++a)
+#pragma unroll
+      for (int b = 0; b < 2; ++b) P1[a][b] = (half8_t){0, 0, 0, 0, 0, 0, 0, 0};
+    {
+      half8_t ka[2][4];
+      rows.read_k(rings.kslot(Ic<0>{}), ka);
+      rows.gemm1(ka, S0);
+    }
+    // Iteration 0 refills K(tbeg)'s slot: every wave's reads of it must be done.
+    sync_ring<(D - 1) * kDmaPerIter>();
+    rows.mask(tbeg, S0);
+    rows.first_tile(S0);
+
+    // ---- loops, unrolled so ring slots and S / P roles are static ----
+    auto group = [&](int j0, auto masked) __attribute__((always_inline)) {
+      static_for(std::make_integer_sequence<int, kUnroll>{}, [&](auto i) __attribute__((always_inline)) {
+        constexpr int I = decltype(i)::value;
+        const int j = j0 + I;
+        if (!decltype(masked)::value || j <= t0) {
+          if constexpr (I % 2 == 0)
+            iteration(i, j, S0, S1, P0, P1, masked, checked);
+          else
+            iteration(i, j, S1, S0, P1, P0, masked, checked);
+        }
+      });
+    };
+    int j0 = 0;
+    if constexpr (!decltype(checked)::value)
+      for (; j0 + kUnroll <= jm; j0 += kUnroll) group(j0, Ic<false>{});
+    for (; j0 <= t0; j0 += kUnroll) group(j0, Ic<true>{});
+  };
+
+  run_pass(Ic<false>{});
+  {
+    // Work-group-wide decision: redo the block if any wave saw a tile out
+    // of range.  Drain this pass's fetches before the rings are refilled.
+    __builtin_amdgcn_s_waitcnt(0);
+    __shared__ int redo;
+    if (threadIdx.x == 0) redo = 0;
+    __syncthreads();
+    if (out_of_range != 0 && lane == 0) redo = 1;
+    __syncthreads();
+    if (redo) {
+      rows.reset();
+      run_pass(Ic<true>{});
+    }
   }
 
   // No fetch may still be writing LDS when the work-group retires or the
