@@ -52,3 +52,31 @@ def assert_close_oracle(out, q16, k16, v16, sm_scale, causal, rows=None, max_abs
     mx, mean = error_stats(got, ref)
     assert mx <= max_abs and mean <= mean_abs, f"max-abs {mx:.3e} mean-abs {mean:.3e}"
     return mx, mean
+
+
+def redo_expected(q16, k16, sm_scale, causal):
+    """True when the kernel's branch-free first pass must hand the block to
+    its checked pass: some row has, in a 64-key tile after its first, a lane
+    half (32 of the 64 keys) whose sum of 2^(s - m0) exceeds 2^15, m0 being
+    the row's max over the first tile and s its base-2 logits."""
+    import numpy as np
+
+    log2e = float(np.float32(1.4426950408889634))
+    q = q16.astype(np.float64)
+    k = k16.astype(np.float64)
+    n = q.shape[2]
+    s = np.einsum("bhid,bhjd->bhij", q, k) * abs(sm_scale) * log2e
+    if sm_scale < 0:
+        s = -s
+    if causal:
+        s = np.where(np.tril(np.ones((n, n), bool)), s, -np.inf)
+    m0 = s[..., :64].max(axis=-1, keepdims=True)
+    # key j of a tile sits in lane half ((j % 32) // 4) % 2
+    half = ((np.arange(64) % 32) // 4) % 2
+    for t0 in range(64, n, 64):
+        p = np.exp2(np.minimum(s[..., t0:t0 + 64] - m0, 200.0))
+        h = half[: p.shape[-1]]
+        for g in (0, 1):
+            if (p[..., h == g].sum(axis=-1) > 2.0 ** 15).any():
+                return True
+    return False

@@ -12,7 +12,7 @@ import pytest
 
 from flashlite_amd import capi
 from flashlite_amd.workloads import WORKLOADS, make_qkv, workload_inputs
-from gpu_util import assert_close_oracle, run_capi, sample_rows, to_dev
+from gpu_util import assert_close_oracle, redo_expected, run_capi, sample_rows, to_dev
 from oracle import error_stats
 
 pytestmark = pytest.mark.gpu
@@ -118,6 +118,8 @@ def test_other_scales(cuda, scale, causal):
     # where one fp16 ulp of the output alone is 3.9e-3; the bound there is
     # the output's own half-ulp on top of the 2e-3 budget.
     q, k, v = make_qkv(1, 4, 257, 64, seed=41)
+    # the peaked cases must take the kernel's checked (rescaling) pass
+    assert redo_expected(q, k, scale, causal) == (scale >= 1.0)
     out = run_capi(q, k, v, scale, causal, cuda)
     assert_close_oracle(out, q, k, v, scale, causal, max_abs=2e-3 if scale < 1 else 4e-3)
 
