@@ -24,11 +24,15 @@ try:
     from . import flash_attn_wmma as _ext
 except ImportError as exc:  # pragma: no cover - exercised only without a build
     raise ImportError(
-        "flashlite_amd: the HIP extension is not built. Run `python -m flashlite_amd.build` "
+        "flashlite_amd: the HIP extension is not built. Run `python flashlite_amd/build.py` "
         "(or `python -c 'import __graft_entry__ as g; g.build()'`) from the repository root."
     ) from exc
 
 forward_flash2 = _ext.forward_flash2
 forward_naive = _ext.forward_naive
+# Beyond the reference surface: strided [B, H, N, 64] views (a [B, N, H, 64]
+# tensor passes as x.transpose(1, 2)), N_k != N_q with the causal diagonal
+# aligned bottom-right, and the fp32 log-sum-exp with return_lse=True.
+forward_flash2_ex = _ext.forward_flash2_ex
 
-__all__ = ["forward_flash2", "forward_naive"]
+__all__ = ["forward_flash2", "forward_naive", "forward_flash2_ex"]

@@ -1,6 +1,8 @@
 """In-tree build of the HIP library and the torch binding.
 
-    python -m flashlite_amd.build
+    python flashlite_amd/build.py
+
+(run as a script: importing the package needs the extension it builds)
 
 1. ``hipcc --offload-arch=gfx950`` compiles the kernels and the C ABI
    (``csrc/*.hip``) into ``flashlite_amd/libflashlite_attn.so``.

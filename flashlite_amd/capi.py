@@ -29,6 +29,7 @@ EXPORTED = (
     "fl_attn_num_configs",
     "fl_attn_config_name",
     "fl_attn_select_config",
+    "fl_attn_fwd_f16_ex",
 )
 
 
@@ -50,6 +51,19 @@ class FlAttnParams(ctypes.Structure):
     ]
 
 
+class FlAttnParamsEx(ctypes.Structure):
+    """Mirror of ``fl_attn_params_ex``: strides {batch, head, row} in elements."""
+
+    _fields_ = [
+        ("base", FlAttnParams),
+        ("q_stride", ctypes.c_int64 * 3),
+        ("k_stride", ctypes.c_int64 * 3),
+        ("v_stride", ctypes.c_int64 * 3),
+        ("o_stride", ctypes.c_int64 * 3),
+        ("lse", ctypes.c_void_p),
+    ]
+
+
 class FlashLiteError(RuntimeError):
     def __init__(self, code: int, message: str):
         super().__init__(f"[{code}] {message}")
@@ -65,7 +79,7 @@ def load(path: str = LIB_PATH) -> ctypes.CDLL:
     if _lib is not None:
         return _lib
     if not os.path.exists(path):
-        raise FileNotFoundError(f"{path} is not built; run `python -m flashlite_amd.build`")
+        raise FileNotFoundError(f"{path} is not built; run `python flashlite_amd/build.py`")
     lib = ctypes.CDLL(path)
     P = ctypes.POINTER(FlAttnParams)
     lib.fl_attn_fwd_f16.argtypes = [P, ctypes.c_void_p]
@@ -82,6 +96,9 @@ def load(path: str = LIB_PATH) -> ctypes.CDLL:
     lib.fl_attn_config_name.restype = ctypes.c_char_p
     lib.fl_attn_select_config.argtypes = [P]
     lib.fl_attn_select_config.restype = ctypes.c_int
+    lib.fl_attn_fwd_f16_ex.argtypes = [ctypes.POINTER(FlAttnParamsEx), ctypes.c_int32,
+                                       ctypes.c_void_p]
+    lib.fl_attn_fwd_f16_ex.restype = ctypes.c_int
     _lib = lib
     return lib
 
@@ -107,6 +124,27 @@ def check(rc: int) -> None:
 def fwd(params: FlAttnParams, stream: int = 0, config: int = -1) -> int:
     """``fl_attn_fwd_f16_cfg``; returns the status code."""
     return load().fl_attn_fwd_f16_cfg(ctypes.byref(params), config, stream or None)
+
+
+def fwd_ex(params: FlAttnParamsEx, stream: int = 0, config: int = -1) -> int:
+    """``fl_attn_fwd_f16_ex``; returns the status code."""
+    return load().fl_attn_fwd_f16_ex(ctypes.byref(params), config, stream or None)
+
+
+def make_params_ex(base: FlAttnParams, q_stride, k_stride, v_stride, o_stride,
+                   lse: int = 0) -> FlAttnParamsEx:
+    """Extended params from a base struct, four {batch, head, row} stride
+    triples (elements) and an optional lse address."""
+    t3 = ctypes.c_int64 * 3
+    return FlAttnParamsEx(base, t3(*q_stride), t3(*k_stride), t3(*v_stride), t3(*o_stride),
+                          lse or None)
+
+
+def tensor_params_ex(q, k, v, o, sm_scale=0.0, causal=False, lse=None) -> FlAttnParamsEx:
+    """Extended params for strided [B, H, N, D] torch views (unit-stride D)."""
+    base = tensor_params(q, k, v, o, sm_scale, causal)
+    strides = [tuple(int(s) for s in t.stride()[:3]) for t in (q, k, v, o)]
+    return make_params_ex(base, *strides, lse=0 if lse is None else lse.data_ptr())
 
 
 def naive(params: FlAttnParams, stream: int = 0) -> int:

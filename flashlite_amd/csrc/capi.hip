@@ -4,7 +4,10 @@
 // Reference host entries: csrc/kernel_flash2.cu:732-839 (flash2) and
 // csrc/kernel_naive.cu:242-323 (naive).  The torch-tensor checks live in the
 // binding (flash_attn.cpp); here are the checks a raw-pointer caller needs,
-// plus the ones the reference skipped (N_k != N_q, 64-bit sizes, alignment).
+// plus the ones the reference skipped (64-bit sizes, alignment).  N_k may
+// differ from N_q: the reference validates that shape but then indexes K and
+// V with N_q (kernel_flash2.cu:84, :425, :752-755); here the keys are
+// addressed with N_k and the causal diagonal is aligned bottom-right.
 
 #include <hip/hip_runtime.h>
 
@@ -47,9 +50,6 @@ int check_common(const fl_attn_params* p, fl::FwdArgs* a, const char* who) {
                 "N_k=%lld D=%lld)",
                 who, (long long)p->batch, (long long)p->heads, (long long)p->seq_q,
                 (long long)p->seq_k, (long long)p->head_dim);
-  if (p->seq_k != p->seq_q)
-    return fail(FL_ERR_UNSUPPORTED, "%s: N_k (%lld) must equal N_q (%lld)", who,
-                (long long)p->seq_k, (long long)p->seq_q);
   const double scale = resolve_scale(p->sm_scale, p->head_dim);
   const float c = (float)(std::fabs(scale) * kLog2eF);
   if (!std::isfinite(scale) || !std::isfinite(c) || c == 0.0f)
@@ -58,29 +58,46 @@ int check_common(const fl_attn_params* p, fl::FwdArgs* a, const char* who) {
   const int64_t bh = p->batch * p->heads;
   if (p->batch != 0 && bh / p->batch != p->heads)
     return fail(FL_ERR_UNSUPPORTED, "%s: B*H overflows", who);
-  if (bh > INT32_MAX || p->seq_q > INT32_MAX || p->head_dim > INT32_MAX)
-    return fail(FL_ERR_UNSUPPORTED, "%s: B*H, N and D must each fit in int32", who);
+  if (bh > INT32_MAX || p->seq_q > INT32_MAX || p->seq_k > INT32_MAX || p->head_dim > INT32_MAX)
+    return fail(FL_ERR_UNSUPPORTED, "%s: B*H, N_q, N_k and D must each fit in int32", who);
   a->q = p->q;
   a->k = p->k;
   a->v = p->v;
   a->o = p->o;
+  a->lse = nullptr;
   a->batch_heads = (int)bh;
+  a->heads = (int)p->heads;
   a->seq = (int)p->seq_q;
+  a->seq_k = (int)p->seq_k;
   a->head_dim = (int)p->head_dim;
   a->scale_log2 = c;
   a->negate = scale < 0.0 ? 1 : 0;
   a->causal = p->causal ? 1 : 0;
+  // contiguous [B, H, N, D]
+  const int64_t d = p->head_dim;
+  a->q_sr = a->o_sr = a->k_sr = a->v_sr = (int)d;
+  a->q_sh = a->o_sh = p->seq_q * d;
+  a->k_sh = a->v_sh = p->seq_k * d;
+  a->q_sb = a->o_sb = p->heads * p->seq_q * d;
+  a->k_sb = a->v_sb = p->heads * p->seq_k * d;
   return FL_OK;
 }
 
+// No query row: nothing to write.  (N_k == 0 with rows is not empty: every
+// row then has no visible key and is written as 0.)
 bool empty_problem(const fl::FwdArgs& a) { return a.batch_heads == 0 || a.seq == 0; }
 
-int check_pointers(const fl_attn_params* p, const char* who, uintptr_t align) {
-  if (!p->q || !p->k || !p->v || !p->o)
+// With N_k == 0 (no keys: every row is written as 0) k and v are never read
+// and may be NULL; the kernels then get q's address in their place.
+int check_pointers(const fl_attn_params* p, fl::FwdArgs* a, const char* who, uintptr_t align) {
+  const bool no_keys = p->seq_k == 0;
+  if (!p->q || !p->o || (!no_keys && (!p->k || !p->v)))
     return fail(FL_ERR_INVALID_ARGUMENT, "%s: q, k, v and o must be non-NULL", who);
   const uintptr_t m = align - 1;
-  if (((uintptr_t)p->q | (uintptr_t)p->k | (uintptr_t)p->v | (uintptr_t)p->o) & m)
+  const uintptr_t kv = no_keys ? 0 : ((uintptr_t)p->k | (uintptr_t)p->v);
+  if (((uintptr_t)p->q | kv | (uintptr_t)p->o) & m)
     return fail(FL_ERR_MISALIGNED, "%s: q, k, v and o must be %u-byte aligned", who, (unsigned)align);
+  if (no_keys) a->k = a->v = p->q;
   return FL_OK;
 }
 
@@ -103,21 +120,35 @@ int select_fa2(const fl::FwdArgs& a) {
   return 0;                                                          // br32_bc64_w1
 }
 
-int check_fa2(const fl_attn_params* p, fl::FwdArgs* a) {
-  const char* who = "fl_attn_fwd_f16";
+int check_fa2(const fl_attn_params* p, fl::FwdArgs* a, const char* who = "fl_attn_fwd_f16") {
   int rc = check_common(p, a, who);
   if (rc != FL_OK) return rc;
   if (p->head_dim != 64)
     return fail(FL_ERR_UNSUPPORTED, "FlashLite WMMA kernel currently requires head_dim == 64");
   // K/V tiles are fetched through 32-bit buffer offsets within one head
-  // (N * 128 bytes, plus one tile of slack).
-  if (a->seq > (INT32_MAX / 128) - 128)
-    return fail(FL_ERR_UNSUPPORTED, "%s: N=%d exceeds the per-head addressing limit (%d)", who, a->seq,
-                (INT32_MAX / 128) - 128);
+  // (N_k rows of 128 bytes, plus one tile of slack).
+  if (a->seq_k > (INT32_MAX / 128) - 128)
+    return fail(FL_ERR_UNSUPPORTED, "%s: N_k=%d exceeds the per-head addressing limit (%d)", who,
+                a->seq_k, (INT32_MAX / 128) - 128);
   // Grid = ceil(N/32) * B*H work-groups at the smallest tile; per-head
   // offsets are 64-bit in the kernel.
   if (((int64_t)a->seq + 31) / 32 * (int64_t)a->batch_heads > INT32_MAX)
     return fail(FL_ERR_UNSUPPORTED, "%s: too many work-groups (B*H*ceil(N/32) > 2^31-1)", who);
+  return FL_OK;
+}
+
+// Strides of one tensor of fl_attn_fwd_f16_ex: every row 16-byte aligned
+// (strides in multiples of 8 halfs), rows at least D apart, and row offsets
+// that fit the kernels' 32-bit row stride.
+int check_strides(const int64_t st[3], const char* name, const char* who) {
+  for (int i = 0; i < 3; ++i)
+    if (st[i] < 0 || st[i] % 8 != 0)
+      return fail(FL_ERR_UNSUPPORTED, "%s: %s strides must be non-negative multiples of 8 elements "
+                  "(got %lld, %lld, %lld)", who, name, (long long)st[0], (long long)st[1],
+                  (long long)st[2]);
+  if (st[2] < 64 || st[2] > INT32_MAX / 2)
+    return fail(FL_ERR_UNSUPPORTED, "%s: %s row stride %lld must be in [64, 2^30)", who, name,
+                (long long)st[2]);
   return FL_OK;
 }
 
@@ -148,7 +179,7 @@ int fl_attn_fwd_f16_cfg(const fl_attn_params* p, int32_t config, void* stream) {
     return fail(FL_ERR_BAD_CONFIG, "fl_attn_fwd_f16: config %d out of range [-1, %d)", (int)config,
                 fl::kNumFa2Configs);
   if (empty_problem(a)) return FL_OK;
-  rc = check_pointers(p, "fl_attn_fwd_f16", 16);
+  rc = check_pointers(p, &a, "fl_attn_fwd_f16", 16);
   if (rc != FL_OK) return rc;
   const int cfg = config < 0 ? select_fa2(a) : config;
   const hipError_t e = fl::launch_fa2(a, cfg, static_cast<hipStream_t>(stream));
@@ -161,18 +192,66 @@ int fl_attn_fwd_f16(const fl_attn_params* p, void* stream) {
   return fl_attn_fwd_f16_cfg(p, -1, stream);
 }
 
+int fl_attn_fwd_f16_ex(const fl_attn_params_ex* p, int32_t config, void* stream) {
+  const char* who = "fl_attn_fwd_f16_ex";
+  if (p == nullptr) return fail(FL_ERR_INVALID_ARGUMENT, "%s: params is NULL", who);
+  fl::FwdArgs a;
+  int rc = check_fa2(&p->base, &a, who);
+  if (rc != FL_OK) return rc;
+  if (config < -1 || config >= fl::kNumFa2Configs)
+    return fail(FL_ERR_BAD_CONFIG, "%s: config %d out of range [-1, %d)", who, (int)config,
+                fl::kNumFa2Configs);
+  const int64_t* st[4] = {p->q_stride, p->k_stride, p->v_stride, p->o_stride};
+  const char* names[4] = {"q", "k", "v", "o"};
+  const bool no_keys = a.seq_k == 0;  // k and v are never read
+  for (int i = 0; i < 4; ++i) {
+    if (no_keys && (i == 1 || i == 2)) continue;
+    rc = check_strides(st[i], names[i], who);
+    if (rc != FL_OK) return rc;
+  }
+  for (int i = 1; i <= 2; ++i)
+    if ((a.seq_k + 128LL) * st[i][2] * 2 > INT32_MAX)
+      return fail(FL_ERR_UNSUPPORTED, "%s: N_k=%d rows of stride %lld exceed the per-head "
+                  "addressing limit of %s (2^31 bytes)", who, a.seq_k, (long long)st[i][2],
+                  names[i]);
+  if ((uintptr_t)p->lse & 3)
+    return fail(FL_ERR_MISALIGNED, "%s: lse must be 4-byte aligned", who);
+  a.q_sb = p->q_stride[0];
+  a.q_sh = p->q_stride[1];
+  a.q_sr = (int)p->q_stride[2];
+  if (!no_keys) {
+    a.k_sb = p->k_stride[0];
+    a.k_sh = p->k_stride[1];
+    a.k_sr = (int)p->k_stride[2];
+    a.v_sb = p->v_stride[0];
+    a.v_sh = p->v_stride[1];
+    a.v_sr = (int)p->v_stride[2];
+  }
+  a.o_sb = p->o_stride[0];
+  a.o_sh = p->o_stride[1];
+  a.o_sr = (int)p->o_stride[2];
+  a.lse = p->lse;
+  if (empty_problem(a)) return FL_OK;
+  rc = check_pointers(&p->base, &a, who, 16);
+  if (rc != FL_OK) return rc;
+  const int cfg = config < 0 ? select_fa2(a) : config;
+  const hipError_t e = fl::launch_fa2(a, cfg, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return fail(FL_ERR_LAUNCH, "%s: launch failed: %s", who, hipGetErrorString(e));
+  return FL_OK;
+}
+
 int fl_attn_naive_f16(const fl_attn_params* p, void* stream) {
   const char* who = "fl_attn_naive_f16";
   fl::FwdArgs a;
   int rc = check_common(p, &a, who);
   if (rc != FL_OK) return rc;
   if (empty_problem(a)) return FL_OK;
-  if (a.seq > fl::naive_max_seq(a.head_dim))
-    return fail(FL_ERR_UNSUPPORTED, "%s: N=%d exceeds the LDS capacity of the naive kernel (max %lld at D=%d)",
-                who, a.seq, (long long)fl::naive_max_seq(a.head_dim), a.head_dim);
+  if (a.seq_k > fl::naive_max_seq(a.head_dim))
+    return fail(FL_ERR_UNSUPPORTED, "%s: N_k=%d exceeds the LDS capacity of the naive kernel (max %lld at D=%d)",
+                who, a.seq_k, (long long)fl::naive_max_seq(a.head_dim), a.head_dim);
   if (a.batch_heads > 65535)
     return fail(FL_ERR_UNSUPPORTED, "%s: B*H=%d exceeds the grid limit 65535", who, a.batch_heads);
-  rc = check_pointers(p, who, 2);
+  rc = check_pointers(p, &a, who, 2);
   if (rc != FL_OK) return rc;
   const hipError_t e = fl::launch_naive(a, static_cast<hipStream_t>(stream));
   if (e != hipSuccess) return fail(FL_ERR_LAUNCH, "%s: launch failed: %s", who, hipGetErrorString(e));

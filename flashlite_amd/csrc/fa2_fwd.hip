@@ -6,8 +6,10 @@
 // 64-lane wavefronts and MFMA, not a translation; the math and the mask
 // semantics are the same:
 //   O = softmax(Q K^T * sm_scale [+ causal mask]) V,
-//   causal: key j visible to query i iff j <= i (top-left, N_q == N_k),
-//   keys >= N masked, query rows >= N never written (:373, :380),
+//   causal: key j visible to query i iff j <= i (top-left when N_q == N_k;
+//   with N_k != N_q the diagonal is aligned bottom-right, j <= i + N_k - N_q,
+//   and a query row with no visible key returns 0, as :364-365 do),
+//   keys >= N_k masked, query rows >= N_q never written (:373, :380),
 //   P rounded to fp16 before the PV product (:278-285), fp32 row sums.
 //
 // Work decomposition.  A work-group owns 32*W consecutive query rows of one
@@ -131,6 +133,47 @@ __device__ __forceinline__ i32x4_t buffer_rsrc(const void* base, int bytes) {
   return r;
 }
 
+// Addressing of one launch: element strides of q, k, v, o over
+// [batch][head][row] (head_dim is unit stride), the sizes, the causal
+// diagonal offset N_k - N_q, and the optional log-sum-exp output.
+struct Geom {
+  long long q_sb, q_sh, k_sb, k_sh, v_sb, v_sh, o_sb, o_sh;
+  int q_sr, k_sr, v_sr, o_sr;
+  int heads, seq_q, seq_k, coff;
+  float* lse;  // [B*H][N_q] or null
+};
+
+// Per-head base pointers and buffer resources of a work-group.
+struct HeadPtrs {
+  const _Float16* q;
+  _Float16* o;
+  float* lse;
+  i32x4_t rk, rv;
+};
+
+__device__ __forceinline__ HeadPtrs head_ptrs(const Geom& g, int bh, const _Float16* Q,
+                                              const _Float16* K, const _Float16* V, _Float16* O) {
+  const int b = bh / g.heads, h = bh - b * g.heads;
+  HeadPtrs p;
+  p.q = Q + (b * g.q_sb + h * g.q_sh);
+  p.o = O + (b * g.o_sb + h * g.o_sh);
+  p.lse = g.lse ? g.lse + (long long)bh * g.seq_q : nullptr;
+  // num_records covers the last row's 128 bytes; later rows read as zeros.
+  const int kb = g.seq_k > 0 ? (g.seq_k - 1) * (2 * g.k_sr) + kRowBytes : 0;
+  const int vb = g.seq_k > 0 ? (g.seq_k - 1) * (2 * g.v_sr) + kRowBytes : 0;
+  p.rk = buffer_rsrc(K + (b * g.k_sb + h * g.k_sh), kb);
+  p.rv = buffer_rsrc(V + (b * g.v_sb + h * g.v_sh), vb);
+  return p;
+}
+
+// Key tiles a causal block of query rows [q0, q_end) needs: through the
+// diagonal of its last row (at least one, fully masked when no row of the
+// block sees a key).
+__device__ __forceinline__ int causal_tiles(int q_end, int coff) {
+  const int last_key = q_end - 1 + coff;
+  return last_key < 0 ? 1 : last_key / kBc + 1;
+}
+
 __device__ __forceinline__ half4_t lds_read_tr(const uint8_t* p) {
   short4_t s = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
       (short4_t __attribute__((address_space(3)))*)(p));
@@ -220,17 +263,39 @@ struct Rings {
 // i.e. row i/8, physical chunk i%8, which holds logical chunk
 // (i%8) ^ swz(row).  Issued from inline assembly so the compiler does not
 // guard LDS reads of other slots with waits on it; sync_ring<> tracks it.
+template <int kSegs>
+struct FetchOff {
+  int lane[kSegs];  // this lane's byte offset of segment i within a tile
+  int tile_bytes;   // kBc rows
+};
+
 template <int kSegs, bool IS_V>
-__device__ __forceinline__ void fetch_tile(const i32x4_t& rs, const uint8_t* slot, int t,
-                                           int last_tile, int wave, int lane) {
-  t = min(t, last_tile);
+__device__ __forceinline__ FetchOff<kSegs> fetch_offsets(int wave, int lane, int row_bytes) {
+  FetchOff<kSegs> f;
 #pragma unroll
   for (int i = 0; i < kSegs; ++i) {
     const int seg = wave * kSegs + i;
     const int row = 8 * seg + (lane >> 3);
     const int phys = lane & 7;
     const int logical = phys ^ (IS_V ? v_swz(row) : k_swz(row));
-    const int voff = (t * kBc + row) * kRowBytes + 16 * logical;
+    f.lane[i] = row * row_bytes + 16 * logical;
+    // Opaque to the optimiser: keeps the per-tile address an SALU product
+    // plus one add instead of a re-derived 64-bit multiply-add.
+    asm volatile("" : "+v"(f.lane[i]));
+  }
+  f.tile_bytes = kBc * row_bytes;
+  return f;
+}
+
+template <int kSegs>
+__device__ __forceinline__ void fetch_tile(const i32x4_t& rs, const uint8_t* slot, int t,
+                                           int last_tile, int wave, const FetchOff<kSegs>& f) {
+  t = min(t, last_tile);
+  const int tb = t * f.tile_bytes;
+#pragma unroll
+  for (int i = 0; i < kSegs; ++i) {
+    const int seg = wave * kSegs + i;
+    const int voff = tb + f.lane[i];
     const uint32_t lds_base = (uint32_t)(uintptr_t)(slot + 1024 * seg);
     asm volatile("buffer_load_dwordx4 %0, %1, 0 offen lds" : : "v"(voff), "s"(rs), "{m0}"(lds_base));
   }
@@ -241,7 +306,8 @@ __device__ __forceinline__ void fetch_tile(const i32x4_t& rs, const uint8_t* slo
 template <bool CAUSAL, bool SCALED>
 struct Rows {
   int g, col, qw, my_q, seq;
-  int kv_lim;       // keys >= kv_lim are masked (seq, or the end of a split range)
+  int qd, my_d;     // causal diagonals: the last key visible to row qw / my_q
+  int kv_lim;       // keys >= kv_lim are masked (N_k, or the end of a split range)
   int tr_row, tr_col;
   float cr;
   half8_t qf[4];    // Q'^T B-operand
@@ -251,14 +317,16 @@ struct Rows {
   float l;          // this lane's share of the row sum
   half8_t p[2][2];  // fp16 P^T B-operands of the last softmaxed tile
 
-  __device__ __forceinline__ void init(const _Float16* Qh, int lane, int qw_, int seq_, float cq,
-                                       float cr_) {
+  __device__ __forceinline__ void init(const _Float16* Qh, int q_sr, int lane, int qw_, int seq_,
+                                       int seq_k, int coff, float cq, float cr_) {
     g = lane >> 5;
     col = lane & 31;
     qw = qw_;
     my_q = qw + col;
+    qd = qw + coff;
+    my_d = my_q + coff;
     seq = seq_;
-    kv_lim = seq_;
+    kv_lim = seq_k;
     cr = cr_;
     // GEMM2 tr-read address pieces: lane l is lane j = l%16 of 16-lane group
     // G = l/16; it points at key row 4*(G/2) + j/4 (+16t, +8 for the second
@@ -272,7 +340,7 @@ struct Rows {
     for (int s = 0; s < 4; ++s) {
       if (my_q < seq) {
         const half8_t raw =
-            *reinterpret_cast<const half8_t*>(Qh + (size_t)my_q * kD + 16 * s + 8 * g);
+            *reinterpret_cast<const half8_t*>(Qh + (long long)my_q * q_sr + 16 * s + 8 * g);
 #pragma unroll
         for (int e = 0; e < 8; ++e) qf[s][e] = (_Float16)((float)raw[e] * cq);
       } else {
@@ -349,17 +417,17 @@ struct Rows {
       }
     }
   }
-  // Masks keys >= kv_lim and, when causal, keys after the lane's query
+  // Masks keys >= kv_lim and, when causal, keys past the lane's diagonal
   // (tile t).
   __device__ __forceinline__ void mask(int t, float16_t (&s)[2]) const {
     const int k0 = t * kBc;
-    if (k0 + kBc > kv_lim || (CAUSAL && k0 + kBc - 1 > qw)) {
+    if (k0 + kBc > kv_lim || (CAUSAL && k0 + kBc - 1 > qd)) {
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
           const int key = k0 + 32 * kb + 8 * (r >> 2) + 4 * g + (r & 3);
-          const bool ok = key < kv_lim && (!CAUSAL || key <= my_q);
+          const bool ok = key < kv_lim && (!CAUSAL || key <= my_d);
           s[kb][r] = ok ? s[kb][r] : ninf();
         }
     }
@@ -384,9 +452,10 @@ struct Rows {
 #pragma unroll
     for (int r = 0; r < 16; ++r) bias[r] = -mm;
   }
-  // First tile: m = the exact row max.  A row with no key in the tile (only
-  // possible for the second range of a split, where such a row then has no
-  // key in the whole range) gets m = 0 and p = 0 throughout.
+  // First tile: m = the exact row max.  A row with no key in the tile (the
+  // second range of a split, or a row above a bottom-right causal diagonal
+  // when N_q > N_k; such a row then has no key in its whole range) gets
+  // m = 0 and p = 0 throughout.
   __device__ __forceinline__ void first_tile(float16_t (&s)[2]) {
     float m0 = tile_max(s);
     m0 = m0 == ninf() ? 0.0f : m0;
@@ -526,11 +595,18 @@ struct Rows {
     m = mm;
   }
   // O = O^T / l, 16-byte stores of 8 contiguous head dims; rows >= N skipped.
-  __device__ __forceinline__ void store(_Float16* Oh) const {
+  // With `lse`, also the row's log-sum-exp in natural-log units,
+  // ln(sum_j exp(sm_scale q.k_j)) = ln 2 * (m * cr + log2 l) (-inf for a row
+  // with no visible key).
+  __device__ __forceinline__ void store(_Float16* Oh, int o_sr, float* lse) const {
     const float l_tot = pair_sum(l);
     const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
+    if (lse != nullptr && g == 0 && my_q < seq) {
+      const float lg = m * (SCALED ? cr : 1.0f) + __builtin_amdgcn_logf(l_tot);
+      lse[my_q] = l_tot > 0.0f ? 0.693147180559945309f * lg : ninf();
+    }
     if (my_q < seq) {
-      _Float16* orow = Oh + (size_t)my_q * kD;
+      _Float16* orow = Oh + (long long)my_q * o_sr;
 #pragma unroll
       for (int db = 0; db < 2; ++db)
 #pragma unroll
@@ -592,7 +668,7 @@ struct StreamRings {
 template <int W, int D, int SPLIT, bool CAUSAL, bool SCALED>
 __global__ void __launch_bounds__(64 * W * SPLIT, 2)  // 2 waves per SIMD: <= 256 VGPRs
 fa2_fwd_kernel(const _Float16* Q, const _Float16* __restrict__ K,
-               const _Float16* __restrict__ V, _Float16* O, int seq, int nqb,
+               const _Float16* __restrict__ V, _Float16* O, const Geom geom, int nqb,
                float cq, float cr) {
   constexpr int kSlots = D + 1;
   constexpr int kUnroll = (kSlots % 2 == 0) ? kSlots : 2 * kSlots;
@@ -612,18 +688,20 @@ fa2_fwd_kernel(const _Float16* Q, const _Float16* __restrict__ K,
   const int rw = wave - stream * W;  // 32-row block within the work-group
   int bh, qb;
   wg_coords<CAUSAL, (W == 4 && SPLIT == 1) ? 2 : 1>(nqb, bh, qb);
-  const size_t head_off = (size_t)bh * (size_t)seq * kD;
-  const i32x4_t rk = buffer_rsrc(K + head_off, seq * kRowBytes);
-  const i32x4_t rv = buffer_rsrc(V + head_off, seq * kRowBytes);
+  const HeadPtrs hp = head_ptrs(geom, bh, Q, K, V, O);
+  const i32x4_t rk = hp.rk, rv = hp.rv;
+  const FetchOff<kSegs> fk = fetch_offsets<kSegs, false>(rw, lane, 2 * geom.k_sr);
+  const FetchOff<kSegs> fv = fetch_offsets<kSegs, true>(rw, lane, 2 * geom.v_sr);
+  const int seq = geom.seq_q;
   const int q0 = qb * kBr;
   const StreamRings<kSlots> rings = {kring + stream * (kSlots * kTileBytes),
                                      vring + stream * (kSlots * kTileBytes)};
 
   Rows<CAUSAL, SCALED> rows;
-  rows.init(Q + head_off, lane, q0 + 32 * rw, seq, cq, cr);
+  rows.init(hp.q, geom.q_sr, lane, q0 + 32 * rw, seq, geom.seq_k, geom.coff, cq, cr);
 
-  int ntiles = (seq + kBc - 1) / kBc;
-  if (CAUSAL) ntiles = min(ntiles, (min(q0 + kBr, seq) - 1) / kBc + 1);
+  int ntiles = max(1, (geom.seq_k + kBc - 1) / kBc);
+  if (CAUSAL) ntiles = min(ntiles, causal_tiles(min(q0 + kBr, seq), geom.coff));
   // Key tiles [tbeg, tend) of this stream; both streams run t0 + 1
   // iterations (the same barriers), the shorter one on masked tiles.
   constexpr bool kSplit = SPLIT == 2;
@@ -631,7 +709,7 @@ fa2_fwd_kernel(const _Float16* Q, const _Float16* __restrict__ K,
   const int tbeg = stream == 0 ? 0 : t0;
   const int tend = stream == 0 ? t0 : ntiles;
   const int last = max(tend - 1, tbeg);  // fetch clamp
-  if (kSplit && stream == 0) rows.kv_lim = min(seq, t0 * kBc);
+  if (kSplit && stream == 0) rows.kv_lim = min(geom.seq_k, t0 * kBc);
 
   // Iteration j (position I of the unrolled loop), for j = 0 .. t0, on key
   // tile t = tbeg + j: fetch K(t+D+1) and V(t+D-1) into the slots of K(t)
@@ -656,8 +734,8 @@ fa2_fwd_kernel(const _Float16* Q, const _Float16* __restrict__ K,
                        __attribute__((always_inline)) {
     constexpr int I = decltype(i)::value;
     const int t = tbeg + j;
-    fetch_tile<kSegs, false>(rk, rings.kslot(Ic<I + D + 1>{}), t + D + 1, last, rw, lane);
-    fetch_tile<kSegs, true>(rv, rings.vslot(Ic<I + D - 1>{}), t + D - 1, last, rw, lane);
+    fetch_tile<kSegs>(rk, rings.kslot(Ic<I + D + 1>{}), t + D + 1, last, rw, fk);
+    fetch_tile<kSegs>(rv, rings.vslot(Ic<I + D - 1>{}), t + D - 1, last, rw, fv);
     half8_t ka[2][4], va[2][4];
     rows.read_k(rings.kslot(Ic<I + 1>{}), ka);
     rows.read_v(rings.vslot(Ic<I - 1>{}), va);
@@ -678,7 +756,7 @@ fa2_fwd_kernel(const _Float16* Q, const _Float16* __restrict__ K,
   // key limit and, causal, this wave's first query row).  The split point
   // may differ between waves: every iteration has exactly one barrier.
   int tm = rows.kv_lim >> 6;
-  if (CAUSAL) tm = min(tm, (q0 + 32 * rw + 1) >> 6);
+  if (CAUSAL) tm = min(tm, (rows.qd + 1) >> 6);
   const int jm = max(0, tm - tbeg - 1);
 
   auto run_pass = [&](auto checked) __attribute__((always_inline)) {
@@ -690,13 +768,13 @@ fa2_fwd_kernel(const _Float16* Q, const _Float16* __restrict__ K,
         *reinterpret_cast<u32x4_t*>(vring + off) = z;
       __syncthreads();
     }
-    fetch_tile<kSegs, false>(rk, rings.kslot(Ic<0>{}), tbeg, last, rw, lane);
-    fetch_tile<kSegs, false>(rk, rings.kslot(Ic<1>{}), tbeg + 1, last, rw, lane);
+    fetch_tile<kSegs>(rk, rings.kslot(Ic<0>{}), tbeg, last, rw, fk);
+    fetch_tile<kSegs>(rk, rings.kslot(Ic<1>{}), tbeg + 1, last, rw, fk);
     sync_ring<0>();
     static_for(std::make_integer_sequence<int, D - 1>{}, [&](auto i) __attribute__((always_inline)) {
       constexpr int G = decltype(i)::value + 1 - D;  // iteration 1-D+i
-      fetch_tile<kSegs, false>(rk, rings.kslot(Ic<G + D + 1>{}), tbeg + G + D + 1, last, rw, lane);
-      fetch_tile<kSegs, true>(rv, rings.vslot(Ic<G + D - 1>{}), tbeg + G + D - 1, last, rw, lane);
+      fetch_tile<kSegs>(rk, rings.kslot(Ic<G + D + 1>{}), tbeg + G + D + 1, last, rw, fk);
+      fetch_tile<kSegs>(rv, rings.vslot(Ic<G + D - 1>{}), tbeg + G + D - 1, last, rw, fv);
     });
     float16_t S0[2], S1[2];
     half8_t P0[2][2], P1[2][2];
@@ -760,7 +838,7 @@ fa2_fwd_kernel(const _Float16* Q, const _Float16* __restrict__ K,
     if (stream == 1) return;
     rows.merge_partial(part, lane);
   }
-  rows.store(O + head_off);
+  rows.store(hp.o, geom.o_sr, hp.lse);
 }
 
 // ---------------------------------------------------------------------------
@@ -777,7 +855,7 @@ fa2_fwd_kernel(const _Float16* Q, const _Float16* __restrict__ K,
 template <int D, bool CAUSAL, bool SCALED>
 __global__ void __launch_bounds__(512, 1)
 fa2_fwd_pp_kernel(const _Float16* Q, const _Float16* __restrict__ K,
-                  const _Float16* __restrict__ V, _Float16* O, int seq, int nqb,
+                  const _Float16* __restrict__ V, _Float16* O, const Geom geom, int nqb,
                   float cq, float cr) {
   constexpr int kSlots = D + 1;
   constexpr int kBr = 256;
@@ -789,24 +867,26 @@ fa2_fwd_pp_kernel(const _Float16* Q, const _Float16* __restrict__ K,
   const bool group_b = wave >= 4;
   int bh, qb;
   wg_coords<CAUSAL, 1>(nqb, bh, qb);
-  const size_t head_off = (size_t)bh * (size_t)seq * kD;
-  const i32x4_t rk = buffer_rsrc(K + head_off, seq * kRowBytes);
-  const i32x4_t rv = buffer_rsrc(V + head_off, seq * kRowBytes);
+  const HeadPtrs hp = head_ptrs(geom, bh, Q, K, V, O);
+  const i32x4_t rk = hp.rk, rv = hp.rv;
+  const FetchOff<1> fk = fetch_offsets<1, false>(wave, lane, 2 * geom.k_sr);
+  const FetchOff<1> fv = fetch_offsets<1, true>(wave, lane, 2 * geom.v_sr);
+  const int seq = geom.seq_q;
   const int q0 = qb * kBr;
 
   Rows<CAUSAL, SCALED> rows;
-  rows.init(Q + head_off, lane, q0 + 32 * wave, seq, cq, cr);
+  rows.init(hp.q, geom.q_sr, lane, q0 + 32 * wave, seq, geom.seq_k, geom.coff, cq, cr);
 
-  int ntiles = (seq + kBc - 1) / kBc;
-  if (CAUSAL) ntiles = min(ntiles, (min(q0 + kBr, seq) - 1) / kBc + 1);
+  int ntiles = max(1, (geom.seq_k + kBc - 1) / kBc);
+  if (CAUSAL) ntiles = min(ntiles, causal_tiles(min(q0 + kBr, seq), geom.coff));
   const int n = ntiles;
   const int last = n - 1;
 
   // Fetch group u (ring position U = u mod kSlots, static): K(u+D), V(u+D-1).
   auto fetch_group = [&](auto upos, int u) __attribute__((always_inline)) {
     constexpr int U = decltype(upos)::value;
-    fetch_tile<1, false>(rk, rings.kslot(Ic<U + D>{}), u + D, last, wave, lane);
-    fetch_tile<1, true>(rv, rings.vslot(Ic<U + D - 1>{}), max(u + D - 1, 0), last, wave, lane);
+    fetch_tile<1>(rk, rings.kslot(Ic<U + D>{}), u + D, last, wave, fk);
+    fetch_tile<1>(rv, rings.vslot(Ic<U + D - 1>{}), max(u + D - 1, 0), last, wave, fv);
   };
   float16_t S[2];
   // MFMA phase M(j) at ring position J = j mod kSlots: GEMM2(j-1), GEMM1(j).
@@ -897,7 +977,7 @@ fa2_fwd_pp_kernel(const _Float16* Q, const _Float16* __restrict__ K,
   }
 
   __builtin_amdgcn_s_waitcnt(0);
-  rows.store(O + head_off);
+  rows.store(hp.o, geom.o_sr, hp.lse);
 }
 
 // Q is prescaled by cq = +-min(c, 1) in the kernel; the remaining factor
@@ -913,18 +993,41 @@ struct Scales {
   }
 };
 
+Geom make_geom(const FwdArgs& a) {
+  Geom g;
+  g.q_sb = a.q_sb;
+  g.q_sh = a.q_sh;
+  g.k_sb = a.k_sb;
+  g.k_sh = a.k_sh;
+  g.v_sb = a.v_sb;
+  g.v_sh = a.v_sh;
+  g.o_sb = a.o_sb;
+  g.o_sh = a.o_sh;
+  g.q_sr = a.q_sr;
+  g.k_sr = a.k_sr;
+  g.v_sr = a.v_sr;
+  g.o_sr = a.o_sr;
+  g.heads = a.heads;
+  g.seq_q = a.seq;
+  g.seq_k = a.seq_k;
+  g.coff = a.seq_k - a.seq;
+  g.lse = a.lse;
+  return g;
+}
+
 template <template <bool, bool> class Launcher>
 hipError_t dispatch(const FwdArgs& a, hipStream_t stream, int br) {
   const int nqb = (a.seq + br - 1) / br;
   const dim3 grid((unsigned)(nqb * a.batch_heads));
   const Scales sc(a);
+  const Geom g = make_geom(a);
   hipError_t e;
   if (a.causal) {
-    if (sc.scaled) e = Launcher<true, true>::run(a, grid, nqb, sc.cq, sc.cr, stream);
-    else e = Launcher<true, false>::run(a, grid, nqb, sc.cq, sc.cr, stream);
+    if (sc.scaled) e = Launcher<true, true>::run(a, g, grid, nqb, sc.cq, sc.cr, stream);
+    else e = Launcher<true, false>::run(a, g, grid, nqb, sc.cq, sc.cr, stream);
   } else {
-    if (sc.scaled) e = Launcher<false, true>::run(a, grid, nqb, sc.cq, sc.cr, stream);
-    else e = Launcher<false, false>::run(a, grid, nqb, sc.cq, sc.cr, stream);
+    if (sc.scaled) e = Launcher<false, true>::run(a, g, grid, nqb, sc.cq, sc.cr, stream);
+    else e = Launcher<false, false>::run(a, g, grid, nqb, sc.cq, sc.cr, stream);
   }
   return e != hipSuccess ? e : hipGetLastError();
 }
@@ -933,11 +1036,12 @@ template <int W, int D, int SPLIT>
 struct PipelinedLaunch {
   template <bool C, bool S>
   struct L {
-    static hipError_t run(const FwdArgs& a, dim3 grid, int nqb, float cq, float cr, hipStream_t st) {
+    static hipError_t run(const FwdArgs& a, const Geom& g, dim3 grid, int nqb, float cq, float cr,
+                          hipStream_t st) {
       hipLaunchKernelGGL((fa2_fwd_kernel<W, D, SPLIT, C, S>), grid, dim3(64 * W * SPLIT), 0, st,
                          static_cast<const _Float16*>(a.q), static_cast<const _Float16*>(a.k),
-                         static_cast<const _Float16*>(a.v), static_cast<_Float16*>(a.o), a.seq,
-                         nqb, cq, cr);
+                         static_cast<const _Float16*>(a.v), static_cast<_Float16*>(a.o), g, nqb,
+                         cq, cr);
       return hipSuccess;
     }
   };
@@ -947,11 +1051,12 @@ template <int D>
 struct PingPongLaunch {
   template <bool C, bool S>
   struct L {
-    static hipError_t run(const FwdArgs& a, dim3 grid, int nqb, float cq, float cr, hipStream_t st) {
+    static hipError_t run(const FwdArgs& a, const Geom& g, dim3 grid, int nqb, float cq, float cr,
+                          hipStream_t st) {
       hipLaunchKernelGGL((fa2_fwd_pp_kernel<D, C, S>), grid, dim3(512), 0, st,
                          static_cast<const _Float16*>(a.q), static_cast<const _Float16*>(a.k),
-                         static_cast<const _Float16*>(a.v), static_cast<_Float16*>(a.o), a.seq,
-                         nqb, cq, cr);
+                         static_cast<const _Float16*>(a.v), static_cast<_Float16*>(a.o), g, nqb,
+                         cq, cr);
       return hipSuccess;
     }
   };

@@ -8,18 +8,26 @@
 namespace fl {
 
 // Arguments shared by every forward launch.  Sizes are validated by the
-// C-ABI layer before a launch function sees them.
+// C-ABI layer before a launch function sees them.  Tensors are addressed as
+// [batch][head][row][head_dim] with element strides; head_dim is unit
+// stride.  The contiguous layout has row stride D, head stride N*D and
+// batch stride H*N*D.
 struct FwdArgs {
   const void* q;
   const void* k;
   const void* v;
   void* o;
+  float* lse;        // optional [B, H, N_q] fp32 log-sum-exp (natural log), or null
   int batch_heads;   // B*H
-  int seq;           // N (== N_k)
+  int heads;         // H
+  int seq;           // N_q: query (and output) rows
+  int seq_k;         // N_k: key / value rows
   int head_dim;      // D
   float scale_log2;  // |sm_scale| * log2(e), always > 0
   int negate;        // 1 when sm_scale < 0: the kernel flips the sign of Q
-  int causal;
+  int causal;        // key j visible to query i iff j <= i + (N_k - N_q)
+  int64_t q_sb, q_sh, k_sb, k_sh, v_sb, v_sh, o_sb, o_sh;  // batch / head strides
+  int q_sr, k_sr, v_sr, o_sr;                              // row strides
 };
 
 // One FA2 tile configuration: `waves` waves of 64 lanes, each owning 32

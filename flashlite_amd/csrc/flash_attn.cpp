@@ -131,6 +131,61 @@ torch::Tensor flash_attn_forward_flash2(torch::Tensor q, torch::Tensor k, torch:
   return out_tensor;
 }
 
+// Beyond the reference surface: any [B, H, N, 64] strided views with a
+// unit-stride head dimension (e.g. the transpose of a [B, N, H, 64] tensor),
+// N_k != N_q (bottom-right causal), and optionally the fp32 log-sum-exp
+// [B, H, N_q].  Returns `out`, or (out, lse) with return_lse.  An omitted
+// `out` is allocated with q's layout (empty_like keeps dense strides).
+py::object flash_attn_forward_flash2_ex(torch::Tensor q, torch::Tensor k, torch::Tensor v,
+                                        double sm_scale, bool is_causal,
+                                        std::optional<torch::Tensor> out, bool return_lse) {
+  TORCH_CHECK(q.is_cuda() && k.is_cuda() && v.is_cuda(), "All tensors must be on CUDA");
+  TORCH_CHECK(q.dtype() == torch::kHalf && k.dtype() == torch::kHalf && v.dtype() == torch::kHalf,
+              "All tensors must be FP16 (Half)");
+  TORCH_CHECK(q.dim() == 4 && k.dim() == 4 && v.dim() == 4, "Tensors must be 4D [B, H, N, D]");
+  const int64_t batch_size = q.size(0);
+  const int64_t num_heads = q.size(1);
+  const int64_t head_dim = q.size(3);
+  TORCH_CHECK(k.size(0) == batch_size && k.size(1) == num_heads && k.size(3) == head_dim,
+              "Key dimensions must match Query dimensions [B, H, N_k, D]");
+  TORCH_CHECK(v.size(0) == batch_size && v.size(1) == num_heads && v.size(2) == k.size(2) &&
+                  v.size(3) == head_dim,
+              "Value dimensions must match Key dimensions [B, H, N_k, D]");
+  TORCH_CHECK(head_dim == 64, "FlashLite WMMA kernel currently requires head_dim == 64");
+  TORCH_CHECK(q.stride(3) == 1 && k.stride(3) == 1 && v.stride(3) == 1,
+              "The head dimension must have unit stride");
+  check_same_device(q, k, v);
+
+  torch::Tensor out_tensor;
+  if (out.has_value() && out.value().defined()) {
+    out_tensor = out.value();
+    TORCH_CHECK(out_tensor.is_cuda() && out_tensor.stride(3) == 1,
+                "out tensor must be a CUDA tensor with a unit-stride head dimension");
+    TORCH_CHECK(out_tensor.sizes() == q.sizes(), "out tensor shape must match q");
+    TORCH_CHECK(out_tensor.dtype() == torch::kHalf, "out tensor dtype must be FP16");
+    TORCH_CHECK(out_tensor.device() == q.device(), "out tensor must be on the same device as q");
+  } else {
+    out_tensor = torch::empty_like(q);
+  }
+  torch::Tensor lse;
+  if (return_lse)
+    lse = torch::empty({batch_size, num_heads, q.size(2)},
+                       q.options().dtype(torch::kFloat32).memory_format(torch::MemoryFormat::Contiguous));
+
+  const c10::hip::HIPGuardMasqueradingAsCUDA guard(q.device());
+  fl_attn_params_ex p;
+  p.base = make_params(q, k, v, out_tensor, sm_scale, is_causal);
+  const torch::Tensor* ts[4] = {&q, &k, &v, &out_tensor};
+  int64_t* st[4] = {p.q_stride, p.k_stride, p.v_stride, p.o_stride};
+  for (int i = 0; i < 4; ++i)
+    for (int d = 0; d < 3; ++d) st[i][d] = ts[i]->stride(d);
+  p.lse = return_lse ? lse.data_ptr<float>() : nullptr;
+  const int rc = fl_attn_fwd_f16_ex(&p, -1, current_stream(q));
+  TORCH_CHECK(rc == FL_OK, "FlashLite HIP error: ", fl_attn_last_error());
+  if (return_lse) return py::make_tuple(out_tensor, lse);
+  return py::cast(out_tensor);
+}
+
 }  // namespace flash_attn
 
 PYBIND11_MODULE(flash_attn_wmma, m) {
@@ -143,4 +198,10 @@ PYBIND11_MODULE(flash_attn_wmma, m) {
   m.def("forward_flash2", &flash_attn::flash_attn_forward_flash2,
         "FlashAttention-2 forward (gfx950 MFMA)", py::arg("q"), py::arg("k"), py::arg("v"),
         py::arg("sm_scale") = 0.0, py::arg("is_causal") = false, py::arg("out") = py::none());
+
+  m.def("forward_flash2_ex", &flash_attn::flash_attn_forward_flash2_ex,
+        "FlashAttention-2 forward on strided [B, H, N, 64] views, N_k != N_q (bottom-right "
+        "causal), optional log-sum-exp",
+        py::arg("q"), py::arg("k"), py::arg("v"), py::arg("sm_scale") = 0.0,
+        py::arg("is_causal") = false, py::arg("out") = py::none(), py::arg("return_lse") = false);
 }

@@ -13,6 +13,10 @@
 //   * the P.V product splits keys over the 4 waves and head-dim over lanes,
 //     and the four partial rows are added through LDS.
 // Any head_dim >= 1 is accepted (the reference has no restriction either).
+// N_k may differ from N_q (the reference indexes K and V with N_q's head
+// stride, kernel_naive.cu:148, :270); the causal diagonal is then aligned bottom-right
+// (key j visible to query i iff j <= i + N_k - N_q) and a row with no
+// visible key returns 0.
 
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -40,14 +44,14 @@ __device__ __forceinline__ float wave_sum(float x) {
   return x;
 }
 
-// LDS layout (floats): scores[N] | part[kWaves][D] | qrow[D] | red[2*kWaves]
+// LDS layout (floats): scores[N_k] | part[kWaves][D] | qrow[D] | red[2*kWaves]
 __global__ void __launch_bounds__(kThreads)
 naive_fwd_kernel(const _Float16* __restrict__ Q, const _Float16* __restrict__ K,
-                 const _Float16* __restrict__ V, _Float16* __restrict__ O, int seq, int dim,
-                 float c, int causal) {
+                 const _Float16* __restrict__ V, _Float16* __restrict__ O, int seq_q,
+                 int seq_k, int dim, float c, int causal) {
   extern __shared__ float smem[];
   float* scores = smem;
-  float* part = scores + seq;
+  float* part = scores + seq_k;
   float* qrow = part + kWaves * dim;
   float* red = qrow + dim;
 
@@ -57,17 +61,18 @@ naive_fwd_kernel(const _Float16* __restrict__ Q, const _Float16* __restrict__ K,
   const int lane = tid & 63;
   const int wave = tid >> 6;
 
-  const size_t head_off = (size_t)bh * (size_t)seq * (size_t)dim;
-  const _Float16* qp = Q + head_off + (size_t)qi * dim;
-  const _Float16* Kh = K + head_off;
-  const _Float16* Vh = V + head_off;
-  _Float16* op = O + head_off + (size_t)qi * dim;
+  const size_t q_off = (size_t)bh * (size_t)seq_q * (size_t)dim;
+  const size_t kv_off = (size_t)bh * (size_t)seq_k * (size_t)dim;
+  const _Float16* qp = Q + q_off + (size_t)qi * dim;
+  const _Float16* Kh = K + kv_off;
+  const _Float16* Vh = V + kv_off;
+  _Float16* op = O + q_off + (size_t)qi * dim;
 
   for (int d = tid; d < dim; d += kThreads) qrow[d] = (float)qp[d];
   __syncthreads();
 
   // 1. scores in log2 units; keys past the causal limit are never scored
-  const int nvis = causal ? qi + 1 : seq;
+  const int nvis = causal ? min(max(qi + 1 + seq_k - seq_q, 0), seq_k) : seq_k;
   float tmax = -__builtin_huge_valf();
   for (int j = tid; j < nvis; j += kThreads) {
     const _Float16* kr = Kh + (size_t)j * dim;
@@ -133,7 +138,7 @@ int64_t naive_max_seq(int64_t head_dim) {
 
 hipError_t launch_naive(const FwdArgs& a, hipStream_t stream) {
   const dim3 grid((unsigned)a.seq, (unsigned)a.batch_heads);
-  const size_t lds = naive_lds_bytes(a.seq, a.head_dim);
+  const size_t lds = naive_lds_bytes(a.seq_k, a.head_dim);
   // Dynamic LDS above 64 KiB needs the per-function limit raised once.
   static std::once_flag raised;
   static hipError_t raise_err = hipSuccess;
@@ -145,7 +150,7 @@ hipError_t launch_naive(const FwdArgs& a, hipStream_t stream) {
   hipLaunchKernelGGL(naive_fwd_kernel, grid, dim3(kThreads), lds, stream,
                      static_cast<const _Float16*>(a.q), static_cast<const _Float16*>(a.k),
                      static_cast<const _Float16*>(a.v), static_cast<_Float16*>(a.o), a.seq,
-                     a.head_dim, a.negate ? -a.scale_log2 : a.scale_log2, a.causal);
+                     a.seq_k, a.head_dim, a.negate ? -a.scale_log2 : a.scale_log2, a.causal);
   return hipGetLastError();
 }
 

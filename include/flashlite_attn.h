@@ -15,7 +15,9 @@
  * in the binding (flashlite_amd/csrc/flash_attn.cpp) with the reference's
  * messages; the checks below are the ones a raw-pointer caller needs.
  *
- * Layout: q, k, v, o are fp16 [batch, heads, seq, head_dim], contiguous.
+ * Layout: q, o are fp16 [batch, heads, seq_q, head_dim] and k, v fp16
+ * [batch, heads, seq_k, head_dim], contiguous (fl_attn_fwd_f16_ex takes
+ * strides).
  * The library allocates nothing, never synchronises, keeps no mutable global
  * state and may be called from several host threads at once.  Launches are
  * asynchronous on `stream`; results are visible after the stream reaches
@@ -35,24 +37,25 @@ extern "C" {
 enum fl_status {
   FL_OK = 0,
   FL_ERR_INVALID_ARGUMENT = 1, /* NULL pointer, negative size, non-finite scale */
-  FL_ERR_UNSUPPORTED = 2,      /* head_dim != 64 (flash2), seq_k != seq_q, sizes past limits */
+  FL_ERR_UNSUPPORTED = 2,      /* head_dim != 64 (flash2), strides or sizes past limits */
   FL_ERR_MISALIGNED = 3,       /* flash2 needs 16-byte aligned q/k/v/o */
   FL_ERR_LAUNCH = 4,           /* the HIP launch itself failed */
   FL_ERR_BAD_CONFIG = 5        /* forced tile configuration out of range */
 };
 
 typedef struct fl_attn_params {
-  const void* q;      /* fp16 [B, H, N, D] */
-  const void* k;      /* fp16 [B, H, N, D] */
-  const void* v;      /* fp16 [B, H, N, D] */
+  const void* q;      /* fp16 [B, H, N, D]; N = seq_q */
+  const void* k;      /* fp16 [B, H, N_k, D] */
+  const void* v;      /* fp16 [B, H, N_k, D] */
   void* o;            /* fp16 [B, H, N, D], written for rows < N */
   int64_t batch;      /* B */
   int64_t heads;      /* H */
   int64_t seq_q;      /* N (query rows) */
-  int64_t seq_k;      /* key/value rows; must equal seq_q */
+  int64_t seq_k;      /* N_k key/value rows (k, v are [B, H, N_k, D]); may differ from N */
   int64_t head_dim;   /* D */
   double sm_scale;    /* 0.0 means 1/sqrt(D) (kernel_flash2.cu:769-771) */
-  int32_t causal;     /* non-zero: key j visible to query i iff j <= i */
+  int32_t causal;     /* non-zero: key j visible to query i iff j <= i + N_k - N (bottom-right
+                         aligned; top-left when N_k == N); a row with no visible key gets 0 */
 } fl_attn_params;
 
 /*
@@ -71,6 +74,38 @@ int fl_attn_fwd_f16(const fl_attn_params* p, void* stream);
  * every configuration against the oracle.
  */
 int fl_attn_fwd_f16_cfg(const fl_attn_params* p, int32_t config, void* stream);
+
+/*
+ * Strided layouts and the log-sum-exp output.  `base` carries the pointers,
+ * sizes, scale and mask exactly as for fl_attn_fwd_f16 (its layout comment
+ * aside); the strides below replace the contiguous [B, H, N, D] layout.
+ * Each stride triple is {batch, head, row} in elements; head_dim is unit
+ * stride.  A [B, N, H, D] tensor (the layout of the `flash_attn` package,
+ * which the reference's benchmark builds by transposing,
+ * benchmarks/benchmark_throughput.py:110-112) has strides
+ * {N*H*D, D, H*D}.  Strides are non-negative multiples of 8 elements, row
+ * strides in [64, 2^30); K and V rows must lie within 2^31 bytes of their
+ * head's first row.  Output rows must not overlap each other or q, k, v
+ * (o == q with equal strides is allowed, as for fl_attn_fwd_f16).
+ *
+ * lse: optional fp32 [B, H, N] (contiguous), written with each query row's
+ * ln(sum_j exp(sm_scale * q.k_j)) over its visible keys, -inf for a row
+ * with no visible key; NULL to skip.
+ *
+ * No counterpart in the reference, which accepts only contiguous
+ * [B, H, N, 64] tensors (csrc/kernel_flash2.cu:741-757) and returns no
+ * log-sum-exp; `config` as for fl_attn_fwd_f16_cfg.
+ */
+typedef struct fl_attn_params_ex {
+  fl_attn_params base;
+  int64_t q_stride[3];
+  int64_t k_stride[3];
+  int64_t v_stride[3];
+  int64_t o_stride[3];
+  float* lse;
+} fl_attn_params_ex;
+
+int fl_attn_fwd_f16_ex(const fl_attn_params_ex* p, int32_t config, void* stream);
 
 /*
  * Un-fused baseline: one work-group per query row, scores staged in LDS.

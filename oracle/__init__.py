@@ -18,6 +18,8 @@ from .attention import (  # noqa: F401
     attention_flops,
     attention_fp32,
     attention_fp64,
+    attention_lse,
+    causal_visible,
     error_stats,
     resolve_sm_scale,
     sm_scale_log2,

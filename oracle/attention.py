@@ -18,6 +18,18 @@ What it restates (reference = thebigblender/FlashLite, files under
   ``kernel_flash2.cu:299-309``), so a row's weights are a softmax over its
   visible keys only.  Every row has at least one visible key when
   ``N_q == N_k`` (key 0), so no row is fully masked.
+* N_k != N_q (not supported by the reference, which indexes K and V with
+  N_q, ``kernel_flash2.cu:84, :425``): keys are K's own rows, and the causal
+  diagonal is aligned bottom-right -- key ``j`` visible to query ``i`` iff
+  ``j <= i + N_k - N_q`` (the convention of PyTorch's ``causal_lower_right``
+  and of the ``flash_attn`` package).  A query row with no visible key
+  returns 0, which is the reference's fully-masked-row rule
+  (``inv_l = l > 0 ? 1/l : 0``, ``kernel_flash2.cu:364-365``).
+* ``attention_lse`` -- each row's log-sum-exp ``ln sum_j exp(s_ij)`` over
+  its visible keys (``-inf`` for a row with none): the quantity a flash
+  kernel's (m, l) state encodes, ``m * ln 2 + ln l`` in the reference's
+  base-2 units (``kernel_flash2.cu:251-254, :339``); the reference itself
+  does not return it.
 * ``resolve_sm_scale`` -- the ``sm_scale == 0.0`` sentinel meaning
   ``1/sqrt(D)`` computed in float32 (``kernel_flash2.cu:769-771``,
   ``kernel_naive.cu:278-280``) and the base-2 prescale
@@ -67,9 +79,19 @@ def sm_scale_log2(sm_scale: float) -> np.float32:
 
 
 def _softmax_rows(s: np.ndarray) -> np.ndarray:
+    """Row softmax; a row of only -inf (no visible key) gives zeros."""
     m = np.max(s, axis=-1, keepdims=True)
+    m = np.where(np.isfinite(m), m, 0.0).astype(s.dtype)
     p = np.exp(s - m)
-    return p / np.sum(p, axis=-1, keepdims=True)
+    tot = np.sum(p, axis=-1, keepdims=True)
+    return p / np.where(tot > 0, tot, 1.0).astype(s.dtype)
+
+
+def causal_visible(rows, nq: int, nk: int) -> np.ndarray:
+    """Boolean [len(rows), nk]: key j visible to query i iff j <= i + nk - nq
+    (top-left when nk == nq)."""
+    rows = np.asarray(rows, dtype=np.int64)
+    return np.arange(nk)[None, :] <= rows[:, None] + (nk - nq)
 
 
 def _attention(q, k, v, sm_scale, causal, dtype, row_chunk, rows):
@@ -79,20 +101,17 @@ def _attention(q, k, v, sm_scale, causal, dtype, row_chunk, rows):
     nk = k.shape[2]
     if k.shape != (b, h, nk, d) or v.shape != (b, h, nk, d):
         raise ValueError("k and v must be [B, H, N_k, D] matching q")
-    if causal and nq != nk:
-        raise ValueError("causal oracle requires N_q == N_k (top-left mask)")
     rows = np.arange(nq) if rows is None else np.asarray(rows, dtype=np.int64)
     scale = dtype(resolve_sm_scale(sm_scale, d))
     out = np.empty((b, h, len(rows), d), dtype=dtype)
     kt = np.swapaxes(k.astype(dtype), -1, -2)  # [B, H, D, N_k]
     vv = v.astype(dtype)
-    cols = np.arange(nk)
     for c0 in range(0, len(rows), row_chunk):
         sel = rows[c0:c0 + row_chunk]
         qq = q[:, :, sel, :].astype(dtype)
         s = np.matmul(qq, kt) * scale  # [B, H, rows, N_k]
         if causal:
-            s = np.where(cols[None, :] <= sel[:, None], s, dtype(-np.inf))
+            s = np.where(causal_visible(sel, nq, nk), s, dtype(-np.inf))
         p = _softmax_rows(s)
         out[:, :, c0:c0 + len(sel), :] = np.matmul(p, vv)
     return out
@@ -125,6 +144,22 @@ def attention_fp64(q, k, v, sm_scale=0.0, causal=False, rows=None, row_chunk=Non
     return _attention(q, k, v, sm_scale, causal, np.float64, row_chunk, rows)
 
 
+def attention_lse(q, k, sm_scale=0.0, causal=False, dtype=np.float64):
+    """Per-row log-sum-exp [B, H, N_q] of the scaled (and masked) scores,
+    natural log; -inf for a row with no visible key."""
+    b, h, nq, d = q.shape
+    nk = k.shape[2]
+    scale = dtype(resolve_sm_scale(sm_scale, d))
+    s = np.matmul(q.astype(dtype), np.swapaxes(k.astype(dtype), -1, -2)) * scale
+    if causal:
+        s = np.where(causal_visible(np.arange(nq), nq, nk), s, dtype(-np.inf))
+    m = np.max(s, axis=-1)
+    mf = np.where(np.isfinite(m), m, 0.0)
+    tot = np.sum(np.exp(s - mf[..., None]), axis=-1)
+    with np.errstate(divide="ignore"):
+        return np.where(tot > 0, mf + np.log(tot), -np.inf)
+
+
 def attention_bruteforce(q, k, v, sm_scale=0.0, causal=False):
     """Scalar float64 loops, one query at a time (tiny shapes only).
 
@@ -142,7 +177,9 @@ def attention_bruteforce(q, k, v, sm_scale=0.0, causal=False):
     for bi in range(b):
         for hi in range(h):
             for i in range(nq):
-                visible = range(i + 1) if causal else range(nk)
+                visible = range(max(0, min(nk, i + 1 + nk - nq))) if causal else range(nk)
+                if len(visible) == 0:
+                    continue  # no visible key: the row stays 0
                 logits = []
                 for j in visible:
                     dot = 0.0

@@ -54,10 +54,61 @@ def test_head_dim_must_be_64_for_flash2():
     assert capi.last_error() == "FlashLite WMMA kernel currently requires head_dim == 64"
 
 
-def test_seq_k_must_equal_seq_q():
-    assert capi.fwd(_p(seq_k=100)) == capi.FL_ERR_UNSUPPORTED
+def test_seq_k_may_differ_from_seq_q():
+    # validated (no launch): the dispatcher picks a configuration
+    assert capi.select_config(_p(seq_k=100)) >= 0
+    assert capi.select_config(_p(seq_q=1, seq_k=4096, causal=True)) >= 0
+    # the key-side limits are checked on N_k
+    assert capi.select_config(_p(seq_q=16, seq_k=1 << 24)) == -1
     assert "N_k" in capi.last_error()
-    assert capi.naive(_p(seq_k=100)) == capi.FL_ERR_UNSUPPORTED
+    assert capi.naive(_p(seq_q=16, seq_k=1 << 20)) == capi.FL_ERR_UNSUPPORTED
+    assert "N_k" in capi.last_error()
+
+
+def _ex(q_stride=(8 * 4096 * 64, 4096 * 64, 64), k_stride=None, v_stride=None, o_stride=None,
+        lse=0, **kw):
+    c = (8 * 4096 * 64, 4096 * 64, 64)
+    return capi.make_params_ex(_p(**kw), q_stride, k_stride or c, v_stride or c, o_stride or c,
+                               lse)
+
+
+def test_ex_null_and_config():
+    lib = capi.load()
+    assert lib.fl_attn_fwd_f16_ex(None, -1, None) == capi.FL_ERR_INVALID_ARGUMENT
+    assert capi.fwd_ex(_ex(), config=6) == capi.FL_ERR_BAD_CONFIG
+    assert capi.fwd_ex(_ex(head_dim=128)) == capi.FL_ERR_UNSUPPORTED
+
+
+def test_ex_stride_checks():
+    # not a multiple of 8 elements (rows would lose 16-byte alignment)
+    assert capi.fwd_ex(_ex(q_stride=(8 * 4096 * 64, 4096 * 64, 68))) == capi.FL_ERR_UNSUPPORTED
+    assert "multiples of 8" in capi.last_error()
+    assert capi.fwd_ex(_ex(k_stride=(4, 4096 * 64, 64))) == capi.FL_ERR_UNSUPPORTED
+    # rows closer than D
+    assert capi.fwd_ex(_ex(o_stride=(0, 0, 32))) == capi.FL_ERR_UNSUPPORTED
+    assert "row stride" in capi.last_error()
+    assert capi.fwd_ex(_ex(v_stride=(-64, 64, 64))) == capi.FL_ERR_UNSUPPORTED
+    # [B, N, H, D] strides are fine; K/V rows must stay within 2^31 bytes of the head
+    bnhd = (4096 * 8 * 64, 64, 8 * 64)
+    big = (1 << 40, 64, 1 << 16)
+    assert capi.fwd_ex(_ex(k_stride=big, batch=1, heads=1, seq_q=1 << 14)) == capi.FL_ERR_UNSUPPORTED
+    assert "addressing limit" in capi.last_error()
+    assert capi.fwd_ex(_ex(q_stride=bnhd, k_stride=bnhd, v_stride=bnhd, o_stride=bnhd,
+                           o=0)) == capi.FL_ERR_INVALID_ARGUMENT  # got past the stride checks
+    assert "non-NULL" in capi.last_error()
+
+
+def test_ex_no_keys_ignores_kv_strides_and_pointers():
+    # N_k = 0: k and v are never read, so neither their strides nor NULL
+    # pointers are errors (o = NULL still is, and shows the checks got there)
+    p = _ex(k_stride=(0, 0, 0), v_stride=(0, 0, 0), seq_k=0, k=0, v=0, o=0)
+    assert capi.fwd_ex(p) == capi.FL_ERR_INVALID_ARGUMENT
+    assert "non-NULL" in capi.last_error()
+
+
+def test_ex_lse_alignment():
+    assert capi.fwd_ex(_ex(lse=A + 2)) == capi.FL_ERR_MISALIGNED
+    assert "lse" in capi.last_error()
 
 
 def test_sequence_addressing_limit():
@@ -131,12 +182,12 @@ def test_error_message_is_thread_local(fn):
     seen = {}
 
     def worker():
-        getattr(capi, fn)(_p(seq_k=3))
+        getattr(capi, fn)(_p(batch=-1))
         seen["msg"] = capi.last_error()
 
     capi.fwd(_p(head_dim=128))
     t = threading.Thread(target=worker)
     t.start()
     t.join()
-    assert "N_k" in seen["msg"]
+    assert "non-negative" in seen["msg"]
     assert capi.last_error() == "FlashLite WMMA kernel currently requires head_dim == 64"

@@ -14,7 +14,8 @@ import pytest
 
 from flashlite_amd.workloads import WORKLOADS, digest, make_qkv, workload_inputs
 from oracle import (attention_bruteforce, attention_bytes, attention_flops, attention_fp32,
-                    attention_fp64, error_stats, resolve_sm_scale, sm_scale_log2)
+                    attention_fp64, attention_lse, causal_visible, error_stats, resolve_sm_scale,
+                    sm_scale_log2)
 
 GOLDEN = os.path.join(os.path.dirname(__file__), "golden")
 
@@ -186,3 +187,93 @@ def test_work_formulas():
     assert attention_flops(2, 8, 4096, 64, False) == 4 * 2 * 8 * 4096 ** 2 * 64
     assert attention_flops(2, 8, 4096, 64, True) == 2 * 2 * 8 * 4096 ** 2 * 64
     assert attention_bytes(2, 8, 4096, 64) == 32 * 2 ** 20
+
+
+# --- N_k != N_q (bottom-right causal) and the log-sum-exp --------------------
+
+def _qkv2(b, h, nq, nk, d, seed):
+    rs = np.random.RandomState(seed)
+    mk = lambda n: rs.standard_normal((b, h, n, d)).astype(np.float32).astype(np.float16)
+    return mk(nq), mk(nk), mk(nk)
+
+
+@pytest.mark.parametrize("nq,nk", [(1, 5), (3, 7), (7, 3), (5, 1), (4, 4), (2, 9)])
+@pytest.mark.parametrize("causal", [False, True])
+def test_rectangular_matches_bruteforce(nq, nk, causal):
+    q, k, v = _qkv2(1, 2, nq, nk, 8, seed=40 + nq * 10 + nk)
+    ref = attention_bruteforce(q, k, v, 0.37, causal)
+    assert error_stats(attention_fp64(q, k, v, 0.37, causal), ref)[0] < 1e-12
+    assert error_stats(attention_fp32(q, k, v, 0.37, causal), ref)[0] < 2e-6
+
+
+@pytest.mark.parametrize("nq,nk", [(37, 100), (100, 37), (64, 200), (1, 130)])
+def test_rectangular_causal_matches_torch_lower_right(nq, nk):
+    """Bottom-right alignment pinned by PyTorch's own causal_lower_right
+    bias (a library routine, independent of this oracle's mask code)."""
+    import torch
+    import torch.nn.functional as F
+    from torch.nn.attention.bias import causal_lower_right
+
+    q, k, v = _qkv2(2, 3, nq, nk, 64, seed=nq + nk)
+    tq, tk, tv = (torch.from_numpy(x.astype(np.float64)) for x in (q, k, v))
+    if nq <= nk:
+        ref = F.scaled_dot_product_attention(tq, tk, tv, attn_mask=causal_lower_right(nq, nk),
+                                             scale=0.125).numpy()
+        assert error_stats(attention_fp64(q, k, v, 0.125, True), ref)[0] < 1e-12
+    else:
+        # rows with no visible key: torch yields NaN there, the reference's rule 0
+        ref = F.scaled_dot_product_attention(tq, tk, tv, attn_mask=causal_lower_right(nq, nk),
+                                             scale=0.125).numpy()
+        out = attention_fp64(q, k, v, 0.125, True)
+        empty = nq - nk
+        assert np.all(out[:, :, :empty, :] == 0.0)
+        assert error_stats(out[:, :, empty:, :], ref[:, :, empty:, :])[0] < 1e-12
+
+
+def test_rectangular_closed_forms():
+    q, _, v = _qkv2(1, 2, 6, 10, 8, seed=50)
+    k = np.ones((1, 2, 10, 8), np.float16)
+    # constant keys: query i averages V[0 .. i + (10 - 6)]
+    c = attention_fp64(q, k, v, 0.7, True)
+    vf = v.astype(np.float64)
+    for i in range(6):
+        assert np.allclose(c[:, :, i, :], vf[:, :, :i + 5, :].mean(axis=2), atol=1e-12)
+    # the last query row sees every key: equals the non-causal last row
+    q, k, v = _qkv2(1, 2, 6, 10, 8, seed=51)
+    assert np.array_equal(attention_fp64(q, k, v, 0.3, True)[:, :, -1],
+                          attention_fp64(q, k, v, 0.3, False)[:, :, -1])
+    # more queries than keys: the first nq - nk rows see nothing and are 0
+    q, k, v = _qkv2(1, 1, 9, 4, 8, seed=52)
+    out = attention_fp64(q, k, v, 0.3, True)
+    assert np.all(out[:, :, :5] == 0.0) and np.all(np.abs(out[:, :, 5:]).sum(-1) > 0)
+    assert np.all(causal_visible(np.arange(9), 9, 4).sum(1) == [0, 0, 0, 0, 0, 1, 2, 3, 4])
+
+
+def test_lse_closed_forms():
+    q, _, _ = _qkv2(1, 2, 7, 11, 16, seed=53)
+    zero_k = np.zeros((1, 2, 11, 16), np.float16)
+    # all scores 0: lse = ln(#visible keys)
+    assert np.allclose(attention_lse(q, zero_k, 0.5, False), math.log(11), atol=1e-15)
+    vis = causal_visible(np.arange(7), 7, 11).sum(1)
+    assert np.allclose(attention_lse(q, zero_k, 0.5, True), np.log(vis)[None, None, :],
+                       atol=1e-15)
+    # a row with no visible key: -inf
+    lse = attention_lse(*_qkv2(1, 1, 5, 2, 8, seed=54)[:2], 0.5, True)
+    assert np.all(np.isneginf(lse[..., :3])) and np.all(np.isfinite(lse[..., 3:]))
+
+
+def test_lse_matches_torch_logsumexp_and_reproduces_output():
+    import torch
+
+    q, k, v = _qkv2(2, 2, 40, 70, 32, seed=55)
+    scale = 0.21
+    s = torch.from_numpy(q.astype(np.float64)) @ torch.from_numpy(k.astype(np.float64)).transpose(-1, -2)
+    s = s * scale
+    mask = torch.from_numpy(causal_visible(np.arange(40), 40, 70))
+    ref = torch.logsumexp(s.masked_fill(~mask, float("-inf")), dim=-1).numpy()
+    lse = attention_lse(q, k, scale, True)
+    assert np.allclose(lse, ref, atol=1e-12)
+    # softmax weights exp(s - lse) reproduce the oracle's output
+    w = np.where(mask.numpy(), np.exp(s.numpy() - lse[..., None]), 0.0)
+    assert np.allclose(w.sum(-1), 1.0, atol=1e-12)
+    assert np.allclose(w @ v.astype(np.float64), attention_fp64(q, k, v, scale, True), atol=1e-12)
