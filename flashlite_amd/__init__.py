@@ -33,6 +33,8 @@ forward_naive = _ext.forward_naive
 # Beyond the reference surface: strided [B, H, N, 64] views (a [B, N, H, 64]
 # tensor passes as x.transpose(1, 2)), N_k != N_q with the causal diagonal
 # aligned bottom-right, and the fp32 log-sum-exp with return_lse=True.
+# num_splits / workspace select split-KV for few query rows over many keys.
 forward_flash2_ex = _ext.forward_flash2_ex
+splitkv_workspace_bytes = _ext.splitkv_workspace_bytes
 
-__all__ = ["forward_flash2", "forward_naive", "forward_flash2_ex"]
+__all__ = ["forward_flash2", "forward_naive", "forward_flash2_ex", "splitkv_workspace_bytes"]

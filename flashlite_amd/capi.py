@@ -30,6 +30,8 @@ EXPORTED = (
     "fl_attn_config_name",
     "fl_attn_select_config",
     "fl_attn_fwd_f16_ex",
+    "fl_attn_splitkv_workspace_bytes",
+    "fl_attn_fwd_f16_splitkv",
 )
 
 
@@ -99,6 +101,11 @@ def load(path: str = LIB_PATH) -> ctypes.CDLL:
     lib.fl_attn_fwd_f16_ex.argtypes = [ctypes.POINTER(FlAttnParamsEx), ctypes.c_int32,
                                        ctypes.c_void_p]
     lib.fl_attn_fwd_f16_ex.restype = ctypes.c_int
+    lib.fl_attn_splitkv_workspace_bytes.argtypes = [ctypes.POINTER(FlAttnParamsEx), ctypes.c_int32]
+    lib.fl_attn_splitkv_workspace_bytes.restype = ctypes.c_int64
+    lib.fl_attn_fwd_f16_splitkv.argtypes = [ctypes.POINTER(FlAttnParamsEx), ctypes.c_int32,
+                                            ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p]
+    lib.fl_attn_fwd_f16_splitkv.restype = ctypes.c_int
     _lib = lib
     return lib
 
@@ -129,6 +136,18 @@ def fwd(params: FlAttnParams, stream: int = 0, config: int = -1) -> int:
 def fwd_ex(params: FlAttnParamsEx, stream: int = 0, config: int = -1) -> int:
     """``fl_attn_fwd_f16_ex``; returns the status code."""
     return load().fl_attn_fwd_f16_ex(ctypes.byref(params), config, stream or None)
+
+
+def splitkv_workspace_bytes(params: FlAttnParamsEx, num_splits: int = 0) -> int:
+    """``fl_attn_splitkv_workspace_bytes``: 0 = no split, -1 = rejected."""
+    return load().fl_attn_splitkv_workspace_bytes(ctypes.byref(params), num_splits)
+
+
+def fwd_splitkv(params: FlAttnParamsEx, workspace: int, workspace_bytes: int, stream: int = 0,
+                num_splits: int = 0) -> int:
+    """``fl_attn_fwd_f16_splitkv``; returns the status code."""
+    return load().fl_attn_fwd_f16_splitkv(ctypes.byref(params), num_splits, workspace or None,
+                                          workspace_bytes, stream or None)
 
 
 def make_params_ex(base: FlAttnParams, q_stride, k_stride, v_stride, o_stride,

@@ -11,6 +11,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
@@ -152,6 +153,79 @@ int check_strides(const int64_t st[3], const char* name, const char* who) {
   return FL_OK;
 }
 
+// Checks of an fl_attn_params_ex and its strides; fills `a`.
+int check_ex(const fl_attn_params_ex* p, fl::FwdArgs* a, const char* who) {
+  if (p == nullptr) return fail(FL_ERR_INVALID_ARGUMENT, "%s: params is NULL", who);
+  int rc = check_fa2(&p->base, a, who);
+  if (rc != FL_OK) return rc;
+  const int64_t* st[4] = {p->q_stride, p->k_stride, p->v_stride, p->o_stride};
+  const char* names[4] = {"q", "k", "v", "o"};
+  const bool no_keys = a->seq_k == 0;  // k and v are never read
+  for (int i = 0; i < 4; ++i) {
+    if (no_keys && (i == 1 || i == 2)) continue;
+    rc = check_strides(st[i], names[i], who);
+    if (rc != FL_OK) return rc;
+  }
+  for (int i = 1; i <= 2; ++i)
+    if ((a->seq_k + 128LL) * st[i][2] * 2 > INT32_MAX)
+      return fail(FL_ERR_UNSUPPORTED, "%s: N_k=%d rows of stride %lld exceed the per-head "
+                  "addressing limit of %s (2^31 bytes)", who, a->seq_k, (long long)st[i][2],
+                  names[i]);
+  if ((uintptr_t)p->lse & 3) return fail(FL_ERR_MISALIGNED, "%s: lse must be 4-byte aligned", who);
+  a->q_sb = p->q_stride[0];
+  a->q_sh = p->q_stride[1];
+  a->q_sr = (int)p->q_stride[2];
+  if (!no_keys) {
+    a->k_sb = p->k_stride[0];
+    a->k_sh = p->k_stride[1];
+    a->k_sr = (int)p->k_stride[2];
+    a->v_sb = p->v_stride[0];
+    a->v_sh = p->v_stride[1];
+    a->v_sr = (int)p->v_stride[2];
+  }
+  a->o_sb = p->o_stride[0];
+  a->o_sh = p->o_stride[1];
+  a->o_sr = (int)p->o_stride[2];
+  a->lse = p->lse;
+  return FL_OK;
+}
+
+// Split-KV plan: waves per work-group by N_q (32 query rows each), number
+// of key chunks, workspace bytes.  nsplit == 0 means "do not split".
+// The library's choice (requested <= 0) splits only when the one-pass grid
+// leaves most SIMDs idle (fewer than 1024 waves) and every chunk keeps at
+// least 2 key tiles; it then aims at about 2048 waves.
+struct KvPlan {
+  int waves, nsplit;
+  int64_t bytes;
+};
+constexpr int kMaxSplits = 256;
+constexpr int64_t kPartFloats = 68;  // per row: O[64], m, l, 2 pad
+
+KvPlan plan_kvsplit(const fl::FwdArgs& a, int32_t requested) {
+  KvPlan p;
+  p.waves = a.seq <= 32 ? 1 : (a.seq <= 64 ? 2 : 4);
+  const int64_t nqb = (a.seq + 32 * p.waves - 1) / (32 * p.waves);
+  const int64_t tiles = std::max<int64_t>(1, (a.seq_k + 63) / 64);
+  const int64_t waves = nqb * a.batch_heads * p.waves;
+  int64_t n;
+  if (requested > 0) {
+    n = std::min<int64_t>({(int64_t)requested, tiles, kMaxSplits});
+  } else if (waves >= 1024 || tiles < 4) {
+    n = 0;
+  } else {
+    n = std::min<int64_t>({(2048 + waves - 1) / waves, tiles / 2, kMaxSplits});
+    if (n < 2) n = 0;
+  }
+  // the chunk kernel's grid (64 * waves lanes per group) must stay below 2^32 lanes
+  const int64_t grid_cap = ((int64_t)UINT32_MAX / (64 * p.waves)) / (nqb * a.batch_heads);
+  n = std::min(n, grid_cap);
+  if (n < 1) n = 0;
+  p.nsplit = (int)n;
+  p.bytes = n * (int64_t)a.batch_heads * a.seq * kPartFloats * (int64_t)sizeof(float);
+  return p;
+}
+
 }  // namespace
 
 extern "C" {
@@ -194,48 +268,51 @@ int fl_attn_fwd_f16(const fl_attn_params* p, void* stream) {
 
 int fl_attn_fwd_f16_ex(const fl_attn_params_ex* p, int32_t config, void* stream) {
   const char* who = "fl_attn_fwd_f16_ex";
-  if (p == nullptr) return fail(FL_ERR_INVALID_ARGUMENT, "%s: params is NULL", who);
   fl::FwdArgs a;
-  int rc = check_fa2(&p->base, &a, who);
+  int rc = check_ex(p, &a, who);
   if (rc != FL_OK) return rc;
   if (config < -1 || config >= fl::kNumFa2Configs)
     return fail(FL_ERR_BAD_CONFIG, "%s: config %d out of range [-1, %d)", who, (int)config,
                 fl::kNumFa2Configs);
-  const int64_t* st[4] = {p->q_stride, p->k_stride, p->v_stride, p->o_stride};
-  const char* names[4] = {"q", "k", "v", "o"};
-  const bool no_keys = a.seq_k == 0;  // k and v are never read
-  for (int i = 0; i < 4; ++i) {
-    if (no_keys && (i == 1 || i == 2)) continue;
-    rc = check_strides(st[i], names[i], who);
-    if (rc != FL_OK) return rc;
-  }
-  for (int i = 1; i <= 2; ++i)
-    if ((a.seq_k + 128LL) * st[i][2] * 2 > INT32_MAX)
-      return fail(FL_ERR_UNSUPPORTED, "%s: N_k=%d rows of stride %lld exceed the per-head "
-                  "addressing limit of %s (2^31 bytes)", who, a.seq_k, (long long)st[i][2],
-                  names[i]);
-  if ((uintptr_t)p->lse & 3)
-    return fail(FL_ERR_MISALIGNED, "%s: lse must be 4-byte aligned", who);
-  a.q_sb = p->q_stride[0];
-  a.q_sh = p->q_stride[1];
-  a.q_sr = (int)p->q_stride[2];
-  if (!no_keys) {
-    a.k_sb = p->k_stride[0];
-    a.k_sh = p->k_stride[1];
-    a.k_sr = (int)p->k_stride[2];
-    a.v_sb = p->v_stride[0];
-    a.v_sh = p->v_stride[1];
-    a.v_sr = (int)p->v_stride[2];
-  }
-  a.o_sb = p->o_stride[0];
-  a.o_sh = p->o_stride[1];
-  a.o_sr = (int)p->o_stride[2];
-  a.lse = p->lse;
   if (empty_problem(a)) return FL_OK;
   rc = check_pointers(&p->base, &a, who, 16);
   if (rc != FL_OK) return rc;
   const int cfg = config < 0 ? select_fa2(a) : config;
   const hipError_t e = fl::launch_fa2(a, cfg, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return fail(FL_ERR_LAUNCH, "%s: launch failed: %s", who, hipGetErrorString(e));
+  return FL_OK;
+}
+
+int64_t fl_attn_splitkv_workspace_bytes(const fl_attn_params_ex* p, int32_t num_splits) {
+  fl::FwdArgs a;
+  if (check_ex(p, &a, "fl_attn_splitkv_workspace_bytes") != FL_OK) return -1;
+  const KvPlan plan = plan_kvsplit(a, num_splits);
+  return plan.nsplit == 0 ? 0 : plan.bytes;
+}
+
+int fl_attn_fwd_f16_splitkv(const fl_attn_params_ex* p, int32_t num_splits, void* workspace,
+                            int64_t workspace_bytes, void* stream) {
+  const char* who = "fl_attn_fwd_f16_splitkv";
+  fl::FwdArgs a;
+  int rc = check_ex(p, &a, who);
+  if (rc != FL_OK) return rc;
+  if (empty_problem(a)) return FL_OK;
+  rc = check_pointers(&p->base, &a, who, 16);
+  if (rc != FL_OK) return rc;
+  const KvPlan plan = plan_kvsplit(a, num_splits);
+  hipError_t e;
+  if (plan.nsplit == 0) {  // the library's choice: one pass, no workspace
+    e = fl::launch_fa2(a, select_fa2(a), static_cast<hipStream_t>(stream));
+  } else {
+    if (workspace == nullptr || workspace_bytes < plan.bytes)
+      return fail(FL_ERR_INVALID_ARGUMENT, "%s: workspace of %lld bytes needed (got %lld%s)", who,
+                  (long long)plan.bytes, (long long)workspace_bytes,
+                  workspace == nullptr ? ", NULL" : "");
+    if ((uintptr_t)workspace & 15)
+      return fail(FL_ERR_MISALIGNED, "%s: workspace must be 16-byte aligned", who);
+    e = fl::launch_kvsplit(a, plan.waves, static_cast<float*>(workspace), plan.nsplit,
+                           static_cast<hipStream_t>(stream));
+  }
   if (e != hipSuccess) return fail(FL_ERR_LAUNCH, "%s: launch failed: %s", who, hipGetErrorString(e));
   return FL_OK;
 }

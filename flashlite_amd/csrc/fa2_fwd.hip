@@ -141,7 +141,14 @@ struct Geom {
   int q_sr, k_sr, v_sr, o_sr;
   int heads, seq_q, seq_k, coff;
   float* lse;  // [B*H][N_q] or null
+  // split-KV launches: partial results [nsplit][B*H][N_q][kPartStride]
+  float* part;
+  int nsplit, batch_heads;
 };
+
+// Floats per row of a split-KV partial result: O[64] unnormalised, the
+// stabiliser in base-2 logit units, the row sum, 2 pad (16-byte rows).
+constexpr int kPartStride = 68;
 
 // Per-head base pointers and buffer resources of a work-group.
 struct HeadPtrs {
@@ -594,6 +601,31 @@ struct Rows {
       for (int r = 0; r < 16; ++r) o[db][r] = a0 * o[db][r] + a1 * part[(16 * db + r) * 64 + lane];
     m = mm;
   }
+  // Split-KV partial of the rows over one key chunk: O unnormalised
+  // (relative to the stabiliser), the stabiliser in base-2 logit units
+  // (m * cr) and the row sum, kPartStride floats per row.  A row with no key
+  // in the chunk stores m = -inf and l = 0.
+  __device__ __forceinline__ void store_partial(float* part) const {
+    const float l_tot = pair_sum(l);
+    if (my_q < seq) {
+      float* r = part + (long long)my_q * kPartStride;
+#pragma unroll
+      for (int db = 0; db < 2; ++db)
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh) {
+          float* dst = r + 32 * db + 16 * hh + 8 * g;
+          const float4 lo = {o[db][8 * hh], o[db][8 * hh + 1], o[db][8 * hh + 2], o[db][8 * hh + 3]};
+          const float4 hi = {o[db][8 * hh + 4], o[db][8 * hh + 5], o[db][8 * hh + 6],
+                             o[db][8 * hh + 7]};
+          *reinterpret_cast<float4*>(dst) = lo;
+          *reinterpret_cast<float4*>(dst + 4) = hi;
+        }
+      if (g == 0) {
+        r[64] = l_tot > 0.0f ? m * (SCALED ? cr : 1.0f) : ninf();
+        r[65] = l_tot;
+      }
+    }
+  }
   // O = O^T / l, 16-byte stores of 8 contiguous head dims; rows >= N skipped.
   // With `lse`, also the row's log-sum-exp in natural-log units,
   // ln(sum_j exp(sm_scale q.k_j)) = ln 2 * (m * cr + log2 l) (-inf for a row
@@ -665,7 +697,10 @@ struct StreamRings {
 // second half of the key range with its own rings (waves w and w + W share
 // a SIMD); the halves are merged through LDS at the end.  That halves the
 // longest key walk, the critical path of causal attention's last q-blocks.
-template <int W, int D, int SPLIT, bool CAUSAL, bool SCALED>
+// KVSPLIT ("split-KV", for few query rows over many keys): work-group i
+// takes key chunk i % nsplit of its query block and writes a partial result
+// (Rows::store_partial) that splitkv_combine_kernel merges.
+template <int W, int D, int SPLIT, bool CAUSAL, bool SCALED, bool KVSPLIT = false>
 __global__ void __launch_bounds__(64 * W * SPLIT, 2)  // 2 waves per SIMD: <= 256 VGPRs
 fa2_fwd_kernel(const _Float16* Q, const _Float16* __restrict__ K,
                const _Float16* __restrict__ V, _Float16* O, const Geom geom, int nqb,
@@ -686,8 +721,16 @@ fa2_fwd_kernel(const _Float16* Q, const _Float16* __restrict__ K,
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int stream = wave / W;       // key-range half
   const int rw = wave - stream * W;  // 32-row block within the work-group
-  int bh, qb;
-  wg_coords<CAUSAL, (W == 4 && SPLIT == 1) ? 2 : 1>(nqb, bh, qb);
+  static_assert(!KVSPLIT || SPLIT == 1, "one split kind at a time");
+  int bh, qb, chunk = 0;
+  if constexpr (KVSPLIT) {
+    const int r = blockIdx.x / geom.nsplit;
+    chunk = blockIdx.x - r * geom.nsplit;
+    bh = r / nqb;
+    qb = r - bh * nqb;
+  } else {
+    wg_coords<CAUSAL, (W == 4 && SPLIT == 1) ? 2 : 1>(nqb, bh, qb);
+  }
   const HeadPtrs hp = head_ptrs(geom, bh, Q, K, V, O);
   const i32x4_t rk = hp.rk, rv = hp.rv;
   const FetchOff<kSegs> fk = fetch_offsets<kSegs, false>(rw, lane, 2 * geom.k_sr);
@@ -700,16 +743,32 @@ fa2_fwd_kernel(const _Float16* Q, const _Float16* __restrict__ K,
   Rows<CAUSAL, SCALED> rows;
   rows.init(hp.q, geom.q_sr, lane, q0 + 32 * rw, seq, geom.seq_k, geom.coff, cq, cr);
 
-  int ntiles = max(1, (geom.seq_k + kBc - 1) / kBc);
+  const int all_tiles = max(1, (geom.seq_k + kBc - 1) / kBc);
+  int ntiles = all_tiles;
   if (CAUSAL) ntiles = min(ntiles, causal_tiles(min(q0 + kBr, seq), geom.coff));
+  // This work-group's key tiles start at cbeg: 0, or its split-KV chunk.
+  int cbeg = 0;
+  float* part = nullptr;
+  if constexpr (KVSPLIT) {
+    const int per = (all_tiles + geom.nsplit - 1) / geom.nsplit;
+    cbeg = chunk * per;
+    const int cend = min(ntiles, cbeg + per);
+    rows.kv_lim = min(geom.seq_k, cend * kBc);
+    ntiles = cend - cbeg;
+    part = geom.part + (long long)(chunk * geom.batch_heads + bh) * seq * kPartStride;
+    if (ntiles <= 0) {  // the whole chunk lies past the causal limit
+      rows.store_partial(part);
+      return;
+    }
+  }
   // Key tiles [tbeg, tend) of this stream; both streams run t0 + 1
   // iterations (the same barriers), the shorter one on masked tiles.
   constexpr bool kSplit = SPLIT == 2;
   const int t0 = kSplit ? (ntiles + 1) / 2 : ntiles;
-  const int tbeg = stream == 0 ? 0 : t0;
-  const int tend = stream == 0 ? t0 : ntiles;
+  const int tbeg = cbeg + (stream == 0 ? 0 : t0);
+  const int tend = cbeg + (stream == 0 ? t0 : ntiles);
   const int last = max(tend - 1, tbeg);  // fetch clamp
-  if (kSplit && stream == 0) rows.kv_lim = min(geom.seq_k, t0 * kBc);
+  if (kSplit && stream == 0) rows.kv_lim = min(rows.kv_lim, tend * kBc);
 
   // Iteration j (position I of the unrolled loop), for j = 0 .. t0, on key
   // tile t = tbeg + j: fetch K(t+D+1) and V(t+D-1) into the slots of K(t)
@@ -832,13 +891,16 @@ fa2_fwd_kernel(const _Float16* Q, const _Float16* __restrict__ K,
   __builtin_amdgcn_s_waitcnt(0);
   if constexpr (SPLIT == 2) {
     __syncthreads();
-    float* part = reinterpret_cast<float*>(kring) + rw * (34 * 64);
-    if (stream == 1) rows.save_partial(part, lane);
+    float* xchg = reinterpret_cast<float*>(kring) + rw * (34 * 64);
+    if (stream == 1) rows.save_partial(xchg, lane);
     __syncthreads();
     if (stream == 1) return;
-    rows.merge_partial(part, lane);
+    rows.merge_partial(xchg, lane);
   }
-  rows.store(hp.o, geom.o_sr, hp.lse);
+  if constexpr (KVSPLIT)
+    rows.store_partial(part);
+  else
+    rows.store(hp.o, geom.o_sr, hp.lse);
 }
 
 // ---------------------------------------------------------------------------
@@ -980,6 +1042,45 @@ fa2_fwd_pp_kernel(const _Float16* Q, const _Float16* __restrict__ K,
   rows.store(hp.o, geom.o_sr, hp.lse);
 }
 
+// ---------------------------------------------------------------------------
+// Split-KV combine: one wave per query row merges the nsplit partials of the
+// row (O unnormalised at stabiliser m_s, row sum l_s) at their largest m:
+//   O = sum_s 2^(m_s - M) O_s / sum_s 2^(m_s - M) l_s,
+// and writes O (fp16, lane = head dim) and, when asked, the log-sum-exp.
+__device__ __forceinline__ float wave_max64(float x) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) x = fmaxf(x, __shfl_xor(x, m, 64));
+  return x;
+}
+
+__global__ void __launch_bounds__(256)
+splitkv_combine_kernel(_Float16* O, const Geom geom) {
+  const int lane = threadIdx.x & 63;
+  const int row_id = blockIdx.x * 4 + (threadIdx.x >> 6);  // bh * N_q + row
+  if (row_id >= geom.batch_heads * geom.seq_q) return;
+  const int bh = row_id / geom.seq_q, row = row_id - bh * geom.seq_q;
+  const long long split_stride = (long long)geom.batch_heads * geom.seq_q * kPartStride;
+  const float* p0 = geom.part + (long long)row_id * kPartStride;
+  float mx = ninf();
+  for (int s = lane; s < geom.nsplit; s += 64) mx = fmaxf(mx, p0[s * split_stride + 64]);
+  mx = wave_max64(mx);
+  float acc = 0.0f, lsum = 0.0f;
+  for (int s = 0; s < geom.nsplit; ++s) {
+    const float* ps = p0 + s * split_stride;
+    const float m = ps[64];
+    if (m == ninf()) continue;  // no key of this chunk is visible to the row
+    const float w = __builtin_amdgcn_exp2f(m - mx);
+    lsum += w * ps[65];
+    acc += w * ps[lane];
+  }
+  const int b = bh / geom.heads, h = bh - b * geom.heads;
+  _Float16* orow = O + (b * geom.o_sb + h * geom.o_sh) + (long long)row * geom.o_sr;
+  orow[lane] = (_Float16)(lsum > 0.0f ? acc / lsum : 0.0f);
+  if (geom.lse != nullptr && lane == 0)
+    geom.lse[row_id] =
+        lsum > 0.0f ? 0.693147180559945309f * (mx + __builtin_amdgcn_logf(lsum)) : ninf();
+}
+
 // Q is prescaled by cq = +-min(c, 1) in the kernel; the remaining factor
 // cr = c / |cq| (1 unless c > 1) is applied to the scores.
 struct Scales {
@@ -1012,6 +1113,9 @@ Geom make_geom(const FwdArgs& a) {
   g.seq_k = a.seq_k;
   g.coff = a.seq_k - a.seq;
   g.lse = a.lse;
+  g.part = nullptr;
+  g.nsplit = 1;
+  g.batch_heads = a.batch_heads;
   return g;
 }
 
@@ -1062,7 +1166,51 @@ struct PingPongLaunch {
   };
 };
 
+// Split-KV: the chunk kernel (grid = query blocks x chunks) and the
+// combine kernel, back to back on the stream.
+template <int W, int D>
+hipError_t launch_kvsplit_w(const FwdArgs& a, float* part, int nsplit, hipStream_t st) {
+  constexpr int br = 32 * W;
+  const int nqb = (a.seq + br - 1) / br;
+  const Scales sc(a);
+  Geom g = make_geom(a);
+  g.part = part;
+  g.nsplit = nsplit;
+  const dim3 grid((unsigned)(nqb * a.batch_heads * nsplit));
+  const dim3 block(64 * W);
+  const _Float16 *q = static_cast<const _Float16*>(a.q), *k = static_cast<const _Float16*>(a.k),
+                 *v = static_cast<const _Float16*>(a.v);
+  _Float16* o = static_cast<_Float16*>(a.o);
+  if (a.causal) {
+    if (sc.scaled)
+      hipLaunchKernelGGL((fa2_fwd_kernel<W, D, 1, true, true, true>), grid, block, 0, st, q, k, v, o, g, nqb, sc.cq, sc.cr);
+    else
+      hipLaunchKernelGGL((fa2_fwd_kernel<W, D, 1, true, false, true>), grid, block, 0, st, q, k, v, o, g, nqb, sc.cq, sc.cr);
+  } else {
+    if (sc.scaled)
+      hipLaunchKernelGGL((fa2_fwd_kernel<W, D, 1, false, true, true>), grid, block, 0, st, q, k, v, o, g, nqb, sc.cq, sc.cr);
+    else
+      hipLaunchKernelGGL((fa2_fwd_kernel<W, D, 1, false, false, true>), grid, block, 0, st, q, k, v, o, g, nqb, sc.cq, sc.cr);
+  }
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  const int rows = a.batch_heads * a.seq;
+  hipLaunchKernelGGL(splitkv_combine_kernel, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, st, o,
+                     g);
+  return hipGetLastError();
+}
+
 }  // namespace
+
+hipError_t launch_kvsplit(const FwdArgs& a, int waves, float* part, int nsplit,
+                          hipStream_t stream) {
+  switch (waves) {
+    case 1: return launch_kvsplit_w<1, 1>(a, part, nsplit, stream);
+    case 2: return launch_kvsplit_w<2, 3>(a, part, nsplit, stream);
+    case 4: return launch_kvsplit_w<4, 3>(a, part, nsplit, stream);
+    default: return hipErrorInvalidValue;
+  }
+}
 
 const Fa2Config kFa2Configs[kNumFa2Configs] = {
     {1, "br32_bc64_w1"},

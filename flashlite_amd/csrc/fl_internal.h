@@ -43,6 +43,13 @@ extern const Fa2Config kFa2Configs[kNumFa2Configs];
 // Launches the FA2 kernel for configuration `cfg` on `stream`.
 hipError_t launch_fa2(const FwdArgs& a, int cfg, hipStream_t stream);
 
+// Split-KV ("flash-decoding"): `waves` (1, 2 or 4) waves of 32 query rows
+// per work-group, the key range cut into `nsplit` chunks whose partial
+// results go to `part` (nsplit * B*H * N_q * 68 floats, 16-byte aligned),
+// then merged by a second kernel on the same stream.
+hipError_t launch_kvsplit(const FwdArgs& a, int waves, float* part, int nsplit,
+                          hipStream_t stream);
+
 // Largest seq the naive kernel can stage in LDS for this head_dim.
 int64_t naive_max_seq(int64_t head_dim);
 hipError_t launch_naive(const FwdArgs& a, hipStream_t stream);

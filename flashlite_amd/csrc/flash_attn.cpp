@@ -133,12 +133,19 @@ torch::Tensor flash_attn_forward_flash2(torch::Tensor q, torch::Tensor k, torch:
 
 // Beyond the reference surface: any [B, H, N, 64] strided views with a
 // unit-stride head dimension (e.g. the transpose of a [B, N, H, 64] tensor),
-// N_k != N_q (bottom-right causal), and optionally the fp32 log-sum-exp
-// [B, H, N_q].  Returns `out`, or (out, lse) with return_lse.  An omitted
-// `out` is allocated with q's layout (empty_like keeps dense strides).
+// N_k != N_q (bottom-right causal), optionally the fp32 log-sum-exp
+// [B, H, N_q], and split-KV for few query rows over many keys.  Returns
+// `out`, or (out, lse) with return_lse.  An omitted `out` is allocated with
+// q's layout (empty_like keeps dense strides).
+// num_splits: 0 = the library's choice, 1 = one pass, n > 1 = n key chunks.
+// A split-KV call needs a workspace: `workspace` (any device tensor of
+// enough bytes, reused across calls for an allocation-free loop) or else
+// one from the caching allocator.
 py::object flash_attn_forward_flash2_ex(torch::Tensor q, torch::Tensor k, torch::Tensor v,
                                         double sm_scale, bool is_causal,
-                                        std::optional<torch::Tensor> out, bool return_lse) {
+                                        std::optional<torch::Tensor> out, bool return_lse,
+                                        int64_t num_splits,
+                                        std::optional<torch::Tensor> workspace) {
   TORCH_CHECK(q.is_cuda() && k.is_cuda() && v.is_cuda(), "All tensors must be on CUDA");
   TORCH_CHECK(q.dtype() == torch::kHalf && k.dtype() == torch::kHalf && v.dtype() == torch::kHalf,
               "All tensors must be FP16 (Half)");
@@ -180,7 +187,26 @@ py::object flash_attn_forward_flash2_ex(torch::Tensor q, torch::Tensor k, torch:
   for (int i = 0; i < 4; ++i)
     for (int d = 0; d < 3; ++d) st[i][d] = ts[i]->stride(d);
   p.lse = return_lse ? lse.data_ptr<float>() : nullptr;
-  const int rc = fl_attn_fwd_f16_ex(&p, -1, current_stream(q));
+  TORCH_CHECK(num_splits >= 0 && num_splits <= INT32_MAX, "num_splits must be >= 0");
+  const int64_t ws_bytes =
+      num_splits == 1 ? 0 : fl_attn_splitkv_workspace_bytes(&p, (int32_t)num_splits);
+  TORCH_CHECK(ws_bytes >= 0, "FlashLite HIP error: ", fl_attn_last_error());
+  int rc;
+  if (ws_bytes == 0) {
+    rc = fl_attn_fwd_f16_ex(&p, -1, current_stream(q));
+  } else {
+    torch::Tensor ws;
+    if (workspace.has_value() && workspace.value().defined() &&
+        workspace.value().nbytes() >= (size_t)ws_bytes) {
+      ws = workspace.value();
+      TORCH_CHECK(ws.is_cuda() && ws.device() == q.device() && ws.is_contiguous(),
+                  "workspace must be a contiguous tensor on q's device");
+    } else {
+      ws = torch::empty({(ws_bytes + 3) / 4}, q.options().dtype(torch::kFloat32));
+    }
+    rc = fl_attn_fwd_f16_splitkv(&p, (int32_t)num_splits, ws.data_ptr(), (int64_t)ws.nbytes(),
+                                 current_stream(q));
+  }
   TORCH_CHECK(rc == FL_OK, "FlashLite HIP error: ", fl_attn_last_error());
   if (return_lse) return py::make_tuple(out_tensor, lse);
   return py::cast(out_tensor);
@@ -203,5 +229,27 @@ PYBIND11_MODULE(flash_attn_wmma, m) {
         "FlashAttention-2 forward on strided [B, H, N, 64] views, N_k != N_q (bottom-right "
         "causal), optional log-sum-exp",
         py::arg("q"), py::arg("k"), py::arg("v"), py::arg("sm_scale") = 0.0,
-        py::arg("is_causal") = false, py::arg("out") = py::none(), py::arg("return_lse") = false);
+        py::arg("is_causal") = false, py::arg("out") = py::none(), py::arg("return_lse") = false,
+        py::arg("num_splits") = 0, py::arg("workspace") = py::none());
+
+  m.def("splitkv_workspace_bytes",
+        [](torch::Tensor q, torch::Tensor k, bool is_causal, int64_t num_splits) {
+          fl_attn_params_ex p;
+          p.base = fl_attn_params{nullptr, nullptr, nullptr, nullptr, q.size(0), q.size(1),
+                                  q.size(2), k.size(2), q.size(3), 0.0, is_causal ? 1 : 0};
+          const int64_t qs[3] = {q.stride(0), q.stride(1), q.stride(2)};
+          const int64_t ks[3] = {k.stride(0), k.stride(1), k.stride(2)};
+          for (int d = 0; d < 3; ++d) {
+            p.q_stride[d] = p.o_stride[d] = qs[d];
+            p.k_stride[d] = p.v_stride[d] = ks[d];
+          }
+          p.lse = nullptr;
+          if (num_splits == 1) return (int64_t)0;
+          const int64_t b = fl_attn_splitkv_workspace_bytes(&p, (int32_t)num_splits);
+          TORCH_CHECK(b >= 0, "FlashLite HIP error: ", fl_attn_last_error());
+          return b;
+        },
+        "Workspace bytes forward_flash2_ex needs for these q / k shapes and num_splits "
+        "(0 when it runs one pass)",
+        py::arg("q"), py::arg("k"), py::arg("is_causal") = false, py::arg("num_splits") = 0);
 }

@@ -108,6 +108,31 @@ typedef struct fl_attn_params_ex {
 int fl_attn_fwd_f16_ex(const fl_attn_params_ex* p, int32_t config, void* stream);
 
 /*
+ * Split-KV forward ("flash-decoding"), for few query rows over many keys:
+ * the key range of every (batch, head) is cut into chunks processed by
+ * separate work-groups, whose partial results (unnormalised O, stabiliser,
+ * row sum) go to `workspace`; a second kernel on the same stream merges
+ * them into O (and lse).  Same parameters, layouts and results as
+ * fl_attn_fwd_f16_ex up to fp32 rounding.
+ *
+ * num_splits > 0 asks for that many chunks (at most the number of 64-key
+ * tiles, and 256); num_splits <= 0 lets the library choose, which may be
+ * "no split": then the one-pass kernel runs and no workspace is needed.
+ * fl_attn_splitkv_workspace_bytes returns the bytes a call with the same
+ * `p` and `num_splits` needs (0 when it will not split, -1 if `p` is
+ * rejected).  The workspace is 16-byte aligned device memory owned by the
+ * caller; calls that may overlap must not share one.
+ *
+ * No counterpart in the reference (one work-group per 64/128 query rows,
+ * csrc/kernel_flash2.cu:786-835, which leaves a decode step with N = 1 on a
+ * handful of CUs); its README advertises `out=` for serving/decode loops
+ * (README.md:119-126).
+ */
+int64_t fl_attn_splitkv_workspace_bytes(const fl_attn_params_ex* p, int32_t num_splits);
+int fl_attn_fwd_f16_splitkv(const fl_attn_params_ex* p, int32_t num_splits, void* workspace,
+                            int64_t workspace_bytes, void* stream);
+
+/*
  * Un-fused baseline: one work-group per query row, scores staged in LDS.
  * Any head_dim >= 1; seq limited by LDS (about 40k keys at D=64).
  * Replaces flash_attn_forward_naive's scale handling and launch

@@ -21,7 +21,7 @@ def test_library_loads_and_exports_header_symbols():
     lib = capi.load()
     with open(HEADER) as f:
         text = f.read()
-    declared = set(re.findall(r"^\s*(?:int|const char\*)\s+(fl_\w+)\s*\(", text, re.M))
+    declared = set(re.findall(r"^\s*(?:int|int64_t|const char\*)\s+(fl_\w+)\s*\(", text, re.M))
     assert declared == set(capi.EXPORTED)
     for name in declared:
         assert isinstance(getattr(lib, name), ctypes._CFuncPtr)
@@ -191,3 +191,41 @@ def test_error_message_is_thread_local(fn):
     t.join()
     assert "non-negative" in seen["msg"]
     assert capi.last_error() == "FlashLite WMMA kernel currently requires head_dim == 64"
+
+
+def test_splitkv_plan():
+    c = (8 * 1 * 64, 1 * 64, 64)
+    kc = (8 * 4096 * 64, 4096 * 64, 64)
+
+    def bytes_for(nq, nk, splits, batch=2, heads=8, causal=False):
+        base = _p(batch=batch, heads=heads, seq_q=nq, seq_k=nk, causal=causal)
+        qs = (heads * nq * 64, nq * 64, 64)
+        ks = (heads * nk * 64, nk * 64, 64)
+        return capi.splitkv_workspace_bytes(capi.make_params_ex(base, qs, ks, ks, qs), splits)
+
+    # decode step B2 H8, one query over 4096 keys: 16 one-wave groups would
+    # leave the GPU idle; the library splits into 32 chunks of 2 tiles
+    assert bytes_for(1, 4096, 0) == 32 * 16 * 1 * 68 * 4
+    # the headline shape already fills the GPU: no split
+    assert bytes_for(4096, 4096, 0) == 0
+    # too few keys to split
+    assert bytes_for(1, 192, 0) == 0
+    # forced: as asked, clamped to the number of 64-key tiles
+    assert bytes_for(4096, 4096, 5) == 5 * 16 * 4096 * 68 * 4
+    assert bytes_for(3, 130, 100) == 3 * 16 * 3 * 68 * 4
+    assert bytes_for(1, 1 << 20, 1000) == 256 * 16 * 68 * 4
+    # rejected params
+    assert bytes_for(1, 4096, 0, heads=-1) == -1
+
+
+def test_splitkv_workspace_checks():
+    qs = (8 * 64, 64, 64)
+    ks = (8 * 4096 * 64, 4096 * 64, 64)
+    p = capi.make_params_ex(_p(seq_q=1, seq_k=4096), qs, ks, ks, qs)
+    need = capi.splitkv_workspace_bytes(p, 0)
+    assert need > 0
+    assert capi.fwd_splitkv(p, 0, need) == capi.FL_ERR_INVALID_ARGUMENT
+    assert "workspace" in capi.last_error() and "NULL" in capi.last_error()
+    assert capi.fwd_splitkv(p, A + 0x400000, need - 4) == capi.FL_ERR_INVALID_ARGUMENT
+    assert capi.fwd_splitkv(p, A + 0x400008, need) == capi.FL_ERR_MISALIGNED
+    assert capi.load().fl_attn_fwd_f16_splitkv(None, 0, None, 0, None) == capi.FL_ERR_INVALID_ARGUMENT

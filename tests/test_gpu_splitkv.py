@@ -1,0 +1,110 @@
+"""GPU parity of split-KV ("flash-decoding"): the key range cut into chunks,
+partial results merged by a second kernel.  Same tolerances as the one-pass
+kernel against the fp32 oracle (max-abs 2e-3, mean-abs 2e-4; log-sum-exp
+2e-3 / 3e-4, see test_gpu_rect_strided.py), on decode-like shapes (one or a
+few query rows over many keys), both masks (causal aligned bottom-right),
+forced and automatic chunk counts, empty chunks past the causal limit."""
+
+import numpy as np
+import pytest
+
+from flashlite_amd import capi
+from gpu_util import assert_close_oracle, to_dev
+from oracle import attention_fp32, attention_lse, error_stats
+
+pytestmark = pytest.mark.gpu
+
+LSE_MAX_ABS = 2e-3
+LSE_MEAN_ABS = 3e-4
+
+
+def _qkv(b, h, nq, nk, seed):
+    rs = np.random.RandomState(seed)
+    mk = lambda n: rs.standard_normal((b, h, n, 64)).astype(np.float32).astype(np.float16)
+    return mk(nq), mk(nk), mk(nk)
+
+
+def _run_split(tq, tk, tv, sm_scale, causal, splits, lse=True, o_fill=float("nan")):
+    import torch
+
+    dev = tq.device
+    o = torch.full_like(tq, o_fill)
+    ls = torch.full(tq.shape[:3], float("nan"), dtype=torch.float32, device=dev) if lse else None
+    p = capi.tensor_params_ex(tq, tk, tv, o, sm_scale, causal, lse=ls)
+    need = capi.splitkv_workspace_bytes(p, splits)
+    assert need >= 0, capi.last_error()
+    ws = torch.full((max(need, 4) // 4,), float("nan"), dtype=torch.float32, device=dev)
+    capi.check(capi.fwd_splitkv(p, ws.data_ptr() if need else 0, need,
+                                torch.cuda.current_stream(dev).cuda_stream, splits))
+    torch.cuda.synchronize(dev)
+    return o, ls, need
+
+
+SHAPES = [(1, 4096), (1, 1000), (4, 777), (32, 4096), (33, 2048), (100, 3000), (1, 64),
+          (100, 130)]
+
+
+@pytest.mark.parametrize("nq,nk", SHAPES)
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("splits", [1, 3, 0, 1000])
+def test_splitkv_matches_oracle(cuda, nq, nk, causal, splits):
+    q16, k16, v16 = _qkv(2, 4, nq, nk, seed=nq * 13 + nk)
+    tq, tk, tv = (to_dev(x, cuda) for x in (q16, k16, v16))
+    o, ls, need = _run_split(tq, tk, tv, 0.125, causal, splits)
+    if splits > 0:
+        tiles = (nk + 63) // 64
+        assert need == min(splits, tiles, 256) * 2 * 4 * nq * 68 * 4
+    out = o.float().cpu().numpy()
+    assert_close_oracle(out, q16, k16, v16, 0.125, causal,
+                        ref=attention_fp32(q16, k16, v16, 0.125, causal))
+    lse = ls.cpu().numpy()
+    ref = attention_lse(q16, k16, 0.125, causal)
+    assert np.array_equal(np.isneginf(lse), np.isneginf(ref))
+    fin = np.isfinite(ref)
+    mx, mean = error_stats(lse[fin], ref[fin])
+    assert mx <= LSE_MAX_ABS and mean <= LSE_MEAN_ABS, f"lse max-abs {mx:.3e} mean-abs {mean:.3e}"
+
+
+def test_splitkv_auto_choice(cuda):
+    # a decode step on a small batch splits; the headline shape does not
+    q16, k16, v16 = _qkv(2, 8, 1, 4096, seed=1)
+    tq, tk, tv = (to_dev(x, cuda) for x in (q16, k16, v16))
+    _, _, need = _run_split(tq, tk, tv, 0.125, False, 0)
+    assert need == 32 * 16 * 68 * 4
+
+
+def test_splitkv_strided_and_deterministic(cuda):
+    import torch
+
+    q16, k16, v16 = _qkv(2, 3, 5, 2000, seed=2)
+    tq, tk, tv = (to_dev(x, cuda) for x in (q16, k16, v16))
+    a, la, _ = _run_split(tq, tk, tv, 0.125, True, 7)
+    b, lb, _ = _run_split(tq, tk, tv, 0.125, True, 7)
+    assert torch.equal(a, b) and torch.equal(la, lb)
+    # [B, N, H, D] storage gives the same bits
+    qb, kb, vb = (x.transpose(1, 2).contiguous().transpose(1, 2) for x in (tq, tk, tv))
+    c, lc, _ = _run_split(qb, kb, vb, 0.125, True, 7)
+    assert torch.equal(c, a) and torch.equal(lc, la)
+
+
+def test_binding_splitkv(cuda):
+    import torch
+
+    import flashlite_amd as fl
+
+    q16, k16, v16 = _qkv(2, 8, 1, 4096, seed=3)
+    q, k, v = (to_dev(x, cuda) for x in (q16, k16, v16))
+    need = fl.splitkv_workspace_bytes(q, k, False, 0)
+    assert need > 0
+    ws = torch.empty(need // 4, dtype=torch.float32, device=cuda)
+    out = torch.empty_like(q)
+    got, lse = fl.forward_flash2_ex(q, k, v, 0.125, False, out=out, return_lse=True, workspace=ws)
+    torch.cuda.synchronize()
+    assert got.data_ptr() == out.data_ptr()
+    assert_close_oracle(got.float().cpu().numpy(), q16, k16, v16, 0.125, False)
+    ref_lse = attention_lse(q16, k16, 0.125, False)
+    assert error_stats(lse.cpu().numpy(), ref_lse)[0] <= LSE_MAX_ABS
+    # num_splits=1: the one-pass kernel, bit-identical to forward_flash2
+    one = fl.forward_flash2_ex(q, k, v, 0.125, False, num_splits=1)
+    assert torch.equal(one, fl.forward_flash2(q, k, v, 0.125, False))
+    assert fl.splitkv_workspace_bytes(q, k, False, 1) == 0
