@@ -192,9 +192,13 @@ int check_ex(const fl_attn_params_ex* p, fl::FwdArgs* a, const char* who) {
 
 // Split-KV plan: waves per work-group by N_q (32 query rows each), number
 // of key chunks, workspace bytes.  nsplit == 0 means "do not split".
-// The library's choice (requested <= 0) splits only when the one-pass grid
-// leaves most SIMDs idle (fewer than 1024 waves) and every chunk keeps at
-// least 2 key tiles; it then aims at about 2048 waves.
+// The library's choice (requested <= 0), from decode sweeps on MI355X
+// (B2 H8 and B1 H16 with N_q 1-16 over 4k-64k keys, B32 H32 over 4k): with
+// at most 128 query rows and fewer query-row groups than CUs, cut each key
+// range so that the groups times chunks cover the 256 CUs once, keeping at
+// least 4 key tiles per chunk (more chunks measured slower: per-work-group
+// start-up); with more single-wave groups (N_q <= 32), chunks of 8 tiles up
+// to 8 chunks when the range is long (>= 32 tiles).  Otherwise one pass.
 struct KvPlan {
   int waves, nsplit;
   int64_t bytes;
@@ -203,20 +207,23 @@ constexpr int kMaxSplits = 256;
 constexpr int64_t kPartFloats = 68;  // per row: O[64], m, l, 2 pad
 
 KvPlan plan_kvsplit(const fl::FwdArgs& a, int32_t requested) {
+  constexpr int64_t kCus = 256;
   KvPlan p;
   p.waves = a.seq <= 32 ? 1 : (a.seq <= 64 ? 2 : 4);
   const int64_t nqb = (a.seq + 32 * p.waves - 1) / (32 * p.waves);
   const int64_t tiles = std::max<int64_t>(1, (a.seq_k + 63) / 64);
-  const int64_t waves = nqb * a.batch_heads * p.waves;
+  const int64_t groups = nqb * a.batch_heads;
   int64_t n;
   if (requested > 0) {
     n = std::min<int64_t>({(int64_t)requested, tiles, kMaxSplits});
-  } else if (waves >= 1024 || tiles < 4) {
-    n = 0;
+  } else if (a.seq > 128) {
+    n = 0;  // long query ranges: the one-pass kernel's groups fill the GPU
+  } else if (groups < kCus) {
+    n = std::min<int64_t>({(kCus + groups - 1) / groups, tiles / 4, kMaxSplits});
   } else {
-    n = std::min<int64_t>({(2048 + waves - 1) / waves, tiles / 2, kMaxSplits});
-    if (n < 2) n = 0;
+    n = (a.seq <= 32 && tiles >= 32) ? std::min<int64_t>(8, tiles / 8) : 0;
   }
+  if (requested <= 0 && n < 2) n = 0;
   // the chunk kernel's grid (64 * waves lanes per group) must stay below 2^32 lanes
   const int64_t grid_cap = ((int64_t)UINT32_MAX / (64 * p.waves)) / (nqb * a.batch_heads);
   n = std::min(n, grid_cap);

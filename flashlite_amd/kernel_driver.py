@@ -13,6 +13,12 @@ mean launch time measured with HIP events on that stream.
 ``--copy-mib M`` instead runs an elementwise fp16 kernel that reads M MiB and
 writes M MiB (``torch.mul(src, 1, out=dst)``): the reference point that
 scales the HBM byte counters (FETCH_SIZE / WRITE_SIZE) of a profile.
+
+``--decode B H NQ NK`` runs a decode-shaped call (NQ query rows over NK
+keys, seeded N(0,1) inputs) through ``fl_attn_fwd_f16_splitkv`` with
+``--splits S`` (1 = one pass, 0 = the library's choice, n = n key chunks)
+and reports the K/V read rate against 8 TB/s: bytes = 2 * B*H*NK*64*2
+(K and V once) + Q and O.
 """
 
 from __future__ import annotations
@@ -29,9 +35,15 @@ def main(argv=None):
     ap.add_argument("--iters", type=int, default=20)
     ap.add_argument("--naive", action="store_true")
     ap.add_argument("--copy-mib", type=int, default=0, help="run the calibration copy instead")
+    ap.add_argument("--decode", type=int, nargs=4, metavar=("B", "H", "NQ", "NK"), default=None)
+    ap.add_argument("--splits", type=int, default=0)
+    ap.add_argument("--causal-decode", type=int, default=0)
     args = ap.parse_args(argv)
 
     import torch
+
+    if args.decode:
+        return _decode(args, torch)
 
     if args.copy_mib:
         n = args.copy_mib * (1 << 20) // 2
@@ -78,6 +90,46 @@ def main(argv=None):
     name = "naive" if args.naive else capi.config_name(cfg)
     print(f"{args.workload} causal={args.causal} {name}: {us:.2f} us/launch, "
           f"{flops / us / 1e6:.1f} TFLOP/s", flush=True)
+
+
+def _decode(args, torch):
+    import numpy as np
+
+    from flashlite_amd import capi
+
+    b, h, nq, nk = args.decode
+    dev = torch.device("cuda:0")
+    rs = np.random.RandomState(7)
+    mk = lambda n: torch.from_numpy(
+        rs.standard_normal((b, h, n, 64)).astype(np.float32).astype(np.float16)).to(dev)
+    q, k, v = mk(nq), mk(nk), mk(nk)
+    o = torch.empty_like(q)
+    stream = torch.cuda.current_stream().cuda_stream
+    p = capi.tensor_params_ex(q, k, v, o, 0.125, bool(args.causal_decode))
+    need = 0 if args.splits == 1 else capi.splitkv_workspace_bytes(p, args.splits)
+    ws = torch.empty(max(need, 16) // 4, dtype=torch.float32, device=dev)
+
+    def launch():
+        if need == 0:
+            capi.check(capi.fwd_ex(p, stream, -1))
+        else:
+            capi.check(capi.fwd_splitkv(p, ws.data_ptr(), need, stream, args.splits))
+
+    launch()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(args.iters):
+        launch()
+    end.record()
+    torch.cuda.synchronize()
+    us = start.elapsed_time(end) * 1e3 / args.iters
+    nbytes = 2 * b * h * nk * 64 * 2 + 2 * b * h * nq * 64 * 2
+    chunks = need // (b * h * nq * 68 * 4) if need else 1
+    print(f"decode B{b} H{h} NQ{nq} NK{nk} causal={args.causal_decode} chunks={chunks}: "
+          f"{us:.2f} us/call, {nbytes / us / 1e3:.1f} GB/s ({nbytes / us / 1e3 / 8000:.1%} of 8 TB/s)",
+          flush=True)
+    return 0
 
 
 if __name__ == "__main__":

@@ -204,12 +204,21 @@ def test_splitkv_plan():
         return capi.splitkv_workspace_bytes(capi.make_params_ex(base, qs, ks, ks, qs), splits)
 
     # decode step B2 H8, one query over 4096 keys: 16 one-wave groups would
-    # leave the GPU idle; the library splits into 32 chunks of 2 tiles
-    assert bytes_for(1, 4096, 0) == 32 * 16 * 1 * 68 * 4
-    # the headline shape already fills the GPU: no split
-    assert bytes_for(4096, 4096, 0) == 0
-    # too few keys to split
+    # leave most CUs idle; 16 chunks of 4 tiles cover the 256 CUs once
+    assert bytes_for(1, 4096, 0) == 16 * 16 * 1 * 68 * 4
+    assert bytes_for(1, 1 << 16, 0) == 16 * 16 * 1 * 68 * 4
+    # fewer than 8 tiles: at most tiles / 4 chunks, and no split below 2
+    assert bytes_for(1, 512, 0) == 2 * 16 * 1 * 68 * 4
     assert bytes_for(1, 192, 0) == 0
+    # many groups (B32 H32): chunks of 8 tiles, at most 8, on long ranges only
+    assert bytes_for(1, 4096, 0, batch=32, heads=32) == 8 * 1024 * 68 * 4
+    assert bytes_for(1, 1024, 0, batch=32, heads=32) == 0
+    assert bytes_for(16, 4096, 0, batch=32, heads=32) == 8 * 1024 * 16 * 68 * 4
+    assert bytes_for(64, 4096, 0, batch=32, heads=32) == 0
+    # long query ranges (the headline shape): one pass
+    assert bytes_for(4096, 4096, 0) == 0
+    assert bytes_for(129, 1 << 16, 0) == 0
+    assert bytes_for(128, 1 << 16, 0) == 16 * 16 * 128 * 68 * 4
     # forced: as asked, clamped to the number of 64-key tiles
     assert bytes_for(4096, 4096, 5) == 5 * 16 * 4096 * 68 * 4
     assert bytes_for(3, 130, 100) == 3 * 16 * 3 * 68 * 4
