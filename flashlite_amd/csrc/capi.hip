@@ -114,9 +114,9 @@ int check_pointers(const fl_attn_params* p, fl::FwdArgs* a, const char* who, uin
 int select_fa2(const fl::FwdArgs& a) {
   constexpr int64_t kCus = 256;
   auto wgs = [&](int64_t br) { return (a.seq + br - 1) / br * (int64_t)a.batch_heads; };
-  if (!a.causal && wgs(256) >= kCus) return 3;                       // br256_bc64_w8
+  if (!a.causal && wgs(256) >= kCus) return 6;                       // br256_bc64_w8_slot
   if (!a.causal && a.seq >= 2048 && wgs(128) < 2 * kCus) return 5;  // br128_bc64_w4_split2
-  if (wgs(128) >= kCus / 4) return 2;                                // br128_bc64_w4
+  if (wgs(128) >= kCus / 4) return 7;                                // br128_bc64_w4_slot
   if (wgs(64) >= kCus / 4) return 1;                                 // br64_bc64_w2
   return 0;                                                          // br32_bc64_w1
 }

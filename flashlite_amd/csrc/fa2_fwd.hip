@@ -364,6 +364,12 @@ struct Rows {
     l = 0.0f;
   }
 
+  // Makes the per-lane index fields opaque, so addresses derived from them
+  // are recomputed after this point instead of being kept live (and, under
+  // register pressure, spilled) from an earlier use.
+  __device__ __forceinline__ void launder() {
+    asm volatile("" : "+v"(col), "+v"(g), "+v"(my_q), "+v"(tr_row), "+v"(tr_col));
+  }
   // K operands of GEMM1 (both 32-key blocks, 4 head-dim steps each).
   __device__ __forceinline__ void read_k(const uint8_t* kt, half8_t (&ka)[2][4]) const {
 #pragma unroll
@@ -424,20 +430,165 @@ struct Rows {
       }
     }
   }
+  // A operands of single MFMAs: 32 K rows of key block kb at head-dim step
+  // st (one ds_read_b128), or V^T of head-dim block db at key step t (two
+  // ds_read_b64_tr_b16); the same reads as read_k / read_v.
+  __device__ __forceinline__ half8_t read_k_op(const uint8_t* kt, int kb, int st) const {
+    const int row = 32 * kb + col;
+    const int ch = 2 * st + g;
+    return *reinterpret_cast<const half8_t*>(kt + row * kRowBytes + 16 * (ch ^ k_swz(row)));
+  }
+  __device__ __forceinline__ half8_t read_v_op(const uint8_t* vt, int db, int t) const {
+    const int r1 = 16 * t + tr_row;
+    const int r2 = r1 + 8;
+    const int dcol = 32 * db + tr_col;
+    const int ch = dcol >> 3, hb = ((dcol >> 2) & 1) * 8;
+    const half4_t lo = lds_read_tr(vt + r1 * kRowBytes + 16 * (ch ^ v_swz(r1)) + hb);
+    const half4_t hi = lds_read_tr(vt + r2 * kRowBytes + 16 * (ch ^ v_swz(r2)) + hb);
+    return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+  }
+  // Slot map of the skewed slot schedule (fa2_fwd_slot_kernel).  Iteration
+  // j has 16 MFMA slots; slot L = 2u + q:
+  //   q = 0, u < 4:  S[1] (+)= K(j) rows 32-63 . Q'(st = u)    GEMM1, tile j
+  //   q = 0, u >= 4: S[0] (+)= K(j+1) rows 0-31 . Q'(st = u-4)  GEMM1, tile j+1
+  //   q = 1:         O[u & 1] += V^T(j-1)(key step u/2) . P(j-1) GEMM2
+  // The exponentials of slots 0-7 read S[0] (tile j) and those of slots
+  // 8-15 read S[1] (tile j), so each block is rewritten only after its
+  // scores are consumed: one S buffer instead of two.
+  template <int L>
+  __device__ __forceinline__ half8_t read_slot(const uint8_t* k_cur, const uint8_t* k_next,
+                                               const uint8_t* vt) const {
+    constexpr int u = L >> 1;
+    if constexpr ((L & 1) == 0)
+      return u < 4 ? read_k_op(k_cur, 1, u) : read_k_op(k_next, 0, u - 4);
+    else
+      return read_v_op(vt, u & 1, u >> 1);
+  }
+  template <int L>
+  __device__ __forceinline__ void mfma_slot(const half8_t& a, float16_t (&s)[2],
+                                            const half8_t (&pp)[2][2]) {
+    constexpr int u = L >> 1;
+    if constexpr ((L & 1) == 0) {
+      constexpr int kb = u < 4 ? 1 : 0, st = u & 3;
+      s[kb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, qf[st], st == 0 ? bias : s[kb], 0, 0, 0);
+    } else {
+      constexpr int db = u & 1, t = u >> 1;
+      o[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, pp[t >> 1][t & 1], o[db], 0, 0, 0);
+    }
+  }
+  // Softmax share of slot I: scores 2(I%8), 2(I%8)+1 of key block I/8 ->
+  // two exponentials and one fp16 pack into dword I of the tile's P operand
+  // (exponentiate() spread over 16 slots).
+  template <int I>
+  __device__ __forceinline__ void exp_slot(const float16_t (&s)[2], half8_t (&pn)[2][2]) const {
+    constexpr int kb = I >> 3, r = 2 * (I & 7), h = r >> 3, e = r & 7;
+    float x0 = s[kb][r], x1 = s[kb][r + 1];
+    if (SCALED) {
+      x0 *= cr;
+      x1 *= cr;
+    }
+    const float e0 = __builtin_amdgcn_exp2f(x0), e1 = __builtin_amdgcn_exp2f(x1);
+    pn[kb][h][e] = (_Float16)e0;
+    pn[kb][h][e + 1] = (_Float16)e1;
+  }
+  // Dword i (0-15) of a tile's P operand: the fp16 pair of slot i.
+  __device__ __forceinline__ static half2_t p_pair(const half8_t (&pn)[2][2], int i) {
+    const half8_t& v = pn[i >> 3][(i >> 2) & 1];
+    const int e = 2 * (i & 3);
+    return (half2_t){v[e], v[e + 1]};
+  }
+  // Row-sum share of slot I: a pairwise tree of packed fp16 additions over
+  // the tile's P, i.e. the fp16-rounded p that GEMM2 multiplies (level 1
+  // at odd slots, level 2 every 4th, level 3 every 8th; sum_root finishes
+  // it).  One v_pk_add_f16 per slot instead of two fp32 adds keeps a slot's
+  // VALU work within what issues under one MFMA.  t[0..7] level 1, t[8..11]
+  // level 2, t[12..13] level 3.
+  template <int I>
+  __device__ __forceinline__ static void sum_slot(const half8_t (&pn)[2][2], half2_t (&t)[14]) {
+    if constexpr (I & 1) t[I >> 1] = p_pair(pn, I - 1) + p_pair(pn, I);
+    if constexpr ((I & 3) == 3) t[8 + (I >> 2)] = t[(I >> 1) - 1] + t[I >> 1];
+    if constexpr ((I & 7) == 7) t[12 + (I >> 3)] = t[8 + (I >> 2) - 1] + t[8 + (I >> 2)];
+  }
+  // fp32 row-sum share of slot I: the slot's two p, recomputed from the
+  // scores (the exponentials of exp_slot, which the compiler shares), in
+  // four partial chains.
+  template <int I>
+  __device__ __forceinline__ static void sum_slot_f32(const float16_t (&s)[2], float (&sum)[4],
+                                                      float crr) {
+    constexpr int kb = I >> 3, r = 2 * (I & 7);
+    float x0 = s[kb][r], x1 = s[kb][r + 1];
+    if (SCALED) {
+      x0 *= crr;
+      x1 *= crr;
+    }
+    const float e = __builtin_amdgcn_exp2f(x0) + __builtin_amdgcn_exp2f(x1);
+    if constexpr (I < 4)
+      sum[I] = e;
+    else
+      sum[I & 3] += e;
+  }
+  // This lane's tile sum in fp32 from the two level-3 nodes (each half of
+  // the root sums 16 of the lane's 32 values).  A tile whose sum leaves the
+  // fp16-safe range overflows to inf here or exceeds kSumLimit; either way
+  // the caller's range check sends the block to the checked pass.
+  __device__ __forceinline__ static float sum_root(const half2_t (&t)[14]) {
+    const half2_t r = t[12] + t[13];
+    return (float)r[0] + (float)r[1];
+  }
   // Masks keys >= kv_lim and, when causal, keys past the lane's diagonal
-  // (tile t).
+  // (tile t).  Score r of block kb is key k0 + 4g + c with the constant
+  // c = 32kb + 8(r/4) + r%4, so one per-lane bound on c decides every score
+  // (no per-score key indices to keep live).
   __device__ __forceinline__ void mask(int t, float16_t (&s)[2]) const {
     const int k0 = t * kBc;
     if (k0 + kBc > kv_lim || (CAUSAL && k0 + kBc - 1 > qd)) {
+      const int base = k0 + 4 * g;
+      int lim = kv_lim - base;                    // visible iff c < lim
+      if (CAUSAL) lim = min(lim, my_d + 1 - base);
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-          const int key = k0 + 32 * kb + 8 * (r >> 2) + 4 * g + (r & 3);
-          const bool ok = key < kv_lim && (!CAUSAL || key <= my_d);
-          s[kb][r] = ok ? s[kb][r] : ninf();
+          const int c = 32 * kb + 8 * (r >> 2) + (r & 3);
+          s[kb][r] = c < lim ? s[kb][r] : ninf();
         }
     }
+  }
+  // The same for key block KB of tile t alone.
+  template <int KB>
+  __device__ __forceinline__ void mask_block(int t, float16_t& s) const {
+    const int k0 = t * kBc + 32 * KB;
+    if (k0 + 32 > kv_lim || (CAUSAL && k0 + 31 > qd)) {
+      const int base = k0 + 4 * g;
+      int lim = kv_lim - base;
+      if (CAUSAL) lim = min(lim, my_d + 1 - base);
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int c = 8 * (r >> 2) + (r & 3);
+        s[r] = c < lim ? s[r] : ninf();
+      }
+    }
+  }
+  // One key tile, unpipelined, with the stabiliser checked: the recompute
+  // pass for blocks whose first pass saw a tile sum out of range.  S = the
+  // tile's scores (GEMM1 done, masked); P and the sums follow, and when a
+  // lane's tile sum leaves the fp16-safe range m moves up to the tile's row
+  // max, with O and l rescaled, before the tile is exponentiated again.
+  __device__ __forceinline__ void softmax_checked(float16_t (&s)[2], half8_t (&pn)[2][2]) {
+    float sum = exponentiate(s, pn);
+    if (__builtin_amdgcn_ballot_w64(!(sum <= kSumLimit)) != 0) {
+      const float d = fmaxf(tile_max(s), 0.0f);
+      const float alpha = __builtin_amdgcn_exp2f(-(SCALED ? cr : 1.0f) * d);
+      l *= alpha;
+#pragma unroll
+      for (int db = 0; db < 2; ++db)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) o[db][r] *= alpha;
+      sub(s, d);
+      set_m(m + d);
+      sum = exponentiate(s, pn);
+    }
+    l += sum;
   }
   // Row max of a tile (both halves of the row).
   __device__ __forceinline__ float tile_max(const float16_t (&s)[2]) const {
@@ -1042,6 +1193,225 @@ fa2_fwd_pp_kernel(const _Float16* Q, const _Float16* __restrict__ K,
   rows.store(hp.o, geom.o_sr, hp.lse);
 }
 
+// End of a slot-scheduled iteration: this wave's LDS fetches older than its
+// newest kVm have landed and all but its newest kLgkm LDS reads (the
+// operands read ahead for the next iteration) have completed; barrier.
+template <int kVm, int kLgkm>
+__device__ __forceinline__ void sync_ring_ahead() {
+  static_assert(kVm >= 0 && kVm < 64 && kLgkm >= 0 && kLgkm < 16, "waitcnt range");
+  __builtin_amdgcn_sched_barrier(0);
+  asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(%1)\n\ts_barrier" : : "n"(kVm), "n"(kLgkm) : "memory");
+  __builtin_amdgcn_sched_barrier(0);
+}
+
+// ---------------------------------------------------------------------------
+// Slot-scheduled pipeline: W waves of 32 query rows, one key stream.
+//
+// Same work per iteration j as fa2_fwd_kernel (GEMM1, GEMM2 of tile j-1
+// with P(j-1), softmax of tile j), laid out as 16 MFMA slots separated by
+// scheduling fences (slot map: Rows::read_slot / mfma_slot).  Each slot
+// carries two exponentials of the softmax with their fp16 pack and row-sum
+// share, and the LDS read of the A operand of slot +kAhead.  Measured on
+// gfx950: two exponentials and two simple VALU ops issue free under one
+// 32x32x16 MFMA, while longer runs of exponentials between MFMAs stall the
+// matrix core, so the even spread is what keeps it busy.  GEMM1 is skewed
+// by half a tile (key block 1 of tile j in slots 0-6, block 0 of tile j+1
+// in slots 8-14) so that one S buffer serves both the scores being
+// exponentiated and the ones being computed.
+//
+// The operands of the next iteration's first kAhead slots are read at the
+// end of this one (K(j+1) block 1 and V(j)), so no iteration starts by
+// waiting for LDS.  Iteration j reads K(j), K(j+1), V(j-1) and V(j); the
+// barrier ending it publishes K(j+2) and V(j+1).  K is fetched FV+1 tiles
+// ahead and V FV, into rings of FV+2 slots each, with FV-1 fetch groups in
+// flight at a barrier.  Slot reuse: K(X) lands in the slot of K(X-FV-2),
+// last read in iteration X-FV-2 and fetched in iteration X-FV-1; V(X) in
+// that of V(X-FV-2), last read in iteration X-FV-1 and fetched in X-FV.
+//
+// Row sums: a packed-fp16 tree (Rows::sum_slot) on tiles that need no mask,
+// fp32 adds on the masked ones (diagonal / tail), where a short causal row
+// sums a few p.  Blocks whose first pass saw a tile sum out of the
+// fp16-safe range are recomputed by a plain one-tile-per-step checked pass.
+template <int W, int FV, bool CAUSAL, bool SCALED>
+__global__ void __launch_bounds__(64 * W, 2)  // <= 256 VGPRs: 2 waves per SIMD at W = 8
+fa2_fwd_slot_kernel(const _Float16* Q, const _Float16* __restrict__ K,
+                    const _Float16* __restrict__ V, _Float16* O, const Geom geom, int nqb,
+                    float cq, float cr) {
+  constexpr int FK = FV + 1;
+  constexpr int kSlots = FV + 2;  // per ring
+  constexpr int kUnroll = (kSlots % 2 == 0) ? kSlots : 2 * kSlots;
+  constexpr int kBr = 32 * W;
+  constexpr int kSegs = 8 / W;
+  constexpr int kDmaPerIter = 2 * kSegs;
+  constexpr int kAhead = 6;  // slots between an operand's LDS read and its MFMA
+  // LDS reads of the first kAhead slots (K slots: 1, V slots: 2).
+  constexpr int kTailReads = kAhead + kAhead / 2;
+  constexpr int kRingBytes = kSlots * kTileBytes;
+  constexpr int kWgPerCu = (2 * 2 * kRingBytes <= 160 * 1024) ? 2 : 1;
+  static_assert(kSegs * W == 8, "tile split");
+  static_assert(FV >= 2 && FV <= 6, "fetch distance");
+  static_assert(kAhead % 2 == 0 && kAhead < 16, "read-ahead");
+  __shared__ __attribute__((aligned(16))) uint8_t kring[kRingBytes];
+  __shared__ __attribute__((aligned(16))) uint8_t vring[kRingBytes];
+
+  const int lane = threadIdx.x & 63;
+  const int rw = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  int bh, qb;
+  wg_coords<CAUSAL, kWgPerCu>(nqb, bh, qb);
+  const HeadPtrs hp = head_ptrs(geom, bh, Q, K, V, O);
+  const i32x4_t rk = hp.rk, rv = hp.rv;
+  const FetchOff<kSegs> fk = fetch_offsets<kSegs, false>(rw, lane, 2 * geom.k_sr);
+  const FetchOff<kSegs> fv = fetch_offsets<kSegs, true>(rw, lane, 2 * geom.v_sr);
+  const int seq = geom.seq_q;
+  const int q0 = qb * kBr;
+  const StreamRings<kSlots> rings = {kring, vring};
+
+  int ntiles = max(1, (geom.seq_k + kBc - 1) / kBc);
+  if (CAUSAL) ntiles = min(ntiles, causal_tiles(min(q0 + kBr, seq), geom.coff));
+  const int t0 = ntiles;  // iterations 0 .. t0; the last one only drains GEMM2
+  const int last = ntiles - 1;
+
+  // Prologue fetch groups -FK .. -1 (V tiles < 0 read as zeros through the
+  // buffer bound, which also zeroes the slot GEMM2(-1) reads under P = 0),
+  // issued before the Q loads so the two latencies overlap.
+  static_for(std::make_integer_sequence<int, FK>{}, [&](auto i) __attribute__((always_inline)) {
+    constexpr int G = decltype(i)::value - FK;
+    fetch_tile<kSegs>(rk, rings.kslot(Ic<G + FK>{}), G + FK, last, rw, fk);
+    fetch_tile<kSegs>(rv, rings.vslot(Ic<G + FV>{}), G + FV, last, rw, fv);
+  });
+  Rows<CAUSAL, SCALED> rows;
+  rows.init(hp.q, geom.q_sr, lane, q0 + 32 * rw, seq, geom.seq_k, geom.coff, cq, cr);
+
+  // Iterations j < jm need no mask on tiles j and j + 1.
+  int tm = rows.kv_lim >> 6;
+  if (CAUSAL) tm = min(tm, (rows.qd + 1) >> 6);
+  const int jm = max(0, tm - 1);
+
+  // ---- first pass ----
+  sync_ring_ahead<(FK - 1) * kDmaPerIter, 0>();  // K(0)
+  float16_t S[2];
+  half8_t P0[2][2], P1[2][2];
+#pragma unroll
+  for (int a = 0; a < 2; ++a)
+#pragma unroll
+    for (int b = 0; b < 2; ++b) P1[a][b] = (half8_t){0, 0, 0, 0, 0, 0, 0, 0};
+  {
+    // S(0) with the exact row max; iteration 0 recomputes block 1 against it.
+    half8_t ka[2][4];
+    rows.read_k(rings.kslot(Ic<0>{}), ka);
+    rows.gemm1(ka, S);
+  }
+  rows.mask(0, S);
+  rows.first_tile(S);
+  sync_ring_ahead<(FV - 1) * kDmaPerIter, 0>();  // K(1), V(0)
+  half8_t ahead[kAhead];
+  static_for(std::make_integer_sequence<int, kAhead>{}, [&](auto a) __attribute__((always_inline)) {
+    constexpr int L = decltype(a)::value;
+    ahead[L] = rows.template read_slot<L>(rings.kslot(Ic<0>{}), rings.kslot(Ic<1>{}),
+                                          rings.vslot(Ic<-1>{}));
+  });
+
+  uint64_t out_of_range = 0;
+  // Iteration j at unrolled position I (ring slots static): fetch K(j+FK)
+  // and V(j+FV); 16 slots; the range check of tile j's sum; on MASKED
+  // iterations, mask block 1 of tile j (after slot 7, before its
+  // exponentials) and block 0 of tile j+1; publish K(j+2), V(j+1).
+  auto iteration = [&](auto i, int j, half8_t (&P)[2][2], const half8_t (&Pp)[2][2],
+                       auto masked) __attribute__((always_inline)) {
+    constexpr int I = decltype(i)::value;
+    constexpr bool kMasked = decltype(masked)::value;
+    fetch_tile<kSegs>(rk, rings.kslot(Ic<I + FK>{}), j + FK, last, rw, fk);
+    fetch_tile<kSegs>(rv, rings.vslot(Ic<I + FV>{}), j + FV, last, rw, fv);
+    half8_t op[16];
+#pragma unroll
+    for (int a = 0; a < kAhead; ++a) op[a] = ahead[a];
+    half2_t tree[14];
+    float sum[4];
+    static_for(std::make_integer_sequence<int, 16>{}, [&](auto sl) __attribute__((always_inline)) {
+      constexpr int L = decltype(sl)::value;
+      // The MFMA goes first: its operand's wait then never covers the read
+      // issued in the same slot.
+      rows.template mfma_slot<L>(op[L], S, Pp);
+      if constexpr (L + kAhead < 16)
+        op[L + kAhead] = rows.template read_slot<L + kAhead>(
+            rings.kslot(Ic<I>{}), rings.kslot(Ic<I + 1>{}), rings.vslot(Ic<I - 1>{}));
+      else
+        ahead[L + kAhead - 16] = rows.template read_slot<L + kAhead - 16>(
+            rings.kslot(Ic<I + 1>{}), rings.kslot(Ic<I + 2>{}), rings.vslot(Ic<I>{}));
+      rows.template exp_slot<L>(S, P);
+      if constexpr (!kMasked)
+        Rows<CAUSAL, SCALED>::template sum_slot<L>(P, tree);
+      else
+        Rows<CAUSAL, SCALED>::template sum_slot_f32<L>(S, sum, rows.cr);
+      if constexpr (kMasked && L == 7) rows.template mask_block<1>(j, S[1]);
+      __builtin_amdgcn_sched_barrier(0);
+    });
+    const float tot = !kMasked ? Rows<CAUSAL, SCALED>::sum_root(tree)
+                               : (sum[0] + sum[1]) + (sum[2] + sum[3]);
+    rows.l += tot;
+    out_of_range |= __builtin_amdgcn_ballot_w64(!(tot <= kSumLimit));
+    if constexpr (kMasked) rows.template mask_block<0>(j + 1, S[0]);
+    sync_ring_ahead<(FV - 1) * kDmaPerIter, kTailReads>();
+  };
+  auto group = [&](int j0, auto masked) __attribute__((always_inline)) {
+    static_for(std::make_integer_sequence<int, kUnroll>{}, [&](auto i) __attribute__((always_inline)) {
+      constexpr int I = decltype(i)::value;
+      const int j = j0 + I;
+      if (!decltype(masked)::value || j <= t0) {
+        if constexpr (I % 2 == 0)
+          iteration(i, j, P0, P1, masked);
+        else
+          iteration(i, j, P1, P0, masked);
+      }
+    });
+  };
+  {
+    int j0 = 0;
+    for (; j0 + kUnroll <= jm; j0 += kUnroll) group(j0, Ic<false>{});
+    for (; j0 <= t0; j0 += kUnroll) group(j0, Ic<true>{});
+  }
+
+  // ---- checked pass, when any wave saw a tile sum out of range ----
+  // The work-group's flag lives in K ring slot 1, which the checked pass
+  // never refills (the rings are idle here: every wave has drained its
+  // fetches and reads before the first barrier).  No extra LDS, so two
+  // 80 KiB work-groups still fit one CU.
+  __builtin_amdgcn_s_waitcnt(0);
+  int* redo = reinterpret_cast<int*>(rings.kslot(Ic<1>{}));
+  __syncthreads();
+  if (threadIdx.x == 0) *redo = 0;
+  __syncthreads();
+  if (out_of_range != 0 && lane == 0) *redo = 1;
+  __syncthreads();
+  if (*redo) {
+    rows.launder();
+    rows.reset();
+    for (int t = 0; t < ntiles; ++t) {
+      fetch_tile<kSegs>(rk, rings.kslot(Ic<0>{}), t, last, rw, fk);
+      fetch_tile<kSegs>(rv, rings.vslot(Ic<0>{}), t, last, rw, fv);
+      sync_ring_ahead<0, 0>();
+      float16_t Sc[2];
+      half8_t Pc[2][2];
+      {
+        half8_t ka[2][4];
+        rows.read_k(rings.kslot(Ic<0>{}), ka);
+        rows.gemm1(ka, Sc);
+      }
+      rows.mask(t, Sc);
+      if (t == 0) rows.first_tile(Sc);
+      rows.softmax_checked(Sc, Pc);
+      {
+        half8_t va[2][4];
+        rows.read_v(rings.vslot(Ic<0>{}), va);
+        rows.gemm2(va, Pc);
+      }
+      sync_ring_ahead<0, 0>();  // every wave's reads done before the next fetch
+    }
+  }
+  rows.launder();
+  rows.store(hp.o, geom.o_sr, hp.lse);
+}
+
 // ---------------------------------------------------------------------------
 // Split-KV combine: one wave per query row merges the nsplit partials of the
 // row (O unnormalised at stabiliser m_s, row sum l_s) at their largest m:
@@ -1166,6 +1536,21 @@ struct PingPongLaunch {
   };
 };
 
+template <int W, int FV>
+struct SlotLaunch {
+  template <bool C, bool S>
+  struct L {
+    static hipError_t run(const FwdArgs& a, const Geom& g, dim3 grid, int nqb, float cq, float cr,
+                          hipStream_t st) {
+      hipLaunchKernelGGL((fa2_fwd_slot_kernel<W, FV, C, S>), grid, dim3(64 * W), 0, st,
+                         static_cast<const _Float16*>(a.q), static_cast<const _Float16*>(a.k),
+                         static_cast<const _Float16*>(a.v), static_cast<_Float16*>(a.o), g, nqb,
+                         cq, cr);
+      return hipSuccess;
+    }
+  };
+};
+
 // Split-KV: the chunk kernel (grid = query blocks x chunks) and the
 // combine kernel, back to back on the stream.
 template <int W, int D>
@@ -1219,6 +1604,8 @@ const Fa2Config kFa2Configs[kNumFa2Configs] = {
     {8, "br256_bc64_w8"},
     {8, "br256_bc64_w8_pingpong"},
     {8, "br128_bc64_w4_split2"},
+    {8, "br256_bc64_w8_slot"},
+    {4, "br128_bc64_w4_slot"},
 };
 
 // Fetch distance: three tiles ahead where LDS allows (64 KiB of rings per
@@ -1231,6 +1618,8 @@ hipError_t launch_fa2(const FwdArgs& a, int cfg, hipStream_t stream) {
     case 3: return dispatch<PipelinedLaunch<8, 3, 1>::L>(a, stream, 256);
     case 4: return dispatch<PingPongLaunch<3>::L>(a, stream, 256);
     case 5: return dispatch<PipelinedLaunch<4, 3, 2>::L>(a, stream, 128);
+    case 6: return dispatch<SlotLaunch<8, 4>::L>(a, stream, 256);
+    case 7: return dispatch<SlotLaunch<4, 3>::L>(a, stream, 128);
     default: return hipErrorInvalidValue;
   }
 }

@@ -37,7 +37,7 @@ struct Fa2Config {
   const char* name;
 };
 
-constexpr int kNumFa2Configs = 6;
+constexpr int kNumFa2Configs = 8;
 extern const Fa2Config kFa2Configs[kNumFa2Configs];
 
 // Launches the FA2 kernel for configuration `cfg` on `stream`.

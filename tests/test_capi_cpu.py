@@ -28,11 +28,12 @@ def test_library_loads_and_exports_header_symbols():
 
 
 def test_config_table():
-    assert capi.num_configs() == 6
-    names = [capi.config_name(i) for i in range(6)]
+    assert capi.num_configs() == 8
+    names = [capi.config_name(i) for i in range(8)]
     assert names == ["br32_bc64_w1", "br64_bc64_w2", "br128_bc64_w4", "br256_bc64_w8",
-                     "br256_bc64_w8_pingpong", "br128_bc64_w4_split2"]
-    assert capi.config_name(6) is None and capi.config_name(-1) is None
+                     "br256_bc64_w8_pingpong", "br128_bc64_w4_split2", "br256_bc64_w8_slot",
+                     "br128_bc64_w4_slot"]
+    assert capi.config_name(8) is None and capi.config_name(-1) is None
 
 
 def _p(**kw):
@@ -75,7 +76,7 @@ def _ex(q_stride=(8 * 4096 * 64, 4096 * 64, 64), k_stride=None, v_stride=None, o
 def test_ex_null_and_config():
     lib = capi.load()
     assert lib.fl_attn_fwd_f16_ex(None, -1, None) == capi.FL_ERR_INVALID_ARGUMENT
-    assert capi.fwd_ex(_ex(), config=6) == capi.FL_ERR_BAD_CONFIG
+    assert capi.fwd_ex(_ex(), config=8) == capi.FL_ERR_BAD_CONFIG
     assert capi.fwd_ex(_ex(head_dim=128)) == capi.FL_ERR_UNSUPPORTED
 
 
@@ -137,7 +138,7 @@ def test_non_finite_scale():
 
 
 def test_bad_config():
-    assert capi.fwd(_p(), config=6) == capi.FL_ERR_BAD_CONFIG
+    assert capi.fwd(_p(), config=8) == capi.FL_ERR_BAD_CONFIG
     assert capi.fwd(_p(), config=-2) == capi.FL_ERR_BAD_CONFIG
 
 
@@ -157,19 +158,19 @@ def test_naive_limits():
 
 def test_dispatcher_choices():
     sel = lambda **kw: capi.select_config(_p(**kw))  # noqa: E731
-    # non-causal: 8-wave 256-row groups when there is one per CU
-    assert sel(batch=2, heads=8, seq_q=4096) == 3      # 256 groups
-    assert sel(batch=1, heads=16, seq_q=16384) == 3
-    assert sel(batch=32, heads=32, seq_q=256) == 3
+    # non-causal: 8-wave 256-row slot-scheduled groups when there is one per CU
+    assert sel(batch=2, heads=8, seq_q=4096) == 6      # 256 groups
+    assert sel(batch=1, heads=16, seq_q=16384) == 6
+    assert sel(batch=32, heads=32, seq_q=256) == 6
     # fewer than two 128-row groups per CU at N >= 2048: split key range
     assert sel(batch=2, heads=8, seq_q=2048) == 5      # 256 groups of 128 rows
     assert sel(batch=1, heads=1, seq_q=4096) == 5
-    # causal: 128-row groups balanced by dispatch order
-    assert sel(batch=2, heads=8, seq_q=4096, causal=True) == 2
-    assert sel(batch=1, heads=16, seq_q=16384, causal=True) == 2
-    assert sel(batch=32, heads=32, seq_q=256, causal=True) == 2
+    # causal: 128-row slot-scheduled groups balanced by dispatch order
+    assert sel(batch=2, heads=8, seq_q=4096, causal=True) == 7
+    assert sel(batch=1, heads=16, seq_q=16384, causal=True) == 7
+    assert sel(batch=32, heads=32, seq_q=256, causal=True) == 7
     # small problems: smaller groups
-    assert sel(batch=2, heads=8, seq_q=512) == 2       # 64 groups of 128 rows
+    assert sel(batch=2, heads=8, seq_q=512) == 7       # 64 groups of 128 rows
     assert sel(batch=2, heads=4, seq_q=512) == 1       # 64 groups of 64 rows
     assert sel(batch=1, heads=1, seq_q=128) == 0
     assert sel(head_dim=80) == -1

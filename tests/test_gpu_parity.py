@@ -18,7 +18,7 @@ from oracle import error_stats
 pytestmark = pytest.mark.gpu
 
 GOLDEN = os.path.join(os.path.dirname(__file__), "golden")
-NCFG = 6  # tile configurations exported by the library
+NCFG = 8  # tile configurations exported by the library
 SPLIT_CFGS = [5]  # the key-range-split configuration
 
 
@@ -26,7 +26,7 @@ def test_num_configs():
     assert capi.num_configs() == NCFG
     assert [capi.config_name(i) for i in range(NCFG)] == [
         "br32_bc64_w1", "br64_bc64_w2", "br128_bc64_w4", "br256_bc64_w8", "br256_bc64_w8_pingpong",
-        "br128_bc64_w4_split2"]
+        "br128_bc64_w4_split2", "br256_bc64_w8_slot", "br128_bc64_w4_slot"]
 
 
 @pytest.mark.parametrize("config", list(range(NCFG)))
@@ -50,7 +50,7 @@ def test_benchmark_configs(cuda, name, causal):
     print(f"{name} causal={causal}: max-abs {mx:.2e} mean-abs {mean:.2e}")
 
 
-@pytest.mark.parametrize("config", [2, 3] + SPLIT_CFGS)
+@pytest.mark.parametrize("config", [2, 3, 6, 7] + SPLIT_CFGS)
 @pytest.mark.parametrize("causal", [False, True])
 def test_headline_each_config(cuda, config, causal):
     w = WORKLOADS["C2_headline_B2H8N4096"]
