@@ -30,6 +30,7 @@ EXPORTED = (
     "fl_attn_config_name",
     "fl_attn_select_config",
     "fl_attn_fwd_f16_ex",
+    "fl_attn_fwd_bf16_ex",
     "fl_attn_splitkv_workspace_bytes",
     "fl_attn_fwd_f16_splitkv",
 )
@@ -101,6 +102,9 @@ def load(path: str = LIB_PATH) -> ctypes.CDLL:
     lib.fl_attn_fwd_f16_ex.argtypes = [ctypes.POINTER(FlAttnParamsEx), ctypes.c_int32,
                                        ctypes.c_void_p]
     lib.fl_attn_fwd_f16_ex.restype = ctypes.c_int
+    lib.fl_attn_fwd_bf16_ex.argtypes = [ctypes.POINTER(FlAttnParamsEx), ctypes.c_int32,
+                                        ctypes.c_void_p]
+    lib.fl_attn_fwd_bf16_ex.restype = ctypes.c_int
     lib.fl_attn_splitkv_workspace_bytes.argtypes = [ctypes.POINTER(FlAttnParamsEx), ctypes.c_int32]
     lib.fl_attn_splitkv_workspace_bytes.restype = ctypes.c_int64
     lib.fl_attn_fwd_f16_splitkv.argtypes = [ctypes.POINTER(FlAttnParamsEx), ctypes.c_int32,
@@ -136,6 +140,11 @@ def fwd(params: FlAttnParams, stream: int = 0, config: int = -1) -> int:
 def fwd_ex(params: FlAttnParamsEx, stream: int = 0, config: int = -1) -> int:
     """``fl_attn_fwd_f16_ex``; returns the status code."""
     return load().fl_attn_fwd_f16_ex(ctypes.byref(params), config, stream or None)
+
+
+def fwd_bf16_ex(params: FlAttnParamsEx, stream: int = 0, config: int = -1) -> int:
+    """``fl_attn_fwd_bf16_ex``; returns the status code."""
+    return load().fl_attn_fwd_bf16_ex(ctypes.byref(params), config, stream or None)
 
 
 def splitkv_workspace_bytes(params: FlAttnParamsEx, num_splits: int = 0) -> int:

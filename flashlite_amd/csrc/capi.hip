@@ -74,6 +74,7 @@ int check_common(const fl_attn_params* p, fl::FwdArgs* a, const char* who) {
   a->scale_log2 = c;
   a->negate = scale < 0.0 ? 1 : 0;
   a->causal = p->causal ? 1 : 0;
+  a->dtype = fl::kDtypeF16;
   // contiguous [B, H, N, D]
   const int64_t d = p->head_dim;
   a->q_sr = a->o_sr = a->k_sr = a->v_sr = (int)d;
@@ -121,16 +122,23 @@ int select_fa2(const fl::FwdArgs& a) {
   return 0;                                                          // br32_bc64_w1
 }
 
-int check_fa2(const fl_attn_params* p, fl::FwdArgs* a, const char* who = "fl_attn_fwd_f16") {
+// `wide`: head_dim 128 accepted as well (the _ex entries; beyond the
+// reference, whose kernels hard-reject D != 64, kernel_flash2.cu:756-757).
+int check_fa2(const fl_attn_params* p, fl::FwdArgs* a, const char* who = "fl_attn_fwd_f16",
+              bool wide = false) {
   int rc = check_common(p, a, who);
   if (rc != FL_OK) return rc;
-  if (p->head_dim != 64)
+  if (wide && p->head_dim != 64 && p->head_dim != 128)
+    return fail(FL_ERR_UNSUPPORTED, "%s: head_dim must be 64 or 128 (got %lld)", who,
+                (long long)p->head_dim);
+  if (!wide && p->head_dim != 64)
     return fail(FL_ERR_UNSUPPORTED, "FlashLite WMMA kernel currently requires head_dim == 64");
   // K/V tiles are fetched through 32-bit buffer offsets within one head
-  // (N_k rows of 128 bytes, plus one tile of slack).
-  if (a->seq_k > (INT32_MAX / 128) - 128)
+  // (N_k rows of 2*D bytes, plus one tile of slack).
+  const int row_bytes = 2 * a->head_dim;
+  if (a->seq_k > (INT32_MAX / row_bytes) - 128)
     return fail(FL_ERR_UNSUPPORTED, "%s: N_k=%d exceeds the per-head addressing limit (%d)", who,
-                a->seq_k, (INT32_MAX / 128) - 128);
+                a->seq_k, (INT32_MAX / row_bytes) - 128);
   // Grid = ceil(N/32) * B*H work-groups at the smallest tile; per-head
   // offsets are 64-bit in the kernel.
   if (((int64_t)a->seq + 31) / 32 * (int64_t)a->batch_heads > INT32_MAX)
@@ -141,29 +149,29 @@ int check_fa2(const fl_attn_params* p, fl::FwdArgs* a, const char* who = "fl_att
 // Strides of one tensor of fl_attn_fwd_f16_ex: every row 16-byte aligned
 // (strides in multiples of 8 halfs), rows at least D apart, and row offsets
 // that fit the kernels' 32-bit row stride.
-int check_strides(const int64_t st[3], const char* name, const char* who) {
+int check_strides(const int64_t st[3], int64_t d, const char* name, const char* who) {
   for (int i = 0; i < 3; ++i)
     if (st[i] < 0 || st[i] % 8 != 0)
       return fail(FL_ERR_UNSUPPORTED, "%s: %s strides must be non-negative multiples of 8 elements "
                   "(got %lld, %lld, %lld)", who, name, (long long)st[0], (long long)st[1],
                   (long long)st[2]);
-  if (st[2] < 64 || st[2] > INT32_MAX / 2)
-    return fail(FL_ERR_UNSUPPORTED, "%s: %s row stride %lld must be in [64, 2^30)", who, name,
-                (long long)st[2]);
+  if (st[2] < d || st[2] > INT32_MAX / 2)
+    return fail(FL_ERR_UNSUPPORTED, "%s: %s row stride %lld must be in [%lld, 2^30)", who, name,
+                (long long)st[2], (long long)d);
   return FL_OK;
 }
 
 // Checks of an fl_attn_params_ex and its strides; fills `a`.
-int check_ex(const fl_attn_params_ex* p, fl::FwdArgs* a, const char* who) {
+int check_ex(const fl_attn_params_ex* p, fl::FwdArgs* a, const char* who, bool wide = false) {
   if (p == nullptr) return fail(FL_ERR_INVALID_ARGUMENT, "%s: params is NULL", who);
-  int rc = check_fa2(&p->base, a, who);
+  int rc = check_fa2(&p->base, a, who, wide);
   if (rc != FL_OK) return rc;
   const int64_t* st[4] = {p->q_stride, p->k_stride, p->v_stride, p->o_stride};
   const char* names[4] = {"q", "k", "v", "o"};
   const bool no_keys = a->seq_k == 0;  // k and v are never read
   for (int i = 0; i < 4; ++i) {
     if (no_keys && (i == 1 || i == 2)) continue;
-    rc = check_strides(st[i], names[i], who);
+    rc = check_strides(st[i], a->head_dim, names[i], who);
     if (rc != FL_OK) return rc;
   }
   for (int i = 1; i <= 2; ++i)
@@ -233,6 +241,42 @@ KvPlan plan_kvsplit(const fl::FwdArgs& a, int32_t requested) {
   return p;
 }
 
+// fp16 at head_dim 64 has every tile configuration; bf16 and head_dim 128
+// have the two slot-scheduled ones, chosen by the same rule as the fp16
+// dispatcher's first choices.
+bool narrow_configs(const fl::FwdArgs& a) {
+  return a.dtype != fl::kDtypeF16 || a.head_dim != 64;
+}
+
+int select_any(const fl::FwdArgs& a) {
+  if (!narrow_configs(a)) return select_fa2(a);
+  constexpr int64_t kCus = 256;
+  const int64_t wgs256 = (a.seq + 255) / 256 * (int64_t)a.batch_heads;
+  return (!a.causal && wgs256 >= kCus) ? fl::kSlotW8Config : fl::kSlotW4Config;
+}
+
+int fwd_ex(const fl_attn_params_ex* p, int32_t config, void* stream, int dtype, const char* who) {
+  fl::FwdArgs a;
+  int rc = check_ex(p, &a, who, /*wide=*/true);
+  if (rc != FL_OK) return rc;
+  a.dtype = dtype;
+  if (config < -1 || config >= fl::kNumFa2Configs)
+    return fail(FL_ERR_BAD_CONFIG, "%s: config %d out of range [-1, %d)", who, (int)config,
+                fl::kNumFa2Configs);
+  if (narrow_configs(a) && config >= 0 && config != fl::kSlotW8Config &&
+      config != fl::kSlotW4Config)
+    return fail(FL_ERR_BAD_CONFIG, "%s: config %d is not built for %s at head_dim %d (use -1, %d or %d)",
+                who, (int)config, dtype == fl::kDtypeBF16 ? "bf16" : "fp16", a.head_dim,
+                fl::kSlotW8Config, fl::kSlotW4Config);
+  if (empty_problem(a)) return FL_OK;
+  rc = check_pointers(&p->base, &a, who, 16);
+  if (rc != FL_OK) return rc;
+  const int cfg = config < 0 ? select_any(a) : config;
+  const hipError_t e = fl::launch_fa2(a, cfg, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return fail(FL_ERR_LAUNCH, "%s: launch failed: %s", who, hipGetErrorString(e));
+  return FL_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -274,20 +318,11 @@ int fl_attn_fwd_f16(const fl_attn_params* p, void* stream) {
 }
 
 int fl_attn_fwd_f16_ex(const fl_attn_params_ex* p, int32_t config, void* stream) {
-  const char* who = "fl_attn_fwd_f16_ex";
-  fl::FwdArgs a;
-  int rc = check_ex(p, &a, who);
-  if (rc != FL_OK) return rc;
-  if (config < -1 || config >= fl::kNumFa2Configs)
-    return fail(FL_ERR_BAD_CONFIG, "%s: config %d out of range [-1, %d)", who, (int)config,
-                fl::kNumFa2Configs);
-  if (empty_problem(a)) return FL_OK;
-  rc = check_pointers(&p->base, &a, who, 16);
-  if (rc != FL_OK) return rc;
-  const int cfg = config < 0 ? select_fa2(a) : config;
-  const hipError_t e = fl::launch_fa2(a, cfg, static_cast<hipStream_t>(stream));
-  if (e != hipSuccess) return fail(FL_ERR_LAUNCH, "%s: launch failed: %s", who, hipGetErrorString(e));
-  return FL_OK;
+  return fwd_ex(p, config, stream, fl::kDtypeF16, "fl_attn_fwd_f16_ex");
+}
+
+int fl_attn_fwd_bf16_ex(const fl_attn_params_ex* p, int32_t config, void* stream) {
+  return fwd_ex(p, config, stream, fl::kDtypeBF16, "fl_attn_fwd_bf16_ex");
 }
 
 int64_t fl_attn_splitkv_workspace_bytes(const fl_attn_params_ex* p, int32_t num_splits) {

@@ -96,6 +96,29 @@ typedef short short4_t __attribute__((ext_vector_type(4)));
 typedef float float16_t __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 typedef int i32x4_t __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
+
+// Operand vectors and the 32x32x16 MFMA of one 16-bit element type (fp16:
+// the reference's type; bf16: beyond it).  Both accumulate in fp32.
+template <class T>
+struct Elem;
+template <>
+struct Elem<_Float16> {
+  using v8 = half8_t;
+  using v4 = half4_t;
+  __device__ __forceinline__ static float16_t mfma(const v8& a, const v8& b, const float16_t& c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+  }
+};
+template <>
+struct Elem<__bf16> {
+  using v8 = bf16x8_t;
+  using v4 = bf16x4_t;
+  __device__ __forceinline__ static float16_t mfma(const v8& a, const v8& b, const float16_t& c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+  }
+};
 
 constexpr int kD = 64;                       // head dim
 constexpr int kBc = 64;                      // keys per KV tile
@@ -151,23 +174,25 @@ struct Geom {
 constexpr int kPartStride = 68;
 
 // Per-head base pointers and buffer resources of a work-group.
+template <class T = _Float16>
 struct HeadPtrs {
-  const _Float16* q;
-  _Float16* o;
+  const T* q;
+  T* o;
   float* lse;
   i32x4_t rk, rv;
 };
 
-__device__ __forceinline__ HeadPtrs head_ptrs(const Geom& g, int bh, const _Float16* Q,
-                                              const _Float16* K, const _Float16* V, _Float16* O) {
+template <class T, int kRowB = kRowBytes>
+__device__ __forceinline__ HeadPtrs<T> head_ptrs(const Geom& g, int bh, const T* Q, const T* K,
+                                                 const T* V, T* O) {
   const int b = bh / g.heads, h = bh - b * g.heads;
-  HeadPtrs p;
+  HeadPtrs<T> p;
   p.q = Q + (b * g.q_sb + h * g.q_sh);
   p.o = O + (b * g.o_sb + h * g.o_sh);
   p.lse = g.lse ? g.lse + (long long)bh * g.seq_q : nullptr;
-  // num_records covers the last row's 128 bytes; later rows read as zeros.
-  const int kb = g.seq_k > 0 ? (g.seq_k - 1) * (2 * g.k_sr) + kRowBytes : 0;
-  const int vb = g.seq_k > 0 ? (g.seq_k - 1) * (2 * g.v_sr) + kRowBytes : 0;
+  // num_records covers the last row's kRowB bytes; later rows read as zeros.
+  const int kb = g.seq_k > 0 ? (g.seq_k - 1) * (2 * g.k_sr) + kRowB : 0;
+  const int vb = g.seq_k > 0 ? (g.seq_k - 1) * (2 * g.v_sr) + kRowB : 0;
   p.rk = buffer_rsrc(K + (b * g.k_sb + h * g.k_sh), kb);
   p.rv = buffer_rsrc(V + (b * g.v_sb + h * g.v_sh), vb);
   return p;
@@ -181,10 +206,11 @@ __device__ __forceinline__ int causal_tiles(int q_end, int coff) {
   return last_key < 0 ? 1 : last_key / kBc + 1;
 }
 
-__device__ __forceinline__ half4_t lds_read_tr(const uint8_t* p) {
+template <class V4 = half4_t>
+__device__ __forceinline__ V4 lds_read_tr(const uint8_t* p) {
   short4_t s = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
       (short4_t __attribute__((address_space(3)))*)(p));
-  return __builtin_bit_cast(half4_t, s);
+  return __builtin_bit_cast(V4, s);
 }
 
 // End of a step: this wave's LDS fetches older than its newest `pending`
@@ -310,21 +336,24 @@ __device__ __forceinline__ void fetch_tile(const i32x4_t& rs, const uint8_t* slo
 
 // The 32 query rows one wave owns: prescaled Q, running max, row sums and
 // O accumulator, plus the tile-level building blocks.
-template <bool CAUSAL, bool SCALED>
+template <bool CAUSAL, bool SCALED, class T = _Float16>
 struct Rows {
+  using E = Elem<T>;
+  using V8 = typename E::v8;
+  using V4 = typename E::v4;
   int g, col, qw, my_q, seq;
   int qd, my_d;     // causal diagonals: the last key visible to row qw / my_q
   int kv_lim;       // keys >= kv_lim are masked (N_k, or the end of a split range)
   int tr_row, tr_col;
   float cr;
-  half8_t qf[4];    // Q'^T B-operand
+  V8 qf[4];    // Q'^T B-operand
   float16_t o[2];   // O^T accumulator, d-blocks 0 / 1
   float16_t bias;   // -m broadcast, GEMM1's accumulator input
   float m;          // running stabiliser, units of t = q'.k
   float l;          // this lane's share of the row sum
-  half8_t p[2][2];  // fp16 P^T B-operands of the last softmaxed tile
+  V8 p[2][2];  // fp16 P^T B-operands of the last softmaxed tile
 
-  __device__ __forceinline__ void init(const _Float16* Qh, int q_sr, int lane, int qw_, int seq_,
+  __device__ __forceinline__ void init(const T* Qh, int q_sr, int lane, int qw_, int seq_,
                                        int seq_k, int coff, float cq, float cr_) {
     g = lane >> 5;
     col = lane & 31;
@@ -346,12 +375,12 @@ struct Rows {
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
       if (my_q < seq) {
-        const half8_t raw =
-            *reinterpret_cast<const half8_t*>(Qh + (long long)my_q * q_sr + 16 * s + 8 * g);
+        const V8 raw =
+            *reinterpret_cast<const V8*>(Qh + (long long)my_q * q_sr + 16 * s + 8 * g);
 #pragma unroll
-        for (int e = 0; e < 8; ++e) qf[s][e] = (_Float16)((float)raw[e] * cq);
+        for (int e = 0; e < 8; ++e) qf[s][e] = (T)((float)raw[e] * cq);
       } else {
-        qf[s] = (half8_t){0, 0, 0, 0, 0, 0, 0, 0};
+        qf[s] = (V8){0, 0, 0, 0, 0, 0, 0, 0};
       }
     }
 #pragma unroll
@@ -371,7 +400,7 @@ struct Rows {
     asm volatile("" : "+v"(col), "+v"(g), "+v"(my_q), "+v"(tr_row), "+v"(tr_col));
   }
   // K operands of GEMM1 (both 32-key blocks, 4 head-dim steps each).
-  __device__ __forceinline__ void read_k(const uint8_t* kt, half8_t (&ka)[2][4]) const {
+  __device__ __forceinline__ void read_k(const uint8_t* kt, V8 (&ka)[2][4]) const {
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) {
       const int row = 32 * kb + col;
@@ -379,12 +408,12 @@ struct Rows {
       for (int st = 0; st < 4; ++st) {
         const int ch = 2 * st + g;
         ka[kb][st] =
-            *reinterpret_cast<const half8_t*>(kt + row * kRowBytes + 16 * (ch ^ k_swz(row)));
+            *reinterpret_cast<const V8*>(kt + row * kRowBytes + 16 * (ch ^ k_swz(row)));
       }
     }
   }
   // V^T operands of GEMM2 (2 d-blocks x 4 16-key steps).
-  __device__ __forceinline__ void read_v(const uint8_t* vt, half8_t (&va)[2][4]) const {
+  __device__ __forceinline__ void read_v(const uint8_t* vt, V8 (&va)[2][4]) const {
 #pragma unroll
     for (int db = 0; db < 2; ++db)
 #pragma unroll
@@ -393,58 +422,57 @@ struct Rows {
         const int r2 = r1 + 8;
         const int dcol = 32 * db + tr_col;
         const int ch = dcol >> 3, hb = ((dcol >> 2) & 1) * 8;
-        const half4_t lo = lds_read_tr(vt + r1 * kRowBytes + 16 * (ch ^ v_swz(r1)) + hb);
-        const half4_t hi = lds_read_tr(vt + r2 * kRowBytes + 16 * (ch ^ v_swz(r2)) + hb);
+        const V4 lo = lds_read_tr<V4>(vt + r1 * kRowBytes + 16 * (ch ^ v_swz(r1)) + hb);
+        const V4 hi = lds_read_tr<V4>(vt + r2 * kRowBytes + 16 * (ch ^ v_swz(r2)) + hb);
         va[db][t] = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
       }
   }
   // GEMM1: s[kb] = K[32kb + row] . Q'^T - m.
-  __device__ __forceinline__ void gemm1(const half8_t (&ka)[2][4], float16_t (&s)[2]) const {
+  __device__ __forceinline__ void gemm1(const V8 (&ka)[2][4], float16_t (&s)[2]) const {
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
       for (int st = 0; st < 4; ++st)
-        s[kb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka[kb][st], qf[st], st == 0 ? bias : s[kb],
-                                                       0, 0, 0);
+        s[kb] = E::mfma(ka[kb][st], qf[st], st == 0 ? bias : s[kb]);
   }
   // GEMM2: O^T += V^T . P^T
-  __device__ __forceinline__ void gemm2(const half8_t (&va)[2][4], const half8_t (&pp)[2][2]) {
+  __device__ __forceinline__ void gemm2(const V8 (&va)[2][4], const V8 (&pp)[2][2]) {
 #pragma unroll
     for (int db = 0; db < 2; ++db)
 #pragma unroll
       for (int t = 0; t < 4; ++t)
-        o[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va[db][t], pp[t >> 1][t & 1], o[db], 0, 0, 0);
+        o[db] = E::mfma(va[db][t], pp[t >> 1][t & 1], o[db]);
   }
-  __device__ __forceinline__ void gemm2(const half8_t (&va)[2][4]) { gemm2(va, p); }
+  __device__ __forceinline__ void gemm2(const V8 (&va)[2][4]) { gemm2(va, p); }
   // GEMM1 of one tile and GEMM2 of another, issued as four interleaved
   // accumulation chains (s[0], o[0], s[1], o[1]) so consecutive MFMAs never
   // depend on each other.
-  __device__ __forceinline__ void gemm12(const half8_t (&ka)[2][4], float16_t (&s)[2],
-                                         const half8_t (&va)[2][4], const half8_t (&pp)[2][2]) {
+  __device__ __forceinline__ void gemm12(const V8 (&ka)[2][4], float16_t (&s)[2],
+                                         const V8 (&va)[2][4], const V8 (&pp)[2][2]) {
 #pragma unroll
     for (int st = 0; st < 4; ++st) {
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
-        s[h] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka[h][st], qf[st], st == 0 ? bias : s[h], 0, 0, 0);
-        o[h] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va[h][st], pp[st >> 1][st & 1], o[h], 0, 0, 0);
+        s[h] = E::mfma(ka[h][st], qf[st], st == 0 ? bias : s[h]);
+        o[h] = E::mfma(va[h][st], pp[st >> 1][st & 1], o[h]);
       }
     }
   }
   // A operands of single MFMAs: 32 K rows of key block kb at head-dim step
   // st (one ds_read_b128), or V^T of head-dim block db at key step t (two
   // ds_read_b64_tr_b16); the same reads as read_k / read_v.
-  __device__ __forceinline__ half8_t read_k_op(const uint8_t* kt, int kb, int st) const {
+  __device__ __forceinline__ V8 read_k_op(const uint8_t* kt, int kb, int st) const {
     const int row = 32 * kb + col;
     const int ch = 2 * st + g;
-    return *reinterpret_cast<const half8_t*>(kt + row * kRowBytes + 16 * (ch ^ k_swz(row)));
+    return *reinterpret_cast<const V8*>(kt + row * kRowBytes + 16 * (ch ^ k_swz(row)));
   }
-  __device__ __forceinline__ half8_t read_v_op(const uint8_t* vt, int db, int t) const {
+  __device__ __forceinline__ V8 read_v_op(const uint8_t* vt, int db, int t) const {
     const int r1 = 16 * t + tr_row;
     const int r2 = r1 + 8;
     const int dcol = 32 * db + tr_col;
     const int ch = dcol >> 3, hb = ((dcol >> 2) & 1) * 8;
-    const half4_t lo = lds_read_tr(vt + r1 * kRowBytes + 16 * (ch ^ v_swz(r1)) + hb);
-    const half4_t hi = lds_read_tr(vt + r2 * kRowBytes + 16 * (ch ^ v_swz(r2)) + hb);
+    const V4 lo = lds_read_tr<V4>(vt + r1 * kRowBytes + 16 * (ch ^ v_swz(r1)) + hb);
+    const V4 hi = lds_read_tr<V4>(vt + r2 * kRowBytes + 16 * (ch ^ v_swz(r2)) + hb);
     return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
   }
   // Slot map of the skewed slot schedule (fa2_fwd_slot_kernel).  Iteration
@@ -456,7 +484,7 @@ struct Rows {
   // 8-15 read S[1] (tile j), so each block is rewritten only after its
   // scores are consumed: one S buffer instead of two.
   template <int L>
-  __device__ __forceinline__ half8_t read_slot(const uint8_t* k_cur, const uint8_t* k_next,
+  __device__ __forceinline__ V8 read_slot(const uint8_t* k_cur, const uint8_t* k_next,
                                                const uint8_t* vt) const {
     constexpr int u = L >> 1;
     if constexpr ((L & 1) == 0)
@@ -465,22 +493,22 @@ struct Rows {
       return read_v_op(vt, u & 1, u >> 1);
   }
   template <int L>
-  __device__ __forceinline__ void mfma_slot(const half8_t& a, float16_t (&s)[2],
-                                            const half8_t (&pp)[2][2]) {
+  __device__ __forceinline__ void mfma_slot(const V8& a, float16_t (&s)[2],
+                                            const V8 (&pp)[2][2]) {
     constexpr int u = L >> 1;
     if constexpr ((L & 1) == 0) {
       constexpr int kb = u < 4 ? 1 : 0, st = u & 3;
-      s[kb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, qf[st], st == 0 ? bias : s[kb], 0, 0, 0);
+      s[kb] = E::mfma(a, qf[st], st == 0 ? bias : s[kb]);
     } else {
       constexpr int db = u & 1, t = u >> 1;
-      o[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, pp[t >> 1][t & 1], o[db], 0, 0, 0);
+      o[db] = E::mfma(a, pp[t >> 1][t & 1], o[db]);
     }
   }
   // Softmax share of slot I: scores 2(I%8), 2(I%8)+1 of key block I/8 ->
   // two exponentials and one fp16 pack into dword I of the tile's P operand
   // (exponentiate() spread over 16 slots).
   template <int I>
-  __device__ __forceinline__ void exp_slot(const float16_t (&s)[2], half8_t (&pn)[2][2]) const {
+  __device__ __forceinline__ void exp_slot(const float16_t (&s)[2], V8 (&pn)[2][2]) const {
     constexpr int kb = I >> 3, r = 2 * (I & 7), h = r >> 3, e = r & 7;
     float x0 = s[kb][r], x1 = s[kb][r + 1];
     if (SCALED) {
@@ -488,8 +516,8 @@ struct Rows {
       x1 *= cr;
     }
     const float e0 = __builtin_amdgcn_exp2f(x0), e1 = __builtin_amdgcn_exp2f(x1);
-    pn[kb][h][e] = (_Float16)e0;
-    pn[kb][h][e + 1] = (_Float16)e1;
+    pn[kb][h][e] = (T)e0;
+    pn[kb][h][e + 1] = (T)e1;
   }
   // Dword i (0-15) of a tile's P operand: the fp16 pair of slot i.
   __device__ __forceinline__ static half2_t p_pair(const half8_t (&pn)[2][2], int i) {
@@ -574,7 +602,7 @@ struct Rows {
   // tile's scores (GEMM1 done, masked); P and the sums follow, and when a
   // lane's tile sum leaves the fp16-safe range m moves up to the tile's row
   // max, with O and l rescaled, before the tile is exponentiated again.
-  __device__ __forceinline__ void softmax_checked(float16_t (&s)[2], half8_t (&pn)[2][2]) {
+  __device__ __forceinline__ void softmax_checked(float16_t (&s)[2], V8 (&pn)[2][2]) {
     float sum = exponentiate(s, pn);
     if (__builtin_amdgcn_ballot_w64(!(sum <= kSumLimit)) != 0) {
       const float d = fmaxf(tile_max(s), 0.0f);
@@ -624,7 +652,7 @@ struct Rows {
   // this lane's sum of p, taken in fp32 over four chains.  (The row sum uses
   // v_add_f32 rather than v_dot2_f32_f16 on the packed p: on gfx950 the dot2
   // instructions do not issue alongside MFMA work, adds and conversions do.)
-  __device__ __forceinline__ float exponentiate(const float16_t (&s)[2], half8_t (&pn)[2][2]) const {
+  __device__ __forceinline__ float exponentiate(const float16_t (&s)[2], V8 (&pn)[2][2]) const {
     float sum[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb)
@@ -638,8 +666,8 @@ struct Rows {
             x1 *= cr;
           }
           const float e0 = __builtin_amdgcn_exp2f(x0), e1 = __builtin_amdgcn_exp2f(x1);
-          pn[kb][h][e] = (_Float16)e0;
-          pn[kb][h][e + 1] = (_Float16)e1;
+          pn[kb][h][e] = (T)e0;
+          pn[kb][h][e + 1] = (T)e1;
           sum[2 * kb + h] += e0 + e1;
         }
     return (sum[0] + sum[1]) + (sum[2] + sum[3]);
@@ -648,7 +676,7 @@ struct Rows {
   // Softmax of tile j into pn at the current m, no rescaling: returns the
   // lanes whose tile sum left the range where every p is a finite fp16
   // (also catches inf / NaN); the caller then recomputes with rescaling.
-  __device__ __forceinline__ uint64_t softmax_fast(const float16_t (&s)[2], half8_t (&pn)[2][2]) {
+  __device__ __forceinline__ uint64_t softmax_fast(const float16_t (&s)[2], V8 (&pn)[2][2]) {
     const float sum = exponentiate(s, pn);
     l += sum;
     return __builtin_amdgcn_ballot_w64(!(sum <= kSumLimit));
@@ -672,7 +700,7 @@ struct Rows {
   // Nothing in the common path depends on a comparison, so the exponentials
   // are free to interleave with both GEMMs.
   template <class F>
-  __device__ __forceinline__ void softmax_trailing(float16_t (&s)[2], half8_t (&pn)[2][2],
+  __device__ __forceinline__ void softmax_trailing(float16_t (&s)[2], V8 (&pn)[2][2],
                                                    F&& on_shift) {
     float sum = exponentiate(s, pn);
     // Keep the fp16 packing ahead of the branch (it would otherwise be sunk
@@ -781,7 +809,7 @@ struct Rows {
   // With `lse`, also the row's log-sum-exp in natural-log units,
   // ln(sum_j exp(sm_scale q.k_j)) = ln 2 * (m * cr + log2 l) (-inf for a row
   // with no visible key).
-  __device__ __forceinline__ void store(_Float16* Oh, int o_sr, float* lse) const {
+  __device__ __forceinline__ void store(T* Oh, int o_sr, float* lse) const {
     const float l_tot = pair_sum(l);
     const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
     if (lse != nullptr && g == 0 && my_q < seq) {
@@ -789,15 +817,15 @@ struct Rows {
       lse[my_q] = l_tot > 0.0f ? 0.693147180559945309f * lg : ninf();
     }
     if (my_q < seq) {
-      _Float16* orow = Oh + (long long)my_q * o_sr;
+      T* orow = Oh + (long long)my_q * o_sr;
 #pragma unroll
       for (int db = 0; db < 2; ++db)
 #pragma unroll
         for (int hh = 0; hh < 2; ++hh) {
-          half8_t out;
+          V8 out;
 #pragma unroll
-          for (int e = 0; e < 8; ++e) out[e] = (_Float16)(o[db][8 * hh + e] * inv);
-          *reinterpret_cast<half8_t*>(orow + 32 * db + 16 * hh + 8 * g) = out;
+          for (int e = 0; e < 8; ++e) out[e] = (T)(o[db][8 * hh + e] * inv);
+          *reinterpret_cast<V8*>(orow + 32 * db + 16 * hh + 8 * g) = out;
         }
     }
   }
@@ -1232,11 +1260,15 @@ __device__ __forceinline__ void sync_ring_ahead() {
 // fp32 adds on the masked ones (diagonal / tail), where a short causal row
 // sums a few p.  Blocks whose first pass saw a tile sum out of the
 // fp16-safe range are recomputed by a plain one-tile-per-step checked pass.
-template <int W, int FV, bool CAUSAL, bool SCALED>
+template <int W, int FV, bool CAUSAL, bool SCALED, class T = _Float16>
 __global__ void __launch_bounds__(64 * W, 2)  // <= 256 VGPRs: 2 waves per SIMD at W = 8
-fa2_fwd_slot_kernel(const _Float16* Q, const _Float16* __restrict__ K,
-                    const _Float16* __restrict__ V, _Float16* O, const Geom geom, int nqb,
-                    float cq, float cr) {
+fa2_fwd_slot_kernel(const T* Q, const T* __restrict__ K, const T* __restrict__ V, T* O,
+                    const Geom geom, int nqb, float cq, float cr) {
+  using RowsT = Rows<CAUSAL, SCALED, T>;
+  using V8 = typename RowsT::V8;
+  // fp16: unmasked tiles sum P with the packed-fp16 tree; bf16 P keeps
+  // fp32 sums throughout (an 8-bit mantissa tree would cost accuracy).
+  constexpr bool kFp16 = __is_same(T, _Float16);
   constexpr int FK = FV + 1;
   constexpr int kSlots = FV + 2;  // per ring
   constexpr int kUnroll = (kSlots % 2 == 0) ? kSlots : 2 * kSlots;
@@ -1247,7 +1279,9 @@ fa2_fwd_slot_kernel(const _Float16* Q, const _Float16* __restrict__ K,
   // LDS reads of the first kAhead slots (K slots: 1, V slots: 2).
   constexpr int kTailReads = kAhead + kAhead / 2;
   constexpr int kRingBytes = kSlots * kTileBytes;
-  constexpr int kWgPerCu = (2 * 2 * kRingBytes <= 160 * 1024) ? 2 : 1;
+  // Two work-groups share a CU when both rings fit its 160 KiB and the
+  // waves fit two per SIMD (<= 4 waves each).
+  constexpr int kWgPerCu = (W <= 4 && 2 * 2 * kRingBytes <= 160 * 1024) ? 2 : 1;
   static_assert(kSegs * W == 8, "tile split");
   static_assert(FV >= 2 && FV <= 6, "fetch distance");
   static_assert(kAhead % 2 == 0 && kAhead < 16, "read-ahead");
@@ -1258,7 +1292,7 @@ fa2_fwd_slot_kernel(const _Float16* Q, const _Float16* __restrict__ K,
   const int rw = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   int bh, qb;
   wg_coords<CAUSAL, kWgPerCu>(nqb, bh, qb);
-  const HeadPtrs hp = head_ptrs(geom, bh, Q, K, V, O);
+  const HeadPtrs<T> hp = head_ptrs(geom, bh, Q, K, V, O);
   const i32x4_t rk = hp.rk, rv = hp.rv;
   const FetchOff<kSegs> fk = fetch_offsets<kSegs, false>(rw, lane, 2 * geom.k_sr);
   const FetchOff<kSegs> fv = fetch_offsets<kSegs, true>(rw, lane, 2 * geom.v_sr);
@@ -1279,7 +1313,7 @@ fa2_fwd_slot_kernel(const _Float16* Q, const _Float16* __restrict__ K,
     fetch_tile<kSegs>(rk, rings.kslot(Ic<G + FK>{}), G + FK, last, rw, fk);
     fetch_tile<kSegs>(rv, rings.vslot(Ic<G + FV>{}), G + FV, last, rw, fv);
   });
-  Rows<CAUSAL, SCALED> rows;
+  RowsT rows;
   rows.init(hp.q, geom.q_sr, lane, q0 + 32 * rw, seq, geom.seq_k, geom.coff, cq, cr);
 
   // Iterations j < jm need no mask on tiles j and j + 1.
@@ -1290,21 +1324,21 @@ fa2_fwd_slot_kernel(const _Float16* Q, const _Float16* __restrict__ K,
   // ---- first pass ----
   sync_ring_ahead<(FK - 1) * kDmaPerIter, 0>();  // K(0)
   float16_t S[2];
-  half8_t P0[2][2], P1[2][2];
+  V8 P0[2][2], P1[2][2];
 #pragma unroll
   for (int a = 0; a < 2; ++a)
 #pragma unroll
-    for (int b = 0; b < 2; ++b) P1[a][b] = (half8_t){0, 0, 0, 0, 0, 0, 0, 0};
+    for (int b = 0; b < 2; ++b) P1[a][b] = (V8){0, 0, 0, 0, 0, 0, 0, 0};
   {
     // S(0) with the exact row max; iteration 0 recomputes block 1 against it.
-    half8_t ka[2][4];
+    V8 ka[2][4];
     rows.read_k(rings.kslot(Ic<0>{}), ka);
     rows.gemm1(ka, S);
   }
   rows.mask(0, S);
   rows.first_tile(S);
   sync_ring_ahead<(FV - 1) * kDmaPerIter, 0>();  // K(1), V(0)
-  half8_t ahead[kAhead];
+  V8 ahead[kAhead];
   static_for(std::make_integer_sequence<int, kAhead>{}, [&](auto a) __attribute__((always_inline)) {
     constexpr int L = decltype(a)::value;
     ahead[L] = rows.template read_slot<L>(rings.kslot(Ic<0>{}), rings.kslot(Ic<1>{}),
@@ -1316,13 +1350,13 @@ fa2_fwd_slot_kernel(const _Float16* Q, const _Float16* __restrict__ K,
   // and V(j+FV); 16 slots; the range check of tile j's sum; on MASKED
   // iterations, mask block 1 of tile j (after slot 7, before its
   // exponentials) and block 0 of tile j+1; publish K(j+2), V(j+1).
-  auto iteration = [&](auto i, int j, half8_t (&P)[2][2], const half8_t (&Pp)[2][2],
+  auto iteration = [&](auto i, int j, V8 (&P)[2][2], const V8 (&Pp)[2][2],
                        auto masked) __attribute__((always_inline)) {
     constexpr int I = decltype(i)::value;
     constexpr bool kMasked = decltype(masked)::value;
     fetch_tile<kSegs>(rk, rings.kslot(Ic<I + FK>{}), j + FK, last, rw, fk);
     fetch_tile<kSegs>(rv, rings.vslot(Ic<I + FV>{}), j + FV, last, rw, fv);
-    half8_t op[16];
+    V8 op[16];
 #pragma unroll
     for (int a = 0; a < kAhead; ++a) op[a] = ahead[a];
     half2_t tree[14];
@@ -1339,15 +1373,18 @@ fa2_fwd_slot_kernel(const _Float16* Q, const _Float16* __restrict__ K,
         ahead[L + kAhead - 16] = rows.template read_slot<L + kAhead - 16>(
             rings.kslot(Ic<I + 1>{}), rings.kslot(Ic<I + 2>{}), rings.vslot(Ic<I>{}));
       rows.template exp_slot<L>(S, P);
-      if constexpr (!kMasked)
-        Rows<CAUSAL, SCALED>::template sum_slot<L>(P, tree);
+      if constexpr (kFp16 && !kMasked)
+        RowsT::template sum_slot<L>(P, tree);
       else
-        Rows<CAUSAL, SCALED>::template sum_slot_f32<L>(S, sum, rows.cr);
+        RowsT::template sum_slot_f32<L>(S, sum, rows.cr);
       if constexpr (kMasked && L == 7) rows.template mask_block<1>(j, S[1]);
       __builtin_amdgcn_sched_barrier(0);
     });
-    const float tot = !kMasked ? Rows<CAUSAL, SCALED>::sum_root(tree)
-                               : (sum[0] + sum[1]) + (sum[2] + sum[3]);
+    float tot;
+    if constexpr (kFp16 && !kMasked)
+      tot = RowsT::sum_root(tree);
+    else
+      tot = (sum[0] + sum[1]) + (sum[2] + sum[3]);
     rows.l += tot;
     out_of_range |= __builtin_amdgcn_ballot_w64(!(tot <= kSumLimit));
     if constexpr (kMasked) rows.template mask_block<0>(j + 1, S[0]);
@@ -1391,9 +1428,9 @@ fa2_fwd_slot_kernel(const _Float16* Q, const _Float16* __restrict__ K,
       fetch_tile<kSegs>(rv, rings.vslot(Ic<0>{}), t, last, rw, fv);
       sync_ring_ahead<0, 0>();
       float16_t Sc[2];
-      half8_t Pc[2][2];
+      V8 Pc[2][2];
       {
-        half8_t ka[2][4];
+        V8 ka[2][4];
         rows.read_k(rings.kslot(Ic<0>{}), ka);
         rows.gemm1(ka, Sc);
       }
@@ -1401,11 +1438,410 @@ fa2_fwd_slot_kernel(const _Float16* Q, const _Float16* __restrict__ K,
       if (t == 0) rows.first_tile(Sc);
       rows.softmax_checked(Sc, Pc);
       {
-        half8_t va[2][4];
+        V8 va[2][4];
         rows.read_v(rings.vslot(Ic<0>{}), va);
         rows.gemm2(va, Pc);
       }
       sync_ring_ahead<0, 0>();  // every wave's reads done before the next fetch
+    }
+  }
+  rows.launder();
+  rows.store(hp.o, geom.o_sr, hp.lse);
+}
+
+// ---------------------------------------------------------------------------
+// Head dim 128 (beyond the reference, whose kernels take D = 64 only,
+// kernel_flash2.cu:756-757).  Key tiles of 32 rows x 256 bytes keep the
+// 8 KiB tile of D = 64, so an iteration is again 16 MFMA slots: GEMM1 is one
+// 32-key block over 8 head-dim steps (one chain), GEMM2 four head-dim
+// blocks over 2 key steps.  With 16 scores per lane per tile there is one
+// exponential per MFMA, so the softmax VALU work fits under the matrix
+// core with room to spare and the row sums stay fp32.
+constexpr int kD2 = 128;
+constexpr int kBc2 = 32;
+constexpr int kRowBytes2 = 2 * kD2;  // 256
+
+// DMA lane offsets for 256-byte rows: segment i of wave w is rows
+// 4(w kSegs + i) .. +3; lane l lands at byte 16 l of it, i.e. row l/16,
+// physical chunk l%16, which holds logical chunk (l%16) ^ swz(row) (the
+// swizzles flip the low 3 chunk bits only).
+template <int kSegs, bool IS_V>
+__device__ __forceinline__ FetchOff<kSegs> fetch_offsets128(int wave, int lane, int row_bytes) {
+  FetchOff<kSegs> f;
+#pragma unroll
+  for (int i = 0; i < kSegs; ++i) {
+    const int seg = wave * kSegs + i;
+    const int row = 4 * seg + (lane >> 4);
+    const int phys = lane & 15;
+    const int logical = phys ^ (IS_V ? v_swz(row) : k_swz(row));
+    f.lane[i] = row * row_bytes + 16 * logical;
+    asm volatile("" : "+v"(f.lane[i]));
+  }
+  f.tile_bytes = kBc2 * row_bytes;
+  return f;
+}
+
+// The 32 query rows one wave owns at head dim 128 (same lane roles as Rows:
+// one query per lane, 16 of a 32-key block's scores per lane).
+template <bool CAUSAL, bool SCALED, class T>
+struct Rows128 {
+  using E = Elem<T>;
+  using V8 = typename E::v8;
+  using V4 = typename E::v4;
+  int g, col, qw, my_q, seq, qd, my_d, kv_lim, tr_row, tr_col;
+  float cr;
+  V8 qf[8];          // Q'^T B-operand, head-dim steps 0-7
+  float16_t o[4];    // O^T accumulator, head-dim blocks 0-3
+  float16_t bias;    // -m broadcast
+  float m, l;
+
+  __device__ __forceinline__ void init(const T* Qh, int q_sr, int lane, int qw_, int seq_,
+                                       int seq_k, int coff, float cq, float cr_) {
+    g = lane >> 5;
+    col = lane & 31;
+    qw = qw_;
+    my_q = qw + col;
+    qd = qw + coff;
+    my_d = my_q + coff;
+    seq = seq_;
+    kv_lim = seq_k;
+    cr = cr_;
+    const int trG = lane >> 4, trj = lane & 15;
+    tr_row = 4 * (trG >> 1) + (trj >> 2);
+    const int tr_x = trj & 3;
+    tr_col = 16 * (trG & 1) + 4 * (((tr_x & 1) << 1) | (tr_x >> 1));
+#pragma unroll
+    for (int s = 0; s < 8; ++s) {
+      if (my_q < seq) {
+        const V8 raw = *reinterpret_cast<const V8*>(Qh + (long long)my_q * q_sr + 16 * s + 8 * g);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) qf[s][e] = (T)((float)raw[e] * cq);
+      } else {
+        qf[s] = (V8){0, 0, 0, 0, 0, 0, 0, 0};
+      }
+    }
+    reset();
+  }
+  __device__ __forceinline__ void launder() {
+    asm volatile("" : "+v"(col), "+v"(g), "+v"(my_q), "+v"(tr_row), "+v"(tr_col));
+  }
+  __device__ __forceinline__ void set_m(float mm) {
+    m = mm;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) bias[r] = -mm;
+  }
+  __device__ __forceinline__ void reset() {
+#pragma unroll
+    for (int db = 0; db < 4; ++db)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) o[db][r] = 0.0f;
+    set_m(0.0f);
+    l = 0.0f;
+  }
+  __device__ __forceinline__ V8 read_k_op(const uint8_t* kt, int st) const {
+    const int ch = 2 * st + g;
+    return *reinterpret_cast<const V8*>(kt + col * kRowBytes2 + 16 * (ch ^ k_swz(col)));
+  }
+  __device__ __forceinline__ V8 read_v_op(const uint8_t* vt, int db, int t) const {
+    const int r1 = 16 * t + tr_row;
+    const int r2 = r1 + 8;
+    const int dcol = 32 * db + tr_col;
+    const int ch = dcol >> 3, hb = ((dcol >> 2) & 1) * 8;
+    const V4 lo = lds_read_tr<V4>(vt + r1 * kRowBytes2 + 16 * (ch ^ v_swz(r1)) + hb);
+    const V4 hi = lds_read_tr<V4>(vt + r2 * kRowBytes2 + 16 * (ch ^ v_swz(r2)) + hb);
+    return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+  }
+  // Slot map: L even, GEMM1 head-dim step L/2 of the next tile (one chain,
+  // steps two slots apart); L odd, u = L/2: GEMM2 head-dim block u % 4 at
+  // key step u / 4.
+  template <int L>
+  __device__ __forceinline__ V8 read_slot(const uint8_t* kt, const uint8_t* vt) const {
+    constexpr int u = L >> 1;
+    if constexpr ((L & 1) == 0)
+      return read_k_op(kt, u);
+    else
+      return read_v_op(vt, u & 3, u >> 2);
+  }
+  template <int L>
+  __device__ __forceinline__ void mfma_slot(const V8& a, float16_t& sn, const V8 (&pp)[2]) {
+    constexpr int u = L >> 1;
+    if constexpr ((L & 1) == 0)
+      sn = E::mfma(a, qf[u], u == 0 ? bias : sn);
+    else
+      o[u & 3] = E::mfma(a, pp[u >> 2], o[u & 3]);
+  }
+  // Softmax share of slot L: score L -> one exponential, its element of
+  // the P operand (P[t] holds keys 16t + 4g + {0..3, 8..11}) and the fp32
+  // row sum in four chains.
+  template <int L>
+  __device__ __forceinline__ void exp_slot(const float16_t& s, V8 (&pn)[2], float (&sum)[4]) const {
+    float x = s[L];
+    if (SCALED) x *= cr;
+    const float e = __builtin_amdgcn_exp2f(x);
+    pn[L >> 3][L & 7] = (T)e;
+    if constexpr (L < 4)
+      sum[L] = e;
+    else
+      sum[L & 3] += e;
+  }
+  // Keys >= kv_lim and, causal, past the lane's diagonal, of tile t.
+  __device__ __forceinline__ void mask(int t, float16_t& s) const {
+    const int k0 = t * kBc2;
+    if (k0 + kBc2 > kv_lim || (CAUSAL && k0 + kBc2 - 1 > qd)) {
+      const int base = k0 + 4 * g;
+      int lim = kv_lim - base;
+      if (CAUSAL) lim = min(lim, my_d + 1 - base);
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int c = 8 * (r >> 2) + (r & 3);
+        s[r] = c < lim ? s[r] : ninf();
+      }
+    }
+  }
+  __device__ __forceinline__ float tile_max(const float16_t& s) const {
+    float mx = ninf();
+#pragma unroll
+    for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[r]);
+    return pair_max(mx);
+  }
+  __device__ __forceinline__ static void sub(float16_t& s, float d) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) s[r] -= d;
+  }
+  __device__ __forceinline__ void first_tile(float16_t& s) {
+    float m0 = tile_max(s);
+    m0 = m0 == ninf() ? 0.0f : m0;
+    sub(s, m0);
+    set_m(m0);
+  }
+  __device__ __forceinline__ float exponentiate(const float16_t& s, V8 (&pn)[2]) const {
+    float sum[2] = {0.0f, 0.0f};
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      float x = s[r];
+      if (SCALED) x *= cr;
+      const float e = __builtin_amdgcn_exp2f(x);
+      pn[r >> 3][r & 7] = (T)e;
+      sum[r & 1] += e;
+    }
+    return sum[0] + sum[1];
+  }
+  // As Rows::softmax_checked, for one 32-key tile.
+  __device__ __forceinline__ void softmax_checked(float16_t& s, V8 (&pn)[2]) {
+    float sum = exponentiate(s, pn);
+    if (__builtin_amdgcn_ballot_w64(!(sum <= kSumLimit)) != 0) {
+      const float d = fmaxf(tile_max(s), 0.0f);
+      const float alpha = __builtin_amdgcn_exp2f(-(SCALED ? cr : 1.0f) * d);
+      l *= alpha;
+#pragma unroll
+      for (int db = 0; db < 4; ++db)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) o[db][r] *= alpha;
+      sub(s, d);
+      set_m(m + d);
+      sum = exponentiate(s, pn);
+    }
+    l += sum;
+  }
+  // O = O^T / l, 16-byte stores of 8 contiguous head dims; the log-sum-exp
+  // as in Rows::store.
+  __device__ __forceinline__ void store(T* Oh, int o_sr, float* lse) const {
+    const float l_tot = pair_sum(l);
+    const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
+    if (lse != nullptr && g == 0 && my_q < seq) {
+      const float lg = m * (SCALED ? cr : 1.0f) + __builtin_amdgcn_logf(l_tot);
+      lse[my_q] = l_tot > 0.0f ? 0.693147180559945309f * lg : ninf();
+    }
+    if (my_q < seq) {
+      T* orow = Oh + (long long)my_q * o_sr;
+#pragma unroll
+      for (int db = 0; db < 4; ++db)
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh) {
+          V8 out;
+#pragma unroll
+          for (int e = 0; e < 8; ++e) out[e] = (T)(o[db][8 * hh + e] * inv);
+          *reinterpret_cast<V8*>(orow + 32 * db + 16 * hh + 8 * g) = out;
+        }
+    }
+  }
+};
+
+// Causal key tiles of 32 keys a block of query rows [q0, q_end) needs.
+__device__ __forceinline__ int causal_tiles32(int q_end, int coff) {
+  const int last_key = q_end - 1 + coff;
+  return last_key < 0 ? 1 : last_key / kBc2 + 1;
+}
+
+// Slot-scheduled head-dim-128 pipeline: W waves of 32 query rows.  Iteration
+// j: GEMM1 of tile j+1 (even slots), GEMM2 of tile j-1 with P(j-1) (odd
+// slots), the softmax of tile j (one exponential per slot), the LDS read of
+// the operand of slot +kAhead.  S and P are double-buffered.  The operands
+// of the next iteration's first kAhead slots come from K(j+2) and V(j), so
+// the barrier ending iteration j publishes K(j+3) and V(j+1); K is fetched
+// FK tiles ahead and V FK-2 into rings of FK slots, FK-3 fetch groups in
+// flight at a barrier.  Slot reuse: K(X) lands in the slot of K(X-FK), last
+// read in iteration X-FK-1; V(X) in that of V(X-FK), last read in iteration
+// X-FK+1 (fetched in iteration X-FK+2).  Masked tiles, the range check and
+// the checked recompute pass follow fa2_fwd_slot_kernel.
+template <int W, int FK, int AHEAD, bool CAUSAL, bool SCALED, class T>
+__global__ void __launch_bounds__(64 * W, 2)
+fa2_fwd_d128_kernel(const T* Q, const T* __restrict__ K, const T* __restrict__ V, T* O,
+                    const Geom geom, int nqb, float cq, float cr) {
+  using RowsT = Rows128<CAUSAL, SCALED, T>;
+  using V8 = typename RowsT::V8;
+  constexpr int FV = FK - 2;
+  constexpr int kSlots = FK;
+  constexpr int kUnroll = (kSlots % 2 == 0) ? kSlots : 2 * kSlots;
+  constexpr int kBr = 32 * W;
+  constexpr int kSegs = 8 / W;
+  constexpr int kDmaPerIter = 2 * kSegs;
+  constexpr int kAhead = AHEAD;  // slots between an operand's LDS read and its MFMA
+  constexpr int kTailReads = kAhead + kAhead / 2;  // K slots: 1 read, V slots: 2
+  constexpr int kRingBytes = kSlots * kTileBytes;
+  // Two work-groups share a CU when both rings fit its 160 KiB and the
+  // waves fit two per SIMD (<= 4 waves each).
+  constexpr int kWgPerCu = (W <= 4 && 2 * 2 * kRingBytes <= 160 * 1024) ? 2 : 1;
+  static_assert(kSegs * W == 8, "tile split");
+  static_assert(FK >= 4 && FK <= 8, "fetch distance");
+  static_assert(kAhead % 2 == 0 && kAhead < 16, "read-ahead");
+  static_assert(kTileBytes == kBc2 * kRowBytes2, "tile size");
+  __shared__ __attribute__((aligned(16))) uint8_t kring[kRingBytes];
+  __shared__ __attribute__((aligned(16))) uint8_t vring[kRingBytes];
+
+  const int lane = threadIdx.x & 63;
+  const int rw = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  int bh, qb;
+  wg_coords<CAUSAL, kWgPerCu>(nqb, bh, qb);
+  const HeadPtrs<T> hp = head_ptrs<T, kRowBytes2>(geom, bh, Q, K, V, O);
+  const i32x4_t rk = hp.rk, rv = hp.rv;
+  const FetchOff<kSegs> fk = fetch_offsets128<kSegs, false>(rw, lane, 2 * geom.k_sr);
+  const FetchOff<kSegs> fv = fetch_offsets128<kSegs, true>(rw, lane, 2 * geom.v_sr);
+  const int seq = geom.seq_q;
+  const int q0 = qb * kBr;
+  const StreamRings<kSlots> rings = {kring, vring};
+
+  int ntiles = max(1, (geom.seq_k + kBc2 - 1) / kBc2);
+  if (CAUSAL) ntiles = min(ntiles, causal_tiles32(min(q0 + kBr, seq), geom.coff));
+  const int t0 = ntiles;
+  const int last = ntiles - 1;
+
+  static_for(std::make_integer_sequence<int, FK>{}, [&](auto i) __attribute__((always_inline)) {
+    constexpr int G = decltype(i)::value - FK;
+    fetch_tile<kSegs>(rk, rings.kslot(Ic<G + FK>{}), G + FK, last, rw, fk);
+    fetch_tile<kSegs>(rv, rings.vslot(Ic<G + FV>{}), G + FV, last, rw, fv);
+  });
+  RowsT rows;
+  rows.init(hp.q, geom.q_sr, lane, q0 + 32 * rw, seq, geom.seq_k, geom.coff, cq, cr);
+
+  // Iterations j < jm need no mask on tile j + 1.
+  int tm = rows.kv_lim / kBc2;
+  if (CAUSAL) tm = min(tm, (rows.qd + 1) / kBc2);
+  const int jm = max(0, tm - 1);
+
+  sync_ring_ahead<(FK - 1) * kDmaPerIter, 0>();  // K(0)
+  float16_t S0, S1;
+  V8 P0[2], P1[2];
+  P1[0] = P1[1] = (V8){0, 0, 0, 0, 0, 0, 0, 0};
+  {
+    V8 ka[8];
+#pragma unroll
+    for (int st = 0; st < 8; ++st) ka[st] = rows.read_k_op(rings.kslot(Ic<0>{}), st);
+#pragma unroll
+    for (int st = 0; st < 8; ++st) S0 = RowsT::E::mfma(ka[st], rows.qf[st], st == 0 ? rows.bias : S0);
+  }
+  // Iteration 0 refills K(0)'s slot: every wave's reads of it are done.
+  sync_ring_ahead<(FK - 3) * kDmaPerIter, 0>();  // K(2), V(0)
+  rows.mask(0, S0);
+  rows.first_tile(S0);
+  V8 ahead[kAhead];
+  static_for(std::make_integer_sequence<int, kAhead>{}, [&](auto a) __attribute__((always_inline)) {
+    constexpr int L = decltype(a)::value;
+    ahead[L] = rows.template read_slot<L>(rings.kslot(Ic<1>{}), rings.vslot(Ic<-1>{}));
+  });
+
+  uint64_t out_of_range = 0;
+  auto iteration = [&](auto i, int j, float16_t& S, float16_t& Sn, V8 (&P)[2], const V8 (&Pp)[2],
+                       auto masked) __attribute__((always_inline)) {
+    constexpr int I = decltype(i)::value;
+    fetch_tile<kSegs>(rk, rings.kslot(Ic<I + FK>{}), j + FK, last, rw, fk);
+    fetch_tile<kSegs>(rv, rings.vslot(Ic<I + FV>{}), j + FV, last, rw, fv);
+    V8 op[16];
+#pragma unroll
+    for (int a = 0; a < kAhead; ++a) op[a] = ahead[a];
+    float sum[4];
+    static_for(std::make_integer_sequence<int, 16>{}, [&](auto sl) __attribute__((always_inline)) {
+      constexpr int L = decltype(sl)::value;
+      rows.template mfma_slot<L>(op[L], Sn, Pp);
+      if constexpr (L + kAhead < 16)
+        op[L + kAhead] = rows.template read_slot<L + kAhead>(rings.kslot(Ic<I + 1>{}),
+                                                             rings.vslot(Ic<I - 1>{}));
+      else
+        ahead[L + kAhead - 16] = rows.template read_slot<L + kAhead - 16>(
+            rings.kslot(Ic<I + 2>{}), rings.vslot(Ic<I>{}));
+      rows.template exp_slot<L>(S, P, sum);
+      __builtin_amdgcn_sched_barrier(0);
+    });
+    const float tot = (sum[0] + sum[1]) + (sum[2] + sum[3]);
+    rows.l += tot;
+    out_of_range |= __builtin_amdgcn_ballot_w64(!(tot <= kSumLimit));
+    if constexpr (decltype(masked)::value) rows.mask(j + 1, Sn);
+    sync_ring_ahead<(FK - 3) * kDmaPerIter, kTailReads>();
+  };
+  auto group = [&](int j0, auto masked) __attribute__((always_inline)) {
+    static_for(std::make_integer_sequence<int, kUnroll>{}, [&](auto i) __attribute__((always_inline)) {
+      constexpr int I = decltype(i)::value;
+      const int j = j0 + I;
+      if (!decltype(masked)::value || j <= t0) {
+        if constexpr (I % 2 == 0)
+          iteration(i, j, S0, S1, P0, P1, masked);
+        else
+          iteration(i, j, S1, S0, P1, P0, masked);
+      }
+    });
+  };
+  {
+    int j0 = 0;
+    for (; j0 + kUnroll <= jm; j0 += kUnroll) group(j0, Ic<false>{});
+    for (; j0 <= t0; j0 += kUnroll) group(j0, Ic<true>{});
+  }
+
+  // Checked pass (as in fa2_fwd_slot_kernel); the flag lives in K ring slot 1.
+  __builtin_amdgcn_s_waitcnt(0);
+  int* redo = reinterpret_cast<int*>(rings.kslot(Ic<1>{}));
+  __syncthreads();
+  if (threadIdx.x == 0) *redo = 0;
+  __syncthreads();
+  if (out_of_range != 0 && lane == 0) *redo = 1;
+  __syncthreads();
+  if (*redo) {
+    rows.launder();
+    rows.reset();
+    for (int t = 0; t < ntiles; ++t) {
+      fetch_tile<kSegs>(rk, rings.kslot(Ic<0>{}), t, last, rw, fk);
+      fetch_tile<kSegs>(rv, rings.vslot(Ic<0>{}), t, last, rw, fv);
+      sync_ring_ahead<0, 0>();
+      float16_t Sc;
+      V8 Pc[2];
+      {
+        V8 ka[8];
+#pragma unroll
+        for (int st = 0; st < 8; ++st) ka[st] = rows.read_k_op(rings.kslot(Ic<0>{}), st);
+#pragma unroll
+        for (int st = 0; st < 8; ++st)
+          Sc = RowsT::E::mfma(ka[st], rows.qf[st], st == 0 ? rows.bias : Sc);
+      }
+      rows.mask(t, Sc);
+      if (t == 0) rows.first_tile(Sc);
+      rows.softmax_checked(Sc, Pc);
+      {
+        V8 va[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) va[u] = rows.read_v_op(rings.vslot(Ic<0>{}), u & 3, u >> 2);
+#pragma unroll
+        for (int u = 0; u < 8; ++u) rows.o[u & 3] = RowsT::E::mfma(va[u], Pc[u >> 2], rows.o[u & 3]);
+      }
+      sync_ring_ahead<0, 0>();
     }
   }
   rows.launder();
@@ -1453,13 +1889,20 @@ splitkv_combine_kernel(_Float16* O, const Geom geom) {
 
 // Q is prescaled by cq = +-min(c, 1) in the kernel; the remaining factor
 // cr = c / |cq| (1 unless c > 1) is applied to the scores.
+// bf16 and head_dim 128 keep Q exact (cq = +-1) and scale the fp32 scores
+// instead: a bf16 rounding of the prescaled Q would cost 2^-9 of every
+// score, and at D = 128 the fp16 rounding error of a score grows with
+// sqrt(D) past the fp16 output tolerance at large scales (2.3e-3 measured at
+// sm_scale -0.3), while one exponential per MFMA leaves the extra multiply
+// room under the matrix core.
 struct Scales {
   float cq, cr;
   bool scaled;
   explicit Scales(const FwdArgs& a) {
     const float c = a.scale_log2;
-    cq = (c <= 1.0f ? c : 1.0f) * (a.negate ? -1.0f : 1.0f);
-    cr = c <= 1.0f ? 1.0f : c;
+    const bool exact_q = a.dtype == kDtypeBF16 || a.head_dim == kD2;
+    cq = (c <= 1.0f && !exact_q ? c : 1.0f) * (a.negate ? -1.0f : 1.0f);
+    cr = c <= 1.0f && !exact_q ? 1.0f : c;
     scaled = cr != 1.0f;
   }
 };
@@ -1536,16 +1979,29 @@ struct PingPongLaunch {
   };
 };
 
-template <int W, int FV>
+template <int W, int FV, class T = _Float16>
 struct SlotLaunch {
   template <bool C, bool S>
   struct L {
     static hipError_t run(const FwdArgs& a, const Geom& g, dim3 grid, int nqb, float cq, float cr,
                           hipStream_t st) {
-      hipLaunchKernelGGL((fa2_fwd_slot_kernel<W, FV, C, S>), grid, dim3(64 * W), 0, st,
-                         static_cast<const _Float16*>(a.q), static_cast<const _Float16*>(a.k),
-                         static_cast<const _Float16*>(a.v), static_cast<_Float16*>(a.o), g, nqb,
-                         cq, cr);
+      hipLaunchKernelGGL((fa2_fwd_slot_kernel<W, FV, C, S, T>), grid, dim3(64 * W), 0, st,
+                         static_cast<const T*>(a.q), static_cast<const T*>(a.k),
+                         static_cast<const T*>(a.v), static_cast<T*>(a.o), g, nqb, cq, cr);
+      return hipSuccess;
+    }
+  };
+};
+
+template <int W, int FK, int AHEAD, class T>
+struct D128Launch {
+  template <bool C, bool S>
+  struct L {
+    static hipError_t run(const FwdArgs& a, const Geom& g, dim3 grid, int nqb, float cq, float cr,
+                          hipStream_t st) {
+      hipLaunchKernelGGL((fa2_fwd_d128_kernel<W, FK, AHEAD, C, S, T>), grid, dim3(64 * W), 0, st,
+                         static_cast<const T*>(a.q), static_cast<const T*>(a.k),
+                         static_cast<const T*>(a.v), static_cast<T*>(a.o), g, nqb, cq, cr);
       return hipSuccess;
     }
   };
@@ -1611,6 +2067,21 @@ const Fa2Config kFa2Configs[kNumFa2Configs] = {
 // Fetch distance: three tiles ahead where LDS allows (64 KiB of rings per
 // work-group), one tile for single-wave groups.
 hipError_t launch_fa2(const FwdArgs& a, int cfg, hipStream_t stream) {
+  if (a.head_dim == kD2) {
+    const bool bf = a.dtype == kDtypeBF16;
+    if (cfg == kSlotW8Config)
+      return bf ? dispatch<D128Launch<8, 5, 6, __bf16>::L>(a, stream, 256)
+                : dispatch<D128Launch<8, 5, 6, _Float16>::L>(a, stream, 256);
+    if (cfg == kSlotW4Config)
+      return bf ? dispatch<D128Launch<4, 5, 6, __bf16>::L>(a, stream, 128)
+                : dispatch<D128Launch<4, 5, 6, _Float16>::L>(a, stream, 128);
+    return hipErrorInvalidValue;
+  }
+  if (a.dtype == kDtypeBF16) {
+    if (cfg == kSlotW8Config) return dispatch<SlotLaunch<8, 4, __bf16>::L>(a, stream, 256);
+    if (cfg == kSlotW4Config) return dispatch<SlotLaunch<4, 3, __bf16>::L>(a, stream, 128);
+    return hipErrorInvalidValue;
+  }
   switch (cfg) {
     case 0: return dispatch<PipelinedLaunch<1, 1, 1>::L>(a, stream, 32);
     case 1: return dispatch<PipelinedLaunch<2, 3, 1>::L>(a, stream, 64);

@@ -26,9 +26,13 @@ struct FwdArgs {
   float scale_log2;  // |sm_scale| * log2(e), always > 0
   int negate;        // 1 when sm_scale < 0: the kernel flips the sign of Q
   int causal;        // key j visible to query i iff j <= i + (N_k - N_q)
+  int dtype;         // element type of q, k, v, o: kDtypeF16 or kDtypeBF16
   int64_t q_sb, q_sh, k_sb, k_sh, v_sb, v_sh, o_sb, o_sh;  // batch / head strides
   int q_sr, k_sr, v_sr, o_sr;                              // row strides
 };
+
+constexpr int kDtypeF16 = 0;
+constexpr int kDtypeBF16 = 1;
 
 // One FA2 tile configuration: `waves` waves of 64 lanes, each owning 32
 // query rows, so a work-group covers 32*waves queries; KV tiles of 64 keys.
@@ -40,8 +44,12 @@ struct Fa2Config {
 constexpr int kNumFa2Configs = 8;
 extern const Fa2Config kFa2Configs[kNumFa2Configs];
 
-// Launches the FA2 kernel for configuration `cfg` on `stream`.
+// Launches the FA2 kernel for configuration `cfg` on `stream`.  fp16 at
+// head_dim 64 has every configuration; bf16 and head_dim 128 have the
+// slot-scheduled ones (kSlotW8Config, kSlotW4Config).
 hipError_t launch_fa2(const FwdArgs& a, int cfg, hipStream_t stream);
+constexpr int kSlotW8Config = 6;
+constexpr int kSlotW4Config = 7;
 
 // Split-KV ("flash-decoding"): `waves` (1, 2 or 4) waves of 32 query rows
 // per work-group, the key range cut into `nsplit` chunks whose partial

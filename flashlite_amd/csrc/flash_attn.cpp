@@ -147,8 +147,11 @@ py::object flash_attn_forward_flash2_ex(torch::Tensor q, torch::Tensor k, torch:
                                         int64_t num_splits,
                                         std::optional<torch::Tensor> workspace) {
   TORCH_CHECK(q.is_cuda() && k.is_cuda() && v.is_cuda(), "All tensors must be on CUDA");
-  TORCH_CHECK(q.dtype() == torch::kHalf && k.dtype() == torch::kHalf && v.dtype() == torch::kHalf,
-              "All tensors must be FP16 (Half)");
+  const auto dt = q.scalar_type();
+  TORCH_CHECK((dt == torch::kHalf || dt == torch::kBFloat16) && k.scalar_type() == dt &&
+                  v.scalar_type() == dt,
+              "All tensors must be FP16 (Half), or all BF16");
+  const bool bf16 = dt == torch::kBFloat16;
   TORCH_CHECK(q.dim() == 4 && k.dim() == 4 && v.dim() == 4, "Tensors must be 4D [B, H, N, D]");
   const int64_t batch_size = q.size(0);
   const int64_t num_heads = q.size(1);
@@ -158,7 +161,7 @@ py::object flash_attn_forward_flash2_ex(torch::Tensor q, torch::Tensor k, torch:
   TORCH_CHECK(v.size(0) == batch_size && v.size(1) == num_heads && v.size(2) == k.size(2) &&
                   v.size(3) == head_dim,
               "Value dimensions must match Key dimensions [B, H, N_k, D]");
-  TORCH_CHECK(head_dim == 64, "FlashLite WMMA kernel currently requires head_dim == 64");
+  TORCH_CHECK(head_dim == 64 || head_dim == 128, "forward_flash2_ex requires head_dim 64 or 128");
   TORCH_CHECK(q.stride(3) == 1 && k.stride(3) == 1 && v.stride(3) == 1,
               "The head dimension must have unit stride");
   check_same_device(q, k, v);
@@ -169,7 +172,7 @@ py::object flash_attn_forward_flash2_ex(torch::Tensor q, torch::Tensor k, torch:
     TORCH_CHECK(out_tensor.is_cuda() && out_tensor.stride(3) == 1,
                 "out tensor must be a CUDA tensor with a unit-stride head dimension");
     TORCH_CHECK(out_tensor.sizes() == q.sizes(), "out tensor shape must match q");
-    TORCH_CHECK(out_tensor.dtype() == torch::kHalf, "out tensor dtype must be FP16");
+    TORCH_CHECK(out_tensor.scalar_type() == dt, "out tensor dtype must match q");
     TORCH_CHECK(out_tensor.device() == q.device(), "out tensor must be on the same device as q");
   } else {
     out_tensor = torch::empty_like(q);
@@ -188,12 +191,18 @@ py::object flash_attn_forward_flash2_ex(torch::Tensor q, torch::Tensor k, torch:
     for (int d = 0; d < 3; ++d) st[i][d] = ts[i]->stride(d);
   p.lse = return_lse ? lse.data_ptr<float>() : nullptr;
   TORCH_CHECK(num_splits >= 0 && num_splits <= INT32_MAX, "num_splits must be >= 0");
-  const int64_t ws_bytes =
-      num_splits == 1 ? 0 : fl_attn_splitkv_workspace_bytes(&p, (int32_t)num_splits);
+  // Split-KV is built for fp16 at head_dim 64; bf16 and head_dim 128 run one pass.
+  const bool one_pass_only = bf16 || head_dim != 64;
+  TORCH_CHECK(!one_pass_only || num_splits <= 1,
+              "split-KV (num_splits > 1) needs fp16 tensors with head_dim 64");
+  const int64_t ws_bytes = (num_splits == 1 || one_pass_only)
+                               ? 0
+                               : fl_attn_splitkv_workspace_bytes(&p, (int32_t)num_splits);
   TORCH_CHECK(ws_bytes >= 0, "FlashLite HIP error: ", fl_attn_last_error());
   int rc;
   if (ws_bytes == 0) {
-    rc = fl_attn_fwd_f16_ex(&p, -1, current_stream(q));
+    rc = bf16 ? fl_attn_fwd_bf16_ex(&p, -1, current_stream(q))
+              : fl_attn_fwd_f16_ex(&p, -1, current_stream(q));
   } else {
     torch::Tensor ws;
     if (workspace.has_value() && workspace.value().defined() &&
@@ -226,8 +235,8 @@ PYBIND11_MODULE(flash_attn_wmma, m) {
         py::arg("sm_scale") = 0.0, py::arg("is_causal") = false, py::arg("out") = py::none());
 
   m.def("forward_flash2_ex", &flash_attn::flash_attn_forward_flash2_ex,
-        "FlashAttention-2 forward on strided [B, H, N, 64] views, N_k != N_q (bottom-right "
-        "causal), optional log-sum-exp",
+        "FlashAttention-2 forward on strided [B, H, N, D] views (fp16 or bf16, D 64 or 128), "
+        "N_k != N_q (bottom-right causal), optional log-sum-exp",
         py::arg("q"), py::arg("k"), py::arg("v"), py::arg("sm_scale") = 0.0,
         py::arg("is_causal") = false, py::arg("out") = py::none(), py::arg("return_lse") = false,
         py::arg("num_splits") = 0, py::arg("workspace") = py::none());
@@ -244,7 +253,8 @@ PYBIND11_MODULE(flash_attn_wmma, m) {
             p.k_stride[d] = p.v_stride[d] = ks[d];
           }
           p.lse = nullptr;
-          if (num_splits == 1) return (int64_t)0;
+          if (num_splits == 1 || q.scalar_type() != torch::kHalf || q.size(3) != 64)
+            return (int64_t)0;  // one pass: split-KV is built for fp16 at head_dim 64
           const int64_t b = fl_attn_splitkv_workspace_bytes(&p, (int32_t)num_splits);
           TORCH_CHECK(b >= 0, "FlashLite HIP error: ", fl_attn_last_error());
           return b;

@@ -70,6 +70,33 @@ def make_qkv(batch: int, heads: int, seq: int, head_dim: int, seed: int = 0,
     return tuple(out)
 
 
+def round_bf16(x) -> np.ndarray:
+    """float32 array -> the nearest bfloat16 values (round to nearest, ties to
+    even), returned as float32.  bf16 is the upper half of an IEEE float32,
+    so rounding adds half an ulp of the dropped 16 bits (minus one when the
+    kept low bit is 0, which sends ties to even) and clears them.  NaN and
+    inf are not expected here (inputs are finite normals)."""
+    u = np.ascontiguousarray(x, dtype=np.float32).view(np.uint32).astype(np.uint64)
+    u = (u + 0x7FFF + ((u >> 16) & 1)) & 0xFFFF0000
+    return u.astype(np.uint32).view(np.float32)
+
+
+def make_qkv_bf16(batch: int, heads: int, seq: int, head_dim: int, seed: int = 0,
+                  scale: float = 1.0):
+    """Seeded bf16-valued Q, K, V: the make_qkv draws rounded to bfloat16,
+    held in float32 arrays (numpy has no bfloat16; every value is exactly
+    representable, so ``torch.from_numpy(x).to(torch.bfloat16)`` is exact)."""
+    rs = np.random.RandomState(seed)
+    shape = (batch, heads, seq, head_dim)
+    out = []
+    for _ in range(3):
+        x = rs.standard_normal(size=shape)
+        if scale != 1.0:
+            x = x * scale
+        out.append(round_bf16(x.astype(np.float32)))
+    return tuple(out)
+
+
 def workload_inputs(w: Workload):
     return make_qkv(w.batch, w.heads, w.seq, w.head_dim, w.seed, w.input_scale)
 

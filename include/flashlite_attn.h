@@ -37,7 +37,8 @@ extern "C" {
 enum fl_status {
   FL_OK = 0,
   FL_ERR_INVALID_ARGUMENT = 1, /* NULL pointer, negative size, non-finite scale */
-  FL_ERR_UNSUPPORTED = 2,      /* head_dim != 64 (flash2), strides or sizes past limits */
+  FL_ERR_UNSUPPORTED = 2,      /* head_dim != 64 (flash2; 64 or 128 for the _ex entries),
+                                  strides or sizes past limits */
   FL_ERR_MISALIGNED = 3,       /* flash2 needs 16-byte aligned q/k/v/o */
   FL_ERR_LAUNCH = 4,           /* the HIP launch itself failed */
   FL_ERR_BAD_CONFIG = 5        /* forced tile configuration out of range */
@@ -92,9 +93,17 @@ int fl_attn_fwd_f16_cfg(const fl_attn_params* p, int32_t config, void* stream);
  * ln(sum_j exp(sm_scale * q.k_j)) over its visible keys, -inf for a row
  * with no visible key; NULL to skip.
  *
+ * head_dim is 64 or 128.  At 128, Q enters the MFMA unscaled and the fp32
+ * scores are scaled by sm_scale*log2(e) (at 64, Q is prescaled in fp16 as in
+ * the reference, csrc/kernel_flash2.cu:772).  At 64, `config` is as for
+ * fl_attn_fwd_f16_cfg;
+ * at 128 it is -1 or one of the two slot-scheduled configurations
+ * (6 "br256_bc64_w8_slot", 7 "br128_bc64_w4_slot"; same work-group shapes,
+ * 32-key tiles), FL_ERR_BAD_CONFIG otherwise.
+ *
  * No counterpart in the reference, which accepts only contiguous
  * [B, H, N, 64] tensors (csrc/kernel_flash2.cu:741-757) and returns no
- * log-sum-exp; `config` as for fl_attn_fwd_f16_cfg.
+ * log-sum-exp.
  */
 typedef struct fl_attn_params_ex {
   fl_attn_params base;
@@ -108,7 +117,19 @@ typedef struct fl_attn_params_ex {
 int fl_attn_fwd_f16_ex(const fl_attn_params_ex* p, int32_t config, void* stream);
 
 /*
- * Split-KV forward ("flash-decoding"), for few query rows over many keys:
+ * bf16 q, k, v and o (same layouts, strides, lse and head_dims as
+ * fl_attn_fwd_f16_ex; `config` -1, 6 or 7).  Q enters the MFMA unscaled and
+ * the fp32 scores are scaled by sm_scale*log2(e); P is rounded to bf16
+ * before the PV product and the row sums are fp32.
+ *
+ * No counterpart in the reference, which accepts fp16 only
+ * (csrc/kernel_flash2.cu:745-747).
+ */
+int fl_attn_fwd_bf16_ex(const fl_attn_params_ex* p, int32_t config, void* stream);
+
+/*
+ * Split-KV forward ("flash-decoding"), fp16 at head_dim 64, for few query
+ * rows over many keys:
  * the key range of every (batch, head) is cut into chunks processed by
  * separate work-groups, whose partial results (unnormalised O, stabiliser,
  * row sum) go to `workspace`; a second kernel on the same stream merges

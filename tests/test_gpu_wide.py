@@ -1,0 +1,220 @@
+"""GPU parity of the paths beyond the reference's element type and head dim:
+head_dim 128 (fp16 and bf16) and bf16 at head_dim 64, through the C ABI
+(``fl_attn_fwd_f16_ex`` / ``fl_attn_fwd_bf16_ex``) and the binding
+(``forward_flash2_ex``).  The reference accepts fp16 at D = 64 only
+(csrc/kernel_flash2.cu:745-757).
+
+Tolerances against the fp32 oracle on the same inputs:
+* fp16 (any head dim): the north_star bound, max-abs <= 2e-3, mean-abs <= 2e-4.
+* bf16: 8x that, max-abs <= 1.6e-2 and mean-abs <= 1.6e-3.  bf16 keeps 8
+  significand bits against fp16's 11, so its unit roundoff (2^-8) is 8x
+  fp16's (2^-11); the output rounding alone reaches 2^-9 |O| and P is
+  rounded to bf16 before the PV product.  The inputs are bf16-exact values
+  (``workloads.round_bf16``), so the oracle sees exactly what the kernel reads.
+* log-sum-exp: max-abs <= 2e-3, mean-abs <= 3e-4 (natural-log units) for both
+  types; bf16 and head_dim 128 keep Q unscaled and scale the fp32 scores, so
+  their scores are closer to the oracle's than the D = 64 fp16 path's
+  prescaled ones.
+A strided launch equals the contiguous launch of the same data bit for bit.
+"""
+
+import numpy as np
+import pytest
+
+from flashlite_amd import capi
+from gpu_util import MAX_ABS, MEAN_ABS, sample_rows
+from oracle import attention_fp32, attention_lse, error_stats
+
+pytestmark = pytest.mark.gpu
+
+BF16_MAX_ABS = 8 * MAX_ABS
+BF16_MEAN_ABS = 8 * MEAN_ABS
+LSE_MAX_ABS = 2e-3
+LSE_MEAN_ABS = 3e-4
+SLOT_CFGS = [-1, 6, 7]
+KINDS = [("fp16", 64), ("fp16", 128), ("bf16", 64), ("bf16", 128)]
+WIDE = [k for k in KINDS if k != ("fp16", 64)]
+
+
+def _tol(kind):
+    return (BF16_MAX_ABS, BF16_MEAN_ABS) if kind == "bf16" else (MAX_ABS, MEAN_ABS)
+
+
+def _inputs(kind, b, h, nq, nk, d, seed, qk_scale=1.0):
+    """Seeded inputs (float32 arrays of the element type's values)."""
+    rs = np.random.RandomState(seed)
+    mk = lambda n, c: (rs.standard_normal((b, h, n, d)) * c).astype(np.float32)  # noqa: E731
+    q, k, v = mk(nq, qk_scale), mk(nk, qk_scale), mk(nk, 1.0)
+    if kind == "bf16":
+        from flashlite_amd.workloads import round_bf16
+
+        return tuple(round_bf16(x) for x in (q, k, v))
+    return tuple(x.astype(np.float16).astype(np.float32) for x in (q, k, v))
+
+
+def _torch_dtype(kind):
+    import torch
+
+    return torch.bfloat16 if kind == "bf16" else torch.float16
+
+
+def _run(kind, q, k, v, sm_scale, causal, dev, config=-1, lse=False, views=None):
+    """Launch through the C ABI; `views` maps the contiguous tensors to the
+    strided ones to pass (default: the contiguous tensors)."""
+    import torch
+
+    dt = _torch_dtype(kind)
+    tq, tk, tv = (torch.from_numpy(np.ascontiguousarray(x)).to(dev).to(dt) for x in (q, k, v))
+    o = torch.full_like(tq, float("nan"))
+    if views is not None:
+        tq, tk, tv, o = views(tq, tk, tv, o)
+    ls = torch.full(tq.shape[:3], float("nan"), dtype=torch.float32, device=dev) if lse else None
+    p = capi.tensor_params_ex(tq, tk, tv, o, sm_scale, causal, lse=ls)
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    fn = capi.fwd_bf16_ex if kind == "bf16" else capi.fwd_ex
+    capi.check(fn(p, stream, config))
+    torch.cuda.synchronize(dev)
+    return o.float().cpu().numpy(), (ls.cpu().numpy() if lse else None)
+
+
+def _check(kind, out, ref, what):
+    mx_tol, mean_tol = _tol(kind)
+    assert np.isfinite(out).all(), f"{what}: non-finite (or unwritten) outputs"
+    mx, mean = error_stats(out, ref)
+    assert mx <= mx_tol and mean <= mean_tol, f"{what}: max-abs {mx:.3e} mean-abs {mean:.3e}"
+    return mx, mean
+
+
+RAGGED = [1, 17, 31, 32, 33, 63, 64, 65, 100, 129, 257, 513]
+
+
+@pytest.mark.parametrize("kind,d", WIDE)
+@pytest.mark.parametrize("config", SLOT_CFGS)
+@pytest.mark.parametrize("causal", [False, True])
+def test_ragged(cuda, kind, d, config, causal):
+    for n in RAGGED:
+        q, k, v = _inputs(kind, 2, 3, n, n, d, seed=2000 + n + d)
+        out, _ = _run(kind, q, k, v, 0.0, causal, cuda, config=config)
+        _check(kind, out, attention_fp32(q, k, v, 0.0, causal), f"N={n}")
+
+
+RECT = [(1, 1), (1, 300), (5, 64), (37, 100), (100, 37), (64, 65), (200, 513), (513, 200),
+        (129, 1000), (1000, 129)]
+
+
+@pytest.mark.parametrize("kind,d", WIDE)
+@pytest.mark.parametrize("config", [6, 7])
+@pytest.mark.parametrize("causal", [False, True])
+def test_rectangular_with_lse(cuda, kind, d, config, causal):
+    for nq, nk in RECT:
+        q, k, v = _inputs(kind, 1, 2, nq, nk, d, seed=nq * 7 + nk + d)
+        out, lse = _run(kind, q, k, v, 0.125, causal, cuda, config=config, lse=True)
+        ref = attention_fp32(q, k, v, 0.125, causal)
+        _check(kind, out, ref, f"{nq}x{nk}")
+        ref_lse = attention_lse(q, k, 0.125, causal)
+        fin = np.isfinite(ref_lse)
+        assert np.array_equal(fin, np.isfinite(lse)), f"{nq}x{nk}: lse -inf pattern"
+        mx, mean = error_stats(lse[fin], ref_lse[fin]) if fin.any() else (0.0, 0.0)
+        assert mx <= LSE_MAX_ABS and mean <= LSE_MEAN_ABS, (
+            f"{nq}x{nk}: lse max-abs {mx:.3e} mean-abs {mean:.3e}")
+
+
+@pytest.mark.parametrize("kind,d", KINDS)
+@pytest.mark.parametrize("causal", [False, True])
+def test_headline_shape(cuda, kind, d, causal):
+    """B2 H8 N4096 at each element type and head dim, sampled rows."""
+    q, k, v = _inputs(kind, 2, 8, 4096, 4096, d, seed=77 + d)
+    out, _ = _run(kind, q, k, v, 0.125, causal, cuda)
+    rows = sample_rows(4096, seed=d)
+    ref = attention_fp32(q, k, v, 0.125, causal, rows=rows)
+    _check(kind, out[:, :, rows], ref, f"{kind} D={d}")
+
+
+@pytest.mark.parametrize("kind,d", WIDE)
+@pytest.mark.parametrize("scale,sm", [(1.0, 1.0), (3.0, 1.0), (1.0, -0.3)])
+def test_peaked_and_negative_scales(cuda, kind, d, scale, sm):
+    """Large and negative scales: the stabiliser's checked pass and the sign
+    flip.  Tolerance doubled for |scale| >= 1 as in the fp16 tests (outputs
+    reach |O| ~ 4-5, where one output ulp alone is 2^-9 |O| in bf16)."""
+    q, k, v = _inputs(kind, 1, 2, 300, 300, d, seed=31, qk_scale=scale)
+    for causal in (False, True):
+        out, _ = _run(kind, q, k, v, sm, causal, cuda)
+        ref = attention_fp32(q, k, v, sm, causal)
+        mx_tol, mean_tol = _tol(kind)
+        if abs(sm) >= 1.0:
+            mx_tol *= 2
+        mx, mean = error_stats(out, ref)
+        assert np.isfinite(out).all()
+        assert mx <= mx_tol and mean <= mean_tol, f"causal={causal}: {mx:.3e} {mean:.3e}"
+
+
+@pytest.mark.parametrize("kind,d", WIDE)
+@pytest.mark.parametrize("causal", [False, True])
+def test_strided_bit_exact(cuda, kind, d, causal):
+    """[B, N, H, D] views (the flash_attn layout) and padded rows give the
+    same bits as the contiguous launch."""
+    import torch
+
+    q, k, v = _inputs(kind, 2, 3, 200, 333, d, seed=5 + d)
+    base, _ = _run(kind, q, k, v, 0.125, causal, cuda)
+
+    def bnhd(tq, tk, tv, o):
+        f = lambda t: t.transpose(1, 2).contiguous().transpose(1, 2)  # noqa: E731
+        return f(tq), f(tk), f(tv), f(o)
+
+    def padded(tq, tk, tv, o):
+        def pad(t):
+            b, h, n, dd = t.shape
+            big = torch.zeros((b, h, n, dd + 64), dtype=t.dtype, device=t.device)
+            big[..., :dd] = t
+            return big[..., :dd]
+        return pad(tq), pad(tk), pad(tv), pad(o)
+
+    for views in (bnhd, padded):
+        out, _ = _run(kind, q, k, v, 0.125, causal, cuda, views=views)
+        assert np.array_equal(out, base), views.__name__
+
+
+@pytest.mark.parametrize("kind,d", WIDE)
+def test_config_choice_equal(cuda, kind, d):
+    """The two slot configurations give the same bits (per row they run the
+    same arithmetic in the same order with fp32 row sums; only the
+    work-group shape differs)."""
+    q, k, v = _inputs(kind, 2, 4, 700, 700, d, seed=9)
+    a, _ = _run(kind, q, k, v, 0.125, True, cuda, config=6)
+    b, _ = _run(kind, q, k, v, 0.125, True, cuda, config=7)
+    assert np.array_equal(a, b)
+
+
+def test_binding_wide(cuda):
+    import torch
+
+    import flashlite_amd
+
+    for kind, d in WIDE:
+        q, k, v = _inputs(kind, 1, 4, 257, 300, d, seed=3)
+        dt = _torch_dtype(kind)
+        tq, tk, tv = (torch.from_numpy(x).to(cuda).to(dt) for x in (q, k, v))
+        for causal in (False, True):
+            out, lse = flashlite_amd.forward_flash2_ex(tq, tk, tv, 0.0, causal, return_lse=True)
+            assert out.dtype == dt and lse.dtype == torch.float32
+            _check(kind, out.float().cpu().numpy(), attention_fp32(q, k, v, 0.0, causal),
+                   f"binding {kind} D={d}")
+            buf = torch.empty_like(tq)
+            ret = flashlite_amd.forward_flash2_ex(tq, tk, tv, 0.0, causal, out=buf)
+            assert ret.data_ptr() == buf.data_ptr()
+        with pytest.raises(RuntimeError, match="split-KV"):
+            flashlite_amd.forward_flash2_ex(tq, tk, tv, num_splits=2)
+        with pytest.raises(RuntimeError, match="out tensor dtype must match q"):
+            other = torch.float16 if kind == "bf16" else torch.bfloat16
+            flashlite_amd.forward_flash2_ex(tq, tk, tv, out=torch.empty_like(tq, dtype=other))
+    # the reference surface keeps the reference's checks
+    q16 = torch.zeros((1, 2, 8, 128), dtype=torch.float16, device=cuda)
+    with pytest.raises(RuntimeError, match="requires head_dim == 64"):
+        flashlite_amd.forward_flash2(q16, q16, q16)
+    qb = torch.zeros((1, 2, 8, 64), dtype=torch.bfloat16, device=cuda)
+    with pytest.raises(RuntimeError, match="FP16"):
+        flashlite_amd.forward_flash2(qb, qb, qb)
+    q96 = torch.zeros((1, 2, 8, 96), dtype=torch.float16, device=cuda)
+    with pytest.raises(RuntimeError, match="head_dim 64 or 128"):
+        flashlite_amd.forward_flash2_ex(q96, q96, q96)
