@@ -14,6 +14,11 @@ mean launch time measured with HIP events on that stream.
 writes M MiB (``torch.mul(src, 1, out=dst)``): the reference point that
 scales the HBM byte counters (FETCH_SIZE / WRITE_SIZE) of a profile.
 
+``--dtype bf16`` and/or ``--head-dim 128`` run the workload's shape at that
+element type / head dim through ``fl_attn_fwd_bf16_ex`` or
+``fl_attn_fwd_f16_ex`` (seeded inputs from ``make_qkv`` / ``make_qkv_bf16``;
+``--config`` -1, 6 or 7).
+
 ``--decode B H NQ NK`` runs a decode-shaped call (NQ query rows over NK
 keys, seeded N(0,1) inputs) through ``fl_attn_fwd_f16_splitkv`` with
 ``--splits S`` (1 = one pass, 0 = the library's choice, n = n key chunks)
@@ -38,6 +43,8 @@ def main(argv=None):
     ap.add_argument("--decode", type=int, nargs=4, metavar=("B", "H", "NQ", "NK"), default=None)
     ap.add_argument("--splits", type=int, default=0)
     ap.add_argument("--causal-decode", type=int, default=0)
+    ap.add_argument("--dtype", choices=("fp16", "bf16"), default="fp16")
+    ap.add_argument("--head-dim", type=int, default=0, help="override the workload's head dim")
     args = ap.parse_args(argv)
 
     import torch
@@ -63,18 +70,34 @@ def main(argv=None):
         return 0
 
     from flashlite_amd import capi
-    from flashlite_amd.workloads import WORKLOADS, workload_inputs
+    from flashlite_amd.workloads import WORKLOADS, make_qkv, make_qkv_bf16, workload_inputs
 
     w = WORKLOADS[args.workload]
     dev = torch.device("cuda:0")
-    q, k, v = (torch.from_numpy(x).to(dev) for x in workload_inputs(w))
+    head_dim = args.head_dim or w.head_dim
+    wide = args.dtype == "bf16" or head_dim != 64
+    if wide:
+        gen = make_qkv_bf16 if args.dtype == "bf16" else make_qkv
+        dt = torch.bfloat16 if args.dtype == "bf16" else torch.float16
+        q, k, v = (torch.from_numpy(x).to(dev).to(dt)
+                   for x in gen(w.batch, w.heads, w.seq, head_dim, w.seed, w.input_scale))
+    else:
+        q, k, v = (torch.from_numpy(x).to(dev) for x in workload_inputs(w))
     o = torch.empty_like(q)
-    p = capi.tensor_params(q, k, v, o, w.sm_scale, bool(args.causal))
     stream = torch.cuda.current_stream().cuda_stream
-    cfg = capi.select_config(p) if args.config < 0 else args.config
+    if wide:
+        p = capi.tensor_params_ex(q, k, v, o, w.sm_scale, bool(args.causal))
+        fwd_ex = capi.fwd_bf16_ex if args.dtype == "bf16" else capi.fwd_ex
+        cfg = args.config
+    else:
+        p = capi.tensor_params(q, k, v, o, w.sm_scale, bool(args.causal))
+        cfg = capi.select_config(p) if args.config < 0 else args.config
 
     def launch():
-        rc = capi.naive(p, stream) if args.naive else capi.fwd(p, stream, cfg)
+        if wide:
+            rc = fwd_ex(p, stream, cfg)
+        else:
+            rc = capi.naive(p, stream) if args.naive else capi.fwd(p, stream, cfg)
         capi.check(rc)
 
     launch()
@@ -86,10 +109,10 @@ def main(argv=None):
     end.record()
     torch.cuda.synchronize()
     us = start.elapsed_time(end) * 1e3 / args.iters
-    flops = (2.0 if args.causal else 4.0) * w.batch * w.heads * w.seq ** 2 * w.head_dim
-    name = "naive" if args.naive else capi.config_name(cfg)
-    print(f"{args.workload} causal={args.causal} {name}: {us:.2f} us/launch, "
-          f"{flops / us / 1e6:.1f} TFLOP/s", flush=True)
+    flops = (2.0 if args.causal else 4.0) * w.batch * w.heads * w.seq ** 2 * head_dim
+    name = "naive" if args.naive else ("auto" if cfg < 0 else capi.config_name(cfg))
+    print(f"{args.workload} {args.dtype} D={head_dim} causal={args.causal} {name}: "
+          f"{us:.2f} us/launch, {flops / us / 1e6:.1f} TFLOP/s", flush=True)
 
 
 def _decode(args, torch):
