@@ -103,27 +103,26 @@ int check_pointers(const fl_attn_params* p, fl::FwdArgs* a, const char* who, uin
   return FL_OK;
 }
 
-// Tile-configuration choice for 256 CUs (measured on MI355X; every
-// configuration computes the same result).  Non-causal work-groups are all
-// equally long: one 256-row group of 8 waves per CU when there are enough of
-// them, else the key-range-split 128-row group (8 waves, two key halves)
-// while there are fewer than two 128-row groups per CU.  Causal groups differ
-// in length and are balanced by dispatch order, which needs many of them:
-// 128-row groups of 4 waves, two per CU.  Smaller problems fall back to
-// smaller groups.  Replaces the reference's `seq_len >= 2048 -> Br=128` rule
+// Tile-configuration choice for 256 CUs (measured on MI355X, every
+// configuration computes the same result).  Non-causal: one 256-row group
+// of 8 waves per CU when there are enough of them and the key range is long
+// (N_k >= 4096; shorter ranges measured faster with 128-row groups); the
+// key-range-split 128-row group (8 waves, two key halves) when there are
+// very few groups; otherwise 128-row slot-scheduled groups of 4 waves, two
+// per CU, which also serve causal attention (groups of different lengths,
+// balanced by dispatch order).  Smaller problems fall back to smaller
+// groups.  Replaces the reference's `seq_len >= 2048 -> Br=128` rule
 // (kernel_flash2.cu:786-789), which was sized for 20 SMs.
 int select_fa2(const fl::FwdArgs& a) {
   constexpr int64_t kCus = 256;
   auto wgs = [&](int64_t br) { return (a.seq + br - 1) / br * (int64_t)a.batch_heads; };
-  if (!a.causal && wgs(256) >= kCus) return 6;                       // br256_bc64_w8_slot
-  if (!a.causal && a.seq >= 2048 && wgs(128) < 2 * kCus) return 5;  // br128_bc64_w4_split2
+  if (!a.causal && a.seq_k >= 4096 && wgs(256) >= kCus) return 6;  // br256_bc64_w8_slot
+  if (!a.causal && a.seq >= 2048 && wgs(128) < kCus / 2) return 5;  // br128_bc64_w4_split2
   if (wgs(128) >= kCus / 4) return 7;                                // br128_bc64_w4_slot
   if (wgs(64) >= kCus / 4) return 1;                                 // br64_bc64_w2
   return 0;                                                          // br32_bc64_w1
 }
 
-// `wide`: head_dim 128 accepted as well (the _ex entries; beyond the
-// reference, whose kernels hard-reject D != 64, kernel_flash2.cu:756-757).
 int check_fa2(const fl_attn_params* p, fl::FwdArgs* a, const char* who = "fl_attn_fwd_f16",
               bool wide = false) {
   int rc = check_common(p, a, who);
@@ -252,7 +251,8 @@ int select_any(const fl::FwdArgs& a) {
   if (!narrow_configs(a)) return select_fa2(a);
   constexpr int64_t kCus = 256;
   const int64_t wgs256 = (a.seq + 255) / 256 * (int64_t)a.batch_heads;
-  return (!a.causal && wgs256 >= kCus) ? fl::kSlotW8Config : fl::kSlotW4Config;
+  return (!a.causal && a.seq_k >= 4096 && wgs256 >= kCus) ? fl::kSlotW8Config
+                                                           : fl::kSlotW4Config;
 }
 
 int fwd_ex(const fl_attn_params_ex* p, int32_t config, void* stream, int dtype, const char* who) {

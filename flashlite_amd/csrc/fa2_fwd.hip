@@ -1363,9 +1363,10 @@ fa2_fwd_slot_kernel(const T* Q, const T* __restrict__ K, const T* __restrict__ V
     float sum[4];
     static_for(std::make_integer_sequence<int, 16>{}, [&](auto sl) __attribute__((always_inline)) {
       constexpr int L = decltype(sl)::value;
-      // The MFMA goes first: its operand's wait then never covers the read
-      // issued in the same slot.
+      // The MFMA goes first (fenced): its operand's wait then never covers
+      // the read issued in the same slot.
       rows.template mfma_slot<L>(op[L], S, Pp);
+      __builtin_amdgcn_sched_barrier(0);
       if constexpr (L + kAhead < 16)
         op[L + kAhead] = rows.template read_slot<L + kAhead>(
             rings.kslot(Ic<I>{}), rings.kslot(Ic<I + 1>{}), rings.vslot(Ic<I - 1>{}));
@@ -1773,6 +1774,7 @@ fa2_fwd_d128_kernel(const T* Q, const T* __restrict__ K, const T* __restrict__ V
     static_for(std::make_integer_sequence<int, 16>{}, [&](auto sl) __attribute__((always_inline)) {
       constexpr int L = decltype(sl)::value;
       rows.template mfma_slot<L>(op[L], Sn, Pp);
+      __builtin_amdgcn_sched_barrier(0);
       if constexpr (L + kAhead < 16)
         op[L + kAhead] = rows.template read_slot<L + kAhead>(rings.kslot(Ic<I + 1>{}),
                                                              rings.vslot(Ic<I - 1>{}));

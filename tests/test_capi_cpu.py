@@ -159,12 +159,14 @@ def test_naive_limits():
 def test_dispatcher_choices():
     sel = lambda **kw: capi.select_config(_p(**kw))  # noqa: E731
     # non-causal: 8-wave 256-row slot-scheduled groups when there is one per CU
+    # and the key range is long
     assert sel(batch=2, heads=8, seq_q=4096) == 6      # 256 groups
     assert sel(batch=1, heads=16, seq_q=16384) == 6
-    assert sel(batch=32, heads=32, seq_q=256) == 6
-    # fewer than two 128-row groups per CU at N >= 2048: split key range
-    assert sel(batch=2, heads=8, seq_q=2048) == 5      # 256 groups of 128 rows
+    assert sel(batch=32, heads=32, seq_q=256) == 7     # short keys: 128-row groups
+    assert sel(batch=2, heads=8, seq_q=2048) == 7
+    # very few groups at N >= 2048: split key range
     assert sel(batch=1, heads=1, seq_q=4096) == 5
+    assert sel(batch=1, heads=3, seq_q=4096) == 5      # 96 groups of 128 rows
     # causal: 128-row slot-scheduled groups balanced by dispatch order
     assert sel(batch=2, heads=8, seq_q=4096, causal=True) == 7
     assert sel(batch=1, heads=16, seq_q=16384, causal=True) == 7
