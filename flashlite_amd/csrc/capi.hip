@@ -111,11 +111,17 @@ int check_pointers(const fl_attn_params* p, fl::FwdArgs* a, const char* who, uin
 // very few groups; otherwise 128-row slot-scheduled groups of 4 waves, two
 // per CU, which also serve causal attention (groups of different lengths,
 // balanced by dispatch order).  Smaller problems fall back to smaller
-// groups.  Replaces the reference's `seq_len >= 2048 -> Br=128` rule
-// (kernel_flash2.cu:786-789), which was sized for 20 SMs.
+// groups.  Key ranges of at most 256 keys go to the streaming persistent
+// groups when causal (any count: one buffer holds every key a unit needs)
+// or when there are at least one unit per CU; with fewer non-causal units
+// the 128-row groups measured faster.  Replaces the reference's
+// `seq_len >= 2048 -> Br=128` rule (kernel_flash2.cu:786-789), which was
+// sized for 20 SMs.
 int select_fa2(const fl::FwdArgs& a) {
   constexpr int64_t kCus = 256;
   auto wgs = [&](int64_t br) { return (a.seq + br - 1) / br * (int64_t)a.batch_heads; };
+  if (fl::stream_config_fits(a) && (a.causal || wgs(256) >= kCus))
+    return fl::kStreamConfig;  // br256_kv256_w8_stream
   if (!a.causal && a.seq_k >= 4096 && wgs(256) >= kCus) return 6;  // br256_bc64_w8_slot
   if (!a.causal && a.seq >= 2048 && wgs(128) < kCus / 2) return 5;  // br128_bc64_w4_split2
   if (wgs(128) >= kCus / 4) return 7;                                // br128_bc64_w4_slot
@@ -268,6 +274,9 @@ int fwd_ex(const fl_attn_params_ex* p, int32_t config, void* stream, int dtype, 
     return fail(FL_ERR_BAD_CONFIG, "%s: config %d is not built for %s at head_dim %d (use -1, %d or %d)",
                 who, (int)config, dtype == fl::kDtypeBF16 ? "bf16" : "fp16", a.head_dim,
                 fl::kSlotW8Config, fl::kSlotW4Config);
+  if (config == fl::kStreamConfig && !fl::stream_config_fits(a))
+    return fail(FL_ERR_BAD_CONFIG, "%s: config %d needs N_k <= %d and row strides below 2^22 "
+                "(got N_k %d)", who, (int)config, fl::kStreamMaxKeys, a.seq_k);
   if (empty_problem(a)) return FL_OK;
   rc = check_pointers(&p->base, &a, who, 16);
   if (rc != FL_OK) return rc;
@@ -303,6 +312,9 @@ int fl_attn_fwd_f16_cfg(const fl_attn_params* p, int32_t config, void* stream) {
   if (config < -1 || config >= fl::kNumFa2Configs)
     return fail(FL_ERR_BAD_CONFIG, "fl_attn_fwd_f16: config %d out of range [-1, %d)", (int)config,
                 fl::kNumFa2Configs);
+  if (config == fl::kStreamConfig && !fl::stream_config_fits(a))
+    return fail(FL_ERR_BAD_CONFIG, "fl_attn_fwd_f16: config %d needs N_k <= %d (got %d)",
+                (int)config, fl::kStreamMaxKeys, a.seq_k);
   if (empty_problem(a)) return FL_OK;
   rc = check_pointers(p, &a, "fl_attn_fwd_f16", 16);
   if (rc != FL_OK) return rc;

@@ -353,8 +353,10 @@ struct Rows {
   float l;          // this lane's share of the row sum
   V8 p[2][2];  // fp16 P^T B-operands of the last softmaxed tile
 
-  __device__ __forceinline__ void init(const T* Qh, int q_sr, int lane, int qw_, int seq_,
-                                       int seq_k, int coff, float cq, float cr_) {
+  // Lane placement: rows qw_ .. qw_+31 of a head with seq_ query rows and
+  // seq_k keys (causal diagonal offset coff).
+  __device__ __forceinline__ void place(int lane, int qw_, int seq_, int seq_k, int coff,
+                                        float cr_) {
     g = lane >> 5;
     col = lane & 31;
     qw = qw_;
@@ -371,6 +373,19 @@ struct Rows {
     tr_row = 4 * (trG >> 1) + (trj >> 2);
     const int tr_x = trj & 3;
     tr_col = 16 * (trG & 1) + 4 * (((tr_x & 1) << 1) | (tr_x >> 1));
+  }
+  // Q'^T from the raw 16-byte chunks Q[my_q][16s + 8g .. +7] (s = 0..3).
+  __device__ __forceinline__ void set_q(const u32x4_t (&raw)[4], float cq) {
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      const V8 x = __builtin_bit_cast(V8, raw[s]);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) qf[s][e] = (T)((float)x[e] * cq);
+    }
+  }
+  __device__ __forceinline__ void init(const T* Qh, int q_sr, int lane, int qw_, int seq_,
+                                       int seq_k, int coff, float cq, float cr_) {
+    place(lane, qw_, seq_, seq_k, coff, cr_);
     // Q'^T: lane holds cq * Q[my_q][16s + 8g .. +7] for s = 0..3, in fp16.
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
@@ -828,6 +843,34 @@ struct Rows {
           *reinterpret_cast<V8*>(orow + 32 * db + 16 * hh + 8 * g) = out;
         }
     }
+  }
+  // As store(), through buffer resources whose ranges end at the last valid
+  // row: O (rows r0.. of the resource, row_bytes apart) and the log-sum-exp
+  // (one float per row; an empty range when not requested).  Every lane
+  // issues the same five stores and the hardware drops the out-of-range
+  // ones, so a wave's count of outstanding memory operations is fixed.
+  __device__ __forceinline__ void store_rsrc(__amdgpu_buffer_rsrc_t ro, int r0, int row_bytes,
+                                             __amdgpu_buffer_rsrc_t rl) const {
+    const float l_tot = pair_sum(l);
+    const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
+    const int row = my_q - r0;
+    const float lg = m * (SCALED ? cr : 1.0f) + __builtin_amdgcn_logf(l_tot);
+    const float lse = l_tot > 0.0f ? 0.693147180559945309f * lg : ninf();
+    // Lanes of the second half repeat their row's value: point them past
+    // the range (a row past the end never fits a range of whole rows).
+    const int lse_off = g == 0 ? 4 * row : 0x7ffffff0;
+    __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(lse), rl, lse_off, 0, 0);
+#pragma unroll
+    for (int db = 0; db < 2; ++db)
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh) {
+        V8 out;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) out[e] = (T)(o[db][8 * hh + e] * inv);
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_t, out), ro,
+                                               row * row_bytes + 2 * (32 * db + 16 * hh + 8 * g),
+                                               0, 0);
+      }
   }
 };
 
@@ -1451,6 +1494,139 @@ fa2_fwd_slot_kernel(const T* Q, const T* __restrict__ K, const T* __restrict__ V
 }
 
 // ---------------------------------------------------------------------------
+// Short key ranges (N_k <= 256, e.g. many heads of 256 tokens): a unit is
+// one head's block of up to 256 query rows, whose whole K and V (4 tiles
+// each, 64 KiB) fit one LDS buffer.  A persistent work-group of 8 waves (32
+// rows each) walks units u = blockIdx.x, + gridDim.x, ... through two such
+// buffers: after the barrier that publishes unit i, its waves issue unit
+// i+1's K/V fetches (into the buffer unit i-1 used) and Q loads, then
+// compute unit i and store it.  Per-wave memory operations per unit are
+// fixed (8 fetches, 4 Q loads, 5 stores; out-of-range rows are dropped by
+// the buffer bounds, never branched around), so "unit i's loads have
+// landed" is exactly vmcnt <= 5: only unit i-1's stores may still be in
+// flight.  With one short unit per work-group, the start-up latency of every
+// unit (Q and K/V from HBM) would idle the CU; here it overlaps the previous
+// unit's compute.  Tiles are processed one at a time with the stabiliser
+// checked (Rows::softmax_checked), and no barrier sits inside a unit.
+constexpr int kStreamBr = 256;                           // query rows per unit
+constexpr int kStreamTiles = 4;                          // key tiles per unit (N_k <= 256)
+constexpr int kStreamHalf = kStreamTiles * kTileBytes;   // K (or V) of a unit: 32 KiB
+
+// vmcnt wait then the work-group barrier (a compiler memory barrier too).
+template <int kPending>
+__device__ __forceinline__ void wait_vm_barrier() {
+  static_assert(kPending >= 0 && kPending < 64, "vmcnt range");
+  __builtin_amdgcn_sched_barrier(0);
+  asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" : : "n"(kPending) : "memory");
+  __builtin_amdgcn_sched_barrier(0);
+}
+
+template <bool CAUSAL, bool SCALED, class T = _Float16>
+__global__ void __launch_bounds__(512, 2)  // <= 256 VGPRs: 8 waves, two per SIMD
+fa2_fwd_stream_kernel(const T* Q, const T* __restrict__ K, const T* __restrict__ V, T* O,
+                      const Geom geom, int nqb, int units, float cq, float cr) {
+  using RowsT = Rows<CAUSAL, SCALED, T>;
+  using V8 = typename RowsT::V8;
+  constexpr int kStores = 5;  // Rows::store_rsrc
+  __shared__ __attribute__((aligned(16))) uint8_t buf[2][2 * kStreamHalf];  // [unit parity][K | V]
+
+  const int lane = threadIdx.x & 63;
+  const int rw = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int g = lane >> 5, col = lane & 31;
+  const FetchOff<1> fk = fetch_offsets<1, false>(rw, lane, 2 * geom.k_sr);
+  const FetchOff<1> fv = fetch_offsets<1, true>(rw, lane, 2 * geom.v_sr);
+  const int seq = geom.seq_q;
+  const int qrow_bytes = 2 * geom.q_sr;
+  int ntiles = (geom.seq_k + kBc - 1) / kBc;  // 1..4 (the host checks N_k <= 256)
+  // The wave's 32-row block of a unit.  Waves w and w+4 share a SIMD; under
+  // the causal mask block j needs j/2 + 1 tiles, so pairing blocks j and
+  // 7-j gives every SIMD five tiles per unit instead of four to six.
+  const int blk = CAUSAL && rw >= 4 ? 11 - rw : rw;
+
+  // Unit u's K/V tiles 0..3 into buffer b (rows >= N_k read as zeros) and
+  // this wave's Q rows into raw (rows >= N_q read as zeros).
+  auto issue_loads = [&](int u, int b, u32x4_t (&raw)[4]) __attribute__((always_inline)) {
+    const int bh = u / nqb, qb = u - bh * nqb;
+    const HeadPtrs<T> hp = head_ptrs<T>(geom, bh, Q, K, V, O);
+#pragma unroll
+    for (int t = 0; t < kStreamTiles; ++t) {
+      fetch_tile<1>(hp.rk, buf[b] + t * kTileBytes, t, kStreamTiles - 1, rw, fk);
+      fetch_tile<1>(hp.rv, buf[b] + kStreamHalf + t * kTileBytes, t, kStreamTiles - 1, rw, fv);
+    }
+    const int q0 = qb * kStreamBr;
+    const int valid = min(kStreamBr, seq - q0);
+    const __amdgpu_buffer_rsrc_t rq = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(hp.q + (long long)q0 * geom.q_sr), 0, (valid - 1) * qrow_bytes + kRowBytes,
+        0x00020000);
+    const int off = (32 * blk + col) * qrow_bytes + 16 * g;
+#pragma unroll
+    for (int s = 0; s < 4; ++s)
+      raw[s] = __builtin_amdgcn_raw_buffer_load_b128(rq, off + 32 * s, 0, 0);
+  };
+
+  const int G = gridDim.x;
+  u32x4_t qraw[4];
+  // Unit u in buffer b; its loads have landed and every wave is done with
+  // the other buffer.
+  auto unit = [&](int u, int b) __attribute__((always_inline)) {
+    const int bh = u / nqb, qb = u - bh * nqb;
+    const int q0 = qb * kStreamBr;
+    const int qw = q0 + 32 * blk;
+    RowsT rows;
+    rows.place(lane, qw, seq, geom.seq_k, geom.coff, cr);
+    rows.set_q(qraw, cq);
+    rows.reset();
+    if (u + G < units) issue_loads(u + G, b ^ 1, qraw);
+
+    int nt = ntiles;
+    if (CAUSAL) nt = min(nt, causal_tiles(min(qw + 32, seq), geom.coff));
+    if (qw < seq) {
+      const uint8_t* kb = buf[b];
+      const uint8_t* vb = buf[b] + kStreamHalf;
+      for (int t = 0; t < nt; ++t) {
+        float16_t S[2];
+        V8 P[2][2];
+        {
+          V8 ka[2][4];
+          rows.read_k(kb + t * kTileBytes, ka);
+          rows.gemm1(ka, S);
+        }
+        rows.mask(t, S);
+        if (t == 0) rows.first_tile(S);
+        rows.softmax_checked(S, P);
+        {
+          V8 va[2][4];
+          rows.read_v(vb + t * kTileBytes, va);
+          rows.gemm2(va, P);
+        }
+      }
+    }
+    const int valid = min(kStreamBr, seq - q0);
+    const int b_ = bh / geom.heads, h_ = bh - b_ * geom.heads;
+    T* oh = O + (b_ * geom.o_sb + h_ * geom.o_sh) + (long long)q0 * geom.o_sr;
+    const __amdgpu_buffer_rsrc_t ro = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)oh, 0, (valid - 1) * 2 * geom.o_sr + kRowBytes, 0x00020000);
+    float* lh = geom.lse ? geom.lse + (long long)bh * seq + q0 : geom.lse;
+    const __amdgpu_buffer_rsrc_t rl =
+        __builtin_amdgcn_make_buffer_rsrc((void*)lh, 0, geom.lse ? 4 * valid : 0, 0x00020000);
+    rows.store_rsrc(ro, q0, 2 * geom.o_sr, rl);
+  };
+  // The first unit is peeled off, so at every use of the Q registers the
+  // compiler sees the same order of outstanding operations (their loads,
+  // then one unit's stores) and its own wait stays at vmcnt <= 5 instead of
+  // draining the stores.
+  int u = blockIdx.x;
+  issue_loads(u, 0, qraw);
+  wait_vm_barrier<0>();
+  unit(u, 0);
+  u += G;
+  for (int i = 1; u < units; ++i, u += G) {
+    wait_vm_barrier<kStores>();  // only unit i-1's stores may be in flight
+    unit(u, i & 1);
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Head dim 128 (beyond the reference, whose kernels take D = 64 only,
 // kernel_flash2.cu:756-757).  Key tiles of 32 rows x 256 bytes keep the
 // 8 KiB tile of D = 64, so an iteration is again 16 MFMA slots: GEMM1 is one
@@ -2009,6 +2185,33 @@ struct D128Launch {
   };
 };
 
+// Streaming short-key kernel: one persistent work-group per CU (its two
+// 64 KiB buffers take 128 KiB of the CU's 160 KiB), at most one per unit.
+template <class T>
+hipError_t launch_stream(const FwdArgs& a, hipStream_t st) {
+  constexpr int kCus = 256;
+  const int nqb = (a.seq + kStreamBr - 1) / kStreamBr;
+  const int units = nqb * a.batch_heads;
+  const dim3 grid((unsigned)min(units, kCus));
+  const Scales sc(a);
+  const Geom g = make_geom(a);
+  const T *q = static_cast<const T*>(a.q), *k = static_cast<const T*>(a.k),
+          *v = static_cast<const T*>(a.v);
+  T* o = static_cast<T*>(a.o);
+  if (a.causal) {
+    if (sc.scaled)
+      hipLaunchKernelGGL((fa2_fwd_stream_kernel<true, true, T>), grid, dim3(512), 0, st, q, k, v, o, g, nqb, units, sc.cq, sc.cr);
+    else
+      hipLaunchKernelGGL((fa2_fwd_stream_kernel<true, false, T>), grid, dim3(512), 0, st, q, k, v, o, g, nqb, units, sc.cq, sc.cr);
+  } else {
+    if (sc.scaled)
+      hipLaunchKernelGGL((fa2_fwd_stream_kernel<false, true, T>), grid, dim3(512), 0, st, q, k, v, o, g, nqb, units, sc.cq, sc.cr);
+    else
+      hipLaunchKernelGGL((fa2_fwd_stream_kernel<false, false, T>), grid, dim3(512), 0, st, q, k, v, o, g, nqb, units, sc.cq, sc.cr);
+  }
+  return hipGetLastError();
+}
+
 // Split-KV: the chunk kernel (grid = query blocks x chunks) and the
 // combine kernel, back to back on the stream.
 template <int W, int D>
@@ -2064,7 +2267,14 @@ const Fa2Config kFa2Configs[kNumFa2Configs] = {
     {8, "br128_bc64_w4_split2"},
     {8, "br256_bc64_w8_slot"},
     {4, "br128_bc64_w4_slot"},
+    {8, "br256_kv256_w8_stream"},
 };
+
+bool stream_config_fits(const FwdArgs& a) {
+  return a.seq_k <= kStreamMaxKeys && a.q_sr < kStreamMaxRowStride &&
+         a.k_sr < kStreamMaxRowStride && a.v_sr < kStreamMaxRowStride &&
+         a.o_sr < kStreamMaxRowStride;
+}
 
 // Fetch distance: three tiles ahead where LDS allows (64 KiB of rings per
 // work-group), one tile for single-wave groups.
@@ -2093,6 +2303,7 @@ hipError_t launch_fa2(const FwdArgs& a, int cfg, hipStream_t stream) {
     case 5: return dispatch<PipelinedLaunch<4, 3, 2>::L>(a, stream, 128);
     case 6: return dispatch<SlotLaunch<8, 4>::L>(a, stream, 256);
     case 7: return dispatch<SlotLaunch<4, 3>::L>(a, stream, 128);
+    case 8: return stream_config_fits(a) ? launch_stream<_Float16>(a, stream) : hipErrorInvalidValue;
     default: return hipErrorInvalidValue;
   }
 }

@@ -41,7 +41,7 @@ struct Fa2Config {
   const char* name;
 };
 
-constexpr int kNumFa2Configs = 8;
+constexpr int kNumFa2Configs = 9;
 extern const Fa2Config kFa2Configs[kNumFa2Configs];
 
 // Launches the FA2 kernel for configuration `cfg` on `stream`.  fp16 at
@@ -50,6 +50,13 @@ extern const Fa2Config kFa2Configs[kNumFa2Configs];
 hipError_t launch_fa2(const FwdArgs& a, int cfg, hipStream_t stream);
 constexpr int kSlotW8Config = 6;
 constexpr int kSlotW4Config = 7;
+// Persistent work-groups streaming whole units of 256 query rows whose keys
+// fit one LDS buffer: needs N_k <= kStreamMaxKeys and row strides below
+// kStreamMaxRowStride elements (unit-relative 32-bit buffer offsets).
+constexpr int kStreamConfig = 8;
+constexpr int kStreamMaxKeys = 256;
+constexpr int kStreamMaxRowStride = 1 << 22;
+bool stream_config_fits(const FwdArgs& a);
 
 // Split-KV ("flash-decoding"): `waves` (1, 2 or 4) waves of 32 query rows
 // per work-group, the key range cut into `nsplit` chunks whose partial

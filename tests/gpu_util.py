@@ -10,6 +10,14 @@ from oracle import attention_fp32, error_stats
 MAX_ABS = 2e-3
 MEAN_ABS = 2e-4
 
+# The streaming configuration takes key ranges of at most 256 keys only.
+STREAM_CFG = 8
+STREAM_MAX_KEYS = 256
+
+
+def config_fits(config, n_k):
+    return config != STREAM_CFG or n_k <= STREAM_MAX_KEYS
+
 
 def to_dev(x, dev):
     import torch

@@ -28,12 +28,12 @@ def test_library_loads_and_exports_header_symbols():
 
 
 def test_config_table():
-    assert capi.num_configs() == 8
-    names = [capi.config_name(i) for i in range(8)]
+    assert capi.num_configs() == 9
+    names = [capi.config_name(i) for i in range(9)]
     assert names == ["br32_bc64_w1", "br64_bc64_w2", "br128_bc64_w4", "br256_bc64_w8",
                      "br256_bc64_w8_pingpong", "br128_bc64_w4_split2", "br256_bc64_w8_slot",
-                     "br128_bc64_w4_slot"]
-    assert capi.config_name(8) is None and capi.config_name(-1) is None
+                     "br128_bc64_w4_slot", "br256_kv256_w8_stream"]
+    assert capi.config_name(9) is None and capi.config_name(-1) is None
 
 
 def _p(**kw):
@@ -76,7 +76,10 @@ def _ex(q_stride=(8 * 4096 * 64, 4096 * 64, 64), k_stride=None, v_stride=None, o
 def test_ex_null_and_config():
     lib = capi.load()
     assert lib.fl_attn_fwd_f16_ex(None, -1, None) == capi.FL_ERR_INVALID_ARGUMENT
+    assert capi.fwd_ex(_ex(), config=9) == capi.FL_ERR_BAD_CONFIG
+    # the streaming configuration needs N_k <= 256 (rejected before any pointer check)
     assert capi.fwd_ex(_ex(), config=8) == capi.FL_ERR_BAD_CONFIG
+    assert "needs N_k <= 256" in capi.last_error()
     assert capi.fwd_ex(_ex(head_dim=128)) == capi.FL_ERR_UNSUPPORTED
 
 
@@ -138,8 +141,10 @@ def test_non_finite_scale():
 
 
 def test_bad_config():
-    assert capi.fwd(_p(), config=8) == capi.FL_ERR_BAD_CONFIG
+    assert capi.fwd(_p(), config=9) == capi.FL_ERR_BAD_CONFIG
     assert capi.fwd(_p(), config=-2) == capi.FL_ERR_BAD_CONFIG
+    assert capi.fwd(_p(seq_q=256, seq_k=257), config=8) == capi.FL_ERR_BAD_CONFIG
+    assert "needs N_k <= 256" in capi.last_error()
 
 
 def test_empty_problems_are_noops():
@@ -162,7 +167,10 @@ def test_dispatcher_choices():
     # and the key range is long
     assert sel(batch=2, heads=8, seq_q=4096) == 6      # 256 groups
     assert sel(batch=1, heads=16, seq_q=16384) == 6
-    assert sel(batch=32, heads=32, seq_q=256) == 7     # short keys: 128-row groups
+    # short key ranges (N_k <= 256): streaming groups from one unit per CU
+    assert sel(batch=32, heads=32, seq_q=256) == 8     # 1024 units
+    assert sel(batch=8, heads=32, seq_q=130) == 8      # 256 units
+    assert sel(batch=2, heads=8, seq_q=256) == 1       # 16 units: small groups
     assert sel(batch=2, heads=8, seq_q=2048) == 7
     # very few groups at N >= 2048: split key range
     assert sel(batch=1, heads=1, seq_q=4096) == 5
@@ -170,7 +178,9 @@ def test_dispatcher_choices():
     # causal: 128-row slot-scheduled groups balanced by dispatch order
     assert sel(batch=2, heads=8, seq_q=4096, causal=True) == 7
     assert sel(batch=1, heads=16, seq_q=16384, causal=True) == 7
-    assert sel(batch=32, heads=32, seq_q=256, causal=True) == 7
+    assert sel(batch=32, heads=32, seq_q=256, causal=True) == 8   # streaming, any count
+    assert sel(batch=1, heads=1, seq_q=128, causal=True) == 8
+    assert sel(batch=1, heads=1, seq_q=257, causal=True) == 0     # N_k > 256
     # small problems: smaller groups
     assert sel(batch=2, heads=8, seq_q=512) == 7       # 64 groups of 128 rows
     assert sel(batch=2, heads=4, seq_q=512) == 1       # 64 groups of 64 rows

@@ -12,13 +12,14 @@ import pytest
 
 from flashlite_amd import capi
 from flashlite_amd.workloads import WORKLOADS, make_qkv, workload_inputs
-from gpu_util import assert_close_oracle, redo_expected, run_capi, sample_rows, to_dev
+from gpu_util import (assert_close_oracle, config_fits, redo_expected, run_capi, sample_rows,
+                      to_dev)
 from oracle import error_stats
 
 pytestmark = pytest.mark.gpu
 
 GOLDEN = os.path.join(os.path.dirname(__file__), "golden")
-NCFG = 8  # tile configurations exported by the library
+NCFG = 9  # tile configurations exported by the library
 SPLIT_CFGS = [5]  # the key-range-split configuration
 
 
@@ -26,7 +27,8 @@ def test_num_configs():
     assert capi.num_configs() == NCFG
     assert [capi.config_name(i) for i in range(NCFG)] == [
         "br32_bc64_w1", "br64_bc64_w2", "br128_bc64_w4", "br256_bc64_w8", "br256_bc64_w8_pingpong",
-        "br128_bc64_w4_split2", "br256_bc64_w8_slot", "br128_bc64_w4_slot"]
+        "br128_bc64_w4_split2", "br256_bc64_w8_slot", "br128_bc64_w4_slot",
+        "br256_kv256_w8_stream"]
 
 
 @pytest.mark.parametrize("config", list(range(NCFG)))
@@ -95,6 +97,10 @@ RAGGED = [1, 2, 3, 17, 31, 32, 33, 63, 64, 65, 100, 127, 128, 129, 191, 255, 256
 def test_ragged_all_configs(cuda, config, causal):
     for n in RAGGED:
         q, k, v = make_qkv(2, 3, n, 64, seed=1000 + n)
+        if not config_fits(config, n):
+            with pytest.raises(RuntimeError, match="needs N_k <= 256"):
+                run_capi(q, k, v, 0.125, causal, cuda, config=config)
+            continue
         out = run_capi(q, k, v, 0.125, causal, cuda, config=config)
         try:
             assert_close_oracle(out, q, k, v, 0.125, causal)
