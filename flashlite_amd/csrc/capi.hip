@@ -112,16 +112,14 @@ int check_pointers(const fl_attn_params* p, fl::FwdArgs* a, const char* who, uin
 // per CU, which also serve causal attention (groups of different lengths,
 // balanced by dispatch order).  Smaller problems fall back to smaller
 // groups.  Key ranges of at most 256 keys go to the streaming persistent
-// groups when causal (any count: one buffer holds every key a unit needs)
-// or when there are at least one unit per CU; with fewer non-causal units
-// the 128-row groups measured faster.  Replaces the reference's
+// groups (measured at least as fast as every other configuration from 16
+// to 2048 units, both masks).  Replaces the reference's
 // `seq_len >= 2048 -> Br=128` rule (kernel_flash2.cu:786-789), which was
 // sized for 20 SMs.
 int select_fa2(const fl::FwdArgs& a) {
   constexpr int64_t kCus = 256;
   auto wgs = [&](int64_t br) { return (a.seq + br - 1) / br * (int64_t)a.batch_heads; };
-  if (fl::stream_config_fits(a) && (a.causal || wgs(256) >= kCus))
-    return fl::kStreamConfig;  // br256_kv256_w8_stream
+  if (fl::stream_config_fits(a)) return fl::kStreamConfig;  // br256_kv256_w8_stream
   if (!a.causal && a.seq_k >= 4096 && wgs(256) >= kCus) return 6;  // br256_bc64_w8_slot
   if (!a.causal && a.seq >= 2048 && wgs(128) < kCus / 2) return 5;  // br128_bc64_w4_split2
   if (wgs(128) >= kCus / 4) return 7;                                // br128_bc64_w4_slot

@@ -1498,16 +1498,20 @@ fa2_fwd_slot_kernel(const T* Q, const T* __restrict__ K, const T* __restrict__ V
 // one head's block of up to 256 query rows, whose whole K and V (4 tiles
 // each, 64 KiB) fit one LDS buffer.  A persistent work-group of 8 waves (32
 // rows each) walks units u = blockIdx.x, + gridDim.x, ... through two such
-// buffers: after the barrier that publishes unit i, its waves issue unit
-// i+1's K/V fetches (into the buffer unit i-1 used) and Q loads, then
-// compute unit i and store it.  Per-wave memory operations per unit are
-// fixed (8 fetches, 4 Q loads, 5 stores; out-of-range rows are dropped by
-// the buffer bounds, never branched around), so "unit i's loads have
-// landed" is exactly vmcnt <= 5: only unit i-1's stores may still be in
-// flight.  With one short unit per work-group, the start-up latency of every
-// unit (Q and K/V from HBM) would idle the CU; here it overlaps the previous
-// unit's compute.  Tiles are processed one at a time with the stabiliser
-// checked (Rows::softmax_checked), and no barrier sits inside a unit.
+// buffers: after the barrier that publishes unit i, each wave reads its Q
+// rows, then issues unit i+1's K/V fetches (into the buffer unit i-1 used)
+// and its own next Q rows (into the 4 KiB it just read), then computes unit
+// i and stores it.  Per-wave memory operations per unit are fixed (8 K/V
+// and 4 Q fetches, 5 stores; out-of-range rows are dropped by the buffer
+// bounds, never branched around), so "unit i's loads have landed" is
+// exactly vmcnt <= 5: only unit i-1's stores may still be in flight.  With
+// one short unit per work-group, the start-up latency of every unit (Q and
+// K/V from HBM) would idle the CU; here it overlaps the previous unit's
+// compute.  LDS: 2 x 64 KiB of K/V + 32 KiB of Q = all 160 KiB of the CU.
+// Within a unit no barrier is needed: every key tile is resident, so each
+// wave pipelines its own tiles (GEMM1 of tile t+1 and GEMM2 of tile t-1
+// beside the softmax of tile t) and, in the rare case its stabiliser check
+// fails, recomputes them one at a time (Rows::softmax_checked).
 constexpr int kStreamBr = 256;                           // query rows per unit
 constexpr int kStreamTiles = 4;                          // key tiles per unit (N_k <= 256)
 constexpr int kStreamHalf = kStreamTiles * kTileBytes;   // K (or V) of a unit: 32 KiB
@@ -1529,6 +1533,7 @@ fa2_fwd_stream_kernel(const T* Q, const T* __restrict__ K, const T* __restrict__
   using V8 = typename RowsT::V8;
   constexpr int kStores = 5;  // Rows::store_rsrc
   __shared__ __attribute__((aligned(16))) uint8_t buf[2][2 * kStreamHalf];  // [unit parity][K | V]
+  __shared__ __attribute__((aligned(16))) uint8_t qbuf[8 * 4096];            // 32 Q rows per wave
 
   const int lane = threadIdx.x & 63;
   const int rw = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -1544,8 +1549,17 @@ fa2_fwd_stream_kernel(const T* Q, const T* __restrict__ K, const T* __restrict__
   const int blk = CAUSAL && rw >= 4 ? 11 - rw : rw;
 
   // Unit u's K/V tiles 0..3 into buffer b (rows >= N_k read as zeros) and
-  // this wave's Q rows into raw (rows >= N_q read as zeros).
-  auto issue_loads = [&](int u, int b, u32x4_t (&raw)[4]) __attribute__((always_inline)) {
+  // this wave's 32 Q rows into its 4 KiB of qbuf (rows >= N_q read as
+  // zeros), all by LDS DMA; chunks swizzled as K tiles are.
+  int qoff[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int lrow = 8 * i + (lane >> 3);
+    qoff[i] = (32 * blk + lrow) * qrow_bytes + 16 * ((lane & 7) ^ k_swz(lrow));
+    asm volatile("" : "+v"(qoff[i]));
+  }
+  uint8_t* const qdst = qbuf + 4096 * rw;
+  auto issue_loads = [&](int u, int b) __attribute__((always_inline)) {
     const int bh = u / nqb, qb = u - bh * nqb;
     const HeadPtrs<T> hp = head_ptrs<T>(geom, bh, Q, K, V, O);
 #pragma unroll
@@ -1555,17 +1569,17 @@ fa2_fwd_stream_kernel(const T* Q, const T* __restrict__ K, const T* __restrict__
     }
     const int q0 = qb * kStreamBr;
     const int valid = min(kStreamBr, seq - q0);
-    const __amdgpu_buffer_rsrc_t rq = __builtin_amdgcn_make_buffer_rsrc(
-        (void*)(hp.q + (long long)q0 * geom.q_sr), 0, (valid - 1) * qrow_bytes + kRowBytes,
-        0x00020000);
-    const int off = (32 * blk + col) * qrow_bytes + 16 * g;
+    const i32x4_t rq =
+        buffer_rsrc(hp.q + (long long)q0 * geom.q_sr, (valid - 1) * qrow_bytes + kRowBytes);
 #pragma unroll
-    for (int s = 0; s < 4; ++s)
-      raw[s] = __builtin_amdgcn_raw_buffer_load_b128(rq, off + 32 * s, 0, 0);
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t lds_base = (uint32_t)(uintptr_t)(qdst + 1024 * i);
+      asm volatile("buffer_load_dwordx4 %0, %1, 0 offen lds" : : "v"(qoff[i]), "s"(rq),
+                   "{m0}"(lds_base));
+    }
   };
 
   const int G = gridDim.x;
-  u32x4_t qraw[4];
   // Unit u in buffer b; its loads have landed and every wave is done with
   // the other buffer.
   auto unit = [&](int u, int b) __attribute__((always_inline)) {
@@ -1574,30 +1588,96 @@ fa2_fwd_stream_kernel(const T* Q, const T* __restrict__ K, const T* __restrict__
     const int qw = q0 + 32 * blk;
     RowsT rows;
     rows.place(lane, qw, seq, geom.seq_k, geom.coff, cr);
-    rows.set_q(qraw, cq);
+    {
+      u32x4_t raw[4];
+#pragma unroll
+      for (int s = 0; s < 4; ++s)
+        raw[s] = *reinterpret_cast<const u32x4_t*>(qdst + 128 * col +
+                                                    16 * ((2 * s + g) ^ k_swz(col)));
+      rows.set_q(raw, cq);
+    }
     rows.reset();
-    if (u + G < units) issue_loads(u + G, b ^ 1, qraw);
+    // This wave's Q reads are done before its DMA refills the same rows.
+    asm volatile("s_waitcnt lgkmcnt(0)" : : : "memory");
+    if (u + G < units) issue_loads(u + G, b ^ 1);
 
     int nt = ntiles;
     if (CAUSAL) nt = min(nt, causal_tiles(min(qw + 32, seq), geom.coff));
     if (qw < seq) {
       const uint8_t* kb = buf[b];
       const uint8_t* vb = buf[b] + kStreamHalf;
-      for (int t = 0; t < nt; ++t) {
-        float16_t S[2];
+      // Units with at least 3 tiles for this wave: a software-pipelined
+      // first pass.  Step t issues GEMM2 of tile t-1 (with P(t-1), whose
+      // registers the softmax of S(t) then refills) and GEMM1 of tile t+1,
+      // both MFMA chains independent of that softmax, with the stabiliser m
+      // fixed at tile 0's exact row max; out_of_range records, branch-free,
+      // any tile sum that left the fp16-safe range.  The last step's GEMM1
+      // (tile nt, never used) reads other finite LDS data and is masked;
+      // below 3 tiles that waste outweighs the overlap and the tiles go
+      // straight to the one-at-a-time checked loop.
+      bool checked = nt < 3;
+      if (!checked) {
+        uint64_t out_of_range = 0;
+        float16_t S0[2], S1[2];
         V8 P[2][2];
         {
           V8 ka[2][4];
-          rows.read_k(kb + t * kTileBytes, ka);
-          rows.gemm1(ka, S);
+          rows.read_k(kb, ka);
+          rows.gemm1(ka, S0);
         }
-        rows.mask(t, S);
-        if (t == 0) rows.first_tile(S);
-        rows.softmax_checked(S, P);
+        rows.mask(0, S0);
+        rows.first_tile(S0);
+        auto step = [&](int t, float16_t (&S)[2], float16_t (&Sn)[2]) __attribute__((always_inline)) {
+          V8 ka[2][4];
+          rows.read_k(kb + (t + 1) * kTileBytes, ka);
+          if (t > 0) {
+            V8 va[2][4];
+            rows.read_v(vb + (t - 1) * kTileBytes, va);
+            rows.gemm2(va, P);
+          }
+          rows.gemm1(ka, Sn);
+          out_of_range |= rows.softmax_fast(S, P);
+          rows.mask(t + 1, Sn);
+        };
+        // At most kStreamTiles steps: unrolled, so S0 / S1 keep fixed roles.
+        step(0, S0, S1);
+        static_for(std::make_integer_sequence<int, kStreamTiles - 1>{}, [&](auto i)
+                   __attribute__((always_inline)) {
+          constexpr int t = decltype(i)::value + 1;
+          if (t < nt) {
+            if constexpr (t & 1)
+              step(t, S1, S0);
+            else
+              step(t, S0, S1);
+          }
+        });
         {
           V8 va[2][4];
-          rows.read_v(vb + t * kTileBytes, va);
+          rows.read_v(vb + (nt - 1) * kTileBytes, va);
           rows.gemm2(va, P);
+        }
+        checked = out_of_range != 0;
+      }
+      // The checked loop: one tile at a time, rescaling when a row max rises
+      // (also the recompute for a wave whose first pass left the range).
+      if (checked) {
+        rows.reset();
+        for (int t = 0; t < nt; ++t) {
+          float16_t S[2];
+          V8 P[2][2];
+          {
+            V8 ka[2][4];
+            rows.read_k(kb + t * kTileBytes, ka);
+            rows.gemm1(ka, S);
+          }
+          rows.mask(t, S);
+          if (t == 0) rows.first_tile(S);
+          rows.softmax_checked(S, P);
+          {
+            V8 va[2][4];
+            rows.read_v(vb + t * kTileBytes, va);
+            rows.gemm2(va, P);
+          }
         }
       }
     }
@@ -1611,12 +1691,10 @@ fa2_fwd_stream_kernel(const T* Q, const T* __restrict__ K, const T* __restrict__
         __builtin_amdgcn_make_buffer_rsrc((void*)lh, 0, geom.lse ? 4 * valid : 0, 0x00020000);
     rows.store_rsrc(ro, q0, 2 * geom.o_sr, rl);
   };
-  // The first unit is peeled off, so at every use of the Q registers the
-  // compiler sees the same order of outstanding operations (their loads,
-  // then one unit's stores) and its own wait stays at vmcnt <= 5 instead of
-  // draining the stores.
+  // The first unit is peeled off: its wait also covers the launch's first
+  // loads, and every later one has exactly one unit's stores behind it.
   int u = blockIdx.x;
-  issue_loads(u, 0, qraw);
+  issue_loads(u, 0);
   wait_vm_barrier<0>();
   unit(u, 0);
   u += G;

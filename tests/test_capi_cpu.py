@@ -167,10 +167,11 @@ def test_dispatcher_choices():
     # and the key range is long
     assert sel(batch=2, heads=8, seq_q=4096) == 6      # 256 groups
     assert sel(batch=1, heads=16, seq_q=16384) == 6
-    # short key ranges (N_k <= 256): streaming groups from one unit per CU
+    # short key ranges (N_k <= 256): streaming groups
     assert sel(batch=32, heads=32, seq_q=256) == 8     # 1024 units
     assert sel(batch=8, heads=32, seq_q=130) == 8      # 256 units
-    assert sel(batch=2, heads=8, seq_q=256) == 1       # 16 units: small groups
+    assert sel(batch=2, heads=8, seq_q=256) == 8       # 16 units
+    assert sel(batch=1, heads=1, seq_q=1000, seq_k=256) == 8
     assert sel(batch=2, heads=8, seq_q=2048) == 7
     # very few groups at N >= 2048: split key range
     assert sel(batch=1, heads=1, seq_q=4096) == 5
@@ -184,7 +185,7 @@ def test_dispatcher_choices():
     # small problems: smaller groups
     assert sel(batch=2, heads=8, seq_q=512) == 7       # 64 groups of 128 rows
     assert sel(batch=2, heads=4, seq_q=512) == 1       # 64 groups of 64 rows
-    assert sel(batch=1, heads=1, seq_q=128) == 0
+    assert sel(batch=1, heads=1, seq_q=257) == 0
     assert sel(head_dim=80) == -1
 
 
