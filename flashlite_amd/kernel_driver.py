@@ -19,6 +19,10 @@ element type / head dim through ``fl_attn_fwd_bf16_ex`` or
 ``fl_attn_fwd_f16_ex`` (seeded inputs from ``make_qkv`` / ``make_qkv_bf16``;
 ``--config`` -1, 6 or 7).
 
+``--shape B H N`` replaces the workload's shape (fp16, D = 64, N_q = N_k = N,
+sm_scale 1/8, ``make_qkv`` inputs with seed 1): sweeps over shapes the
+workloads do not name.
+
 ``--decode B H NQ NK`` runs a decode-shaped call (NQ query rows over NK
 keys, seeded N(0,1) inputs) through ``fl_attn_fwd_f16_splitkv`` with
 ``--splits S`` (1 = one pass, 0 = the library's choice, n = n key chunks)
@@ -45,6 +49,7 @@ def main(argv=None):
     ap.add_argument("--causal-decode", type=int, default=0)
     ap.add_argument("--dtype", choices=("fp16", "bf16"), default="fp16")
     ap.add_argument("--head-dim", type=int, default=0, help="override the workload's head dim")
+    ap.add_argument("--shape", type=int, nargs=3, metavar=("B", "H", "N"), default=None)
     args = ap.parse_args(argv)
 
     import torch
@@ -73,6 +78,11 @@ def main(argv=None):
     from flashlite_amd.workloads import WORKLOADS, make_qkv, make_qkv_bf16, workload_inputs
 
     w = WORKLOADS[args.workload]
+    if args.shape:
+        from flashlite_amd.workloads import Workload
+
+        b, h, n = args.shape
+        w = Workload(f"B{b}H{h}N{n}", b, h, n, 64, (False, True), 1)
     dev = torch.device("cuda:0")
     head_dim = args.head_dim or w.head_dim
     wide = args.dtype == "bf16" or head_dim != 64
@@ -111,7 +121,7 @@ def main(argv=None):
     us = start.elapsed_time(end) * 1e3 / args.iters
     flops = (2.0 if args.causal else 4.0) * w.batch * w.heads * w.seq ** 2 * head_dim
     name = "naive" if args.naive else ("auto" if cfg < 0 else capi.config_name(cfg))
-    print(f"{args.workload} {args.dtype} D={head_dim} causal={args.causal} {name}: "
+    print(f"{w.name} {args.dtype} D={head_dim} causal={args.causal} {name}: "
           f"{us:.2f} us/launch, {flops / us / 1e6:.1f} TFLOP/s", flush=True)
 
 

@@ -72,7 +72,9 @@ int fl_attn_fwd_f16(const fl_attn_params* p, void* stream);
  * [0, fl_attn_num_configs()), or -1 for the dispatcher's choice).  Replaces
  * the reference's two hard-wired launch branches (Br=64 / Br=128,
  * csrc/kernel_flash2.cu:789-835); used by sweeps and by tests that check
- * every configuration against the oracle.
+ * every configuration against the oracle.  Configuration 8
+ * (br256_kv256_w8_stream) takes N_k <= 256 only and returns
+ * FL_ERR_BAD_CONFIG otherwise.
  */
 int fl_attn_fwd_f16_cfg(const fl_attn_params* p, int32_t config, void* stream);
 
