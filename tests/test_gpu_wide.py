@@ -11,10 +11,13 @@ Tolerances against the fp32 oracle on the same inputs:
   fp16's (2^-11); the output rounding alone reaches 2^-9 |O| and P is
   rounded to bf16 before the PV product.  The inputs are bf16-exact values
   (``workloads.round_bf16``), so the oracle sees exactly what the kernel reads.
-* log-sum-exp: max-abs <= 2e-3, mean-abs <= 3e-4 (natural-log units) for both
-  types; bf16 and head_dim 128 keep Q unscaled and scale the fp32 scores, so
-  their scores are closer to the oracle's than the D = 64 fp16 path's
-  prescaled ones.
+* log-sum-exp (natural-log units): max-abs <= 2e-3 for both types; mean-abs
+  <= 3e-4 for fp16 and 1e-3 for bf16.  bf16 and head_dim 128 keep Q unscaled
+  and scale the fp32 scores, so their scores are closer to the oracle's than
+  the D = 64 fp16 path's prescaled ones; but at D = 64 the bf16 row sum l is
+  taken on the matrix core over the bf16-rounded p that weight V (relative
+  error up to 2^-9 = 1.95e-3 each, about 2^-10 on average), so ln l carries
+  about 1e-3 on rows that see few keys.
 A strided launch equals the contiguous launch of the same data bit for bit.
 """
 
@@ -30,7 +33,7 @@ pytestmark = pytest.mark.gpu
 BF16_MAX_ABS = 8 * MAX_ABS
 BF16_MEAN_ABS = 8 * MEAN_ABS
 LSE_MAX_ABS = 2e-3
-LSE_MEAN_ABS = 3e-4
+LSE_MEAN_ABS = {"fp16": 3e-4, "bf16": 1e-3}
 SLOT_CFGS = [-1, 6, 7]
 KINDS = [("fp16", 64), ("fp16", 128), ("bf16", 64), ("bf16", 128)]
 WIDE = [k for k in KINDS if k != ("fp16", 64)]
@@ -115,7 +118,7 @@ def test_rectangular_with_lse(cuda, kind, d, config, causal):
         fin = np.isfinite(ref_lse)
         assert np.array_equal(fin, np.isfinite(lse)), f"{nq}x{nk}: lse -inf pattern"
         mx, mean = error_stats(lse[fin], ref_lse[fin]) if fin.any() else (0.0, 0.0)
-        assert mx <= LSE_MAX_ABS and mean <= LSE_MEAN_ABS, (
+        assert mx <= LSE_MAX_ABS and mean <= LSE_MEAN_ABS[kind], (
             f"{nq}x{nk}: lse max-abs {mx:.3e} mean-abs {mean:.3e}")
 
 
