@@ -2411,11 +2411,11 @@ hipError_t launch_fa2(const FwdArgs& a, int cfg, hipStream_t stream) {
   if (a.head_dim == kD2) {
     const bool bf = a.dtype == kDtypeBF16;
     if (cfg == kSlotW8Config)
-      return bf ? dispatch<D128Launch<8, 5, 6, __bf16>::L>(a, stream, 256)
-                : dispatch<D128Launch<8, 5, 6, _Float16>::L>(a, stream, 256);
+      return bf ? dispatch<D128Launch<8, 5, 4, __bf16>::L>(a, stream, 256)
+                : dispatch<D128Launch<8, 5, 4, _Float16>::L>(a, stream, 256);
     if (cfg == kSlotW4Config)
-      return bf ? dispatch<D128Launch<4, 5, 6, __bf16>::L>(a, stream, 128)
-                : dispatch<D128Launch<4, 5, 6, _Float16>::L>(a, stream, 128);
+      return bf ? dispatch<D128Launch<4, 5, 4, __bf16>::L>(a, stream, 128)
+                : dispatch<D128Launch<4, 5, 4, _Float16>::L>(a, stream, 128);
     return hipErrorInvalidValue;
   }
   if (a.dtype == kDtypeBF16) {
