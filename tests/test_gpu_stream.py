@@ -51,6 +51,7 @@ SHAPES = [
     (9, 61, 33, 200),      # 549 units (odd rounds), N_k > N_q
     (3, 5, 700, 256),      # 3 units per head (N_q > 256)
     (2, 2, 513, 129),      # N_q > N_k, rows with no visible key when causal
+    (64, 48, 96, 160),     # 3072 units: 12 per work-group, both buffers reused many times
 ]
 
 
