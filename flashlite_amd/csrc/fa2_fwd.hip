@@ -1,4 +1,5 @@
-// FlashAttention-2 forward for gfx950 (MI355X, CDNA4), fp16 in / fp32 accumulate.
+// FlashAttention-2 forward for gfx950 (MI355X, CDNA4), fp16 (and bf16) in /
+// fp32 accumulate, head_dim 64 (and 128).
 //
 // Reference: csrc/kernel_flash2.cu of thebigblender/FlashLite -- the two
 // kernels flash_attn2_wmma_br64_kernel (:54-387) and
@@ -34,19 +35,22 @@
 // swapped via the tr-read addresses) so each lane ends with 8 contiguous
 // head-dim values per accumulator half: the epilogue stores 16-byte vectors.
 //
-// Softmax, at one exp per score.  Q is prescaled by c = |sm_scale| * log2 e
-// (the reference's prescale, kernel_flash2.cu:772) when c <= 1, so GEMM1
+// Softmax, at one exp per score.  For fp16 at head_dim 64, Q is prescaled
+// by c = |sm_scale| * log2 e (the reference's prescale,
+// kernel_flash2.cu:772) when c <= 1, so GEMM1
 // returns base-2 logits; the running stabiliser m enters as the MFMA
 // accumulator's initial value, so GEMM1 returns logit - m and p = v_exp_f32
 // of the accumulator.  m is the exact row max of the first tile and later
 // only moves when a tile would push p out of range (a stale m is exact math
 // since softmax is shift invariant; m never exceeds the running max, so the
-// row sum stays >= 1).  p is packed to fp16 for GEMM2; row sums add the fp32
-// p with v_add_f32 (the reference also sums fp32 p, :339) -- on gfx950
-// v_dot2_f32_f16 would stall the matrix core, plain VALU ops do not.  Each
-// lane sums its own keys and the two halves of a row meet once, in the
-// epilogue.  When c > 1 (SCALED) Q keeps its scale and the logits are
-// multiplied by c instead, so |Q'| never exceeds |Q|.
+// row sum stays >= 1).  p is packed to fp16 for GEMM2.  Row sums: fp32 adds
+// of the fp32 p (the reference also sums fp32 p, :339) in the older
+// schedules; the slot schedule sums fp16 tiles with a packed-fp16 tree of
+// the rounded p and bf16 tiles on the matrix core (Rows::init_msum) --
+// v_dot2_f32_f16 would stall the matrix core.  Each lane sums its own keys
+// and the two halves of a row meet once, in the epilogue.  When c > 1
+// (SCALED) Q keeps its scale and the logits are multiplied by c instead, so
+// |Q'| never exceeds |Q|.
 //
 // K/V staging.  Tiles are fetched straight into LDS with buffer_load ... lds
 // (no VGPRs, no LDS-store instructions; rows past N read as zeros through
@@ -56,6 +60,14 @@
 // makes a tile visible.
 //
 // Schedules:
+//   fa2_fwd_slot_kernel (W = 8 or 4; the dispatcher's choice for N_k > 256):
+//     16 fenced MFMA slots per tile, each carrying two exponentials and the
+//     LDS read of a later slot's operand; GEMM1 skewed by half a tile so one
+//     score buffer serves both the tile being exponentiated and the next.
+//   fa2_fwd_stream_kernel (N_k <= 256): one persistent 8-wave work-group per
+//     CU walks whole units (a head's 256-row block with all its keys) through
+//     two LDS buffers, loading the next unit while it computes the current.
+//   fa2_fwd_d128_kernel (head_dim 128): the slot schedule over 32-key tiles.
 //   fa2_fwd_kernel (any W; SPLIT = 1 or 2): iteration j runs GEMM1 of tile
 //     j+1, GEMM2 of tile j-1 and the softmax of tile j -- three independent
 //     pieces of work the compiler interleaves -- and checks the stabiliser
@@ -67,7 +79,8 @@
 //     4-7 alternate an MFMA phase (GEMM2 of tile j-1 + GEMM1 of tile j) and
 //     a softmax phase, with a barrier per phase.
 //   The ping-pong kernel decides the stabiliser before the exponentials
-//   (Rows::restabilise); it is kept as a selectable, tested alternative.
+//   (Rows::restabilise).  fa2_fwd_kernel serves small problems and split-KV;
+//   the ping-pong kernel is kept as a selectable, tested alternative.
 //
 // Causal.  Keys after a lane's query and keys >= N are masked to -inf on the
 // diagonal and tail tiles only; work-groups are fed to each XCD heaviest
