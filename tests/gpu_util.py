@@ -72,16 +72,17 @@ def redo_expected(q16, k16, sm_scale, causal):
     log2e = float(np.float32(1.4426950408889634))
     q = q16.astype(np.float64)
     k = k16.astype(np.float64)
-    n = q.shape[2]
+    nq, nk = q.shape[2], k.shape[2]
     s = np.einsum("bhid,bhjd->bhij", q, k) * abs(sm_scale) * log2e
     if sm_scale < 0:
         s = -s
-    if causal:
-        s = np.where(np.tril(np.ones((n, n), bool)), s, -np.inf)
+    if causal:  # bottom-right aligned: key j is visible to row i when j <= i + nk - nq
+        vis = np.arange(nk)[None, :] <= np.arange(nq)[:, None] + (nk - nq)
+        s = np.where(vis, s, -np.inf)
     m0 = s[..., :64].max(axis=-1, keepdims=True)
     # key j of a tile sits in lane half ((j % 32) // 4) % 2
     half = ((np.arange(64) % 32) // 4) % 2
-    for t0 in range(64, n, 64):
+    for t0 in range(64, nk, 64):
         p = np.exp2(np.minimum(s[..., t0:t0 + 64] - m0, 200.0))
         h = half[: p.shape[-1]]
         for g in (0, 1):

@@ -130,6 +130,21 @@ def test_other_scales(cuda, scale, causal):
     assert_close_oracle(out, q, k, v, scale, causal, max_abs=2e-3 if scale < 1 else 4e-3)
 
 
+@pytest.mark.parametrize("config", range(NCFG))
+@pytest.mark.parametrize("scale", [1.0, 3.0])
+@pytest.mark.parametrize("causal", [False, True])
+def test_peaked_every_config(cuda, config, scale, causal):
+    # Every configuration's work-group-wide redo decision: the peaked inputs
+    # send blocks to the checked pass, whose flag each kernel keeps in its
+    # idle ring memory.  300 query rows give 1-10 work-groups per head, so
+    # groups that redo run beside groups that do not.
+    n = 256 if not config_fits(config, 300) else 300
+    q, k, v = make_qkv(1, 4, n, 64, seed=47)
+    assert redo_expected(q, k, scale, causal)
+    out = run_capi(q, k, v, scale, causal, cuda, config=config)
+    assert_close_oracle(out, q, k, v, scale, causal, max_abs=4e-3)
+
+
 def test_deterministic(cuda):
     q, k, v = make_qkv(2, 8, 1000, 64, seed=51)
     for causal in (False, True):

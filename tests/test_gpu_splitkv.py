@@ -65,6 +65,30 @@ def test_splitkv_matches_oracle(cuda, nq, nk, causal, splits):
     assert mx <= LSE_MAX_ABS and mean <= LSE_MEAN_ABS, f"lse max-abs {mx:.3e} mean-abs {mean:.3e}"
 
 
+@pytest.mark.parametrize("nq", [1, 40, 100])  # 1-, 2- and 4-wave chunks
+@pytest.mark.parametrize("causal", [False, True])
+def test_splitkv_peaked(cuda, nq, causal):
+    # sm_scale 3 (logits with std ~24) and, in the second tile of every
+    # chunk (5 chunks of 5 tiles), a copy of query row 0 as a key: every
+    # chunk measures that key far above its first tile and takes the checked
+    # pass; the combine kernel merges partials whose maxima differ by hundreds
+    from gpu_util import redo_expected
+
+    q16, k16, v16 = _qkv(1, 4, nq, 1500, seed=nq + 5)
+    per = 5 * 64
+    for c0 in range(0, 1500, per):
+        k16[:, :, c0 + 64 + 7] = q16[:, :, 0]
+        # chunk starts are tile-aligned: the chunk alone shows the condition
+        assert redo_expected(q16, k16[:, :, c0:c0 + per], 3.0, False)
+    tq, tk, tv = (to_dev(x, cuda) for x in (q16, k16, v16))
+    o, ls, _ = _run_split(tq, tk, tv, 3.0, causal, 5)
+    assert_close_oracle(o.float().cpu().numpy(), q16, k16, v16, 3.0, causal, max_abs=4e-3,
+                        ref=attention_fp32(q16, k16, v16, 3.0, causal))
+    lse, ref = ls.cpu().numpy(), attention_lse(q16, k16, 3.0, causal)
+    mx, mean = error_stats(lse, ref)
+    assert mx <= LSE_MAX_ABS and mean <= LSE_MEAN_ABS, f"lse max-abs {mx:.3e} mean-abs {mean:.3e}"
+
+
 def test_splitkv_auto_choice(cuda):
     # a decode step on a small batch splits; the headline shape does not
     q16, k16, v16 = _qkv(2, 8, 1, 4096, seed=1)
