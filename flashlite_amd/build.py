@@ -5,7 +5,10 @@
 (run as a script: importing the package needs the extension it builds)
 
 1. ``hipcc --offload-arch=gfx950`` compiles the kernels and the C ABI
-   (``csrc/*.hip``) into ``flashlite_amd/libflashlite_attn.so``.
+   (``csrc/*.hip``, one object per source, in parallel) and links them
+   into ``flashlite_amd/libflashlite_attn.so``.  The diagnostic kernels
+   (``csrc/diag.hip``, not part of the attention path) become
+   ``flashlite_amd/libflashlite_diag.so``.
 2. The host C++ compiler compiles the binding (``csrc/flash_attn.cpp``)
    against the torch headers into
    ``flashlite_amd/flash_attn_wmma<EXT_SUFFIX>``, linked to the library
@@ -22,6 +25,8 @@ import shutil
 import subprocess
 import sys
 import sysconfig
+import tempfile
+from concurrent.futures import ThreadPoolExecutor
 
 PKG_DIR = os.path.dirname(os.path.abspath(__file__))
 REPO_DIR = os.path.dirname(PKG_DIR)
@@ -31,13 +36,16 @@ ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
 ARCH = "gfx950"
 
 LIB_NAME = "libflashlite_attn.so"
+DIAG_LIB_NAME = "libflashlite_diag.so"
 EXT_NAME = "flash_attn_wmma"
 
-HIP_SOURCES = ["fa2_fwd.hip", "naive_fwd.hip", "capi.hip"]
+HIP_SOURCES = ["fa2_fwd.hip", "fa2_pipe.hip", "fa2_slot.hip", "fa2_stream.hip", "fa2_d128.hip",
+                              "naive_fwd.hip", "capi.hip"]
+DIAG_SOURCES = ["diag.hip"]
 
 # -packed-fp32-ops: keep the compiler from emitting v_pk_{add,mul,fma}_f32.
 HIP_FLAGS = [
-    f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-shared",
+    f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-Wall", "-Wno-unused-command-line-argument",
 ]
@@ -62,17 +70,32 @@ def ext_path() -> str:
     return os.path.join(PKG_DIR, EXT_NAME + sysconfig.get_config_var("EXT_SUFFIX"))
 
 
-def build_library(verbose: bool = False) -> str:
+def _build_shared(sources, out: str, verbose: bool) -> str:
+    """Compiles each source to an object in parallel, then links them."""
     hipcc = os.path.join(ROCM, "bin", "hipcc")
-    out = lib_path()
-    tmp = out + ".tmp"
-    cmd = [hipcc, *HIP_FLAGS, f"-I{INCLUDE}", f"-I{CSRC}",
-           *[os.path.join(CSRC, s) for s in HIP_SOURCES], "-o", tmp]
-    log = _run(cmd)
-    if verbose and log.strip():
-        print(log)
+    with tempfile.TemporaryDirectory(prefix="flashlite_build_") as tmpdir:
+        objs = [os.path.join(tmpdir, os.path.splitext(s)[0] + ".o") for s in sources]
+        cmds = [[hipcc, *HIP_FLAGS, f"-I{INCLUDE}", f"-I{CSRC}", "-c",
+                 os.path.join(CSRC, s), "-o", o] for s, o in zip(sources, objs)]
+        workers = max(1, min(len(cmds), os.cpu_count() or 1, 16))
+        with ThreadPoolExecutor(max_workers=workers) as pool:
+            logs = list(pool.map(_run, cmds))
+        tmp = out + ".tmp"
+        logs.append(_run([hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", tmp]))
+    if verbose:
+        for log in logs:
+            if log.strip():
+                print(log)
     os.replace(tmp, out)
     return out
+
+
+def build_library(verbose: bool = False) -> str:
+    return _build_shared(HIP_SOURCES, lib_path(), verbose)
+
+
+def build_diag_library(verbose: bool = False) -> str:
+    return _build_shared(DIAG_SOURCES, os.path.join(PKG_DIR, DIAG_LIB_NAME), verbose)
 
 
 def build_extension(verbose: bool = False) -> str:
@@ -107,6 +130,7 @@ def build_extension(verbose: bool = False) -> str:
 def build(verbose: bool = False):
     lib = build_library(verbose)
     ext = build_extension(verbose)
+    build_diag_library(verbose)
     return lib, ext
 
 

@@ -189,6 +189,14 @@ def config_name(cfg: int) -> str | None:
     return n.decode() if n else None
 
 
+def config_id(name: str) -> int:
+    """Index of the tile configuration called `name` (KeyError if none)."""
+    for i in range(num_configs()):
+        if config_name(i) == name:
+            return i
+    raise KeyError(name)
+
+
 def select_config(params: FlAttnParams) -> int:
     return load().fl_attn_select_config(ctypes.byref(params))
 

@@ -120,11 +120,11 @@ int select_fa2(const fl::FwdArgs& a) {
   constexpr int64_t kCus = 256;
   auto wgs = [&](int64_t br) { return (a.seq + br - 1) / br * (int64_t)a.batch_heads; };
   if (fl::stream_config_fits(a)) return fl::kStreamConfig;  // br256_kv256_w8_stream
-  if (!a.causal && a.seq_k >= 4096 && wgs(256) >= kCus) return 6;  // br256_bc64_w8_slot
-  if (!a.causal && a.seq >= 2048 && wgs(128) < kCus / 2) return 5;  // br128_bc64_w4_split2
-  if (wgs(128) >= kCus / 4) return 7;                                // br128_bc64_w4_slot
-  if (wgs(64) >= kCus / 4) return 1;                                 // br64_bc64_w2
-  return 0;                                                          // br32_bc64_w1
+  if (!a.causal && a.seq_k >= 4096 && wgs(256) >= kCus) return fl::kSlotW8Config;
+  if (!a.causal && a.seq >= 2048 && wgs(128) < kCus / 2) return fl::kCfgSplit2;
+  if (wgs(128) >= kCus / 4) return fl::kSlotW4Config;
+  if (wgs(64) >= kCus / 4) return fl::kCfgW2;
+  return fl::kCfgW1;
 }
 
 int check_fa2(const fl_attn_params* p, fl::FwdArgs* a, const char* who = "fl_attn_fwd_f16",

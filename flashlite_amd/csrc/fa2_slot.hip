@@ -1,0 +1,276 @@
+// Slot-scheduled schedule (configurations br256_bc64_w8_slot and
+// br128_bc64_w4_slot), fp16 and bf16 at head_dim 64.  Shared building
+// blocks: fa2_common.h.
+
+#include "fa2_common.h"
+
+namespace fl {
+
+namespace {
+
+// ---------------------------------------------------------------------------
+// Slot-scheduled pipeline: W waves of 32 query rows, one key stream.
+//
+// Same work per iteration j as fa2_fwd_kernel (GEMM1, GEMM2 of tile j-1
+// with P(j-1), softmax of tile j), laid out as 16 MFMA slots separated by
+// scheduling fences (slot map: Rows::read_slot / mfma_slot).  Each slot
+// carries two exponentials of the softmax with their fp16 pack and row-sum
+// share, and the LDS read of the A operand of slot +kAhead.  Measured on
+// gfx950: two exponentials and two simple VALU ops issue free under one
+// 32x32x16 MFMA, while longer runs of exponentials between MFMAs stall the
+// matrix core, so the even spread is what keeps it busy.  GEMM1 is skewed
+// by half a tile (key block 1 of tile j in slots 0-6, block 0 of tile j+1
+// in slots 8-14) so that one S buffer serves both the scores being
+// exponentiated and the ones being computed.
+//
+// The operands of the next iteration's first kAhead slots are read at the
+// end of this one (K(j+1) block 1 and V(j)), so no iteration starts by
+// waiting for LDS.  Iteration j reads K(j), K(j+1), V(j-1) and V(j); the
+// barrier ending it publishes K(j+2) and V(j+1).  K is fetched FV+1 tiles
+// ahead and V FV, into rings of FV+2 slots each, with FV-1 fetch groups in
+// flight at a barrier.  Slot reuse: K(X) lands in the slot of K(X-FV-2),
+// last read in iteration X-FV-2 and fetched in iteration X-FV-1; V(X) in
+// that of V(X-FV-2), last read in iteration X-FV-1 and fetched in X-FV.
+//
+// Row sums: a packed-fp16 tree (Rows::sum_slot) on tiles that need no mask,
+// fp32 adds on the masked ones (diagonal / tail), where a short causal row
+// sums a few p.  Blocks whose first pass saw a tile sum out of the
+// fp16-safe range are recomputed by a plain one-tile-per-step checked pass.
+template <int W, int FV, bool CAUSAL, bool SCALED, class T = _Float16>
+__global__ void __launch_bounds__(64 * W, 2)  // <= 256 VGPRs: 2 waves per SIMD at W = 8
+fa2_fwd_slot_kernel(const T* Q, const T* __restrict__ K, const T* __restrict__ V, T* O,
+                    const Geom geom, int nqb, float cq, float cr) {
+  using RowsT = Rows<CAUSAL, SCALED, T>;
+  using V8 = typename RowsT::V8;
+  // fp16: unmasked tiles sum P with the packed-fp16 tree; bf16 P keeps
+  // fp32 sums throughout (an 8-bit mantissa tree would cost accuracy).
+  constexpr bool kFp16 = __is_same(T, _Float16);
+  // bf16: row sums on the matrix core (Rows::init_msum), four 16x16x32 MFMAs
+  // per tile in place of 32 fp32 adds, measured 4-7% faster on B2 H8 N4096.
+  // For fp16 the packed tree's 15 adds cost less than the MFMAs (3% the
+  // other way), so it keeps the tree.
+  constexpr bool kMfmaSum = !kFp16;
+  constexpr int FK = FV + 1;
+  constexpr int kSlots = FV + 2;  // per ring
+  constexpr int kUnroll = (kSlots % 2 == 0) ? kSlots : 2 * kSlots;
+  constexpr int kBr = 32 * W;
+  constexpr int kSegs = 8 / W;
+  constexpr int kDmaPerIter = 2 * kSegs;
+  constexpr int kAhead = 6;  // slots between an operand's LDS read and its MFMA
+  // LDS reads of the first kAhead slots (K slots: 1, V slots: 2).
+  constexpr int kTailReads = kAhead + kAhead / 2;
+  constexpr int kRingBytes = kSlots * kTileBytes;
+  // Two work-groups share a CU when both rings fit its 160 KiB and the
+  // waves fit two per SIMD (<= 4 waves each).
+  constexpr int kWgPerCu = (W <= 4 && 2 * 2 * kRingBytes <= 160 * 1024) ? 2 : 1;
+  static_assert(kSegs * W == 8, "tile split");
+  static_assert(FV >= 2 && FV <= 6, "fetch distance");
+  static_assert(kAhead % 2 == 0 && kAhead < 16, "read-ahead");
+  __shared__ __attribute__((aligned(16))) uint8_t kring[kRingBytes];
+  __shared__ __attribute__((aligned(16))) uint8_t vring[kRingBytes];
+
+  const int lane = threadIdx.x & 63;
+  const int rw = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  int bh, qb;
+  wg_coords<CAUSAL, kWgPerCu>(nqb, bh, qb);
+  const HeadPtrs<T> hp = head_ptrs(geom, bh, Q, K, V, O);
+  const i32x4_t rk = hp.rk, rv = hp.rv;
+  const FetchOff<kSegs> fk = fetch_offsets<kSegs, false>(rw, lane, 2 * geom.k_sr);
+  const FetchOff<kSegs> fv = fetch_offsets<kSegs, true>(rw, lane, 2 * geom.v_sr);
+  const int seq = geom.seq_q;
+  const int q0 = qb * kBr;
+  const StreamRings<kSlots> rings = {kring, vring};
+
+  int ntiles = max(1, (geom.seq_k + kBc - 1) / kBc);
+  if (CAUSAL) ntiles = min(ntiles, causal_tiles(min(q0 + kBr, seq), geom.coff));
+  const int t0 = ntiles;  // iterations 0 .. t0; the last one only drains GEMM2
+  const int last = ntiles - 1;
+
+  // Prologue fetch groups -FK .. -1 (V tiles < 0 read as zeros through the
+  // buffer bound, which also zeroes the slot GEMM2(-1) reads under P = 0),
+  // issued before the Q loads so the two latencies overlap.
+  static_for(std::make_integer_sequence<int, FK>{}, [&](auto i) __attribute__((always_inline)) {
+    constexpr int G = decltype(i)::value - FK;
+    fetch_tile<kSegs>(rk, rings.kslot(Ic<G + FK>{}), G + FK, last, rw, fk);
+    fetch_tile<kSegs>(rv, rings.vslot(Ic<G + FV>{}), G + FV, last, rw, fv);
+  });
+  RowsT rows;
+  rows.init(hp.q, geom.q_sr, lane, q0 + 32 * rw, seq, geom.seq_k, geom.coff, cq, cr);
+  if constexpr (kMfmaSum) rows.init_msum(lane);
+
+  // Iterations j < jm need no mask on tiles j and j + 1.
+  int tm = rows.kv_lim >> 6;
+  if (CAUSAL) tm = min(tm, (rows.qd + 1) >> 6);
+  const int jm = max(0, tm - 1);
+
+  // ---- first pass ----
+  sync_ring_ahead<(FK - 1) * kDmaPerIter, 0>();  // K(0)
+  float16_t S[2];
+  V8 P0[2][2], P1[2][2];
+#pragma unroll
+  for (int a = 0; a < 2; ++a)
+#pragma unroll
+    for (int b = 0; b < 2; ++b) P1[a][b] = (V8){0, 0, 0, 0, 0, 0, 0, 0};
+  {
+    // S(0) with the exact row max; iteration 0 recomputes block 1 against it.
+    V8 ka[2][4];
+    rows.read_k(rings.kslot(Ic<0>{}), ka);
+    rows.gemm1(ka, S);
+  }
+  rows.mask(0, S);
+  rows.first_tile(S);
+  sync_ring_ahead<(FV - 1) * kDmaPerIter, 0>();  // K(1), V(0)
+  V8 ahead[kAhead];
+  static_for(std::make_integer_sequence<int, kAhead>{}, [&](auto a) __attribute__((always_inline)) {
+    constexpr int L = decltype(a)::value;
+    ahead[L] = rows.template read_slot<L>(rings.kslot(Ic<0>{}), rings.kslot(Ic<1>{}),
+                                          rings.vslot(Ic<-1>{}));
+  });
+
+  uint64_t out_of_range = 0;
+  // Iteration j at unrolled position I (ring slots static): fetch K(j+FK)
+  // and V(j+FV); 16 slots; the range check of tile j's sum; on MASKED
+  // iterations, mask block 1 of tile j (after slot 7, before its
+  // exponentials) and block 0 of tile j+1; publish K(j+2), V(j+1).
+  auto iteration = [&](auto i, int j, V8 (&P)[2][2], const V8 (&Pp)[2][2],
+                       auto masked) __attribute__((always_inline)) {
+    constexpr int I = decltype(i)::value;
+    constexpr bool kMasked = decltype(masked)::value;
+    fetch_tile<kSegs>(rk, rings.kslot(Ic<I + FK>{}), j + FK, last, rw, fk);
+    fetch_tile<kSegs>(rv, rings.vslot(Ic<I + FV>{}), j + FV, last, rw, fv);
+    V8 op[16];
+#pragma unroll
+    for (int a = 0; a < kAhead; ++a) op[a] = ahead[a];
+    half2_t tree[14];
+    float sum[4];
+    static_for(std::make_integer_sequence<int, 16>{}, [&](auto sl) __attribute__((always_inline)) {
+      constexpr int L = decltype(sl)::value;
+      // The MFMA goes first (fenced): its operand's wait then never covers
+      // the read issued in the same slot.
+      rows.template mfma_slot<L, kMfmaSum>(op[L], S, Pp);
+      __builtin_amdgcn_sched_barrier(0);
+      if constexpr (L + kAhead < 16)
+        op[L + kAhead] = rows.template read_slot<L + kAhead>(
+            rings.kslot(Ic<I>{}), rings.kslot(Ic<I + 1>{}), rings.vslot(Ic<I - 1>{}));
+      else
+        ahead[L + kAhead - 16] = rows.template read_slot<L + kAhead - 16>(
+            rings.kslot(Ic<I + 1>{}), rings.kslot(Ic<I + 2>{}), rings.vslot(Ic<I>{}));
+      rows.template exp_slot<L>(S, P);
+      if constexpr (kMfmaSum)
+        ;
+      else if constexpr (kFp16 && !kMasked)
+        RowsT::template sum_slot<L>(P, tree);
+      else
+        RowsT::template sum_slot_f32<L>(S, sum, rows.cr);
+      if constexpr (kMasked && L == 7) rows.template mask_block<1>(j, S[1]);
+      __builtin_amdgcn_sched_barrier(0);
+    });
+    if constexpr (!kMfmaSum) {
+      float tot;
+      if constexpr (kFp16 && !kMasked)
+        tot = RowsT::sum_root(tree);
+      else
+        tot = (sum[0] + sum[1]) + (sum[2] + sum[3]);
+      rows.l += tot;
+      out_of_range |= __builtin_amdgcn_ballot_w64(!(tot <= kSumLimit));
+    }
+    if constexpr (kMasked) rows.template mask_block<0>(j + 1, S[0]);
+    sync_ring_ahead<(FV - 1) * kDmaPerIter, kTailReads>();
+  };
+  auto group = [&](int j0, auto masked) __attribute__((always_inline)) {
+    static_for(std::make_integer_sequence<int, kUnroll>{}, [&](auto i) __attribute__((always_inline)) {
+      constexpr int I = decltype(i)::value;
+      const int j = j0 + I;
+      if (!decltype(masked)::value || j <= t0) {
+        if constexpr (I % 2 == 0)
+          iteration(i, j, P0, P1, masked);
+        else
+          iteration(i, j, P1, P0, masked);
+      }
+    });
+  };
+  {
+    int j0 = 0;
+    for (; j0 + kUnroll <= jm; j0 += kUnroll) group(j0, Ic<false>{});
+    for (; j0 <= t0; j0 += kUnroll) group(j0, Ic<true>{});
+  }
+  if constexpr (kMfmaSum) {
+    // Every p of the first pass is in its row's sum, so a sum within 2^40
+    // bounds every p by 2^40 (finite O terms for any |V| below 2^88); a
+    // larger sum, inf or NaN (a row max far above the first tile's) sends
+    // the block to the checked pass.
+    rows.l = rows.msum_share();
+    out_of_range = __builtin_amdgcn_ballot_w64(!(rows.l <= kMsumLimit));
+  }
+
+  // ---- checked pass, when any wave saw a tile sum out of range ----
+  // The work-group's flag lives in K ring slot 1, which the checked pass
+  // never refills (the rings are idle here: every wave has drained its
+  // fetches and reads before the first barrier).  No extra LDS, so two
+  // 80 KiB work-groups still fit one CU.
+  __builtin_amdgcn_s_waitcnt(0);
+  int* redo = reinterpret_cast<int*>(rings.kslot(Ic<1>{}));
+  __syncthreads();
+  if (threadIdx.x == 0) *redo = 0;
+  __syncthreads();
+  if (out_of_range != 0 && lane == 0) *redo = 1;
+  __syncthreads();
+  if (*redo) {
+    rows.launder();
+    rows.reset();
+    for (int t = 0; t < ntiles; ++t) {
+      fetch_tile<kSegs>(rk, rings.kslot(Ic<0>{}), t, last, rw, fk);
+      fetch_tile<kSegs>(rv, rings.vslot(Ic<0>{}), t, last, rw, fv);
+      sync_ring_ahead<0, 0>();
+      float16_t Sc[2];
+      V8 Pc[2][2];
+      {
+        V8 ka[2][4];
+        rows.read_k(rings.kslot(Ic<0>{}), ka);
+        rows.gemm1(ka, Sc);
+      }
+      rows.mask(t, Sc);
+      if (t == 0) rows.first_tile(Sc);
+      rows.softmax_checked(Sc, Pc);
+      {
+        V8 va[2][4];
+        rows.read_v(rings.vslot(Ic<0>{}), va);
+        rows.gemm2(va, Pc);
+      }
+      sync_ring_ahead<0, 0>();  // every wave's reads done before the next fetch
+    }
+  }
+  rows.launder();
+  rows.store(hp.o, geom.o_sr, hp.lse);
+}
+
+template <int W, int FV, class T = _Float16>
+struct SlotLaunch {
+  template <bool C, bool S>
+  struct L {
+    static hipError_t run(const FwdArgs& a, const Geom& g, dim3 grid, int nqb, float cq, float cr,
+                          hipStream_t st) {
+      hipLaunchKernelGGL((fa2_fwd_slot_kernel<W, FV, C, S, T>), grid, dim3(64 * W), 0, st,
+                         static_cast<const T*>(a.q), static_cast<const T*>(a.k),
+                         static_cast<const T*>(a.v), static_cast<T*>(a.o), g, nqb, cq, cr);
+      return hipSuccess;
+    }
+  };
+};
+
+}  // namespace
+
+// fp16 or bf16 by a.dtype; W = 8 (256-row groups, one per CU, V fetched 4
+// tiles ahead) or 4 (128-row groups, two per CU, 3 tiles ahead).
+hipError_t launch_slot(const FwdArgs& a, int waves, hipStream_t stream) {
+  const bool bf = a.dtype == kDtypeBF16;
+  if (waves == 8)
+    return bf ? dispatch<SlotLaunch<8, 4, __bf16>::L>(a, stream, 256)
+              : dispatch<SlotLaunch<8, 4>::L>(a, stream, 256);
+  if (waves == 4)
+    return bf ? dispatch<SlotLaunch<4, 3, __bf16>::L>(a, stream, 128)
+              : dispatch<SlotLaunch<4, 3>::L>(a, stream, 128);
+  return hipErrorInvalidValue;
+}
+
+}  // namespace fl

@@ -1,5 +1,5 @@
 // Internal interface between the C-ABI layer (capi.hip) and the gfx950
-// kernels (fa2_fwd.hip, naive_fwd.hip).  Host-side only types.
+// kernels (fa2_*.hip, naive_fwd.hip).  Host-side only types.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -41,22 +41,32 @@ struct Fa2Config {
   const char* name;
 };
 
-constexpr int kNumFa2Configs = 9;
+// Configuration ids (indices into kFa2Configs).
+constexpr int kCfgW1 = 0;          // br32_bc64_w1: pipelined, 1 wave
+constexpr int kCfgW2 = 1;          // br64_bc64_w2: pipelined, 2 waves
+constexpr int kCfgSplit2 = 2;      // br128_bc64_w4_split2: 2 x 4 waves, key range halved
+constexpr int kSlotW8Config = 3;   // br256_bc64_w8_slot
+constexpr int kSlotW4Config = 4;   // br128_bc64_w4_slot
+// Persistent work-groups streaming whole units of 256 query rows whose keys
+// fit one LDS buffer: needs N_k <= kStreamMaxKeys and row strides below
+// kStreamMaxRowStride elements (unit-relative 32-bit buffer offsets).
+constexpr int kStreamConfig = 5;   // br256_kv256_w8_stream
+constexpr int kNumFa2Configs = 6;
 extern const Fa2Config kFa2Configs[kNumFa2Configs];
 
 // Launches the FA2 kernel for configuration `cfg` on `stream`.  fp16 at
 // head_dim 64 has every configuration; bf16 and head_dim 128 have the
 // slot-scheduled ones (kSlotW8Config, kSlotW4Config).
 hipError_t launch_fa2(const FwdArgs& a, int cfg, hipStream_t stream);
-constexpr int kSlotW8Config = 6;
-constexpr int kSlotW4Config = 7;
-// Persistent work-groups streaming whole units of 256 query rows whose keys
-// fit one LDS buffer: needs N_k <= kStreamMaxKeys and row strides below
-// kStreamMaxRowStride elements (unit-relative 32-bit buffer offsets).
-constexpr int kStreamConfig = 8;
 constexpr int kStreamMaxKeys = 256;
 constexpr int kStreamMaxRowStride = 1 << 22;
 bool stream_config_fits(const FwdArgs& a);
+
+// Per-schedule launchers behind launch_fa2 (one source file each).
+hipError_t launch_pipe(const FwdArgs& a, int cfg, hipStream_t stream);     // fa2_pipe.hip
+hipError_t launch_slot(const FwdArgs& a, int waves, hipStream_t stream);   // fa2_slot.hip
+hipError_t launch_stream(const FwdArgs& a, hipStream_t stream);            // fa2_stream.hip
+hipError_t launch_d128(const FwdArgs& a, int waves, hipStream_t stream);   // fa2_d128.hip
 
 // Split-KV ("flash-decoding"): `waves` (1, 2 or 4) waves of 32 query rows
 // per work-group, the key range cut into `nsplit` chunks whose partial

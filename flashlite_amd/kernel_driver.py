@@ -28,6 +28,15 @@ keys, seeded N(0,1) inputs) through ``fl_attn_fwd_f16_splitkv`` with
 ``--splits S`` (1 = one pass, 0 = the library's choice, n = n key chunks)
 and reports the K/V read rate against 8 TB/s: bytes = 2 * B*H*NK*64*2
 (K and V once) + Q and O.
+
+``--mfma-clock ROUNDS`` runs the clock calibration of the diagnostic
+library (``libflashlite_diag.so``, ``csrc/diag.hip``): every wave issues
+ROUNDS x 16 independent ``v_mfma_f32_32x32x16_f16`` (``--groups`` work-groups
+of ``--waves`` waves, ``--lds-kib`` of dynamic LDS each, ``--random`` for
+random operands).  With one wave per SIMD the matrix core is busy for
+ROUNDS * 512 shader cycles per wave, so the HIP-event time gives the clock
+the chip sustained; the per-wave ``s_memtime`` / ``s_memrealtime`` deltas
+check that ``s_memtime`` counts those cycles.
 """
 
 from __future__ import annotations
@@ -50,10 +59,17 @@ def main(argv=None):
     ap.add_argument("--dtype", choices=("fp16", "bf16"), default="fp16")
     ap.add_argument("--head-dim", type=int, default=0, help="override the workload's head dim")
     ap.add_argument("--shape", type=int, nargs=3, metavar=("B", "H", "N"), default=None)
+    ap.add_argument("--mfma-clock", type=int, default=0, metavar="ROUNDS")
+    ap.add_argument("--groups", type=int, default=256)
+    ap.add_argument("--waves", type=int, default=4)
+    ap.add_argument("--lds-kib", type=int, default=96)
+    ap.add_argument("--random", type=int, default=1)
     args = ap.parse_args(argv)
 
     import torch
 
+    if args.mfma_clock:
+        return _mfma_clock(args, torch)
     if args.decode:
         return _decode(args, torch)
 
@@ -161,6 +177,55 @@ def _decode(args, torch):
     chunks = need // (b * h * nq * 68 * 4) if need else 1
     print(f"decode B{b} H{h} NQ{nq} NK{nk} causal={args.causal_decode} chunks={chunks}: "
           f"{us:.2f} us/call, {nbytes / us / 1e3:.1f} GB/s ({nbytes / us / 1e3 / 8000:.1%} of 8 TB/s)",
+          flush=True)
+    return 0
+
+
+def _mfma_clock(args, torch):
+    import ctypes
+    import os
+
+    import numpy as np
+
+    lib = ctypes.CDLL(os.path.join(os.path.dirname(os.path.abspath(__file__)), "libflashlite_diag.so"))
+    lib.fl_diag_mfma_clock.argtypes = [ctypes.c_int] * 5 + [ctypes.c_void_p] * 3
+    lib.fl_diag_mfma_clock.restype = ctypes.c_int
+    lib.fl_diag_wall_clock_khz.argtypes = [ctypes.c_int]
+    lib.fl_diag_wall_clock_khz.restype = ctypes.c_int
+    dev = torch.device("cuda:0")
+    nwaves = args.groups * args.waves
+    out = torch.zeros(2 * nwaves, dtype=torch.int64, device=dev)
+    sink = torch.empty(nwaves * 64, dtype=torch.float32, device=dev)
+    stream = torch.cuda.current_stream().cuda_stream
+
+    def launch():
+        rc = lib.fl_diag_mfma_clock(args.groups, args.waves, args.mfma_clock, args.random,
+                                    args.lds_kib * 1024, out.data_ptr(), sink.data_ptr(), stream)
+        if rc != 0:
+            raise RuntimeError(f"fl_diag_mfma_clock failed: hipError {rc}")
+
+    launch()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(args.iters):
+        launch()
+    end.record()
+    torch.cuda.synchronize()
+    us = start.elapsed_time(end) * 1e3 / args.iters
+    d = out.cpu().numpy().reshape(-1, 2).astype(np.float64)
+    khz = lib.fl_diag_wall_clock_khz(0)
+    cyc, real = d[:, 0], d[:, 1]
+    clk = cyc / (real / (khz * 1e3)) / 1e9
+    known = args.mfma_clock * 16 * 32
+    flops = nwaves * args.mfma_clock * 16 * 32768
+    print(f"mfma clock: {args.groups} groups x {args.waves} waves, {args.lds_kib} KiB LDS, "
+          f"rounds {args.mfma_clock}, random {args.random}: {us:.2f} us/launch, "
+          f"{flops / us / 1e6:.1f} TFLOP/s; known MFMA cycles per wave {known}; "
+          f"s_memtime per wave min/median/max {cyc.min():.0f}/{np.median(cyc):.0f}/{cyc.max():.0f} "
+          f"(median/known {np.median(cyc) / known:.4f}); s_memrealtime rate {khz} kHz; "
+          f"s_memtime/s_memrealtime clock min/median/max {clk.min():.3f}/{np.median(clk):.3f}/"
+          f"{clk.max():.3f} GHz; known cycles / event time {known / us / 1e3:.3f} GHz",
           flush=True)
     return 0
 

@@ -10,8 +10,12 @@ from oracle import attention_fp32, error_stats
 MAX_ABS = 2e-3
 MEAN_ABS = 2e-4
 
-# The streaming configuration takes key ranges of at most 256 keys only.
-STREAM_CFG = 8
+# Tile configurations by name.  The streaming configuration takes key ranges
+# of at most 256 keys only.
+SLOT_W8_CFG = capi.config_id("br256_bc64_w8_slot")
+SLOT_W4_CFG = capi.config_id("br128_bc64_w4_slot")
+SPLIT2_CFG = capi.config_id("br128_bc64_w4_split2")
+STREAM_CFG = capi.config_id("br256_kv256_w8_stream")
 STREAM_MAX_KEYS = 256
 
 

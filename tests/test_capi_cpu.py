@@ -15,6 +15,7 @@ HEADER = os.path.join(ROOT, "include", "flashlite_attn.h")
 
 # Fake, 256-byte aligned device addresses: never dereferenced by these tests.
 A = 0x7F0000000000
+STREAM = capi.config_id("br256_kv256_w8_stream")
 
 
 def test_library_loads_and_exports_header_symbols():
@@ -28,12 +29,12 @@ def test_library_loads_and_exports_header_symbols():
 
 
 def test_config_table():
-    assert capi.num_configs() == 9
-    names = [capi.config_name(i) for i in range(9)]
-    assert names == ["br32_bc64_w1", "br64_bc64_w2", "br128_bc64_w4", "br256_bc64_w8",
-                     "br256_bc64_w8_pingpong", "br128_bc64_w4_split2", "br256_bc64_w8_slot",
+    assert capi.num_configs() == 6
+    names = [capi.config_name(i) for i in range(6)]
+    assert names == ["br32_bc64_w1", "br64_bc64_w2", "br128_bc64_w4_split2", "br256_bc64_w8_slot",
                      "br128_bc64_w4_slot", "br256_kv256_w8_stream"]
-    assert capi.config_name(9) is None and capi.config_name(-1) is None
+    assert capi.config_name(6) is None and capi.config_name(-1) is None
+    assert capi.config_id("br256_bc64_w8_slot") == 3
 
 
 def _p(**kw):
@@ -76,9 +77,9 @@ def _ex(q_stride=(8 * 4096 * 64, 4096 * 64, 64), k_stride=None, v_stride=None, o
 def test_ex_null_and_config():
     lib = capi.load()
     assert lib.fl_attn_fwd_f16_ex(None, -1, None) == capi.FL_ERR_INVALID_ARGUMENT
-    assert capi.fwd_ex(_ex(), config=9) == capi.FL_ERR_BAD_CONFIG
+    assert capi.fwd_ex(_ex(), config=capi.num_configs()) == capi.FL_ERR_BAD_CONFIG
     # the streaming configuration needs N_k <= 256 (rejected before any pointer check)
-    assert capi.fwd_ex(_ex(), config=8) == capi.FL_ERR_BAD_CONFIG
+    assert capi.fwd_ex(_ex(), config=STREAM) == capi.FL_ERR_BAD_CONFIG
     assert "needs N_k <= 256" in capi.last_error()
     assert capi.fwd_ex(_ex(head_dim=128)) == capi.FL_ERR_UNSUPPORTED
 
@@ -141,9 +142,9 @@ def test_non_finite_scale():
 
 
 def test_bad_config():
-    assert capi.fwd(_p(), config=9) == capi.FL_ERR_BAD_CONFIG
+    assert capi.fwd(_p(), config=capi.num_configs()) == capi.FL_ERR_BAD_CONFIG
     assert capi.fwd(_p(), config=-2) == capi.FL_ERR_BAD_CONFIG
-    assert capi.fwd(_p(seq_q=256, seq_k=257), config=8) == capi.FL_ERR_BAD_CONFIG
+    assert capi.fwd(_p(seq_q=256, seq_k=257), config=STREAM) == capi.FL_ERR_BAD_CONFIG
     assert "needs N_k <= 256" in capi.last_error()
 
 
@@ -162,31 +163,34 @@ def test_naive_limits():
 
 
 def test_dispatcher_choices():
-    sel = lambda **kw: capi.select_config(_p(**kw))  # noqa: E731
+    sel = lambda **kw: capi.config_name(capi.select_config(_p(**kw)))  # noqa: E731
+    W8, W4, SPLIT, STRM = ("br256_bc64_w8_slot", "br128_bc64_w4_slot", "br128_bc64_w4_split2",
+                           "br256_kv256_w8_stream")
+    W1, W2 = "br32_bc64_w1", "br64_bc64_w2"
     # non-causal: 8-wave 256-row slot-scheduled groups when there is one per CU
     # and the key range is long
-    assert sel(batch=2, heads=8, seq_q=4096) == 6      # 256 groups
-    assert sel(batch=1, heads=16, seq_q=16384) == 6
+    assert sel(batch=2, heads=8, seq_q=4096) == W8      # 256 groups
+    assert sel(batch=1, heads=16, seq_q=16384) == W8
     # short key ranges (N_k <= 256): streaming groups
-    assert sel(batch=32, heads=32, seq_q=256) == 8     # 1024 units
-    assert sel(batch=8, heads=32, seq_q=130) == 8      # 256 units
-    assert sel(batch=2, heads=8, seq_q=256) == 8       # 16 units
-    assert sel(batch=1, heads=1, seq_q=1000, seq_k=256) == 8
-    assert sel(batch=2, heads=8, seq_q=2048) == 7
+    assert sel(batch=32, heads=32, seq_q=256) == STRM     # 1024 units
+    assert sel(batch=8, heads=32, seq_q=130) == STRM      # 256 units
+    assert sel(batch=2, heads=8, seq_q=256) == STRM       # 16 units
+    assert sel(batch=1, heads=1, seq_q=1000, seq_k=256) == STRM
+    assert sel(batch=2, heads=8, seq_q=2048) == W4
     # very few groups at N >= 2048: split key range
-    assert sel(batch=1, heads=1, seq_q=4096) == 5
-    assert sel(batch=1, heads=3, seq_q=4096) == 5      # 96 groups of 128 rows
+    assert sel(batch=1, heads=1, seq_q=4096) == SPLIT
+    assert sel(batch=1, heads=3, seq_q=4096) == SPLIT      # 96 groups of 128 rows
     # causal: 128-row slot-scheduled groups balanced by dispatch order
-    assert sel(batch=2, heads=8, seq_q=4096, causal=True) == 7
-    assert sel(batch=1, heads=16, seq_q=16384, causal=True) == 7
-    assert sel(batch=32, heads=32, seq_q=256, causal=True) == 8   # streaming, any count
-    assert sel(batch=1, heads=1, seq_q=128, causal=True) == 8
-    assert sel(batch=1, heads=1, seq_q=257, causal=True) == 0     # N_k > 256
+    assert sel(batch=2, heads=8, seq_q=4096, causal=True) == W4
+    assert sel(batch=1, heads=16, seq_q=16384, causal=True) == W4
+    assert sel(batch=32, heads=32, seq_q=256, causal=True) == STRM   # streaming, any count
+    assert sel(batch=1, heads=1, seq_q=128, causal=True) == STRM
+    assert sel(batch=1, heads=1, seq_q=257, causal=True) == W1     # N_k > 256
     # small problems: smaller groups
-    assert sel(batch=2, heads=8, seq_q=512) == 7       # 64 groups of 128 rows
-    assert sel(batch=2, heads=4, seq_q=512) == 1       # 64 groups of 64 rows
-    assert sel(batch=1, heads=1, seq_q=257) == 0
-    assert sel(head_dim=80) == -1
+    assert sel(batch=2, heads=8, seq_q=512) == W4       # 64 groups of 128 rows
+    assert sel(batch=2, heads=4, seq_q=512) == W2       # 64 groups of 64 rows
+    assert sel(batch=1, heads=1, seq_q=257) == W1
+    assert capi.select_config(_p(head_dim=80)) == -1
 
 
 @pytest.mark.parametrize("fn", ["fwd", "naive"])

@@ -22,7 +22,7 @@ from oracle import attention_fp32, attention_lse, error_stats
 
 pytestmark = pytest.mark.gpu
 
-NCFG = 9
+NCFG = capi.num_configs()
 LSE_MAX_ABS = 2e-3
 LSE_MEAN_ABS = 3e-4
 

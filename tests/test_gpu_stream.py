@@ -18,7 +18,7 @@ import pytest
 
 from flashlite_amd import capi
 from flashlite_amd.workloads import WORKLOADS, make_qkv, workload_inputs
-from gpu_util import STREAM_CFG, assert_close_oracle, run_capi, to_dev
+from gpu_util import SLOT_W4_CFG, STREAM_CFG, assert_close_oracle, run_capi, to_dev
 from oracle import attention_fp32, attention_lse, error_stats
 
 pytestmark = pytest.mark.gpu
@@ -82,7 +82,7 @@ def test_c4_matches_oracle_and_slot_kernel(cuda, causal):
     # causal row 0 sees only key 0: the output is V[0] exactly
     if causal:
         assert np.array_equal(out[:, :, 0], v[:, :, 0])
-    slot = run_capi(q, k, v, w.sm_scale, causal, cuda, config=7)
+    slot = run_capi(q, k, v, w.sm_scale, causal, cuda, config=SLOT_W4_CFG)
     assert error_stats(out, slot)[0] <= 2e-3
 
 

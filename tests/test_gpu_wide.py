@@ -25,7 +25,7 @@ import numpy as np
 import pytest
 
 from flashlite_amd import capi
-from gpu_util import MAX_ABS, MEAN_ABS, sample_rows
+from gpu_util import MAX_ABS, MEAN_ABS, SLOT_W4_CFG, SLOT_W8_CFG, sample_rows
 from oracle import attention_fp32, attention_lse, error_stats
 
 pytestmark = pytest.mark.gpu
@@ -34,7 +34,7 @@ BF16_MAX_ABS = 8 * MAX_ABS
 BF16_MEAN_ABS = 8 * MEAN_ABS
 LSE_MAX_ABS = 2e-3
 LSE_MEAN_ABS = {"fp16": 3e-4, "bf16": 1e-3}
-SLOT_CFGS = [-1, 6, 7]
+SLOT_CFGS = [-1, SLOT_W8_CFG, SLOT_W4_CFG]
 KINDS = [("fp16", 64), ("fp16", 128), ("bf16", 64), ("bf16", 128)]
 WIDE = [k for k in KINDS if k != ("fp16", 64)]
 
@@ -106,7 +106,7 @@ RECT = [(1, 1), (1, 300), (5, 64), (37, 100), (100, 37), (64, 65), (200, 513), (
 
 
 @pytest.mark.parametrize("kind,d", WIDE)
-@pytest.mark.parametrize("config", [6, 7])
+@pytest.mark.parametrize("config", [SLOT_W8_CFG, SLOT_W4_CFG])
 @pytest.mark.parametrize("causal", [False, True])
 def test_rectangular_with_lse(cuda, kind, d, config, causal):
     for nq, nk in RECT:
@@ -184,8 +184,8 @@ def test_config_choice_equal(cuda, kind, d):
     same arithmetic in the same order with fp32 row sums; only the
     work-group shape differs)."""
     q, k, v = _inputs(kind, 2, 4, 700, 700, d, seed=9)
-    a, _ = _run(kind, q, k, v, 0.125, True, cuda, config=6)
-    b, _ = _run(kind, q, k, v, 0.125, True, cuda, config=7)
+    a, _ = _run(kind, q, k, v, 0.125, True, cuda, config=SLOT_W8_CFG)
+    b, _ = _run(kind, q, k, v, 0.125, True, cuda, config=SLOT_W4_CFG)
     assert np.array_equal(a, b)
 
 
