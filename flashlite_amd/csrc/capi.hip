@@ -75,6 +75,7 @@ int check_common(const fl_attn_params* p, fl::FwdArgs* a, const char* who) {
   a->negate = scale < 0.0 ? 1 : 0;
   a->causal = p->causal ? 1 : 0;
   a->dtype = fl::kDtypeF16;
+  a->exact = 0;
   // contiguous [B, H, N, D]
   const int64_t d = p->head_dim;
   a->q_sr = a->o_sr = a->k_sr = a->v_sr = (int)d;

@@ -555,6 +555,32 @@ struct Rows {
     pn[kb][h][e] = (T)e0;
     pn[kb][h][e + 1] = (T)e1;
   }
+  // The same split in two steps, for schedules that scale one slot ahead:
+  // the scaled scores of slot I's pair (times cr when SCALED) ...
+  template <int I>
+  __device__ __forceinline__ void scale_pair(const float16_t (&s)[2], float (&x)[2]) const {
+    constexpr int kb = I >> 3, r = 2 * (I & 7);
+    x[0] = SCALED ? s[kb][r] * cr : s[kb][r];
+    x[1] = SCALED ? s[kb][r + 1] * cr : s[kb][r + 1];
+  }
+  // ... and their exponentials, packed into dword I of the P operand
+  // (returned for an fp32 row sum).
+  template <int I>
+  __device__ __forceinline__ float exp_pair(const float (&x)[2], V8 (&pn)[2][2]) const {
+    constexpr int kb = I >> 3, r = 2 * (I & 7), h = r >> 3, e = r & 7;
+    const float e0 = __builtin_amdgcn_exp2f(x[0]), e1 = __builtin_amdgcn_exp2f(x[1]);
+    pn[kb][h][e] = (T)e0;
+    pn[kb][h][e + 1] = (T)e1;
+    return e0 + e1;
+  }
+  // fp32 row-sum share of slot I from its pair's sum, in four chains.
+  template <int I>
+  __device__ __forceinline__ static void sum_pair_f32(float e, float (&sum)[4]) {
+    if constexpr (I < 4)
+      sum[I] = e;
+    else
+      sum[I & 3] += e;
+  }
   // Dword i (0-15) of a tile's P operand: the fp16 pair of slot i.
   __device__ __forceinline__ static half2_t p_pair(const half8_t (&pn)[2][2], int i) {
     const half8_t& v = pn[i >> 3][(i >> 2) & 1];
@@ -927,7 +953,9 @@ __device__ __forceinline__ void sync_ring_ahead() {
 constexpr int kD2 = 128;
 
 // Q is prescaled by cq = +-min(c, 1) in the kernel; the remaining factor
-// cr = c / |cq| (1 unless c > 1) is applied to the scores.
+// cr = c / |cq| (1 unless c > 1) is applied to the scores.  The exact
+// configurations keep Q unscaled and scale every fp32 score by c, as the
+// reference does (kernel_flash2.cu:188-195).
 // bf16 and head_dim 128 keep Q exact (cq = +-1) and scale the fp32 scores
 // instead: a bf16 rounding of the prescaled Q would cost 2^-9 of every
 // score, and at D = 128 the fp16 rounding error of a score grows with
@@ -939,7 +967,7 @@ struct Scales {
   bool scaled;
   explicit Scales(const FwdArgs& a) {
     const float c = a.scale_log2;
-    const bool exact_q = a.dtype == kDtypeBF16 || a.head_dim == kD2;
+    const bool exact_q = a.dtype == kDtypeBF16 || a.head_dim == kD2 || a.exact != 0;
     cq = (c <= 1.0f && !exact_q ? c : 1.0f) * (a.negate ? -1.0f : 1.0f);
     cr = c <= 1.0f && !exact_q ? 1.0f : c;
     scaled = cr != 1.0f;

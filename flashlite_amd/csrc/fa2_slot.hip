@@ -4,6 +4,10 @@
 
 #include "fa2_common.h"
 
+#ifndef SLOT_SPLIT_FV
+#define SLOT_SPLIT_FV 3
+#endif
+
 namespace fl {
 
 namespace {
@@ -36,8 +40,24 @@ namespace {
 // fp32 adds on the masked ones (diagonal / tail), where a short causal row
 // sums a few p.  Blocks whose first pass saw a tile sum out of the
 // fp16-safe range are recomputed by a plain one-tile-per-step checked pass.
-template <int W, int FV, bool CAUSAL, bool SCALED, class T = _Float16>
-__global__ void __launch_bounds__(64 * W, 2)  // <= 256 VGPRs: 2 waves per SIMD at W = 8
+//
+// SPLIT = 2 (configuration br128_bc64_w4x2_slot): 2W waves, two per SIMD,
+// hold the same 32W query rows; waves 0..W-1 (stream 0) walk the first
+// ceil(n/2) of the block's n key tiles and waves W..2W-1 (stream 1) the rest,
+// each stream through its own rings, and the halves merge through LDS at
+// the end (Rows::save_partial / merge_partial).  Both streams run the same
+// iterations (the shorter one ends on a fully masked tile), so every wave
+// meets the same barriers.  This halves the longest key walk: a causal
+// work-group's time follows half its tiles, and heaviest-first dispatch of
+// one work-group per CU then balances the CUs.
+//
+// EXACT (the *_exact configurations): the reference's arithmetic on every
+// tile -- Q unscaled (SCALED, the fp32 scores multiplied by sm_scale * log2 e)
+// and fp32 row sums of the unrounded p (Rows::sum_slot_f32), one multiply
+// per score and one more add per pair than the default.
+template <int W, int FV, bool CAUSAL, bool SCALED, class T = _Float16, int SPLIT = 1,
+          bool EXACT = false>
+__global__ void __launch_bounds__(64 * W * SPLIT, 2)  // <= 256 VGPRs: 2 waves per SIMD
 fa2_fwd_slot_kernel(const T* Q, const T* __restrict__ K, const T* __restrict__ V, T* O,
                     const Geom geom, int nqb, float cq, float cr) {
   using RowsT = Rows<CAUSAL, SCALED, T>;
@@ -45,6 +65,9 @@ fa2_fwd_slot_kernel(const T* Q, const T* __restrict__ K, const T* __restrict__ V
   // fp16: unmasked tiles sum P with the packed-fp16 tree; bf16 P keeps
   // fp32 sums throughout (an 8-bit mantissa tree would cost accuracy).
   constexpr bool kFp16 = __is_same(T, _Float16);
+  // The packed-fp16 row-sum tree on unmasked tiles (fp16 unless EXACT).
+  constexpr bool kTree = kFp16 && !EXACT;
+  static_assert(!EXACT || kFp16, "the exact variant is built for fp16");
   // bf16: row sums on the matrix core (Rows::init_msum), four 16x16x32 MFMAs
   // per tile in place of 32 fp32 adds, measured 4-7% faster on B2 H8 N4096.
   // For fp16 the packed tree's 15 adds cost less than the MFMAs (3% the
@@ -62,15 +85,20 @@ fa2_fwd_slot_kernel(const T* Q, const T* __restrict__ K, const T* __restrict__ V
   constexpr int kRingBytes = kSlots * kTileBytes;
   // Two work-groups share a CU when both rings fit its 160 KiB and the
   // waves fit two per SIMD (<= 4 waves each).
-  constexpr int kWgPerCu = (W <= 4 && 2 * 2 * kRingBytes <= 160 * 1024) ? 2 : 1;
+  constexpr int kWgPerCu =
+      (W * SPLIT <= 4 && 2 * 2 * SPLIT * kRingBytes <= 160 * 1024) ? 2 : 1;
   static_assert(kSegs * W == 8, "tile split");
   static_assert(FV >= 2 && FV <= 6, "fetch distance");
   static_assert(kAhead % 2 == 0 && kAhead < 16, "read-ahead");
-  __shared__ __attribute__((aligned(16))) uint8_t kring[kRingBytes];
-  __shared__ __attribute__((aligned(16))) uint8_t vring[kRingBytes];
+  static_assert(SPLIT == 1 || SPLIT == 2, "key-range split");
+  static_assert(SPLIT == 1 || SPLIT * kRingBytes >= W * 34 * 64 * 4, "merge buffer");
+  __shared__ __attribute__((aligned(16))) uint8_t kring[SPLIT * kRingBytes];
+  __shared__ __attribute__((aligned(16))) uint8_t vring[SPLIT * kRingBytes];
 
   const int lane = threadIdx.x & 63;
-  const int rw = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int stream = wave / W;       // key-range half (0 unless SPLIT)
+  const int rw = wave - stream * W;  // 32-row block within the work-group
   int bh, qb;
   wg_coords<CAUSAL, kWgPerCu>(nqb, bh, qb);
   const HeadPtrs<T> hp = head_ptrs(geom, bh, Q, K, V, O);
@@ -79,29 +107,37 @@ fa2_fwd_slot_kernel(const T* Q, const T* __restrict__ K, const T* __restrict__ V
   const FetchOff<kSegs> fv = fetch_offsets<kSegs, true>(rw, lane, 2 * geom.v_sr);
   const int seq = geom.seq_q;
   const int q0 = qb * kBr;
-  const StreamRings<kSlots> rings = {kring, vring};
+  const StreamRings<kSlots> rings = {kring + stream * kRingBytes, vring + stream * kRingBytes};
 
   int ntiles = max(1, (geom.seq_k + kBc - 1) / kBc);
   if (CAUSAL) ntiles = min(ntiles, causal_tiles(min(q0 + kBr, seq), geom.coff));
-  const int t0 = ntiles;  // iterations 0 .. t0; the last one only drains GEMM2
-  const int last = ntiles - 1;
+  // This stream's key tiles [tbeg, tend); iterations 0 .. t0 on tile tbeg + j
+  // (the last one only drains GEMM2; with SPLIT the shorter stream's last
+  // tile lies past the range and is masked).
+  const int t0 = SPLIT == 2 ? (ntiles + 1) / 2 : ntiles;
+  const int tbeg = stream == 0 ? 0 : t0;
+  const int tend = stream == 0 ? t0 : ntiles;
+  const int last = max(tend - 1, tbeg);  // fetch clamp
 
   // Prologue fetch groups -FK .. -1 (V tiles < 0 read as zeros through the
   // buffer bound, which also zeroes the slot GEMM2(-1) reads under P = 0),
   // issued before the Q loads so the two latencies overlap.
   static_for(std::make_integer_sequence<int, FK>{}, [&](auto i) __attribute__((always_inline)) {
     constexpr int G = decltype(i)::value - FK;
-    fetch_tile<kSegs>(rk, rings.kslot(Ic<G + FK>{}), G + FK, last, rw, fk);
-    fetch_tile<kSegs>(rv, rings.vslot(Ic<G + FV>{}), G + FV, last, rw, fv);
+    // (tile tbeg - 1 of stream 1 is a real tile: the zeroed P of
+    // iteration 0 keeps it out of O)
+    fetch_tile<kSegs>(rk, rings.kslot(Ic<G + FK>{}), tbeg + G + FK, last, rw, fk);
+    fetch_tile<kSegs>(rv, rings.vslot(Ic<G + FV>{}), tbeg + G + FV, last, rw, fv);
   });
   RowsT rows;
   rows.init(hp.q, geom.q_sr, lane, q0 + 32 * rw, seq, geom.seq_k, geom.coff, cq, cr);
   if constexpr (kMfmaSum) rows.init_msum(lane);
+  if (SPLIT == 2 && stream == 0) rows.kv_lim = min(rows.kv_lim, tend * kBc);
 
-  // Iterations j < jm need no mask on tiles j and j + 1.
+  // Iterations j < jm need no mask on tiles tbeg + j and tbeg + j + 1.
   int tm = rows.kv_lim >> 6;
   if (CAUSAL) tm = min(tm, (rows.qd + 1) >> 6);
-  const int jm = max(0, tm - 1);
+  const int jm = max(0, tm - tbeg - 1);
 
   // ---- first pass ----
   sync_ring_ahead<(FK - 1) * kDmaPerIter, 0>();  // K(0)
@@ -112,12 +148,13 @@ fa2_fwd_slot_kernel(const T* Q, const T* __restrict__ K, const T* __restrict__ V
 #pragma unroll
     for (int b = 0; b < 2; ++b) P1[a][b] = (V8){0, 0, 0, 0, 0, 0, 0, 0};
   {
-    // S(0) with the exact row max; iteration 0 recomputes block 1 against it.
+    // S(tbeg) with the exact row max; iteration 0 recomputes block 1
+    // against it.
     V8 ka[2][4];
     rows.read_k(rings.kslot(Ic<0>{}), ka);
     rows.gemm1(ka, S);
   }
-  rows.mask(0, S);
+  rows.mask(tbeg, S);
   rows.first_tile(S);
   sync_ring_ahead<(FV - 1) * kDmaPerIter, 0>();  // K(1), V(0)
   V8 ahead[kAhead];
@@ -136,13 +173,16 @@ fa2_fwd_slot_kernel(const T* Q, const T* __restrict__ K, const T* __restrict__ V
                        auto masked) __attribute__((always_inline)) {
     constexpr int I = decltype(i)::value;
     constexpr bool kMasked = decltype(masked)::value;
-    fetch_tile<kSegs>(rk, rings.kslot(Ic<I + FK>{}), j + FK, last, rw, fk);
-    fetch_tile<kSegs>(rv, rings.vslot(Ic<I + FV>{}), j + FV, last, rw, fv);
+    fetch_tile<kSegs>(rk, rings.kslot(Ic<I + FK>{}), tbeg + j + FK, last, rw, fk);
+    fetch_tile<kSegs>(rv, rings.vslot(Ic<I + FV>{}), tbeg + j + FV, last, rw, fv);
     V8 op[16];
 #pragma unroll
     for (int a = 0; a < kAhead; ++a) op[a] = ahead[a];
     half2_t tree[14];
     float sum[4];
+    // SCALED: each slot scales the next slot's pair, so a slot's
+    // exponentials never wait on its own multiplies.
+    float xs[2][2];
     static_for(std::make_integer_sequence<int, 16>{}, [&](auto sl) __attribute__((always_inline)) {
       constexpr int L = decltype(sl)::value;
       // The MFMA goes first (fenced): its operand's wait then never covers
@@ -155,26 +195,28 @@ fa2_fwd_slot_kernel(const T* Q, const T* __restrict__ K, const T* __restrict__ V
       else
         ahead[L + kAhead - 16] = rows.template read_slot<L + kAhead - 16>(
             rings.kslot(Ic<I + 1>{}), rings.kslot(Ic<I + 2>{}), rings.vslot(Ic<I>{}));
-      rows.template exp_slot<L>(S, P);
+      if constexpr (L == 0) rows.template scale_pair<0>(S, xs[0]);
+      const float epair = rows.template exp_pair<L>(xs[L & 1], P);
       if constexpr (kMfmaSum)
         ;
-      else if constexpr (kFp16 && !kMasked)
+      else if constexpr (kTree && !kMasked)
         RowsT::template sum_slot<L>(P, tree);
       else
-        RowsT::template sum_slot_f32<L>(S, sum, rows.cr);
-      if constexpr (kMasked && L == 7) rows.template mask_block<1>(j, S[1]);
+        RowsT::template sum_pair_f32<L>(epair, sum);
+      if constexpr (kMasked && L == 7) rows.template mask_block<1>(tbeg + j, S[1]);
+      if constexpr (L < 15) rows.template scale_pair<L + 1>(S, xs[(L + 1) & 1]);
       __builtin_amdgcn_sched_barrier(0);
     });
     if constexpr (!kMfmaSum) {
       float tot;
-      if constexpr (kFp16 && !kMasked)
+      if constexpr (kTree && !kMasked)
         tot = RowsT::sum_root(tree);
       else
         tot = (sum[0] + sum[1]) + (sum[2] + sum[3]);
       rows.l += tot;
       out_of_range |= __builtin_amdgcn_ballot_w64(!(tot <= kSumLimit));
     }
-    if constexpr (kMasked) rows.template mask_block<0>(j + 1, S[0]);
+    if constexpr (kMasked) rows.template mask_block<0>(tbeg + j + 1, S[0]);
     sync_ring_ahead<(FV - 1) * kDmaPerIter, kTailReads>();
   };
   auto group = [&](int j0, auto masked) __attribute__((always_inline)) {
@@ -204,12 +246,13 @@ fa2_fwd_slot_kernel(const T* Q, const T* __restrict__ K, const T* __restrict__ V
   }
 
   // ---- checked pass, when any wave saw a tile sum out of range ----
-  // The work-group's flag lives in K ring slot 1, which the checked pass
-  // never refills (the rings are idle here: every wave has drained its
-  // fetches and reads before the first barrier).  No extra LDS, so two
-  // 80 KiB work-groups still fit one CU.
+  // The work-group's flag lives in stream 0's K ring slot 1, which the
+  // checked pass never refills (the rings are idle here: every wave has
+  // drained its fetches and reads before the first barrier).  No extra
+  // LDS, so two 80 KiB work-groups still fit one CU.  Both streams read the
+  // one flag, so every wave takes the same barriers.
   __builtin_amdgcn_s_waitcnt(0);
-  int* redo = reinterpret_cast<int*>(rings.kslot(Ic<1>{}));
+  int* redo = reinterpret_cast<int*>(kring + kTileBytes);
   __syncthreads();
   if (threadIdx.x == 0) *redo = 0;
   __syncthreads();
@@ -218,9 +261,10 @@ fa2_fwd_slot_kernel(const T* Q, const T* __restrict__ K, const T* __restrict__ V
   if (*redo) {
     rows.launder();
     rows.reset();
-    for (int t = 0; t < ntiles; ++t) {
-      fetch_tile<kSegs>(rk, rings.kslot(Ic<0>{}), t, last, rw, fk);
-      fetch_tile<kSegs>(rv, rings.vslot(Ic<0>{}), t, last, rw, fv);
+    // Both streams take t0 steps (tile tbeg + t; past tend: masked).
+    for (int t = 0; t < t0; ++t) {
+      fetch_tile<kSegs>(rk, rings.kslot(Ic<0>{}), tbeg + t, last, rw, fk);
+      fetch_tile<kSegs>(rv, rings.vslot(Ic<0>{}), tbeg + t, last, rw, fv);
       sync_ring_ahead<0, 0>();
       float16_t Sc[2];
       V8 Pc[2][2];
@@ -229,7 +273,7 @@ fa2_fwd_slot_kernel(const T* Q, const T* __restrict__ K, const T* __restrict__ V
         rows.read_k(rings.kslot(Ic<0>{}), ka);
         rows.gemm1(ka, Sc);
       }
-      rows.mask(t, Sc);
+      rows.mask(tbeg + t, Sc);
       if (t == 0) rows.first_tile(Sc);
       rows.softmax_checked(Sc, Pc);
       {
@@ -240,17 +284,28 @@ fa2_fwd_slot_kernel(const T* Q, const T* __restrict__ K, const T* __restrict__ V
       sync_ring_ahead<0, 0>();  // every wave's reads done before the next fetch
     }
   }
+  if constexpr (SPLIT == 2) {
+    // Stream 1 hands its O, m, l to stream 0 through the (idle) rings.
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    float* xchg = reinterpret_cast<float*>(kring) + rw * (34 * 64);
+    if (stream == 1) rows.save_partial(xchg, lane);
+    __syncthreads();
+    if (stream == 1) return;
+    rows.merge_partial(xchg, lane);
+  }
   rows.launder();
   rows.store(hp.o, geom.o_sr, hp.lse);
 }
 
-template <int W, int FV, class T = _Float16>
+template <int W, int FV, class T = _Float16, int SPLIT = 1, bool EXACT = false>
 struct SlotLaunch {
   template <bool C, bool S>
   struct L {
     static hipError_t run(const FwdArgs& a, const Geom& g, dim3 grid, int nqb, float cq, float cr,
                           hipStream_t st) {
-      hipLaunchKernelGGL((fa2_fwd_slot_kernel<W, FV, C, S, T>), grid, dim3(64 * W), 0, st,
+      hipLaunchKernelGGL((fa2_fwd_slot_kernel<W, FV, C, S, T, SPLIT, EXACT>), grid, dim3(64 * W * SPLIT),
+                         0, st,
                          static_cast<const T*>(a.q), static_cast<const T*>(a.k),
                          static_cast<const T*>(a.v), static_cast<T*>(a.o), g, nqb, cq, cr);
       return hipSuccess;
@@ -271,6 +326,22 @@ hipError_t launch_slot(const FwdArgs& a, int waves, hipStream_t stream) {
     return bf ? dispatch<SlotLaunch<4, 3, __bf16>::L>(a, stream, 128)
               : dispatch<SlotLaunch<4, 3>::L>(a, stream, 128);
   return hipErrorInvalidValue;
+}
+
+// fp16 with the reference's arithmetic (FwdArgs::exact): W = 8 or 4.
+hipError_t launch_slot_exact(const FwdArgs& a, int waves, hipStream_t stream) {
+  if (a.dtype != kDtypeF16) return hipErrorInvalidValue;
+  FwdArgs e = a;
+  e.exact = 1;
+  if (waves == 8) return dispatch<SlotLaunch<8, 4, _Float16, 1, true>::L>(e, stream, 256);
+  if (waves == 4) return dispatch<SlotLaunch<4, 3, _Float16, 1, true>::L>(e, stream, 128);
+  return hipErrorInvalidValue;
+}
+
+// fp16: 128-row groups of 2 x 4 waves, the key range halved between them.
+hipError_t launch_slot_split(const FwdArgs& a, hipStream_t stream) {
+  if (a.dtype != kDtypeF16) return hipErrorInvalidValue;
+  return dispatch<SlotLaunch<4, SLOT_SPLIT_FV, _Float16, 2>::L>(a, stream, 128);
 }
 
 }  // namespace fl

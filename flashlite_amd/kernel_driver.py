@@ -37,6 +37,12 @@ random operands).  With one wave per SIMD the matrix core is busy for
 ROUNDS * 512 shader cycles per wave, so the HIP-event time gives the clock
 the chip sustained; the per-wave ``s_memtime`` / ``s_memrealtime`` deltas
 check that ``s_memtime`` counts those cycles.
+
+``--mfma-mix MODE`` with ``--mfma-clock ROUNDS`` runs the issue-rate probe
+instead (``fl_diag_mfma_mix``): each of the 16 MFMAs of a round is followed
+by a fixed sequence of independent VALU instructions (MODE 0-8, listed in
+``csrc/diag.hip``), and the s_memtime cycles per MFMA show what issues under
+a running MFMA.
 """
 
 from __future__ import annotations
@@ -64,6 +70,7 @@ def main(argv=None):
     ap.add_argument("--waves", type=int, default=4)
     ap.add_argument("--lds-kib", type=int, default=96)
     ap.add_argument("--random", type=int, default=1)
+    ap.add_argument("--mfma-mix", type=int, default=-1, metavar="MODE")
     args = ap.parse_args(argv)
 
     import torch
@@ -190,6 +197,8 @@ def _mfma_clock(args, torch):
     lib = ctypes.CDLL(os.path.join(os.path.dirname(os.path.abspath(__file__)), "libflashlite_diag.so"))
     lib.fl_diag_mfma_clock.argtypes = [ctypes.c_int] * 5 + [ctypes.c_void_p] * 3
     lib.fl_diag_mfma_clock.restype = ctypes.c_int
+    lib.fl_diag_mfma_mix.argtypes = [ctypes.c_int] * 5 + [ctypes.c_void_p] * 3
+    lib.fl_diag_mfma_mix.restype = ctypes.c_int
     lib.fl_diag_wall_clock_khz.argtypes = [ctypes.c_int]
     lib.fl_diag_wall_clock_khz.restype = ctypes.c_int
     dev = torch.device("cuda:0")
@@ -199,10 +208,15 @@ def _mfma_clock(args, torch):
     stream = torch.cuda.current_stream().cuda_stream
 
     def launch():
-        rc = lib.fl_diag_mfma_clock(args.groups, args.waves, args.mfma_clock, args.random,
-                                    args.lds_kib * 1024, out.data_ptr(), sink.data_ptr(), stream)
+        if args.mfma_mix >= 0:
+            rc = lib.fl_diag_mfma_mix(args.groups, args.waves, args.mfma_clock, args.mfma_mix,
+                                      args.lds_kib * 1024, out.data_ptr(), sink.data_ptr(), stream)
+        else:
+            rc = lib.fl_diag_mfma_clock(args.groups, args.waves, args.mfma_clock, args.random,
+                                        args.lds_kib * 1024, out.data_ptr(), sink.data_ptr(),
+                                        stream)
         if rc != 0:
-            raise RuntimeError(f"fl_diag_mfma_clock failed: hipError {rc}")
+            raise RuntimeError(f"diagnostic launch failed: hipError {rc}")
 
     launch()
     torch.cuda.synchronize()
@@ -219,6 +233,14 @@ def _mfma_clock(args, torch):
     clk = cyc / (real / (khz * 1e3)) / 1e9
     known = args.mfma_clock * 16 * 32
     flops = nwaves * args.mfma_clock * 16 * 32768
+    if args.mfma_mix >= 0:
+        per_simd = max(1, args.waves // 4)
+        print(f"mfma mix mode {args.mfma_mix}: {args.groups} groups x {args.waves} waves "
+              f"({per_simd}/SIMD), rounds {args.mfma_clock}: {us:.2f} us/launch; s_memtime cycles "
+              f"per MFMA per SIMD median {np.median(cyc) / (args.mfma_clock * 16 * per_simd):.2f} "
+              f"(min {cyc.min() / (args.mfma_clock * 16 * per_simd):.2f}); clock "
+              f"{np.median(clk):.3f} GHz", flush=True)
+        return 0
     print(f"mfma clock: {args.groups} groups x {args.waves} waves, {args.lds_kib} KiB LDS, "
           f"rounds {args.mfma_clock}, random {args.random}: {us:.2f} us/launch, "
           f"{flops / us / 1e6:.1f} TFLOP/s; known MFMA cycles per wave {known}; "

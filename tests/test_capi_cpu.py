@@ -29,11 +29,13 @@ def test_library_loads_and_exports_header_symbols():
 
 
 def test_config_table():
-    assert capi.num_configs() == 6
-    names = [capi.config_name(i) for i in range(6)]
+    assert capi.num_configs() == 10
+    names = [capi.config_name(i) for i in range(10)]
     assert names == ["br32_bc64_w1", "br64_bc64_w2", "br128_bc64_w4_split2", "br256_bc64_w8_slot",
-                     "br128_bc64_w4_slot", "br256_kv256_w8_stream"]
-    assert capi.config_name(6) is None and capi.config_name(-1) is None
+                     "br128_bc64_w4_slot", "br256_kv256_w8_stream", "br256_bc64_w4_pair",
+                     "br128_bc64_w4x2_slot", "br256_bc64_w8_slot_exact",
+                     "br128_bc64_w4_slot_exact"]
+    assert capi.config_name(10) is None and capi.config_name(-1) is None
     assert capi.config_id("br256_bc64_w8_slot") == 3
 
 
