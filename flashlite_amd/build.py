@@ -40,7 +40,7 @@ DIAG_LIB_NAME = "libflashlite_diag.so"
 EXT_NAME = "flash_attn_wmma"
 
 HIP_SOURCES = ["fa2_fwd.hip", "fa2_pipe.hip", "fa2_slot.hip", "fa2_stream.hip", "fa2_d128.hip",
-               "fa2_pair.hip",                "naive_fwd.hip", "capi.hip"]
+               "naive_fwd.hip", "capi.hip"]
 DIAG_SOURCES = ["diag.hip"]
 
 # -packed-fp32-ops: keep the compiler from emitting v_pk_{add,mul,fma}_f32.

@@ -1,4 +1,4 @@
-// C-ABI entry points: argument checks, the sm_scale sentinel and prescale,
+// C-ABI entry points: argument checks, the sm_scale sentinel and log2 e factor,
 // the adaptive tile dispatcher, and the launch.
 //
 // Reference host entries: csrc/kernel_flash2.cu:732-839 (flash2) and
@@ -75,7 +75,6 @@ int check_common(const fl_attn_params* p, fl::FwdArgs* a, const char* who) {
   a->negate = scale < 0.0 ? 1 : 0;
   a->causal = p->causal ? 1 : 0;
   a->dtype = fl::kDtypeF16;
-  a->exact = 0;
   // contiguous [B, H, N, D]
   const int64_t d = p->head_dim;
   a->q_sr = a->o_sr = a->k_sr = a->v_sr = (int)d;

@@ -23,7 +23,7 @@
 // k-group g = l/32):
 //   GEMM1  S^T[key][query] = K . Q'^T - m   A = K rows from LDS
 //                                           (ds_read_b128), B = the wave's
-//                                           prescaled Q rows in VGPRs, C = -m.
+//                                           Q rows in VGPRs, C = -m.
 //     Each lane then owns ONE query (column l%32) and 16 of a 32-key block
 //     (rows 8*(r/4) + 4*g + r%4 of accumulator r); the other 16 sit in lane
 //     l^32.  A row max is 16 in-lane ops plus one v_permlane32_swap.
@@ -36,23 +36,25 @@
 // swapped via the tr-read addresses) so each lane ends with 8 contiguous
 // head-dim values per accumulator half: the epilogue stores 16-byte vectors.
 //
-// Softmax, at one exp per score.  The reference scales the fp32 scores by
-// sm_scale * log2 e (kernel_flash2.cu:188-195, :529-536; the factor is
-// computed at :772).  Here, for fp16 at head_dim 64, Q is instead prescaled
-// by c = |sm_scale| * log2 e and rounded to fp16 (when c <= 1), so GEMM1
-// returns base-2 logits with no per-score multiply; the running stabiliser
-// m enters as the MFMA accumulator's initial value, so GEMM1 returns
-// logit - m and p = v_exp_f32 of the accumulator.  m is the exact row max of
-// the first tile and later only moves when a tile would push p out of range
-// (a stale m is exact math since softmax is shift invariant; m never
-// exceeds the running max, so the row sum stays >= 1).  p is packed to fp16
-// for GEMM2.  Row sums: the reference sums the unrounded fp32 p
-// (kernel_flash2.cu:268-276, :339); the fp16 slot schedules sum the
-// fp16-rounded p that GEMM2 multiplies, with a packed-fp16 tree per tile
-// and fp32 across tiles, and bf16 tiles on the matrix core
-// (Rows::init_msum).  Each lane sums its own keys and the two halves of a
-// row meet once, in the epilogue.  When c > 1 (SCALED) Q keeps its scale
-// and the logits are multiplied by c instead, so |Q'| never exceeds |Q|.
+// Softmax, at one exp per score.  As in the reference, Q enters GEMM1
+// unscaled (only the sign of sm_scale is applied, exactly) and each fp32
+// score is multiplied by c = |sm_scale| * log2 e (kernel_flash2.cu:188-195,
+// :529-536; the factor is computed at :772) -- the SCALED template path,
+// one multiply per score.  (Prescaling Q by c instead and rounding it to
+// fp16 saves that multiply but measured 25% more mean error on full
+// outputs.)  The running stabiliser m (in unscaled score units) enters as
+// the MFMA accumulator's initial value, so GEMM1 returns s - m and
+// p = v_exp_f32(c * (s - m)).  m is the exact row max of the first tile and
+// later only moves when a tile would push p out of range (a stale m is
+// exact math since softmax is shift invariant; m never exceeds the running
+// max, so the row sum stays >= 1).  p is packed to fp16 for GEMM2.  Row
+// sums: the reference sums the unrounded fp32 p (kernel_flash2.cu:268-276,
+// :339); the fp16 slot schedules sum the fp16-rounded p that GEMM2
+// multiplies, with a packed-fp16 tree per tile and fp32 across tiles (the
+// same full-output errors as fp32 sums of the unrounded p, to three
+// digits), and bf16 tiles on the matrix core (Rows::init_msum).  Each lane
+// sums its own keys and the two halves of a row meet once, in the
+// epilogue.
 //
 // K/V staging.  Tiles are fetched straight into LDS with buffer_load ... lds
 // (no VGPRs, no LDS-store instructions; rows past N read as zeros through
@@ -330,7 +332,7 @@ __device__ __forceinline__ void fetch_tile(const i32x4_t& rs, const uint8_t* slo
   }
 }
 
-// The 32 query rows one wave owns: prescaled Q, running max, row sums and
+// The 32 query rows one wave owns: Q (sign of sm_scale applied), running max, row sums and
 // O accumulator, plus the tile-level building blocks.
 template <bool CAUSAL, bool SCALED, class T = _Float16>
 struct Rows {
@@ -952,24 +954,16 @@ __device__ __forceinline__ void sync_ring_ahead() {
 // Head dim of the wide kernels (fa2_d128.hip); the other kernels take 64.
 constexpr int kD2 = 128;
 
-// Q is prescaled by cq = +-min(c, 1) in the kernel; the remaining factor
-// cr = c / |cq| (1 unless c > 1) is applied to the scores.  The exact
-// configurations keep Q unscaled and scale every fp32 score by c, as the
-// reference does (kernel_flash2.cu:188-195).
-// bf16 and head_dim 128 keep Q exact (cq = +-1) and scale the fp32 scores
-// instead: a bf16 rounding of the prescaled Q would cost 2^-9 of every
-// score, and at D = 128 the fp16 rounding error of a score grows with
-// sqrt(D) past the fp16 output tolerance at large scales (2.3e-3 measured at
-// sm_scale -0.3), while one exponential per MFMA leaves the extra multiply
-// room under the matrix core.
+// Q enters the kernels unscaled: cq = +-1 carries the sign of sm_scale
+// (exact in any element type) and every fp32 score is multiplied by
+// cr = c = |sm_scale| * log2 e, as in the reference (kernel_flash2.cu:188-195).
+// Only c == 1 exactly skips the multiply (the SCALED = false instances).
 struct Scales {
   float cq, cr;
   bool scaled;
   explicit Scales(const FwdArgs& a) {
-    const float c = a.scale_log2;
-    const bool exact_q = a.dtype == kDtypeBF16 || a.head_dim == kD2 || a.exact != 0;
-    cq = (c <= 1.0f && !exact_q ? c : 1.0f) * (a.negate ? -1.0f : 1.0f);
-    cr = c <= 1.0f && !exact_q ? 1.0f : c;
+    cq = a.negate ? -1.0f : 1.0f;
+    cr = a.scale_log2;
     scaled = cr != 1.0f;
   }
 };

@@ -1,6 +1,6 @@
 // Tile configurations of the FA2 forward and their dispatch to the
 // schedule that implements each (fa2_pipe.hip, fa2_slot.hip, fa2_stream.hip,
-// fa2_d128.hip, fa2_pair.hip).  The dispatcher that picks a configuration for a problem is
+// fa2_d128.hip).  The dispatcher that picks a configuration for a problem is
 // capi.hip's select_fa2.
 
 #include "fl_internal.h"
@@ -10,14 +10,10 @@ namespace fl {
 const Fa2Config kFa2Configs[kNumFa2Configs] = {
     {1, "br32_bc64_w1"},
     {2, "br64_bc64_w2"},
-    {8, "br128_bc64_w4_split2"},
+    {8, "br128_bc64_w4x2_slot"},
     {8, "br256_bc64_w8_slot"},
     {4, "br128_bc64_w4_slot"},
     {8, "br256_kv256_w8_stream"},
-    {4, "br256_bc64_w4_pair"},
-    {8, "br128_bc64_w4x2_slot"},
-    {8, "br256_bc64_w8_slot_exact"},
-    {4, "br128_bc64_w4_slot_exact"},
 };
 
 bool stream_config_fits(const FwdArgs& a) {
@@ -39,15 +35,11 @@ hipError_t launch_fa2(const FwdArgs& a, int cfg, hipStream_t stream) {
   }
   switch (cfg) {
     case kCfgW1:
-    case kCfgW2:
-    case kCfgSplit2: return launch_pipe(a, cfg, stream);
+    case kCfgW2: return launch_pipe(a, cfg, stream);
+    case kCfgSplit2: return launch_slot_split(a, stream);
     case kSlotW8Config: return launch_slot(a, 8, stream);
     case kSlotW4Config: return launch_slot(a, 4, stream);
     case kStreamConfig: return launch_stream(a, stream);
-    case kPairConfig: return launch_pair(a, stream);
-    case kSlotSplitConfig: return launch_slot_split(a, stream);
-    case kSlotW8ExactConfig: return launch_slot_exact(a, 8, stream);
-    case kSlotW4ExactConfig: return launch_slot_exact(a, 4, stream);
     default: return hipErrorInvalidValue;
   }
 }

@@ -1,6 +1,6 @@
-// Pipelined schedule (configurations br32_bc64_w1, br64_bc64_w2 and
-// br128_bc64_w4_split2) and split-KV ("flash-decoding") with its combine
-// kernel.  Shared building blocks: fa2_common.h.
+// Pipelined schedule (configurations br32_bc64_w1 and br64_bc64_w2) and
+// split-KV ("flash-decoding") with its combine kernel.  Shared building
+// blocks: fa2_common.h.
 
 #include "fa2_common.h"
 
@@ -10,15 +10,11 @@ namespace {
 
 // ---------------------------------------------------------------------------
 // Pipelined schedule: W waves of 32 query rows, D = fetch distance in tiles.
-// SPLIT = 2 adds a second set of W waves for the same rows that walks the
-// second half of the key range with its own rings (waves w and w + W share
-// a SIMD); the halves are merged through LDS at the end.  That halves the
-// longest key walk, the critical path of causal attention's last q-blocks.
 // KVSPLIT ("split-KV", for few query rows over many keys): work-group i
 // takes key chunk i % nsplit of its query block and writes a partial result
 // (Rows::store_partial) that splitkv_combine_kernel merges.
-template <int W, int D, int SPLIT, bool CAUSAL, bool SCALED, bool KVSPLIT = false>
-__global__ void __launch_bounds__(64 * W * SPLIT, 2)  // 2 waves per SIMD: <= 256 VGPRs
+template <int W, int D, bool CAUSAL, bool SCALED, bool KVSPLIT = false>
+__global__ void __launch_bounds__(64 * W, 2)  // 2 waves per SIMD: <= 256 VGPRs
 fa2_fwd_kernel(const _Float16* Q, const _Float16* __restrict__ K,
                const _Float16* __restrict__ V, _Float16* O, const Geom geom, int nqb,
                float cq, float cr) {
@@ -27,18 +23,13 @@ fa2_fwd_kernel(const _Float16* Q, const _Float16* __restrict__ K,
   constexpr int kBr = 32 * W;
   constexpr int kSegs = 8 / W;            // 1 KiB DMA segments per wave per tile
   constexpr int kDmaPerIter = 2 * kSegs;  // K + V loads a wave issues per iteration
-  constexpr int kRingBytes = SPLIT * kSlots * kTileBytes;
+  constexpr int kRingBytes = kSlots * kTileBytes;
   static_assert(kSegs * W == 8, "tile split");
-  static_assert(SPLIT == 1 || SPLIT == 2, "key-range split");
-  static_assert(SPLIT == 1 || kRingBytes >= W * 34 * 64 * 4, "merge buffer");
   __shared__ __attribute__((aligned(16))) uint8_t kring[kRingBytes];
   __shared__ __attribute__((aligned(16))) uint8_t vring[kRingBytes];
 
   const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int stream = wave / W;       // key-range half
-  const int rw = wave - stream * W;  // 32-row block within the work-group
-  static_assert(!KVSPLIT || SPLIT == 1, "one split kind at a time");
+  const int rw = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // 32-row block
   int bh, qb, chunk = 0;
   if constexpr (KVSPLIT) {
     const int r = blockIdx.x / geom.nsplit;
@@ -46,7 +37,7 @@ fa2_fwd_kernel(const _Float16* Q, const _Float16* __restrict__ K,
     bh = r / nqb;
     qb = r - bh * nqb;
   } else {
-    wg_coords<CAUSAL, (W == 4 && SPLIT == 1) ? 2 : 1>(nqb, bh, qb);
+    wg_coords<CAUSAL, W == 4 ? 2 : 1>(nqb, bh, qb);
   }
   const HeadPtrs hp = head_ptrs(geom, bh, Q, K, V, O);
   const i32x4_t rk = hp.rk, rv = hp.rv;
@@ -54,8 +45,7 @@ fa2_fwd_kernel(const _Float16* Q, const _Float16* __restrict__ K,
   const FetchOff<kSegs> fv = fetch_offsets<kSegs, true>(rw, lane, 2 * geom.v_sr);
   const int seq = geom.seq_q;
   const int q0 = qb * kBr;
-  const StreamRings<kSlots> rings = {kring + stream * (kSlots * kTileBytes),
-                                     vring + stream * (kSlots * kTileBytes)};
+  const StreamRings<kSlots> rings = {kring, vring};
 
   Rows<CAUSAL, SCALED> rows;
   rows.init(hp.q, geom.q_sr, lane, q0 + 32 * rw, seq, geom.seq_k, geom.coff, cq, cr);
@@ -78,14 +68,11 @@ fa2_fwd_kernel(const _Float16* Q, const _Float16* __restrict__ K,
       return;
     }
   }
-  // Key tiles [tbeg, tend) of this stream; both streams run t0 + 1
-  // iterations (the same barriers), the shorter one on masked tiles.
-  constexpr bool kSplit = SPLIT == 2;
-  const int t0 = kSplit ? (ntiles + 1) / 2 : ntiles;
-  const int tbeg = cbeg + (stream == 0 ? 0 : t0);
-  const int tend = cbeg + (stream == 0 ? t0 : ntiles);
+  // Key tiles [tbeg, tend): t0 + 1 iterations.
+  const int t0 = ntiles;
+  const int tbeg = cbeg;
+  const int tend = cbeg + ntiles;
   const int last = max(tend - 1, tbeg);  // fetch clamp
-  if (kSplit && stream == 0) rows.kv_lim = min(rows.kv_lim, tend * kBc);
 
   // Iteration j (position I of the unrolled loop), for j = 0 .. t0, on key
   // tile t = tbeg + j: fetch K(t+D+1) and V(t+D-1) into the slots of K(t)
@@ -140,7 +127,7 @@ fa2_fwd_kernel(const _Float16* Q, const _Float16* __restrict__ K,
     // 1-D .. -1 in flight; S(tbeg) with the exact row max.
     {
       const u32x4_t z = {0, 0, 0, 0};
-      for (int off = 16 * (int)threadIdx.x; off < kRingBytes; off += 16 * 64 * W * SPLIT)
+      for (int off = 16 * (int)threadIdx.x; off < kRingBytes; off += 16 * 64 * W)
         *reinterpret_cast<u32x4_t*>(vring + off) = z;
       __syncthreads();
     }
@@ -209,17 +196,8 @@ fa2_fwd_kernel(const _Float16* Q, const _Float16* __restrict__ K,
     }
   }
 
-  // No fetch may still be writing LDS when the work-group retires or the
-  // rings are reused for the merge.
+  // No fetch may still be writing LDS when the work-group retires.
   __builtin_amdgcn_s_waitcnt(0);
-  if constexpr (SPLIT == 2) {
-    __syncthreads();
-    float* xchg = reinterpret_cast<float*>(kring) + rw * (34 * 64);
-    if (stream == 1) rows.save_partial(xchg, lane);
-    __syncthreads();
-    if (stream == 1) return;
-    rows.merge_partial(xchg, lane);
-  }
   if constexpr (KVSPLIT)
     rows.store_partial(part);
   else
@@ -265,13 +243,13 @@ splitkv_combine_kernel(_Float16* O, const Geom geom) {
         lsum > 0.0f ? 0.693147180559945309f * (mx + __builtin_amdgcn_logf(lsum)) : ninf();
 }
 
-template <int W, int D, int SPLIT>
+template <int W, int D>
 struct PipelinedLaunch {
   template <bool C, bool S>
   struct L {
     static hipError_t run(const FwdArgs& a, const Geom& g, dim3 grid, int nqb, float cq, float cr,
                           hipStream_t st) {
-      hipLaunchKernelGGL((fa2_fwd_kernel<W, D, SPLIT, C, S>), grid, dim3(64 * W * SPLIT), 0, st,
+      hipLaunchKernelGGL((fa2_fwd_kernel<W, D, C, S>), grid, dim3(64 * W), 0, st,
                          static_cast<const _Float16*>(a.q), static_cast<const _Float16*>(a.k),
                          static_cast<const _Float16*>(a.v), static_cast<_Float16*>(a.o), g, nqb,
                          cq, cr);
@@ -297,14 +275,14 @@ hipError_t launch_kvsplit_w(const FwdArgs& a, float* part, int nsplit, hipStream
   _Float16* o = static_cast<_Float16*>(a.o);
   if (a.causal) {
     if (sc.scaled)
-      hipLaunchKernelGGL((fa2_fwd_kernel<W, D, 1, true, true, true>), grid, block, 0, st, q, k, v, o, g, nqb, sc.cq, sc.cr);
+      hipLaunchKernelGGL((fa2_fwd_kernel<W, D, true, true, true>), grid, block, 0, st, q, k, v, o, g, nqb, sc.cq, sc.cr);
     else
-      hipLaunchKernelGGL((fa2_fwd_kernel<W, D, 1, true, false, true>), grid, block, 0, st, q, k, v, o, g, nqb, sc.cq, sc.cr);
+      hipLaunchKernelGGL((fa2_fwd_kernel<W, D, true, false, true>), grid, block, 0, st, q, k, v, o, g, nqb, sc.cq, sc.cr);
   } else {
     if (sc.scaled)
-      hipLaunchKernelGGL((fa2_fwd_kernel<W, D, 1, false, true, true>), grid, block, 0, st, q, k, v, o, g, nqb, sc.cq, sc.cr);
+      hipLaunchKernelGGL((fa2_fwd_kernel<W, D, false, true, true>), grid, block, 0, st, q, k, v, o, g, nqb, sc.cq, sc.cr);
     else
-      hipLaunchKernelGGL((fa2_fwd_kernel<W, D, 1, false, false, true>), grid, block, 0, st, q, k, v, o, g, nqb, sc.cq, sc.cr);
+      hipLaunchKernelGGL((fa2_fwd_kernel<W, D, false, false, true>), grid, block, 0, st, q, k, v, o, g, nqb, sc.cq, sc.cr);
   }
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
@@ -318,9 +296,8 @@ hipError_t launch_kvsplit_w(const FwdArgs& a, float* part, int nsplit, hipStream
 
 hipError_t launch_pipe(const FwdArgs& a, int cfg, hipStream_t stream) {
   switch (cfg) {
-    case kCfgW1: return dispatch<PipelinedLaunch<1, 1, 1>::L>(a, stream, 32);
-    case kCfgW2: return dispatch<PipelinedLaunch<2, 3, 1>::L>(a, stream, 64);
-    case kCfgSplit2: return dispatch<PipelinedLaunch<4, 3, 2>::L>(a, stream, 128);
+    case kCfgW1: return dispatch<PipelinedLaunch<1, 1>::L>(a, stream, 32);
+    case kCfgW2: return dispatch<PipelinedLaunch<2, 3>::L>(a, stream, 64);
     default: return hipErrorInvalidValue;
   }
 }

@@ -50,13 +50,7 @@ namespace {
 // meets the same barriers.  This halves the longest key walk: a causal
 // work-group's time follows half its tiles, and heaviest-first dispatch of
 // one work-group per CU then balances the CUs.
-//
-// EXACT (the *_exact configurations): the reference's arithmetic on every
-// tile -- Q unscaled (SCALED, the fp32 scores multiplied by sm_scale * log2 e)
-// and fp32 row sums of the unrounded p (Rows::sum_slot_f32), one multiply
-// per score and one more add per pair than the default.
-template <int W, int FV, bool CAUSAL, bool SCALED, class T = _Float16, int SPLIT = 1,
-          bool EXACT = false>
+template <int W, int FV, bool CAUSAL, bool SCALED, class T = _Float16, int SPLIT = 1>
 __global__ void __launch_bounds__(64 * W * SPLIT, 2)  // <= 256 VGPRs: 2 waves per SIMD
 fa2_fwd_slot_kernel(const T* Q, const T* __restrict__ K, const T* __restrict__ V, T* O,
                     const Geom geom, int nqb, float cq, float cr) {
@@ -65,9 +59,8 @@ fa2_fwd_slot_kernel(const T* Q, const T* __restrict__ K, const T* __restrict__ V
   // fp16: unmasked tiles sum P with the packed-fp16 tree; bf16 P keeps
   // fp32 sums throughout (an 8-bit mantissa tree would cost accuracy).
   constexpr bool kFp16 = __is_same(T, _Float16);
-  // The packed-fp16 row-sum tree on unmasked tiles (fp16 unless EXACT).
-  constexpr bool kTree = kFp16 && !EXACT;
-  static_assert(!EXACT || kFp16, "the exact variant is built for fp16");
+  // The packed-fp16 row-sum tree on unmasked tiles (fp16).
+  constexpr bool kTree = kFp16;
   // bf16: row sums on the matrix core (Rows::init_msum), four 16x16x32 MFMAs
   // per tile in place of 32 fp32 adds, measured 4-7% faster on B2 H8 N4096.
   // For fp16 the packed tree's 15 adds cost less than the MFMAs (3% the
@@ -298,13 +291,13 @@ fa2_fwd_slot_kernel(const T* Q, const T* __restrict__ K, const T* __restrict__ V
   rows.store(hp.o, geom.o_sr, hp.lse);
 }
 
-template <int W, int FV, class T = _Float16, int SPLIT = 1, bool EXACT = false>
+template <int W, int FV, class T = _Float16, int SPLIT = 1>
 struct SlotLaunch {
   template <bool C, bool S>
   struct L {
     static hipError_t run(const FwdArgs& a, const Geom& g, dim3 grid, int nqb, float cq, float cr,
                           hipStream_t st) {
-      hipLaunchKernelGGL((fa2_fwd_slot_kernel<W, FV, C, S, T, SPLIT, EXACT>), grid, dim3(64 * W * SPLIT),
+      hipLaunchKernelGGL((fa2_fwd_slot_kernel<W, FV, C, S, T, SPLIT>), grid, dim3(64 * W * SPLIT),
                          0, st,
                          static_cast<const T*>(a.q), static_cast<const T*>(a.k),
                          static_cast<const T*>(a.v), static_cast<T*>(a.o), g, nqb, cq, cr);
@@ -325,16 +318,6 @@ hipError_t launch_slot(const FwdArgs& a, int waves, hipStream_t stream) {
   if (waves == 4)
     return bf ? dispatch<SlotLaunch<4, 3, __bf16>::L>(a, stream, 128)
               : dispatch<SlotLaunch<4, 3>::L>(a, stream, 128);
-  return hipErrorInvalidValue;
-}
-
-// fp16 with the reference's arithmetic (FwdArgs::exact): W = 8 or 4.
-hipError_t launch_slot_exact(const FwdArgs& a, int waves, hipStream_t stream) {
-  if (a.dtype != kDtypeF16) return hipErrorInvalidValue;
-  FwdArgs e = a;
-  e.exact = 1;
-  if (waves == 8) return dispatch<SlotLaunch<8, 4, _Float16, 1, true>::L>(e, stream, 256);
-  if (waves == 4) return dispatch<SlotLaunch<4, 3, _Float16, 1, true>::L>(e, stream, 128);
   return hipErrorInvalidValue;
 }
 

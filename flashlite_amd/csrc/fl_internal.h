@@ -27,8 +27,6 @@ struct FwdArgs {
   int negate;        // 1 when sm_scale < 0: the kernel flips the sign of Q
   int causal;        // key j visible to query i iff j <= i + (N_k - N_q)
   int dtype;         // element type of q, k, v, o: kDtypeF16 or kDtypeBF16
-  int exact;         // 1: the reference's arithmetic (unscaled Q, fp32-scaled scores,
-                     // fp32 row sums of the unrounded p); set by the *_exact configurations
   int64_t q_sb, q_sh, k_sb, k_sh, v_sb, v_sh, o_sb, o_sh;  // batch / head strides
   int q_sr, k_sr, v_sr, o_sr;                              // row strides
 };
@@ -46,19 +44,14 @@ struct Fa2Config {
 // Configuration ids (indices into kFa2Configs).
 constexpr int kCfgW1 = 0;          // br32_bc64_w1: pipelined, 1 wave
 constexpr int kCfgW2 = 1;          // br64_bc64_w2: pipelined, 2 waves
-constexpr int kCfgSplit2 = 2;      // br128_bc64_w4_split2: 2 x 4 waves, key range halved
+constexpr int kCfgSplit2 = 2;      // br128_bc64_w4x2_slot: 2 x 4 waves, key range halved
 constexpr int kSlotW8Config = 3;   // br256_bc64_w8_slot
 constexpr int kSlotW4Config = 4;   // br128_bc64_w4_slot
 // Persistent work-groups streaming whole units of 256 query rows whose keys
 // fit one LDS buffer: needs N_k <= kStreamMaxKeys and row strides below
 // kStreamMaxRowStride elements (unit-relative 32-bit buffer offsets).
 constexpr int kStreamConfig = 5;   // br256_kv256_w8_stream
-constexpr int kPairConfig = 6;     // br256_bc64_w4_pair: 4 waves of 64 rows
-constexpr int kSlotSplitConfig = 7;  // br128_bc64_w4x2_slot: 2 x 4 waves, key range halved
-// The slot configurations with the reference's arithmetic (FwdArgs::exact).
-constexpr int kSlotW8ExactConfig = 8;  // br256_bc64_w8_slot_exact
-constexpr int kSlotW4ExactConfig = 9;  // br128_bc64_w4_slot_exact
-constexpr int kNumFa2Configs = 10;
+constexpr int kNumFa2Configs = 6;
 extern const Fa2Config kFa2Configs[kNumFa2Configs];
 
 // Launches the FA2 kernel for configuration `cfg` on `stream`.  fp16 at
@@ -73,10 +66,8 @@ bool stream_config_fits(const FwdArgs& a);
 hipError_t launch_pipe(const FwdArgs& a, int cfg, hipStream_t stream);     // fa2_pipe.hip
 hipError_t launch_slot(const FwdArgs& a, int waves, hipStream_t stream);   // fa2_slot.hip
 hipError_t launch_slot_split(const FwdArgs& a, hipStream_t stream);        // fa2_slot.hip
-hipError_t launch_slot_exact(const FwdArgs& a, int waves, hipStream_t stream);  // fa2_slot.hip
 hipError_t launch_stream(const FwdArgs& a, hipStream_t stream);            // fa2_stream.hip
 hipError_t launch_d128(const FwdArgs& a, int waves, hipStream_t stream);   // fa2_d128.hip
-hipError_t launch_pair(const FwdArgs& a, hipStream_t stream);              // fa2_pair.hip
 
 // Split-KV ("flash-decoding"): `waves` (1, 2 or 4) waves of 32 query rows
 // per work-group, the key range cut into `nsplit` chunks whose partial

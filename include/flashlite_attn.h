@@ -95,9 +95,9 @@ int fl_attn_fwd_f16_cfg(const fl_attn_params* p, int32_t config, void* stream);
  * ln(sum_j exp(sm_scale * q.k_j)) over its visible keys, -inf for a row
  * with no visible key; NULL to skip.
  *
- * head_dim is 64 or 128.  At 128, Q enters the MFMA unscaled and the fp32
- * scores are scaled by sm_scale*log2(e) (at 64, Q is prescaled in fp16 as in
- * the reference, csrc/kernel_flash2.cu:772).  At 64, `config` is as for
+ * head_dim is 64 or 128.  At both, Q enters the MFMA unscaled and the fp32
+ * scores are scaled by sm_scale*log2(e), as in the reference
+ * (csrc/kernel_flash2.cu:188-195).  At 64, `config` is as for
  * fl_attn_fwd_f16_cfg;
  * at 128 it is -1 or one of the two slot-scheduled configurations
  * (6 "br256_bc64_w8_slot", 7 "br128_bc64_w4_slot"; same work-group shapes,

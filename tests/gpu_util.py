@@ -14,10 +14,8 @@ MEAN_ABS = 2e-4
 # of at most 256 keys only.
 SLOT_W8_CFG = capi.config_id("br256_bc64_w8_slot")
 SLOT_W4_CFG = capi.config_id("br128_bc64_w4_slot")
-SPLIT2_CFG = capi.config_id("br128_bc64_w4_split2")
+SPLIT2_CFG = capi.config_id("br128_bc64_w4x2_slot")
 STREAM_CFG = capi.config_id("br256_kv256_w8_stream")
-PAIR_CFG = capi.config_id("br256_bc64_w4_pair")
-SLOT_SPLIT_CFG = capi.config_id("br128_bc64_w4x2_slot")
 STREAM_MAX_KEYS = 256
 
 

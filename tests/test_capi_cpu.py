@@ -29,13 +29,11 @@ def test_library_loads_and_exports_header_symbols():
 
 
 def test_config_table():
-    assert capi.num_configs() == 10
-    names = [capi.config_name(i) for i in range(10)]
-    assert names == ["br32_bc64_w1", "br64_bc64_w2", "br128_bc64_w4_split2", "br256_bc64_w8_slot",
-                     "br128_bc64_w4_slot", "br256_kv256_w8_stream", "br256_bc64_w4_pair",
-                     "br128_bc64_w4x2_slot", "br256_bc64_w8_slot_exact",
-                     "br128_bc64_w4_slot_exact"]
-    assert capi.config_name(10) is None and capi.config_name(-1) is None
+    assert capi.num_configs() == 6
+    names = [capi.config_name(i) for i in range(6)]
+    assert names == ["br32_bc64_w1", "br64_bc64_w2", "br128_bc64_w4x2_slot", "br256_bc64_w8_slot",
+                     "br128_bc64_w4_slot", "br256_kv256_w8_stream"]
+    assert capi.config_name(6) is None and capi.config_name(-1) is None
     assert capi.config_id("br256_bc64_w8_slot") == 3
 
 
@@ -166,7 +164,7 @@ def test_naive_limits():
 
 def test_dispatcher_choices():
     sel = lambda **kw: capi.config_name(capi.select_config(_p(**kw)))  # noqa: E731
-    W8, W4, SPLIT, STRM = ("br256_bc64_w8_slot", "br128_bc64_w4_slot", "br128_bc64_w4_split2",
+    W8, W4, SPLIT, STRM = ("br256_bc64_w8_slot", "br128_bc64_w4_slot", "br128_bc64_w4x2_slot",
                            "br256_kv256_w8_stream")
     W1, W2 = "br32_bc64_w1", "br64_bc64_w2"
     # non-causal: 8-wave 256-row slot-scheduled groups when there is one per CU

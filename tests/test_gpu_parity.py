@@ -12,23 +12,22 @@ import pytest
 
 from flashlite_amd import capi
 from flashlite_amd.workloads import WORKLOADS, make_qkv, workload_inputs
-from gpu_util import (PAIR_CFG, SLOT_SPLIT_CFG, SLOT_W4_CFG, SLOT_W8_CFG, SPLIT2_CFG, assert_close_oracle, config_fits,
+from gpu_util import (SLOT_W4_CFG, SLOT_W8_CFG, SPLIT2_CFG, assert_close_oracle, config_fits,
                       redo_expected, run_capi, sample_rows, to_dev)
 from oracle import error_stats
 
 pytestmark = pytest.mark.gpu
 
 GOLDEN = os.path.join(os.path.dirname(__file__), "golden")
-NCFG = 10  # tile configurations exported by the library
-SPLIT_CFGS = [SPLIT2_CFG, SLOT_SPLIT_CFG]  # the key-range-split configurations
+NCFG = 6  # tile configurations exported by the library
+SPLIT_CFGS = [SPLIT2_CFG]  # the key-range-split configuration
 
 
 def test_num_configs():
     assert capi.num_configs() == NCFG
     assert [capi.config_name(i) for i in range(NCFG)] == [
-        "br32_bc64_w1", "br64_bc64_w2", "br128_bc64_w4_split2", "br256_bc64_w8_slot",
-        "br128_bc64_w4_slot", "br256_kv256_w8_stream", "br256_bc64_w4_pair",
-        "br128_bc64_w4x2_slot", "br256_bc64_w8_slot_exact", "br128_bc64_w4_slot_exact"]
+        "br32_bc64_w1", "br64_bc64_w2", "br128_bc64_w4x2_slot", "br256_bc64_w8_slot",
+        "br128_bc64_w4_slot", "br256_kv256_w8_stream"]
 
 
 @pytest.mark.parametrize("config", list(range(NCFG)))
@@ -52,7 +51,7 @@ def test_benchmark_configs(cuda, name, causal):
     print(f"{name} causal={causal}: max-abs {mx:.2e} mean-abs {mean:.2e}")
 
 
-@pytest.mark.parametrize("config", [SLOT_W8_CFG, SLOT_W4_CFG, PAIR_CFG] + SPLIT_CFGS)
+@pytest.mark.parametrize("config", [SLOT_W8_CFG, SLOT_W4_CFG] + SPLIT_CFGS)
 @pytest.mark.parametrize("causal", [False, True])
 def test_headline_each_config(cuda, config, causal):
     w = WORKLOADS["C2_headline_B2H8N4096"]

@@ -5,10 +5,9 @@ log-sum-exp output.
 
 Output tolerance as everywhere (north_star): max-abs <= 2e-3, mean-abs <=
 2e-4 against the fp32 oracle.  The log-sum-exp is compared with the fp64
-oracle at max-abs <= 2e-3 and mean-abs <= 3e-4 (natural-log units): the
-kernel forms scores from Q prescaled by sm_scale*log2(e) and rounded to fp16,
-an error of about 2^-12 relative per element that moves a score by ~1e-4 to
-1e-3 at these magnitudes.  A strided launch must equal the contiguous launch
+oracle at max-abs <= 2e-3 and mean-abs <= 3e-4 (natural-log units): l sums
+the fp16-rounded p (2^-12 relative each), which moves ln l by up to ~1e-3 on
+rows that see few keys.  A strided launch must equal the contiguous launch
 of the same data bit for bit: the kernels read the same values in the same
 order.
 """

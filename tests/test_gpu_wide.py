@@ -12,10 +12,9 @@ Tolerances against the fp32 oracle on the same inputs:
   rounded to bf16 before the PV product.  The inputs are bf16-exact values
   (``workloads.round_bf16``), so the oracle sees exactly what the kernel reads.
 * log-sum-exp (natural-log units): max-abs <= 2e-3 for both types; mean-abs
-  <= 3e-4 for fp16 and 1e-3 for bf16.  bf16 and head_dim 128 keep Q unscaled
-  and scale the fp32 scores, so their scores are closer to the oracle's than
-  the D = 64 fp16 path's prescaled ones; but at D = 64 the bf16 row sum l is
-  taken on the matrix core over the bf16-rounded p that weight V (relative
+  <= 3e-4 for fp16 and 1e-3 for bf16.  Every path keeps Q unscaled and
+  scales the fp32 scores, as the reference does; but at D = 64 the bf16 row
+  sum l is taken on the matrix core over the bf16-rounded p that weight V (relative
   error up to 2^-9 = 1.95e-3 each, about 2^-10 on average), so ln l carries
   about 1e-3 on rows that see few keys.
 A strided launch equals the contiguous launch of the same data bit for bit.
