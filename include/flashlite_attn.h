@@ -72,7 +72,7 @@ int fl_attn_fwd_f16(const fl_attn_params* p, void* stream);
  * [0, fl_attn_num_configs()), or -1 for the dispatcher's choice).  Replaces
  * the reference's two hard-wired launch branches (Br=64 / Br=128,
  * csrc/kernel_flash2.cu:789-835); used by sweeps and by tests that check
- * every configuration against the oracle.  Configuration 8
+ * every configuration against the oracle.  Configuration 5
  * (br256_kv256_w8_stream) takes N_k <= 256 only and returns
  * FL_ERR_BAD_CONFIG otherwise.
  */
@@ -100,7 +100,7 @@ int fl_attn_fwd_f16_cfg(const fl_attn_params* p, int32_t config, void* stream);
  * (csrc/kernel_flash2.cu:188-195).  At 64, `config` is as for
  * fl_attn_fwd_f16_cfg;
  * at 128 it is -1 or one of the two slot-scheduled configurations
- * (6 "br256_bc64_w8_slot", 7 "br128_bc64_w4_slot"; same work-group shapes,
+ * (3 "br256_bc64_w8_slot", 4 "br128_bc64_w4_slot"; same work-group shapes,
  * 32-key tiles), FL_ERR_BAD_CONFIG otherwise.
  *
  * No counterpart in the reference, which accepts only contiguous
@@ -120,7 +120,7 @@ int fl_attn_fwd_f16_ex(const fl_attn_params_ex* p, int32_t config, void* stream)
 
 /*
  * bf16 q, k, v and o (same layouts, strides, lse and head_dims as
- * fl_attn_fwd_f16_ex; `config` -1, 6 or 7).  Q enters the MFMA unscaled and
+ * fl_attn_fwd_f16_ex; `config` -1, 3 or 4).  Q enters the MFMA unscaled and
  * the fp32 scores are scaled by sm_scale*log2(e); P is rounded to bf16
  * before the PV product and the row sums are fp32.
  *
