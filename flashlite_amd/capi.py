@@ -33,7 +33,10 @@ EXPORTED = (
     "fl_attn_fwd_bf16_ex",
     "fl_attn_splitkv_workspace_bytes",
     "fl_attn_fwd_f16_splitkv",
+    "fl_attn_fwd_f16_splitkv_noalloc",
 )
+
+SCRATCH_BYTES = 8 << 20  # FL_ATTN_SCRATCH_BYTES
 
 
 class FlAttnParams(ctypes.Structure):
@@ -110,6 +113,9 @@ def load(path: str = LIB_PATH) -> ctypes.CDLL:
     lib.fl_attn_fwd_f16_splitkv.argtypes = [ctypes.POINTER(FlAttnParamsEx), ctypes.c_int32,
                                             ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p]
     lib.fl_attn_fwd_f16_splitkv.restype = ctypes.c_int
+    lib.fl_attn_fwd_f16_splitkv_noalloc.argtypes = [ctypes.POINTER(FlAttnParamsEx), ctypes.c_int32,
+                                                    ctypes.c_void_p]
+    lib.fl_attn_fwd_f16_splitkv_noalloc.restype = ctypes.c_int
     _lib = lib
     return lib
 
@@ -157,6 +163,12 @@ def fwd_splitkv(params: FlAttnParamsEx, workspace: int, workspace_bytes: int, st
     """``fl_attn_fwd_f16_splitkv``; returns the status code."""
     return load().fl_attn_fwd_f16_splitkv(ctypes.byref(params), num_splits, workspace or None,
                                           workspace_bytes, stream or None)
+
+
+def fwd_splitkv_noalloc(params: FlAttnParamsEx, stream: int = 0, num_splits: int = 0) -> int:
+    """``fl_attn_fwd_f16_splitkv_noalloc`` (partials in the library's scratch
+    array); returns the status code."""
+    return load().fl_attn_fwd_f16_splitkv_noalloc(ctypes.byref(params), num_splits, stream or None)
 
 
 def make_params_ex(base: FlAttnParams, q_stride, k_stride, v_stride, o_stride,

@@ -16,6 +16,7 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstdint>
+#include <mutex>
 
 #include "fl_internal.h"
 #include "flashlite_attn.h"
@@ -286,6 +287,43 @@ int fwd_ex(const fl_attn_params_ex* p, int32_t config, void* stream, int dtype, 
 
 }  // namespace
 
+// Allocation-free split-KV.  The partials live in a file-scope device
+// array; every GPU the library runs on holds its own copy, so its address
+// is looked up once per device (with that device current) and cached.  In
+// host code the array's name is only a stand-in for the symbol: the kernels
+// get the looked-up address, never the name.
+static __device__ __align__(256) float scratch[FL_ATTN_SCRATCH_BYTES / sizeof(float)];
+static_assert(FL_ATTN_SCRATCH_BYTES % 256 == 0, "scratch size");
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+int scratch_for_current_device(void** out, const char* who) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess)
+    return fail(FL_ERR_LAUNCH, "%s: hipGetDevice failed: %s", who, hipGetErrorString(e));
+  if (dev < 0 || dev >= kMaxDevices)
+    return fail(FL_ERR_UNSUPPORTED, "%s: device %d beyond the %d the scratch table covers", who,
+                dev, kMaxDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* ptr = nullptr;
+    e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || ptr == nullptr)
+      return fail(FL_ERR_LAUNCH, "%s: hipGetSymbolAddress(scratch) failed on device %d: %s", who,
+                  dev, hipGetErrorString(e));
+    g_scratch_ptr[dev] = ptr;
+  }
+  *out = g_scratch_ptr[dev];
+  return FL_OK;
+}
+
+}  // namespace
+
 extern "C" {
 
 const char* fl_attn_last_error(void) { return g_err; }
@@ -363,6 +401,33 @@ int fl_attn_fwd_f16_splitkv(const fl_attn_params_ex* p, int32_t num_splits, void
     if ((uintptr_t)workspace & 15)
       return fail(FL_ERR_MISALIGNED, "%s: workspace must be 16-byte aligned", who);
     e = fl::launch_kvsplit(a, plan.waves, static_cast<float*>(workspace), plan.nsplit,
+                           static_cast<hipStream_t>(stream));
+  }
+  if (e != hipSuccess) return fail(FL_ERR_LAUNCH, "%s: launch failed: %s", who, hipGetErrorString(e));
+  return FL_OK;
+}
+
+int fl_attn_fwd_f16_splitkv_noalloc(const fl_attn_params_ex* p, int32_t num_splits, void* stream) {
+  const char* who = "fl_attn_fwd_f16_splitkv_noalloc";
+  fl::FwdArgs a;
+  int rc = check_ex(p, &a, who);
+  if (rc != FL_OK) return rc;
+  if (empty_problem(a)) return FL_OK;
+  rc = check_pointers(&p->base, &a, who, 16);
+  if (rc != FL_OK) return rc;
+  const KvPlan plan = plan_kvsplit(a, num_splits);
+  if (plan.nsplit != 0 && plan.bytes > (int64_t)FL_ATTN_SCRATCH_BYTES)
+    return fail(FL_ERR_UNSUPPORTED, "%s: %d key chunks need %lld bytes of scratch, above the "
+                "%lld-byte limit (use fl_attn_fwd_f16_splitkv with a workspace)", who, plan.nsplit,
+                (long long)plan.bytes, (long long)FL_ATTN_SCRATCH_BYTES);
+  hipError_t e;
+  if (plan.nsplit == 0) {
+    e = fl::launch_fa2(a, select_fa2(a), static_cast<hipStream_t>(stream));
+  } else {
+    void* s = nullptr;
+    rc = scratch_for_current_device(&s, who);
+    if (rc != FL_OK) return rc;
+    e = fl::launch_kvsplit(a, plan.waves, static_cast<float*>(s), plan.nsplit,
                            static_cast<hipStream_t>(stream));
   }
   if (e != hipSuccess) return fail(FL_ERR_LAUNCH, "%s: launch failed: %s", who, hipGetErrorString(e));

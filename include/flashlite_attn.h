@@ -19,7 +19,9 @@
  * [batch, heads, seq_k, head_dim], contiguous (fl_attn_fwd_f16_ex takes
  * strides).
  * The library allocates nothing, never synchronises, keeps no mutable global
- * state and may be called from several host threads at once.  Launches are
+ * state (beyond, per GPU, the cached address of the scratch array of
+ * fl_attn_fwd_f16_splitkv_noalloc) and may be called from several host
+ * threads at once.  Launches are
  * asynchronous on `stream`; results are visible after the stream reaches
  * them.  `o` may alias `q` (each work-group reads its own query rows before
  * it writes them); it must not alias `k` or `v`.
@@ -154,6 +156,27 @@ int fl_attn_fwd_bf16_ex(const fl_attn_params_ex* p, int32_t config, void* stream
 int64_t fl_attn_splitkv_workspace_bytes(const fl_attn_params_ex* p, int32_t num_splits);
 int fl_attn_fwd_f16_splitkv(const fl_attn_params_ex* p, int32_t num_splits, void* workspace,
                             int64_t workspace_bytes, void* stream);
+
+/*
+ * fl_attn_fwd_f16_splitkv without a workspace argument and without any
+ * allocation: the partial results go to a scratch array of
+ * FL_ATTN_SCRATCH_BYTES (8 MiB) that the library holds in device memory on
+ * every GPU it runs on, until the process ends.  Same parameters, plan
+ * (num_splits as for fl_attn_fwd_f16_splitkv) and results, bit for bit.
+ * A plan that needs more scratch than the limit (see
+ * fl_attn_splitkv_workspace_bytes) returns FL_ERR_UNSUPPORTED and launches
+ * nothing; a plan with no split runs the one-pass kernel.  Launches on the
+ * current device, into `stream`, which must belong to it.  Every call on a
+ * GPU shares that GPU's array (each call writes every partial it reads, so
+ * nothing has to start at zero): calls that may overlap on one GPU -- other
+ * streams, other host threads -- race and must be serialised by the caller.
+ *
+ * No counterpart in the reference.  For callers that cannot allocate device
+ * memory: code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc.
+ */
+#define FL_ATTN_SCRATCH_BYTES (8 << 20)
+int fl_attn_fwd_f16_splitkv_noalloc(const fl_attn_params_ex* p, int32_t num_splits, void* stream);
 
 /*
  * Un-fused baseline: one work-group per query row, scores staged in LDS.
