@@ -41,7 +41,7 @@ EXT_NAME = "flash_attn_wmma"
 
 HIP_SOURCES = ["fa2_fwd.hip", "fa2_pipe.hip", "fa2_slot.hip", "fa2_stream.hip", "fa2_d128.hip",
                "naive_fwd.hip", "capi.hip"]
-DIAG_SOURCES = ["diag.hip"]
+DIAG_SOURCES = ["diag.hip", "diag_timeline.hip"]
 
 # -packed-fp32-ops: keep the compiler from emitting v_pk_{add,mul,fma}_f32.
 HIP_FLAGS = [
@@ -70,8 +70,11 @@ def ext_path() -> str:
     return os.path.join(PKG_DIR, EXT_NAME + sysconfig.get_config_var("EXT_SUFFIX"))
 
 
-def _build_shared(sources, out: str, verbose: bool) -> str:
-    """Compiles each source to an object in parallel, then links them."""
+def _build_shared(sources, out: str, verbose: bool, exports: str) -> str:
+    """Compiles each source to an object in parallel, then links them,
+    exporting only the C symbols that match `exports` (the internal C++
+    launchers stay local, so two of these libraries in one process never
+    resolve each other's)."""
     hipcc = os.path.join(ROCM, "bin", "hipcc")
     with tempfile.TemporaryDirectory(prefix="flashlite_build_") as tmpdir:
         objs = [os.path.join(tmpdir, os.path.splitext(s)[0] + ".o") for s in sources]
@@ -81,7 +84,11 @@ def _build_shared(sources, out: str, verbose: bool) -> str:
         with ThreadPoolExecutor(max_workers=workers) as pool:
             logs = list(pool.map(_run, cmds))
         tmp = out + ".tmp"
-        logs.append(_run([hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", tmp]))
+        script = os.path.join(tmpdir, "exports.map")
+        with open(script, "w") as f:
+            f.write("{ global: %s; local: *; };\n" % exports)
+        logs.append(_run([hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs,
+                          f"-Wl,--version-script={script}", "-o", tmp]))
     if verbose:
         for log in logs:
             if log.strip():
@@ -91,11 +98,11 @@ def _build_shared(sources, out: str, verbose: bool) -> str:
 
 
 def build_library(verbose: bool = False) -> str:
-    return _build_shared(HIP_SOURCES, lib_path(), verbose)
+    return _build_shared(HIP_SOURCES, lib_path(), verbose, "fl_attn_*")
 
 
 def build_diag_library(verbose: bool = False) -> str:
-    return _build_shared(DIAG_SOURCES, os.path.join(PKG_DIR, DIAG_LIB_NAME), verbose)
+    return _build_shared(DIAG_SOURCES, os.path.join(PKG_DIR, DIAG_LIB_NAME), verbose, "fl_diag_*")
 
 
 def build_extension(verbose: bool = False) -> str:

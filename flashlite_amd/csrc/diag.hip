@@ -169,9 +169,20 @@ __global__ void __launch_bounds__(1024) mfma_mix_kernel(int rounds, unsigned lon
   }
 }
 
+// The launch floor: a kernel that does nothing, launched with a given grid.
+__global__ void empty_kernel() {}
+
 }  // namespace
 
 extern "C" {
+
+// One launch of empty_kernel (groups x 64*waves lanes) on `stream`.
+int fl_diag_empty(int groups, int waves, void* stream) {
+  if (groups < 1 || waves < 1 || waves > 16) return (int)hipErrorInvalidValue;
+  hipLaunchKernelGGL(empty_kernel, dim3((unsigned)groups), dim3((unsigned)(64 * waves)), 0,
+                     (hipStream_t)stream);
+  return (int)hipGetLastError();
+}
 
 // out: 2 * groups * waves uint64 (s_memtime delta, s_memrealtime delta per
 // wave); sink: groups * waves * 64 floats.  Returns a hipError_t.

@@ -1,0 +1,95 @@
+// Diagnostic (not on the product path): the slot-scheduled kernels built
+// with per-wave timeline stamps.  Each wave's lane 0 writes 8 uint64 at
+// out[8 * (group * waves_per_group + wave)]:
+//   [0..4] s_memrealtime at entry, first pass, loop start, loop end, store
+//   [5]    s_memrealtime after the wave's last store has completed
+//   [6]    s_memtime (shader clock) cycles spent in the loop
+//   [7]    iterations << 48 | XCC_ID << 32 | HW_ID
+// so a launch shows where its time goes (start skew, prologue, loop,
+// epilogue), the clock each XCD ran the loop at, and which work-groups
+// shared a CU.  The stamps add a few instructions per wave outside the loop
+// and one wait for the output stores.
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+namespace {
+__device__ unsigned long long* g_fl_timeline;
+}
+
+#define FL_TL_STAMP(name)                                              \
+  const unsigned long long name = __builtin_amdgcn_s_memrealtime();   \
+  const unsigned long long name##_cyc = __builtin_amdgcn_s_memtime(); \
+  (void)name##_cyc
+#define FL_TL_RECORD(wpg, wave, lane, iters, t_entry, t_first, t_loop, t_loop_end, t_store)  \
+  do {                                                                                      \
+    __builtin_amdgcn_s_waitcnt(0);                                                          \
+    const unsigned long long t_exit = __builtin_amdgcn_s_memrealtime();                     \
+    if ((lane) == 0) {                                                                      \
+      unsigned long long* d_ = g_fl_timeline + 8 * ((long long)blockIdx.x * (wpg) + (wave)); \
+      const unsigned hw_ = __builtin_amdgcn_s_getreg((31 << 11) | 4);  /* HW_ID */          \
+      const unsigned xcc_ = __builtin_amdgcn_s_getreg((31 << 11) | 20); /* XCC_ID */        \
+      d_[0] = t_entry;                                                                      \
+      d_[1] = t_first;                                                                      \
+      d_[2] = t_loop;                                                                       \
+      d_[3] = t_loop_end;                                                                   \
+      d_[4] = t_store;                                                                      \
+      d_[5] = t_exit;                                                                       \
+      d_[6] = t_loop_end##_cyc - t_loop##_cyc;                                              \
+      d_[7] = ((unsigned long long)(iters) << 48) |                                         \
+              ((unsigned long long)(xcc_ & 0xff) << 32) | hw_;                              \
+    }                                                                                       \
+  } while (0)
+
+// The instrumented copies get their own launcher names.
+#define launch_slot diag_timeline_launch_slot
+#define launch_slot_split diag_timeline_launch_slot_split
+#include "fa2_slot.hip"
+#undef launch_slot
+#undef launch_slot_split
+
+extern "C" {
+
+// Contiguous fp16 [B, H, N, 64] q, k, v, o; sm_scale 1/8.  mode 8 / 4: the
+// br256_bc64_w8_slot / br128_bc64_w4_slot configurations; 2: the key-range
+// split br128_bc64_w4x2_slot.  `out` holds `out_entries` uint64, at least 8
+// per wave of the grid (B*H*ceil(N/256) groups of 8 waves for mode 8,
+// B*H*ceil(N/128) groups of 4 or 8 waves for modes 4 and 2).  Returns a
+// hipError_t.
+int fl_diag_slot_timeline(int mode, int causal, const void* q, const void* k, const void* v,
+                          void* o, int B, int H, int N, void* out, long long out_entries,
+                          void* stream) {
+  if ((mode != 8 && mode != 4 && mode != 2) || B < 1 || H < 1 || N < 1 || out == nullptr)
+    return (int)hipErrorInvalidValue;
+  const long long rows = mode == 8 ? 256 : 128;
+  const long long waves = mode == 4 ? 4 : 8;
+  if (out_entries < 8 * waves * (long long)B * H * ((N + rows - 1) / rows))
+    return (int)hipErrorInvalidValue;
+  hipError_t e = hipMemcpyToSymbol(HIP_SYMBOL(g_fl_timeline), &out, sizeof(out));
+  if (e != hipSuccess) return (int)e;
+  fl::FwdArgs a{};
+  a.q = q;
+  a.k = k;
+  a.v = v;
+  a.o = o;
+  a.lse = nullptr;
+  a.batch_heads = B * H;
+  a.heads = H;
+  a.seq = N;
+  a.seq_k = N;
+  a.head_dim = 64;
+  a.scale_log2 = (float)(0.125 * 1.4426950408889634);  // as fl_attn_fwd_f16 computes it
+  a.negate = 0;
+  a.causal = causal;
+  a.dtype = fl::kDtypeF16;
+  a.q_sr = a.k_sr = a.v_sr = a.o_sr = 64;
+  a.q_sh = a.k_sh = a.v_sh = a.o_sh = (int64_t)N * 64;
+  a.q_sb = a.k_sb = a.v_sb = a.o_sb = (int64_t)H * N * 64;
+  const auto st = static_cast<hipStream_t>(stream);
+  e = mode == 2 ? fl::diag_timeline_launch_slot_split(a, st)
+                : fl::diag_timeline_launch_slot(a, mode, st);
+  return (int)e;
+}
+
+}  // extern "C"

@@ -8,6 +8,14 @@
 #define SLOT_SPLIT_FV 3
 #endif
 
+// Per-wave timeline stamps (entry, first pass, loop start and end, store,
+// exit), compiled only into the diagnostic library (diag_timeline.hip);
+// empty in the product.
+#ifndef FL_TL_STAMP
+#define FL_TL_STAMP(name)
+#define FL_TL_RECORD(...)
+#endif
+
 namespace fl {
 
 namespace {
@@ -88,6 +96,7 @@ fa2_fwd_slot_kernel(const T* Q, const T* __restrict__ K, const T* __restrict__ V
   __shared__ __attribute__((aligned(16))) uint8_t kring[SPLIT * kRingBytes];
   __shared__ __attribute__((aligned(16))) uint8_t vring[SPLIT * kRingBytes];
 
+  FL_TL_STAMP(tl_entry);
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int stream = wave / W;       // key-range half (0 unless SPLIT)
@@ -133,6 +142,7 @@ fa2_fwd_slot_kernel(const T* Q, const T* __restrict__ K, const T* __restrict__ V
   const int jm = max(0, tm - tbeg - 1);
 
   // ---- first pass ----
+  FL_TL_STAMP(tl_first);
   sync_ring_ahead<(FK - 1) * kDmaPerIter, 0>();  // K(0)
   float16_t S[2];
   V8 P0[2][2], P1[2][2];
@@ -224,11 +234,13 @@ fa2_fwd_slot_kernel(const T* Q, const T* __restrict__ K, const T* __restrict__ V
       }
     });
   };
+  FL_TL_STAMP(tl_loop);
   {
     int j0 = 0;
     for (; j0 + kUnroll <= jm; j0 += kUnroll) group(j0, Ic<false>{});
     for (; j0 <= t0; j0 += kUnroll) group(j0, Ic<true>{});
   }
+  FL_TL_STAMP(tl_loop_end);
   if constexpr (kMfmaSum) {
     // Every p of the first pass is in its row's sum, so a sum within 2^40
     // bounds every p by 2^40 (finite O terms for any |V| below 2^88); a
@@ -284,11 +296,18 @@ fa2_fwd_slot_kernel(const T* Q, const T* __restrict__ K, const T* __restrict__ V
     float* xchg = reinterpret_cast<float*>(kring) + rw * (34 * 64);
     if (stream == 1) rows.save_partial(xchg, lane);
     __syncthreads();
-    if (stream == 1) return;
+    if (stream == 1) {
+      FL_TL_STAMP(tl_store);
+      FL_TL_RECORD(W * SPLIT, wave, lane, t0 + 1, tl_entry, tl_first, tl_loop, tl_loop_end,
+                   tl_store);
+      return;
+    }
     rows.merge_partial(xchg, lane);
   }
   rows.launder();
+  FL_TL_STAMP(tl_store);
   rows.store(hp.o, geom.o_sr, hp.lse);
+  FL_TL_RECORD(W * SPLIT, wave, lane, t0 + 1, tl_entry, tl_first, tl_loop, tl_loop_end, tl_store);
 }
 
 template <int W, int FV, class T = _Float16, int SPLIT = 1>

@@ -17,7 +17,25 @@ scales the HBM byte counters (FETCH_SIZE / WRITE_SIZE) of a profile.
 ``--dtype bf16`` and/or ``--head-dim 128`` run the workload's shape at that
 element type / head dim through ``fl_attn_fwd_bf16_ex`` or
 ``fl_attn_fwd_f16_ex`` (seeded inputs from ``make_qkv`` / ``make_qkv_bf16``;
-``--config`` -1, 6 or 7).
+``--config`` -1, 3 or 4).
+
+``--cold-mib M`` (workloads and ``--decode``) reads and writes an M MiB
+buffer before every launch, evicting the inputs from the L2 caches and the
+256 MiB Infinity Cache (M > 256), and times each launch alone with its own
+HIP event pair; the mean over ``--iters`` launches is printed.
+
+``--timeline MODE`` (MODE 8, 4 or 2: br256_bc64_w8_slot, br128_bc64_w4_slot
+or br128_bc64_w4x2_slot; fp16 D = 64 workloads or ``--shape``, ``--causal``)
+runs the diagnostic build of the slot kernels whose waves stamp their entry,
+loop start and end, and exit (``fl_diag_slot_timeline``), launched
+``--iters`` times back to back, and summarises the last launch: launch span,
+start skew, prologue / loop / epilogue times, the loop clock per XCD
+(s_memtime cycles over s_memrealtime time), and the per-CU work-group
+pairing (iterations and loop time of the groups that shared each CU).
+
+``--empty-kernel G W`` times the launch floor the same way: a kernel that
+does nothing, G work-groups of W waves (``fl_diag_empty`` in the diagnostic
+library), launched back to back through ctypes like the forward calls.
 
 ``--shape B H N`` replaces the workload's shape (fp16, D = 64, N_q = N_k = N,
 sm_scale 1/8, ``make_qkv`` inputs with seed 1): sweeps over shapes the
@@ -71,12 +89,19 @@ def main(argv=None):
     ap.add_argument("--lds-kib", type=int, default=96)
     ap.add_argument("--random", type=int, default=1)
     ap.add_argument("--mfma-mix", type=int, default=-1, metavar="MODE")
+    ap.add_argument("--cold-mib", type=int, default=0, metavar="M")
+    ap.add_argument("--empty-kernel", type=int, nargs=2, metavar=("G", "W"), default=None)
+    ap.add_argument("--timeline", type=int, default=0, metavar="MODE")
     args = ap.parse_args(argv)
 
     import torch
 
     if args.mfma_clock:
         return _mfma_clock(args, torch)
+    if args.empty_kernel:
+        return _empty(args, torch)
+    if args.timeline:
+        return _timeline(args, torch)
     if args.decode:
         return _decode(args, torch)
 
@@ -133,19 +158,13 @@ def main(argv=None):
             rc = capi.naive(p, stream) if args.naive else capi.fwd(p, stream, cfg)
         capi.check(rc)
 
-    launch()
-    torch.cuda.synchronize()
-    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    start.record()
-    for _ in range(args.iters):
-        launch()
-    end.record()
-    torch.cuda.synchronize()
-    us = start.elapsed_time(end) * 1e3 / args.iters
+    us = _time_launches(launch, args, torch)
     flops = (2.0 if args.causal else 4.0) * w.batch * w.heads * w.seq ** 2 * head_dim
+    nbytes = 4 * w.batch * w.heads * w.seq * head_dim * q.element_size()
     name = "naive" if args.naive else ("auto" if cfg < 0 else capi.config_name(cfg))
-    print(f"{w.name} {args.dtype} D={head_dim} causal={args.causal} {name}: "
-          f"{us:.2f} us/launch, {flops / us / 1e6:.1f} TFLOP/s", flush=True)
+    print(f"{w.name} {args.dtype} D={head_dim} causal={args.causal} {name}"
+          f"{' cold' if args.cold_mib else ''}: {us:.2f} us/launch, "
+          f"{flops / us / 1e6:.1f} TFLOP/s, {nbytes / us / 1e3:.1f} GB/s", flush=True)
 
 
 def _decode(args, torch):
@@ -171,30 +190,158 @@ def _decode(args, torch):
         else:
             capi.check(capi.fwd_splitkv(p, ws.data_ptr(), need, stream, args.splits))
 
-    launch()
-    torch.cuda.synchronize()
-    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    start.record()
-    for _ in range(args.iters):
-        launch()
-    end.record()
-    torch.cuda.synchronize()
-    us = start.elapsed_time(end) * 1e3 / args.iters
+    us = _time_launches(launch, args, torch)
     nbytes = 2 * b * h * nk * 64 * 2 + 2 * b * h * nq * 64 * 2
     chunks = need // (b * h * nq * 68 * 4) if need else 1
-    print(f"decode B{b} H{h} NQ{nq} NK{nk} causal={args.causal_decode} chunks={chunks}: "
+    print(f"decode B{b} H{h} NQ{nq} NK{nk} causal={args.causal_decode} chunks={chunks}"
+          f"{' cold' if args.cold_mib else ''}: "
           f"{us:.2f} us/call, {nbytes / us / 1e3:.1f} GB/s ({nbytes / us / 1e3 / 8000:.1%} of 8 TB/s)",
           flush=True)
     return 0
 
 
-def _mfma_clock(args, torch):
+def _time_launches(launch, args, torch):
+    """Mean microseconds per launch: one warm-up, then ``args.iters``
+    launches between two events (warm), or, with ``--cold-mib``, each launch
+    between its own event pair after a pass over the eviction buffer."""
+    launch()
+    torch.cuda.synchronize()
+    if not args.cold_mib:
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
+        for _ in range(args.iters):
+            launch()
+        end.record()
+        torch.cuda.synchronize()
+        return start.elapsed_time(end) * 1e3 / args.iters
+    flush = torch.zeros(args.cold_mib * (1 << 20) // 4, dtype=torch.float32, device="cuda:0")
+    pairs = []
+    for _ in range(args.iters):
+        flush.add_(1.0)
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s.record()
+        launch()
+        e.record()
+        pairs.append((s, e))
+    torch.cuda.synchronize()
+    return sum(s.elapsed_time(e) for s, e in pairs) * 1e3 / len(pairs)
+
+
+def _diag_lib():
     import ctypes
     import os
 
+    return ctypes.CDLL(os.path.join(os.path.dirname(os.path.abspath(__file__)),
+                                    "libflashlite_diag.so"))
+
+
+def _empty(args, torch):
+    import ctypes
+
+    lib = _diag_lib()
+    lib.fl_diag_empty.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_void_p]
+    lib.fl_diag_empty.restype = ctypes.c_int
+    groups, waves = args.empty_kernel
+    stream = torch.cuda.current_stream().cuda_stream
+
+    def launch():
+        rc = lib.fl_diag_empty(groups, waves, stream)
+        if rc != 0:
+            raise RuntimeError(f"diagnostic launch failed: hipError {rc}")
+
+    us = _time_launches(launch, args, torch)
+    print(f"empty kernel {groups} groups x {waves} waves{' cold' if args.cold_mib else ''}: "
+          f"{us:.2f} us/launch", flush=True)
+    return 0
+
+
+def _timeline(args, torch):
+    import collections
+    import ctypes
+
     import numpy as np
 
-    lib = ctypes.CDLL(os.path.join(os.path.dirname(os.path.abspath(__file__)), "libflashlite_diag.so"))
+    from flashlite_amd.workloads import WORKLOADS, Workload, workload_inputs
+
+    w = WORKLOADS[args.workload]
+    if args.shape:
+        b, h, n = args.shape
+        w = Workload(f"B{b}H{h}N{n}", b, h, n, 64, (False, True), 1)
+    if w.head_dim != 64:
+        raise SystemExit("--timeline runs fp16 at head_dim 64")
+    lib = _diag_lib()
+    lib.fl_diag_slot_timeline.argtypes = ([ctypes.c_int] * 2 + [ctypes.c_void_p] * 4 +
+                                          [ctypes.c_int] * 3 + [ctypes.c_void_p, ctypes.c_longlong,
+                                                                ctypes.c_void_p])
+    lib.fl_diag_slot_timeline.restype = ctypes.c_int
+    lib.fl_diag_wall_clock_khz.argtypes = [ctypes.c_int]
+    lib.fl_diag_wall_clock_khz.restype = ctypes.c_int
+    dev = torch.device("cuda:0")
+    q, k, v = (torch.from_numpy(x).to(dev) for x in workload_inputs(w))
+    o = torch.empty_like(q)
+    mode = args.timeline
+    rows, wpg = (256, 8) if mode == 8 else (128, 4 if mode == 4 else 8)
+    groups = w.batch * w.heads * ((w.seq + rows - 1) // rows)
+    out = torch.zeros(groups * wpg * 8, dtype=torch.int64, device=dev)
+    stream = torch.cuda.current_stream().cuda_stream
+
+    def launch():
+        rc = lib.fl_diag_slot_timeline(mode, args.causal, q.data_ptr(), k.data_ptr(), v.data_ptr(),
+                                       o.data_ptr(), w.batch, w.heads, w.seq, out.data_ptr(),
+                                       out.numel(), stream)
+        if rc != 0:
+            raise RuntimeError(f"diagnostic launch failed: hipError {rc}")
+
+    us = _time_launches(launch, args, torch)
+    d = out.cpu().numpy().reshape(-1, 8).astype(np.int64)
+    d = d[d[:, 7] != 0]  # every wave that stamped
+    tick_us = 1e3 / lib.fl_diag_wall_clock_khz(0)
+    t = (d[:, :6] - d[:, 0].min()) * tick_us
+    iters = d[:, 7] >> 48
+    xcc = (d[:, 7] >> 32) & 0xFF
+    hw = d[:, 7] & 0xFFFFFFFF
+    loop = t[:, 3] - t[:, 2]
+    clk = d[:, 6] / np.maximum(loop, 1e-9) / 1e3  # GHz
+    names = {8: "br256_bc64_w8_slot", 4: "br128_bc64_w4_slot", 2: "br128_bc64_w4x2_slot"}
+    print(f"timeline {w.name} causal={args.causal} {names[mode]}: {us:.2f} us/launch over "
+          f"{args.iters} launches (events); last launch: {len(d)} waves, span "
+          f"{t[:, 5].max():.2f} us (first entry to last exit), start skew {t[:, 0].max():.2f} us",
+          flush=True)
+    pct = lambda x: (f"min {x.min():7.2f}  p50 {np.median(x):7.2f}  p90 "  # noqa: E731
+                     f"{np.percentile(x, 90):7.2f}  max {x.max():7.2f} us")
+    print(f"  entry -> loop start (prologue)  {pct(t[:, 2] - t[:, 0])}")
+    print(f"  loop                            {pct(loop)}")
+    print(f"  loop end -> exit (epilogue)     {pct(t[:, 5] - t[:, 3])}")
+    print(f"  loop cycles per iteration p50 {np.median(d[:, 6] / iters):.0f}; loop clock "
+          f"min {clk.min():.3f} p50 {np.median(clk):.3f} max {clk.max():.3f} GHz")
+    for x in range(8):
+        m = xcc == x
+        if m.any():
+            print(f"  XCD {x}: {m.sum():4d} waves, exits {t[m, 5].min():6.2f}-{t[m, 5].max():6.2f} us, "
+                  f"loop p50 {np.median(loop[m]):6.2f} us at {np.median(clk[m]):.3f} GHz")
+    # work-groups per CU (XCC_ID; SE, SH and CU ids, HW_ID bits 8-15) and their loop work
+    cu_key = xcc * 256 + ((hw >> 8) & 0xFF)
+    if len(d) % wpg == 0:
+        per_cu = collections.defaultdict(list)
+        for g in range(len(d) // wpg):
+            sl = slice(g * wpg, (g + 1) * wpg)
+            per_cu[cu_key[sl][0]].append((int(iters[sl].max()), float(loop[sl].max()),
+                                          float(t[sl, 5].max())))
+        ends = np.array([max(x[2] for x in v) for v in per_cu.values()])
+        print(f"  {len(per_cu)} CUs; CU finish min {ends.min():.2f} p50 {np.median(ends):.2f} "
+              f"max {ends.max():.2f} us")
+        for key in sorted(per_cu, key=lambda c: -max(x[2] for x in per_cu[c]))[:3]:
+            print("  latest CU: " + ", ".join(f"{n} it / loop {lt:.1f} us / exit {e:.1f} us"
+                                              for n, lt, e in sorted(per_cu[key])))
+    return 0
+
+
+def _mfma_clock(args, torch):
+    import ctypes
+
+    import numpy as np
+
+    lib = _diag_lib()
     lib.fl_diag_mfma_clock.argtypes = [ctypes.c_int] * 5 + [ctypes.c_void_p] * 3
     lib.fl_diag_mfma_clock.restype = ctypes.c_int
     lib.fl_diag_mfma_mix.argtypes = [ctypes.c_int] * 5 + [ctypes.c_void_p] * 3

@@ -55,14 +55,37 @@ def sample_rows(n, count=256, seed=0):
     return np.array(sorted(rows), dtype=np.int64)
 
 
+def half_ulp(ref, mant_bits=10):
+    """Half a unit in the last place of |ref| in a binary format with
+    `mant_bits` stored significand bits (10: fp16, 7: bf16), elementwise:
+    2^(floor(log2 |x|) - mant_bits - 1), floored at fp16's subnormal step."""
+    _, e = np.frexp(np.abs(np.asarray(ref, dtype=np.float64)))  # |x| = f 2^e, f in [0.5, 1)
+    e = np.where(np.asarray(ref) == 0, -64, e)
+    return np.ldexp(1.0, np.maximum(e - 1 - mant_bits - 1, -25))
+
+
 def assert_close_oracle(out, q16, k16, v16, sm_scale, causal, rows=None, max_abs=MAX_ABS,
-                        mean_abs=MEAN_ABS, ref=None):
+                        mean_abs=MEAN_ABS, ref=None, peaked=False, mant_bits=10):
+    """max-abs <= max_abs and mean-abs <= mean_abs against the fp32 oracle.
+
+    peaked=True (a nearly one-hot softmax, |O| near a single V row of 4-5):
+    the max-abs bound holds per element on top of the output's own rounding,
+    |out - ref| <= max_abs + half_ulp(|ref|); the mean bound is unchanged."""
     if ref is None:
         ref = attention_fp32(q16, k16, v16, sm_scale, causal, rows=rows)
     got = out if rows is None else out[:, :, rows]
     assert np.isfinite(got).all(), "non-finite (or unwritten) outputs"
     mx, mean = error_stats(got, ref)
-    assert mx <= max_abs and mean <= mean_abs, f"max-abs {mx:.3e} mean-abs {mean:.3e}"
+    if peaked:
+        err = np.abs(got.astype(np.float64) - ref.astype(np.float64))
+        excess = err - (max_abs + half_ulp(ref, mant_bits))
+        worst = np.unravel_index(np.argmax(excess), excess.shape)
+        assert excess[worst] <= 0, (
+            f"element {worst}: |out - ref| {err[worst]:.3e} above {max_abs:.1e} + half-ulp of "
+            f"|ref| {abs(float(ref[worst])):.3e}")
+        assert mean <= mean_abs, f"mean-abs {mean:.3e}"
+    else:
+        assert mx <= max_abs and mean <= mean_abs, f"max-abs {mx:.3e} mean-abs {mean:.3e}"
     return mx, mean
 
 

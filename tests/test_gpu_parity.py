@@ -43,11 +43,11 @@ def test_c0_golden(cuda, config, causal):
                                   "C2_headline_B2H8N4096"])
 @pytest.mark.parametrize("causal", [False, True])
 def test_benchmark_configs(cuda, name, causal):
+    # every output row, the headline shape included
     w = WORKLOADS[name]
     q, k, v = workload_inputs(w)
     out = run_capi(q, k, v, w.sm_scale, causal, cuda)
-    rows = None if w.seq <= 1024 else sample_rows(w.seq, seed=w.seed)
-    mx, mean = assert_close_oracle(out, q, k, v, w.sm_scale, causal, rows=rows)
+    mx, mean = assert_close_oracle(out, q, k, v, w.sm_scale, causal)
     print(f"{name} causal={causal}: max-abs {mx:.2e} mean-abs {mean:.2e}")
 
 
@@ -67,16 +67,15 @@ def test_split_scales(cuda, config, scale, causal):
     # peaked softmax: the stabiliser moves in both key ranges before the merge
     q, k, v = make_qkv(1, 4, 700, 64, seed=43)
     out = run_capi(q, k, v, scale, causal, cuda, config=config)
-    assert_close_oracle(out, q, k, v, scale, causal, max_abs=2e-3 if scale < 1 else 4e-3)
+    assert_close_oracle(out, q, k, v, scale, causal, peaked=scale >= 1)
 
 
 def test_c3_long_causal(cuda):
     w = WORKLOADS["C3_long_B1H16N16384"]
     q, k, v = workload_inputs(w)
     out = run_capi(q, k, v, w.sm_scale, True, cuda)
-    rows = sample_rows(w.seq, count=192, seed=w.seed)
-    mx, mean = assert_close_oracle(out, q, k, v, w.sm_scale, True, rows=rows)
-    print(f"C3 sampled {len(rows)} rows: max-abs {mx:.2e} mean-abs {mean:.2e}")
+    mx, mean = assert_close_oracle(out, q, k, v, w.sm_scale, True)  # all 16384 rows
+    print(f"C3 all rows: max-abs {mx:.2e} mean-abs {mean:.2e}")
     # causal row 0 sees only key 0: the output is V[0] exactly
     assert np.array_equal(out[:, :, 0], v[:, :, 0])
 
@@ -120,13 +119,13 @@ def test_other_scales(cuda, scale, causal):
     # 1.0 and 3.0 make the softmax nearly one-hot (logits with std 8 and 24);
     # the negative scale exercises the sign flip of Q.
     # For scale >= 1 the output is nearly a single V row, so |O| reaches 4-5
-    # where one fp16 ulp of the output alone is 3.9e-3; the bound there is
-    # the output's own half-ulp on top of the 2e-3 budget.
+    # where one fp16 ulp of the output alone is 3.9e-3; the bound there is,
+    # per element, the output's own half-ulp on top of the 2e-3 budget.
     q, k, v = make_qkv(1, 4, 257, 64, seed=41)
     # the peaked cases must take the kernel's checked (rescaling) pass
     assert redo_expected(q, k, scale, causal) == (scale >= 1.0)
     out = run_capi(q, k, v, scale, causal, cuda)
-    assert_close_oracle(out, q, k, v, scale, causal, max_abs=2e-3 if scale < 1 else 4e-3)
+    assert_close_oracle(out, q, k, v, scale, causal, peaked=scale >= 1)
 
 
 @pytest.mark.parametrize("config", range(NCFG))
@@ -141,7 +140,7 @@ def test_peaked_every_config(cuda, config, scale, causal):
     q, k, v = make_qkv(1, 4, n, 64, seed=47)
     assert redo_expected(q, k, scale, causal)
     out = run_capi(q, k, v, scale, causal, cuda, config=config)
-    assert_close_oracle(out, q, k, v, scale, causal, max_abs=4e-3)
+    assert_close_oracle(out, q, k, v, scale, causal, peaked=True)
 
 
 def test_deterministic(cuda):

@@ -82,7 +82,7 @@ def test_splitkv_peaked(cuda, nq, causal):
         assert redo_expected(q16, k16[:, :, c0:c0 + per], 3.0, False)
     tq, tk, tv = (to_dev(x, cuda) for x in (q16, k16, v16))
     o, ls, _ = _run_split(tq, tk, tv, 3.0, causal, 5)
-    assert_close_oracle(o.float().cpu().numpy(), q16, k16, v16, 3.0, causal, max_abs=4e-3,
+    assert_close_oracle(o.float().cpu().numpy(), q16, k16, v16, 3.0, causal, peaked=True,
                         ref=attention_fp32(q16, k16, v16, 3.0, causal))
     lse, ref = ls.cpu().numpy(), attention_lse(q16, k16, 3.0, causal)
     mx, mean = error_stats(lse, ref)
