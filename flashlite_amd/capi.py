@@ -34,8 +34,6 @@ EXPORTED = (
     "fl_attn_splitkv_workspace_bytes",
     "fl_attn_fwd_f16_splitkv",
     "fl_attn_fwd_f16_splitkv_noalloc",
-    "fl_attn_fwd_workspace_bytes",
-    "fl_attn_fwd_f16_ws",
 )
 
 SCRATCH_BYTES = 8 << 20  # FL_ATTN_SCRATCH_BYTES
@@ -118,11 +116,6 @@ def load(path: str = LIB_PATH) -> ctypes.CDLL:
     lib.fl_attn_fwd_f16_splitkv_noalloc.argtypes = [ctypes.POINTER(FlAttnParamsEx), ctypes.c_int32,
                                                     ctypes.c_void_p]
     lib.fl_attn_fwd_f16_splitkv_noalloc.restype = ctypes.c_int
-    lib.fl_attn_fwd_workspace_bytes.argtypes = [ctypes.POINTER(FlAttnParamsEx)]
-    lib.fl_attn_fwd_workspace_bytes.restype = ctypes.c_int64
-    lib.fl_attn_fwd_f16_ws.argtypes = [ctypes.POINTER(FlAttnParamsEx), ctypes.c_void_p,
-                                       ctypes.c_int64, ctypes.c_void_p]
-    lib.fl_attn_fwd_f16_ws.restype = ctypes.c_int
     _lib = lib
     return lib
 
@@ -176,18 +169,6 @@ def fwd_splitkv_noalloc(params: FlAttnParamsEx, stream: int = 0, num_splits: int
     """``fl_attn_fwd_f16_splitkv_noalloc`` (partials in the library's scratch
     array); returns the status code."""
     return load().fl_attn_fwd_f16_splitkv_noalloc(ctypes.byref(params), num_splits, stream or None)
-
-
-def fwd_workspace_bytes(params: FlAttnParamsEx) -> int:
-    """``fl_attn_fwd_workspace_bytes``: 0 = no workspace used, -1 = rejected."""
-    return load().fl_attn_fwd_workspace_bytes(ctypes.byref(params))
-
-
-def fwd_ws(params: FlAttnParamsEx, workspace: int, workspace_bytes: int, stream: int = 0) -> int:
-    """``fl_attn_fwd_f16_ws`` (the workspace must start zero-filled; the call
-    leaves it so); returns the status code."""
-    return load().fl_attn_fwd_f16_ws(ctypes.byref(params), workspace or None, workspace_bytes,
-                                     stream or None)
 
 
 def make_params_ex(base: FlAttnParams, q_stride, k_stride, v_stride, o_stride,

@@ -248,12 +248,6 @@ KvPlan plan_kvsplit(const fl::FwdArgs& a, int32_t requested) {
 // fp16 at head_dim 64 has every tile configuration; bf16 and head_dim 128
 // have the two slot-scheduled ones, chosen by the same rule as the fp16
 // dispatcher's first choices.
-// The balanced causal launch replaces the dispatcher's 128-row slot
-// configuration where it applies (fl::bal_fits).
-bool use_balanced(const fl::FwdArgs& a) {
-  return fl::bal_fits(a) && select_fa2(a) == fl::kSlotW4Config;
-}
-
 bool narrow_configs(const fl::FwdArgs& a) {
   return a.dtype != fl::kDtypeF16 || a.head_dim != 64;
 }
@@ -384,37 +378,6 @@ int64_t fl_attn_splitkv_workspace_bytes(const fl_attn_params_ex* p, int32_t num_
   if (check_ex(p, &a, "fl_attn_splitkv_workspace_bytes") != FL_OK) return -1;
   const KvPlan plan = plan_kvsplit(a, num_splits);
   return plan.nsplit == 0 ? 0 : plan.bytes;
-}
-
-int64_t fl_attn_fwd_workspace_bytes(const fl_attn_params_ex* p) {
-  fl::FwdArgs a;
-  if (check_ex(p, &a, "fl_attn_fwd_workspace_bytes") != FL_OK) return -1;
-  return use_balanced(a) ? fl::bal_workspace_bytes(a) : 0;
-}
-
-int fl_attn_fwd_f16_ws(const fl_attn_params_ex* p, void* workspace, int64_t workspace_bytes,
-                       void* stream) {
-  const char* who = "fl_attn_fwd_f16_ws";
-  fl::FwdArgs a;
-  int rc = check_ex(p, &a, who);
-  if (rc != FL_OK) return rc;
-  if (empty_problem(a)) return FL_OK;
-  rc = check_pointers(&p->base, &a, who, 16);
-  if (rc != FL_OK) return rc;
-  hipError_t e;
-  if (use_balanced(a)) {
-    const int64_t need = fl::bal_workspace_bytes(a);
-    if (workspace == nullptr || workspace_bytes < need)
-      return fail(FL_ERR_INVALID_ARGUMENT, "%s: workspace of %lld bytes needed (got %lld%s)", who,
-                  (long long)need, (long long)workspace_bytes, workspace == nullptr ? ", NULL" : "");
-    if ((uintptr_t)workspace & 255)
-      return fail(FL_ERR_MISALIGNED, "%s: workspace must be 256-byte aligned", who);
-    e = fl::launch_slot_balanced(a, workspace, static_cast<hipStream_t>(stream));
-  } else {
-    e = fl::launch_fa2(a, select_fa2(a), static_cast<hipStream_t>(stream));
-  }
-  if (e != hipSuccess) return fail(FL_ERR_LAUNCH, "%s: launch failed: %s", who, hipGetErrorString(e));
-  return FL_OK;
 }
 
 int fl_attn_fwd_f16_splitkv(const fl_attn_params_ex* p, int32_t num_splits, void* workspace,

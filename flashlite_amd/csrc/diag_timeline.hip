@@ -45,33 +45,27 @@ __device__ unsigned long long* g_fl_timeline;
 // The instrumented copies get their own launcher names.
 #define launch_slot diag_timeline_launch_slot
 #define launch_slot_split diag_timeline_launch_slot_split
-#define launch_slot_balanced diag_timeline_launch_slot_balanced
 #include "fa2_slot.hip"
 #undef launch_slot
 #undef launch_slot_split
-#undef launch_slot_balanced
 
 extern "C" {
 
 // Contiguous fp16 [B, H, N, 64] q, k, v, o; sm_scale 1/8.  mode 8 / 4: the
 // br256_bc64_w8_slot / br128_bc64_w4_slot configurations; 2: the key-range
-// split br128_bc64_w4x2_slot; 5: the balanced causal launch, whose
-// zero-filled `workspace` (bal_workspace_bytes) it leaves zero-filled.
-// `out` holds `out_entries` uint64, at least 8 per wave of the grid
-// (B*H*ceil(N/256) groups of 8 waves for mode 8, B*H*ceil(N/128) groups of 4
-// or 8 waves for modes 4 and 2, B*H*3N/256 groups of 4 waves for mode 5).
-// Returns a hipError_t.
+// split br128_bc64_w4x2_slot.  `out` holds `out_entries` uint64, at least 8
+// per wave of the grid (B*H*ceil(N/256) groups of 8 waves for mode 8,
+// B*H*ceil(N/128) groups of 4 or 8 waves for modes 4 and 2).  Returns a
+// hipError_t.
 int fl_diag_slot_timeline(int mode, int causal, const void* q, const void* k, const void* v,
                           void* o, int B, int H, int N, void* out, long long out_entries,
-                          void* workspace, void* stream) {
-  if ((mode != 8 && mode != 4 && mode != 2 && mode != 5) || B < 1 || H < 1 || N < 1 ||
-      out == nullptr)
+                          void* stream) {
+  if ((mode != 8 && mode != 4 && mode != 2) || B < 1 || H < 1 || N < 1 || out == nullptr)
     return (int)hipErrorInvalidValue;
   const long long rows = mode == 8 ? 256 : 128;
-  const long long waves = (mode == 4 || mode == 5) ? 4 : 8;
-  const long long groups =
-      mode == 5 ? (long long)B * H * 3 * (N / 256) : (long long)B * H * ((N + rows - 1) / rows);
-  if (out_entries < 8 * waves * groups) return (int)hipErrorInvalidValue;
+  const long long waves = mode == 4 ? 4 : 8;
+  if (out_entries < 8 * waves * (long long)B * H * ((N + rows - 1) / rows))
+    return (int)hipErrorInvalidValue;
   hipError_t e = hipMemcpyToSymbol(HIP_SYMBOL(g_fl_timeline), &out, sizeof(out));
   if (e != hipSuccess) return (int)e;
   fl::FwdArgs a{};
@@ -93,10 +87,6 @@ int fl_diag_slot_timeline(int mode, int causal, const void* q, const void* k, co
   a.q_sh = a.k_sh = a.v_sh = a.o_sh = (int64_t)N * 64;
   a.q_sb = a.k_sb = a.v_sb = a.o_sb = (int64_t)H * N * 64;
   const auto st = static_cast<hipStream_t>(stream);
-  if (mode == 5) {
-    if (!fl::bal_fits(a) || workspace == nullptr) return (int)hipErrorInvalidValue;
-    return (int)fl::diag_timeline_launch_slot_balanced(a, workspace, st);
-  }
   e = mode == 2 ? fl::diag_timeline_launch_slot_split(a, st)
                 : fl::diag_timeline_launch_slot(a, mode, st);
   return (int)e;

@@ -179,12 +179,9 @@ struct Geom {
   int q_sr, k_sr, v_sr, o_sr;
   int heads, seq_q, seq_k, coff;
   float* lse;  // [B*H][N_q] or null
-  // split-KV launches: partial results [nsplit][B*H][N_q][kPartStride];
-  // balanced causal launches: per split block, its waves' partials
+  // split-KV launches: partial results [nsplit][B*H][N_q][kPartStride]
   float* part;
   int nsplit, batch_heads;
-  // balanced causal launches: per split block, {arrivals, published}
-  unsigned* sem;
 };
 
 // Floats per row of a split-KV partial result: O[64] unnormalised, the
@@ -820,61 +817,31 @@ struct Rows {
     l += exponentiate(s);
   }
   // Split key range: the partner wave holds the same rows over a disjoint
-  // key range.  Its O, m and l go through LDS, or (kGlobal) device memory
-  // shared with another work-group, as part[k * 64 + lane] (k < 32: O, 32:
-  // m, 33: l) and are combined at the larger m.  kGlobal moves them as
-  // relaxed device-scope atomics: each access is coherent across XCDs by
-  // itself, with no cache-wide write-back or invalidation; the caller orders
-  // them against its flag.
-  template <bool kGlobal = false>
-  static __device__ __forceinline__ void put_part(float* part, int i, float x) {
-    if constexpr (kGlobal)
-      __hip_atomic_store(part + i, x, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    else
-      part[i] = x;
-  }
-  template <bool kGlobal = false>
-  static __device__ __forceinline__ float get_part(const float* part, int i) {
-    if constexpr (kGlobal)
-      return __hip_atomic_load(part + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    else
-      return part[i];
-  }
-  template <bool kGlobal = false>
+  // key range.  Its O, m and l go through LDS as part[k * 64 + lane]
+  // (k < 32: O, 32: m, 33: l) and are combined at the larger m.
   __device__ __forceinline__ void save_partial(float* part, int lane) const {
 #pragma unroll
     for (int db = 0; db < 2; ++db)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) put_part<kGlobal>(part, (16 * db + r) * 64 + lane, o[db][r]);
-    put_part<kGlobal>(part, 32 * 64 + lane, m);
-    put_part<kGlobal>(part, 33 * 64 + lane, l);
+      for (int r = 0; r < 16; ++r) part[(16 * db + r) * 64 + lane] = o[db][r];
+    part[32 * 64 + lane] = m;
+    part[33 * 64 + lane] = l;
   }
-  // A row with no key in one range (l == 0 across the lane pair) takes the
-  // other's values.  `self_first`: these registers hold the lower key range.
-  // The lower range's term is the fused one, a_lo * x_lo + (a_hi * x_hi
-  // rounded), so the result has the same bits whichever range holds the
-  // registers.
-  template <bool kGlobal = false>
-  __device__ __forceinline__ void merge_partial(const float* part, int lane,
-                                                bool self_first = true) {
-    const float m1 = get_part<kGlobal>(part, 32 * 64 + lane);
-    const float l1 = get_part<kGlobal>(part, 33 * 64 + lane);
+  // Symmetric in the two ranges: a row with no key in one range (l == 0
+  // across the lane pair) takes the other's values.
+  __device__ __forceinline__ void merge_partial(const float* part, int lane) {
+    const float m1 = part[32 * 64 + lane], l1 = part[33 * 64 + lane];
     const bool has0 = pair_sum(l) > 0.0f;
     const bool has1 = pair_sum(l1) > 0.0f;
     const float mm = has0 ? (has1 ? fmaxf(m, m1) : m) : m1;
     const float k = SCALED ? cr : 1.0f;
     const float a0 = has0 ? __builtin_amdgcn_exp2f(k * (m - mm)) : 0.0f;
     const float a1 = has1 ? __builtin_amdgcn_exp2f(k * (m1 - mm)) : 0.0f;
-    auto mix = [&](float self, float other) {
-      return self_first ? __builtin_fmaf(a0, self, a1 * other)
-                        : __builtin_fmaf(a1, other, a0 * self);
-    };
-    l = mix(l, l1);
+    l = a0 * l + a1 * l1;
 #pragma unroll
     for (int db = 0; db < 2; ++db)
 #pragma unroll
-      for (int r = 0; r < 16; ++r)
-        o[db][r] = mix(o[db][r], get_part<kGlobal>(part, (16 * db + r) * 64 + lane));
+      for (int r = 0; r < 16; ++r) o[db][r] = a0 * o[db][r] + a1 * part[(16 * db + r) * 64 + lane];
     m = mm;
   }
   // Split-KV partial of the rows over one key chunk: O unnormalised
@@ -1023,7 +990,6 @@ inline Geom make_geom(const FwdArgs& a) {
   g.part = nullptr;
   g.nsplit = 1;
   g.batch_heads = a.batch_heads;
-  g.sem = nullptr;
   return g;
 }
 

@@ -21,94 +21,6 @@ namespace fl {
 namespace {
 
 // ---------------------------------------------------------------------------
-// Balanced causal dispatch (BAL).  A head has nqb = 2M blocks of 128 rows
-// (M even); block qb sees 2(qb+1) key tiles.  Blocks qb >= M become two
-// items of qb+1 tiles (half 1: tiles [0, qb+1), half 2: the rest, diagonal
-// included), blocks qb < M one item of 2(qb+1) tiles: 3M items.  bal_item
-// maps rank r (0 = heaviest) to its item: sizes v = 2M .. M+1 come as the
-// two halves of block v-1 followed, for even v, by the whole block v/2-1;
-// the whole blocks qb < M/2 follow in decreasing size.
-__device__ __forceinline__ void bal_item(int M, int r, int& qb, int& half) {
-  const int pairs = M >> 1;  // (even v, odd v) size pairs: 5 items each
-  if (r < 5 * pairs) {
-    const int p = r / 5, s = r - 5 * p;
-    const int ve = 2 * M - 2 * p;
-    if (s < 2) {
-      qb = ve - 1;  // halves of size ve
-      half = 1 + s;
-    } else if (s == 2) {
-      qb = (ve >> 1) - 1;  // whole block of size ve
-      half = 0;
-    } else {
-      qb = ve - 2;  // halves of size ve - 1
-      half = s - 2;
-    }
-  } else {
-    qb = pairs - 1 - (r - 5 * pairs);
-    half = 0;
-  }
-}
-
-// Grid: 8 XCDs x hx heads x 3M items; work-group i runs on XCD i % 8, which
-// takes heads [hx * (i % 8), +hx) and their items heaviest first (heads
-// interleaved), so both halves of a block share an XCD.
-__device__ __forceinline__ void bal_coords(int nqb, int& bh, int& qb, int& half) {
-  const int M = nqb >> 1;
-  const int hx = (gridDim.x >> 3) / (3 * M);
-  const int k = blockIdx.x >> 3;
-  bh = (blockIdx.x & 7) * hx + k % hx;
-  bal_item(M, k / hx, qb, half);
-}
-
-// The two halves of split block sb = bh*M + qb-M meet in the workspace:
-// sem[2 sb] counts arrivals, sem[2 sb + 1] says the first half's partials
-// (one wave's O, m, l per kBalPartFloats, Rows::save_partial layout) are
-// stored.  The first to arrive stores and publishes and retires (false);
-// the second waits for the flag, which the first is already on its way to
-// setting, merges (true), and leaves both words at zero for the next call.
-// The wait is bounded (kBalSpinLimit polls) so that no wave can hang.
-// Every access to the workspace is a relaxed device-scope atomic, coherent
-// by itself across XCDs; the partials are ordered before the flag by
-// waiting for their stores, and after it by the barrier that follows the
-// wait.  (Acquire/release orderings would write back and invalidate the
-// whole L2 of the XCD at every meeting, which measured 2.4x slower.)
-constexpr int kBalPartFloats = 34 * 64;
-constexpr unsigned kBalSpinLimit = 1u << 22;
-
-template <int W, class R>
-__device__ __forceinline__ bool bal_meet(const Geom& g, int nqb, int bh, int qb, int half, int rw,
-                                         int lane, R& rows, uint8_t* lds_idle) {
-  const int M = nqb >> 1;
-  const long long sb = (long long)bh * M + (qb - M);
-  unsigned* sem = g.sem + 2 * sb;
-  float* part = g.part + (sb * W + rw) * kBalPartFloats;
-  // a word of the idle K ring (not the checked pass's flag)
-  int* order = reinterpret_cast<int*>(lds_idle) + 4;
-  if (threadIdx.x == 0)
-    *order = (int)__hip_atomic_fetch_add(sem, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  __syncthreads();
-  if (*order == 0) {
-    rows.template save_partial<true>(part, lane);
-    __builtin_amdgcn_s_waitcnt(0);  // this wave's partial stores acknowledged ...
-    __syncthreads();                // ... and every wave's, before the flag
-    if (threadIdx.x == 0)
-      __hip_atomic_store(sem + 1, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    return false;
-  }
-  if (threadIdx.x == 0) {
-    for (unsigned n = 0; n < kBalSpinLimit; ++n) {
-      if (__hip_atomic_load(sem + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0u) break;
-      __builtin_amdgcn_s_sleep(1);
-    }
-    __hip_atomic_store(sem + 1, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __hip_atomic_store(sem, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  }
-  __syncthreads();  // the flag seen before any wave loads the partials
-  rows.template merge_partial<true>(part, lane, /*self_first=*/half == 1);
-  return true;
-}
-
-// ---------------------------------------------------------------------------
 // Slot-scheduled pipeline: W waves of 32 query rows, one key stream.
 //
 // Same work per iteration j as fa2_fwd_kernel (GEMM1, GEMM2 of tile j-1
@@ -146,18 +58,7 @@ __device__ __forceinline__ bool bal_meet(const Geom& g, int nqb, int bh, int qb,
 // meets the same barriers.  This halves the longest key walk: a causal
 // work-group's time follows half its tiles, and heaviest-first dispatch of
 // one work-group per CU then balances the CUs.
-//
-// BAL (configuration br128_bc64_w4_bal, causal N_q = N_k): the heavier half
-// of the 128-row blocks (block qb of nqb = 2M sees 2(qb+1) key tiles; qb >=
-// M) is cut into two work-groups of qb+1 tiles each, the lighter half runs
-// whole, and the 3M items of a head are dispatched heaviest first
-// (bal_coords), so that the two work-groups sharing a CU carry similar work
-// and every CU about the same total.  The two halves of a block meet in the
-// caller's workspace: the first to finish stores its O, m and l
-// (Rows::save_partial) and publishes them, the second merges them into its
-// own (Rows::merge_partial) and writes the output.
-template <int W, int FV, bool CAUSAL, bool SCALED, class T = _Float16, int SPLIT = 1,
-          bool BAL = false>
+template <int W, int FV, bool CAUSAL, bool SCALED, class T = _Float16, int SPLIT = 1>
 __global__ void __launch_bounds__(64 * W * SPLIT, 2)  // <= 256 VGPRs: 2 waves per SIMD
 fa2_fwd_slot_kernel(const T* Q, const T* __restrict__ K, const T* __restrict__ V, T* O,
                     const Geom geom, int nqb, float cq, float cr) {
@@ -192,7 +93,6 @@ fa2_fwd_slot_kernel(const T* Q, const T* __restrict__ K, const T* __restrict__ V
   static_assert(kAhead % 2 == 0 && kAhead < 16, "read-ahead");
   static_assert(SPLIT == 1 || SPLIT == 2, "key-range split");
   static_assert(SPLIT == 1 || SPLIT * kRingBytes >= W * 34 * 64 * 4, "merge buffer");
-  static_assert(!BAL || (CAUSAL && SPLIT == 1 && W == 4), "balanced causal: 4-wave groups");
   __shared__ __attribute__((aligned(16))) uint8_t kring[SPLIT * kRingBytes];
   __shared__ __attribute__((aligned(16))) uint8_t vring[SPLIT * kRingBytes];
 
@@ -201,11 +101,8 @@ fa2_fwd_slot_kernel(const T* Q, const T* __restrict__ K, const T* __restrict__ V
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int stream = wave / W;       // key-range half (0 unless SPLIT)
   const int rw = wave - stream * W;  // 32-row block within the work-group
-  int bh, qb, half = 0;  // half: 0 whole block, 1 / 2 first / second key half
-  if constexpr (BAL)
-    bal_coords(nqb, bh, qb, half);
-  else
-    wg_coords<CAUSAL, kWgPerCu>(nqb, bh, qb);
+  int bh, qb;
+  wg_coords<CAUSAL, kWgPerCu>(nqb, bh, qb);
   const HeadPtrs<T> hp = head_ptrs(geom, bh, Q, K, V, O);
   const i32x4_t rk = hp.rk, rv = hp.rv;
   const FetchOff<kSegs> fk = fetch_offsets<kSegs, false>(rw, lane, 2 * geom.k_sr);
@@ -219,11 +116,9 @@ fa2_fwd_slot_kernel(const T* Q, const T* __restrict__ K, const T* __restrict__ V
   // This stream's key tiles [tbeg, tend); iterations 0 .. t0 on tile tbeg + j
   // (the last one only drains GEMM2; with SPLIT the shorter stream's last
   // tile lies past the range and is masked).
-  const bool halved = SPLIT == 2 || half != 0;
-  const bool second = SPLIT == 2 ? stream == 1 : half == 2;
-  const int t0 = halved ? (ntiles + 1) / 2 : ntiles;
-  const int tbeg = second ? t0 : 0;
-  const int tend = second ? ntiles : t0;
+  const int t0 = SPLIT == 2 ? (ntiles + 1) / 2 : ntiles;
+  const int tbeg = stream == 0 ? 0 : t0;
+  const int tend = stream == 0 ? t0 : ntiles;
   const int last = max(tend - 1, tbeg);  // fetch clamp
 
   // Prologue fetch groups -FK .. -1 (V tiles < 0 read as zeros through the
@@ -239,7 +134,7 @@ fa2_fwd_slot_kernel(const T* Q, const T* __restrict__ K, const T* __restrict__ V
   RowsT rows;
   rows.init(hp.q, geom.q_sr, lane, q0 + 32 * rw, seq, geom.seq_k, geom.coff, cq, cr);
   if constexpr (kMfmaSum) rows.init_msum(lane);
-  if (halved && !second) rows.kv_lim = min(rows.kv_lim, tend * kBc);
+  if (SPLIT == 2 && stream == 0) rows.kv_lim = min(rows.kv_lim, tend * kBc);
 
   // Iterations j < jm need no mask on tiles tbeg + j and tbeg + j + 1.
   int tm = rows.kv_lim >> 6;
@@ -409,27 +304,19 @@ fa2_fwd_slot_kernel(const T* Q, const T* __restrict__ K, const T* __restrict__ V
     }
     rows.merge_partial(xchg, lane);
   }
-  if constexpr (BAL) {
-    if (half != 0 && !bal_meet<W>(geom, nqb, bh, qb, half, rw, lane, rows, kring + kTileBytes)) {
-      FL_TL_STAMP(tl_published);
-      FL_TL_RECORD(W, wave, lane, t0 + 1, tl_entry, tl_first, tl_loop, tl_loop_end, tl_published);
-      return;
-    }
-  }
   rows.launder();
   FL_TL_STAMP(tl_store);
   rows.store(hp.o, geom.o_sr, hp.lse);
   FL_TL_RECORD(W * SPLIT, wave, lane, t0 + 1, tl_entry, tl_first, tl_loop, tl_loop_end, tl_store);
 }
 
-template <int W, int FV, class T = _Float16, int SPLIT = 1, bool BAL = false>
+template <int W, int FV, class T = _Float16, int SPLIT = 1>
 struct SlotLaunch {
   template <bool C, bool S>
   struct L {
     static hipError_t run(const FwdArgs& a, const Geom& g, dim3 grid, int nqb, float cq, float cr,
                           hipStream_t st) {
-      hipLaunchKernelGGL((fa2_fwd_slot_kernel<W, FV, C, S, T, SPLIT, BAL>), grid,
-                         dim3(64 * W * SPLIT),
+      hipLaunchKernelGGL((fa2_fwd_slot_kernel<W, FV, C, S, T, SPLIT>), grid, dim3(64 * W * SPLIT),
                          0, st,
                          static_cast<const T*>(a.q), static_cast<const T*>(a.k),
                          static_cast<const T*>(a.v), static_cast<T*>(a.o), g, nqb, cq, cr);
@@ -451,25 +338,6 @@ hipError_t launch_slot(const FwdArgs& a, int waves, hipStream_t stream) {
     return bf ? dispatch<SlotLaunch<4, 3, __bf16>::L>(a, stream, 128)
               : dispatch<SlotLaunch<4, 3>::L>(a, stream, 128);
   return hipErrorInvalidValue;
-}
-
-// Balanced causal (fp16, head_dim 64, N_q = N_k; bal_fits): 128-row
-// groups of 4 waves, the heavy blocks' key ranges halved between two groups
-// that merge through `workspace` (bal_workspace_bytes; its first
-// bal_sem_bytes must be zero, and are left zero).
-hipError_t launch_slot_balanced(const FwdArgs& a, void* workspace, hipStream_t stream) {
-  if (!bal_fits(a) || workspace == nullptr) return hipErrorInvalidValue;
-  const int nqb = a.seq / 128;
-  Geom g = make_geom(a);
-  g.sem = static_cast<unsigned*>(workspace);
-  g.part = reinterpret_cast<float*>(static_cast<char*>(workspace) + bal_sem_bytes(a));
-  const dim3 grid((unsigned)(a.batch_heads * 3 * (nqb / 2)));
-  const Scales sc(a);
-  using Bal = SlotLaunch<4, 3, _Float16, 1, true>;
-  const hipError_t e =
-      sc.scaled ? Bal::template L<true, true>::run(a, g, grid, nqb, sc.cq, sc.cr, stream)
-                : Bal::template L<true, false>::run(a, g, grid, nqb, sc.cq, sc.cr, stream);
-  return e != hipSuccess ? e : hipGetLastError();
 }
 
 // fp16: 128-row groups of 2 x 4 waves, the key range halved between them.

@@ -66,25 +66,6 @@ bool stream_config_fits(const FwdArgs& a);
 hipError_t launch_pipe(const FwdArgs& a, int cfg, hipStream_t stream);     // fa2_pipe.hip
 hipError_t launch_slot(const FwdArgs& a, int waves, hipStream_t stream);   // fa2_slot.hip
 hipError_t launch_slot_split(const FwdArgs& a, hipStream_t stream);        // fa2_slot.hip
-hipError_t launch_slot_balanced(const FwdArgs& a, void* workspace,
-                                hipStream_t stream);                       // fa2_slot.hip
-
-// Balanced causal launches (launch_slot_balanced): fp16 at head_dim 64,
-// causal with N_q = N_k a multiple of 512 and at least 1024 (nqb = N/128
-// blocks, nqb % 4 == 0), B*H a multiple of 8 (whole heads per XCD).  The
-// workspace holds 2 uint32 per split block (zero between calls), padded to
-// 256 bytes, then each split block's 4 waves x 34 x 64 floats of partials.
-inline bool bal_fits(const FwdArgs& a) {
-  return a.causal && a.dtype == kDtypeF16 && a.head_dim == 64 && a.seq == a.seq_k &&
-         a.seq >= 1024 && a.seq % 512 == 0 && a.batch_heads % 8 == 0;
-}
-inline int64_t bal_split_blocks(const FwdArgs& a) { return (int64_t)a.batch_heads * (a.seq / 256); }
-inline int64_t bal_sem_bytes(const FwdArgs& a) {
-  return (bal_split_blocks(a) * 8 + 255) / 256 * 256;
-}
-inline int64_t bal_workspace_bytes(const FwdArgs& a) {
-  return bal_sem_bytes(a) + bal_split_blocks(a) * 4 * 34 * 64 * 4;
-}
 hipError_t launch_stream(const FwdArgs& a, hipStream_t stream);            // fa2_stream.hip
 hipError_t launch_d128(const FwdArgs& a, int waves, hipStream_t stream);   // fa2_d128.hip
 

@@ -19,10 +19,7 @@
 #include <ATen/hip/impl/HIPGuardImplMasqueradingAsCUDA.h>
 #include <ATen/hip/impl/HIPStreamMasqueradingAsCUDA.h>
 
-#include <map>
-#include <mutex>
 #include <optional>
-#include <utility>
 
 #include "flashlite_attn.h"
 
@@ -55,45 +52,6 @@ fl_attn_params make_params(const torch::Tensor& q, const torch::Tensor& k, const
 void check_same_device(const torch::Tensor& q, const torch::Tensor& k, const torch::Tensor& v) {
   TORCH_CHECK(k.device() == q.device() && v.device() == q.device(),
               "All tensors must be on the same device");
-}
-
-fl_attn_params_ex ex_params(const fl_attn_params& base, const torch::Tensor& q,
-                            const torch::Tensor& k, const torch::Tensor& v, const torch::Tensor& o,
-                            float* lse) {
-  fl_attn_params_ex p;
-  p.base = base;
-  const torch::Tensor* ts[4] = {&q, &k, &v, &o};
-  int64_t* st[4] = {p.q_stride, p.k_stride, p.v_stride, p.o_stride};
-  for (int i = 0; i < 4; ++i)
-    for (int d = 0; d < 3; ++d) st[i][d] = ts[i]->stride(d);
-  p.lse = lse;
-  return p;
-}
-
-// The workspace of the balanced causal launch (fl_attn_fwd_f16_ws), one per
-// device and stream: zero-filled when allocated, and left zero-filled by
-// every call, so later calls on that stream reuse it without allocating.
-// The map is never destroyed (no device memory is freed at process exit).
-torch::Tensor balanced_workspace(const torch::Tensor& q, int64_t bytes) {
-  static std::mutex mu;
-  static auto* cache = new std::map<std::pair<int, void*>, torch::Tensor>();
-  const std::lock_guard<std::mutex> lock(mu);
-  const auto key = std::make_pair((int)q.device().index(), current_stream(q));
-  auto it = cache->find(key);
-  if (it != cache->end() && (int64_t)it->second.nbytes() >= bytes) return it->second;
-  torch::Tensor ws = torch::zeros({(bytes + 255) / 256 * 64}, q.options().dtype(torch::kFloat32));
-  (*cache)[key] = ws;
-  return ws;
-}
-
-// fp16 at head_dim 64 through the C ABI: the balanced causal launch where the
-// library uses one, else the one-pass dispatcher (fl_attn_fwd_f16_ex).
-int fwd_f16_choice(const fl_attn_params_ex& p, const torch::Tensor& q) {
-  const int64_t ws_bytes = fl_attn_fwd_workspace_bytes(&p);
-  if (ws_bytes < 0) return FL_ERR_INVALID_ARGUMENT;
-  if (ws_bytes == 0) return fl_attn_fwd_f16_ex(&p, -1, current_stream(q));
-  const torch::Tensor ws = balanced_workspace(q, ws_bytes);
-  return fl_attn_fwd_f16_ws(&p, ws.data_ptr(), (int64_t)ws.nbytes(), current_stream(q));
 }
 
 }  // namespace
@@ -167,8 +125,8 @@ torch::Tensor flash_attn_forward_flash2(torch::Tensor q, torch::Tensor k, torch:
   }
 
   const c10::hip::HIPGuardMasqueradingAsCUDA guard(q.device());
-  const fl_attn_params p = make_params(q, k, v, out_tensor, sm_scale, is_causal);
-  const int rc = fwd_f16_choice(ex_params(p, q, k, v, out_tensor, nullptr), q);
+  fl_attn_params p = make_params(q, k, v, out_tensor, sm_scale, is_causal);
+  const int rc = fl_attn_fwd_f16(&p, current_stream(q));
   TORCH_CHECK(rc == FL_OK, "FlashLite HIP error: ", fl_attn_last_error());
   return out_tensor;
 }
@@ -225,9 +183,13 @@ py::object flash_attn_forward_flash2_ex(torch::Tensor q, torch::Tensor k, torch:
                        q.options().dtype(torch::kFloat32).memory_format(torch::MemoryFormat::Contiguous));
 
   const c10::hip::HIPGuardMasqueradingAsCUDA guard(q.device());
-  const fl_attn_params_ex p =
-      ex_params(make_params(q, k, v, out_tensor, sm_scale, is_causal), q, k, v, out_tensor,
-                return_lse ? lse.data_ptr<float>() : nullptr);
+  fl_attn_params_ex p;
+  p.base = make_params(q, k, v, out_tensor, sm_scale, is_causal);
+  const torch::Tensor* ts[4] = {&q, &k, &v, &out_tensor};
+  int64_t* st[4] = {p.q_stride, p.k_stride, p.v_stride, p.o_stride};
+  for (int i = 0; i < 4; ++i)
+    for (int d = 0; d < 3; ++d) st[i][d] = ts[i]->stride(d);
+  p.lse = return_lse ? lse.data_ptr<float>() : nullptr;
   TORCH_CHECK(num_splits >= 0 && num_splits <= INT32_MAX, "num_splits must be >= 0");
   // Split-KV is built for fp16 at head_dim 64; bf16 and head_dim 128 run one pass.
   const bool one_pass_only = bf16 || head_dim != 64;
@@ -239,12 +201,8 @@ py::object flash_attn_forward_flash2_ex(torch::Tensor q, torch::Tensor k, torch:
   TORCH_CHECK(ws_bytes >= 0, "FlashLite HIP error: ", fl_attn_last_error());
   int rc;
   if (ws_bytes == 0) {
-    if (bf16)
-      rc = fl_attn_fwd_bf16_ex(&p, -1, current_stream(q));
-    else if (head_dim != 64 || num_splits == 1)
-      rc = fl_attn_fwd_f16_ex(&p, -1, current_stream(q));
-    else
-      rc = fwd_f16_choice(p, q);
+    rc = bf16 ? fl_attn_fwd_bf16_ex(&p, -1, current_stream(q))
+              : fl_attn_fwd_f16_ex(&p, -1, current_stream(q));
   } else {
     torch::Tensor ws;
     if (workspace.has_value() && workspace.value().defined() &&

@@ -19,18 +19,13 @@ element type / head dim through ``fl_attn_fwd_bf16_ex`` or
 ``fl_attn_fwd_f16_ex`` (seeded inputs from ``make_qkv`` / ``make_qkv_bf16``;
 ``--config`` -1, 3 or 4).
 
-``--balanced`` (fp16 D = 64 workloads) launches through
-``fl_attn_fwd_f16_ws`` with a zero-filled workspace: the balanced causal
-launch where it applies, else the one-pass dispatcher.
-
 ``--cold-mib M`` (workloads and ``--decode``) reads and writes an M MiB
 buffer before every launch, evicting the inputs from the L2 caches and the
 256 MiB Infinity Cache (M > 256), and times each launch alone with its own
 HIP event pair; the mean over ``--iters`` launches is printed.
 
-``--timeline MODE`` (MODE 8, 4, 2 or 5: br256_bc64_w8_slot,
-br128_bc64_w4_slot, br128_bc64_w4x2_slot or the balanced causal launch;
-fp16 D = 64 workloads or ``--shape``, ``--causal``)
+``--timeline MODE`` (MODE 8, 4 or 2: br256_bc64_w8_slot, br128_bc64_w4_slot
+or br128_bc64_w4x2_slot; fp16 D = 64 workloads or ``--shape``, ``--causal``)
 runs the diagnostic build of the slot kernels whose waves stamp their entry,
 loop start and end, and exit (``fl_diag_slot_timeline``), launched
 ``--iters`` times back to back, and summarises the last launch: launch span,
@@ -97,7 +92,6 @@ def main(argv=None):
     ap.add_argument("--cold-mib", type=int, default=0, metavar="M")
     ap.add_argument("--empty-kernel", type=int, nargs=2, metavar=("G", "W"), default=None)
     ap.add_argument("--timeline", type=int, default=0, metavar="MODE")
-    ap.add_argument("--balanced", action="store_true")
     args = ap.parse_args(argv)
 
     import torch
@@ -149,16 +143,10 @@ def main(argv=None):
         q, k, v = (torch.from_numpy(x).to(dev) for x in workload_inputs(w))
     o = torch.empty_like(q)
     stream = torch.cuda.current_stream().cuda_stream
-    ws = None
     if wide:
         p = capi.tensor_params_ex(q, k, v, o, w.sm_scale, bool(args.causal))
         fwd_ex = capi.fwd_bf16_ex if args.dtype == "bf16" else capi.fwd_ex
         cfg = args.config
-    elif args.balanced:
-        p = capi.tensor_params_ex(q, k, v, o, w.sm_scale, bool(args.causal))
-        need = capi.fwd_workspace_bytes(p)
-        ws = torch.zeros(max(need, 256) // 4, dtype=torch.float32, device=dev)
-        cfg = -1
     else:
         p = capi.tensor_params(q, k, v, o, w.sm_scale, bool(args.causal))
         cfg = capi.select_config(p) if args.config < 0 else args.config
@@ -166,8 +154,6 @@ def main(argv=None):
     def launch():
         if wide:
             rc = fwd_ex(p, stream, cfg)
-        elif ws is not None:
-            rc = capi.fwd_ws(p, ws.data_ptr(), ws.numel() * 4, stream)
         else:
             rc = capi.naive(p, stream) if args.naive else capi.fwd(p, stream, cfg)
         capi.check(rc)
@@ -176,8 +162,6 @@ def main(argv=None):
     flops = (2.0 if args.causal else 4.0) * w.batch * w.heads * w.seq ** 2 * head_dim
     nbytes = 4 * w.batch * w.heads * w.seq * head_dim * q.element_size()
     name = "naive" if args.naive else ("auto" if cfg < 0 else capi.config_name(cfg))
-    if ws is not None:
-        name = "balanced" if need > 0 else "auto (balanced launch does not apply)"
     print(f"{w.name} {args.dtype} D={head_dim} causal={args.causal} {name}"
           f"{' cold' if args.cold_mib else ''}: {us:.2f} us/launch, "
           f"{flops / us / 1e6:.1f} TFLOP/s, {nbytes / us / 1e3:.1f} GB/s", flush=True)
@@ -288,7 +272,7 @@ def _timeline(args, torch):
     lib = _diag_lib()
     lib.fl_diag_slot_timeline.argtypes = ([ctypes.c_int] * 2 + [ctypes.c_void_p] * 4 +
                                           [ctypes.c_int] * 3 + [ctypes.c_void_p, ctypes.c_longlong,
-                                                                ctypes.c_void_p, ctypes.c_void_p])
+                                                                ctypes.c_void_p])
     lib.fl_diag_slot_timeline.restype = ctypes.c_int
     lib.fl_diag_wall_clock_khz.argtypes = [ctypes.c_int]
     lib.fl_diag_wall_clock_khz.restype = ctypes.c_int
@@ -296,23 +280,15 @@ def _timeline(args, torch):
     q, k, v = (torch.from_numpy(x).to(dev) for x in workload_inputs(w))
     o = torch.empty_like(q)
     mode = args.timeline
-    rows, wpg = (256, 8) if mode == 8 else (128, 4 if mode in (4, 5) else 8)
+    rows, wpg = (256, 8) if mode == 8 else (128, 4 if mode == 4 else 8)
     groups = w.batch * w.heads * ((w.seq + rows - 1) // rows)
-    ws = None
-    if mode == 5:
-        from flashlite_amd import capi
-
-        groups = w.batch * w.heads * 3 * (w.seq // 256)
-        p = capi.tensor_params_ex(q, k, v, o, w.sm_scale, True)
-        ws = torch.zeros(max(capi.fwd_workspace_bytes(p), 256) // 4, dtype=torch.float32,
-                         device=dev)
     out = torch.zeros(groups * wpg * 8, dtype=torch.int64, device=dev)
     stream = torch.cuda.current_stream().cuda_stream
 
     def launch():
         rc = lib.fl_diag_slot_timeline(mode, args.causal, q.data_ptr(), k.data_ptr(), v.data_ptr(),
                                        o.data_ptr(), w.batch, w.heads, w.seq, out.data_ptr(),
-                                       out.numel(), 0 if ws is None else ws.data_ptr(), stream)
+                                       out.numel(), stream)
         if rc != 0:
             raise RuntimeError(f"diagnostic launch failed: hipError {rc}")
 
@@ -326,8 +302,7 @@ def _timeline(args, torch):
     hw = d[:, 7] & 0xFFFFFFFF
     loop = t[:, 3] - t[:, 2]
     clk = d[:, 6] / np.maximum(loop, 1e-9) / 1e3  # GHz
-    names = {8: "br256_bc64_w8_slot", 4: "br128_bc64_w4_slot", 2: "br128_bc64_w4x2_slot",
-             5: "balanced causal"}
+    names = {8: "br256_bc64_w8_slot", 4: "br128_bc64_w4_slot", 2: "br128_bc64_w4x2_slot"}
     print(f"timeline {w.name} causal={args.causal} {names[mode]}: {us:.2f} us/launch over "
           f"{args.iters} launches (events); last launch: {len(d)} waves, span "
           f"{t[:, 5].max():.2f} us (first entry to last exit), start skew {t[:, 0].max():.2f} us",

@@ -256,41 +256,3 @@ def test_splitkv_workspace_checks():
     assert capi.fwd_splitkv(p, A + 0x400000, need - 4) == capi.FL_ERR_INVALID_ARGUMENT
     assert capi.fwd_splitkv(p, A + 0x400008, need) == capi.FL_ERR_MISALIGNED
     assert capi.load().fl_attn_fwd_f16_splitkv(None, 0, None, 0, None) == capi.FL_ERR_INVALID_ARGUMENT
-
-
-def _contig_ex(b, h, n, causal, seq_k=None):
-    nk = n if seq_k is None else seq_k
-    qs = (h * n * 64, n * 64, 64)
-    ks = (h * nk * 64, nk * 64, 64)
-    return capi.make_params_ex(_p(batch=b, heads=h, seq_q=n, seq_k=nk, causal=causal), qs, ks, ks,
-                               qs)
-
-
-def test_balanced_workspace_bytes():
-    # causal, N_q = N_k a multiple of 512 (>= 1024), B*H a multiple of 8: one
-    # split block per 256 query rows (the longer half of the 128-row blocks)
-    def want(b, h, n):
-        nsb = b * h * (n // 256)
-        return (nsb * 8 + 255) // 256 * 256 + nsb * 4 * 34 * 64 * 4
-
-    for b, h, n in ((2, 8, 4096), (2, 8, 1024), (1, 16, 16384), (4, 16, 2048)):
-        assert capi.fwd_workspace_bytes(_contig_ex(b, h, n, True)) == want(b, h, n)
-    # where the balanced launch does not apply, no workspace is used
-    for b, h, n, causal, nk in ((2, 8, 4096, False, None), (2, 8, 4000, True, None),
-                                (1, 4, 4096, True, None), (2, 8, 512, True, None),
-                                (2, 8, 4096, True, 4608), (32, 32, 256, True, None)):
-        assert capi.fwd_workspace_bytes(_contig_ex(b, h, n, causal, nk)) == 0, (b, h, n, causal)
-    bad = _contig_ex(2, 8, 4096, True)
-    bad.base.heads = -1
-    assert capi.fwd_workspace_bytes(bad) == -1
-
-
-def test_balanced_workspace_checks():
-    p = _contig_ex(2, 8, 4096, True)
-    need = capi.fwd_workspace_bytes(p)
-    assert capi.fwd_ws(p, 0, need) == capi.FL_ERR_INVALID_ARGUMENT
-    assert "workspace" in capi.last_error() and "NULL" in capi.last_error()
-    assert capi.fwd_ws(p, A + 0x400000, need - 4) == capi.FL_ERR_INVALID_ARGUMENT
-    assert capi.fwd_ws(p, A + 0x400010, need) == capi.FL_ERR_MISALIGNED
-    assert "256-byte" in capi.last_error()
-    assert capi.load().fl_attn_fwd_f16_ws(None, None, 0, None) == capi.FL_ERR_INVALID_ARGUMENT
