@@ -39,7 +39,8 @@ LIB_NAME = "libflashlite_attn.so"
 DIAG_LIB_NAME = "libflashlite_diag.so"
 EXT_NAME = "flash_attn_wmma"
 
-HIP_SOURCES = ["fa2_fwd.hip", "fa2_pipe.hip", "fa2_slot.hip", "fa2_stream.hip", "fa2_d128.hip",
+HIP_SOURCES = ["fa2_fwd.hip", "fa2_pipe.hip", "fa2_slot.hip", "fa2_stream.hip", "fa2_short.hip",
+               "fa2_d128.hip",
                "naive_fwd.hip", "capi.hip"]
 DIAG_SOURCES = ["diag.hip", "diag_timeline.hip"]
 

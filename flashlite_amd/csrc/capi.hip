@@ -121,6 +121,9 @@ int select_fa2(const fl::FwdArgs& a) {
   constexpr int64_t kCus = 256;
   auto wgs = [&](int64_t br) { return (a.seq + br - 1) / br * (int64_t)a.batch_heads; };
   if (fl::stream_config_fits(a)) return fl::kStreamConfig;  // br256_kv256_w8_stream
+  // N_k <= 512 with few query blocks: quarter the key range (one 4-wave
+  // work-group per 32 rows; a single round on the CUs).
+  if (fl::quarter_config_fits(a) && wgs(32) <= kCus) return fl::kQuarterConfig;
   if (!a.causal && a.seq_k >= 4096 && wgs(256) >= kCus) return fl::kSlotW8Config;
   if (!a.causal && a.seq >= 2048 && wgs(128) < kCus / 2) return fl::kCfgSplit2;
   if (wgs(128) >= kCus / 4) return fl::kSlotW4Config;
@@ -276,6 +279,9 @@ int fwd_ex(const fl_attn_params_ex* p, int32_t config, void* stream, int dtype, 
   if (config == fl::kStreamConfig && !fl::stream_config_fits(a))
     return fail(FL_ERR_BAD_CONFIG, "%s: config %d needs N_k <= %d and row strides below 2^22 "
                 "(got N_k %d)", who, (int)config, fl::kStreamMaxKeys, a.seq_k);
+  if (config == fl::kQuarterConfig && !fl::quarter_config_fits(a))
+    return fail(FL_ERR_BAD_CONFIG, "%s: config %d needs N_k <= %d (got N_k %d)", who, (int)config,
+                fl::kQuarterMaxKeys, a.seq_k);
   if (empty_problem(a)) return FL_OK;
   rc = check_pointers(&p->base, &a, who, 16);
   if (rc != FL_OK) return rc;
@@ -351,6 +357,9 @@ int fl_attn_fwd_f16_cfg(const fl_attn_params* p, int32_t config, void* stream) {
   if (config == fl::kStreamConfig && !fl::stream_config_fits(a))
     return fail(FL_ERR_BAD_CONFIG, "fl_attn_fwd_f16: config %d needs N_k <= %d (got %d)",
                 (int)config, fl::kStreamMaxKeys, a.seq_k);
+  if (config == fl::kQuarterConfig && !fl::quarter_config_fits(a))
+    return fail(FL_ERR_BAD_CONFIG, "fl_attn_fwd_f16: config %d needs N_k <= %d (got %d)",
+                (int)config, fl::kQuarterMaxKeys, a.seq_k);
   if (empty_problem(a)) return FL_OK;
   rc = check_pointers(p, &a, "fl_attn_fwd_f16", 16);
   if (rc != FL_OK) return rc;

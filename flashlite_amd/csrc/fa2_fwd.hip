@@ -1,6 +1,6 @@
 // Tile configurations of the FA2 forward and their dispatch to the
 // schedule that implements each (fa2_pipe.hip, fa2_slot.hip, fa2_stream.hip,
-// fa2_d128.hip).  The dispatcher that picks a configuration for a problem is
+// fa2_short.hip, fa2_d128.hip).  The dispatcher that picks a configuration for a problem is
 // capi.hip's select_fa2.
 
 #include "fl_internal.h"
@@ -14,6 +14,7 @@ const Fa2Config kFa2Configs[kNumFa2Configs] = {
     {8, "br256_bc64_w8_slot"},
     {4, "br128_bc64_w4_slot"},
     {8, "br256_kv256_w8_stream"},
+    {4, "br32_kv512_w4_quarters"},
 };
 
 bool stream_config_fits(const FwdArgs& a) {
@@ -40,6 +41,7 @@ hipError_t launch_fa2(const FwdArgs& a, int cfg, hipStream_t stream) {
     case kSlotW8Config: return launch_slot(a, 8, stream);
     case kSlotW4Config: return launch_slot(a, 4, stream);
     case kStreamConfig: return launch_stream(a, stream);
+    case kQuarterConfig: return launch_quarter(a, stream);
     default: return hipErrorInvalidValue;
   }
 }

@@ -1,0 +1,122 @@
+// Key-quarter schedule for key ranges of at most 512 keys (configuration
+// br32_kv512_w4_quarters).  Shared building blocks: fa2_common.h.
+
+#include "fa2_common.h"
+
+namespace fl {
+
+namespace {
+
+// ---------------------------------------------------------------------------
+// Short key ranges (e.g. C1, B2 H8 N512): the one-pass configurations give
+// each wave 32 query rows and the whole key range, 8 tiles walked one after
+// another by a single wave per SIMD, on 64 work-groups for C1 (a quarter of
+// the CUs).  Here a work-group of 4 waves owns one 32-row query block and
+// wave w the key tiles [2w, 2w+2): a quarter of at most 512 keys.  Each wave
+// fetches its own two K and two V tiles into its own 32 KiB of LDS by DMA
+// and reads nothing another wave wrote, so no barrier precedes the compute;
+// Q goes straight to registers, its load overlapping the fetches.  Each
+// wave runs its tiles through the checked softmax (the stabiliser follows
+// the row max tile by tile, so no second pass), then the quarters' O, m and
+// l merge through LDS at their larger m: 1 into 0 and 3 into 2, then 2 into
+// 0, which stores.  C1 then runs 1024 waves of 2 tiles instead of 256 waves
+// of 8.  LDS: 4 x 32 KiB, one work-group per CU.
+constexpr int kQuarterTiles = 2;                           // key tiles per wave
+constexpr int kQuarterWaveBytes = 2 * kQuarterTiles * kTileBytes;  // K | V, 32 KiB
+
+template <bool CAUSAL, bool SCALED>
+__global__ void __launch_bounds__(256, 1)
+fa2_fwd_quarter_kernel(const _Float16* Q, const _Float16* __restrict__ K,
+                       const _Float16* __restrict__ V, _Float16* O, const Geom geom, int nqb,
+                       float cq, float cr) {
+  using RowsT = Rows<CAUSAL, SCALED, _Float16>;
+  using V8 = typename RowsT::V8;
+  static_assert(4 * kQuarterTiles * kBc == kQuarterMaxKeys, "key range");
+  __shared__ __attribute__((aligned(16))) uint8_t buf[4][kQuarterWaveBytes];
+
+  const int lane = threadIdx.x & 63;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // key quarter
+  const int bh = blockIdx.x / nqb, qb = blockIdx.x - bh * nqb;
+  const HeadPtrs<_Float16> hp = head_ptrs(geom, bh, Q, K, V, O);
+  const int seq = geom.seq_q;
+  const int q0 = 32 * qb;
+  int ntiles = (geom.seq_k + kBc - 1) / kBc;
+  if (CAUSAL) ntiles = min(ntiles, causal_tiles(min(q0 + 32, seq), geom.coff));
+  const int t0 = kQuarterTiles * w;
+  const int t1 = min(t0 + kQuarterTiles, ntiles);
+  uint8_t* const kb = buf[w];
+  uint8_t* const vb = buf[w] + kQuarterTiles * kTileBytes;
+
+  // This wave's K and V tiles, whole (8 segments each); rows >= N_k read
+  // as zeros through the buffer bound.
+  if (t0 < t1) {
+    const FetchOff<8> fk = fetch_offsets<8, false>(0, lane, 2 * geom.k_sr);
+    const FetchOff<8> fv = fetch_offsets<8, true>(0, lane, 2 * geom.v_sr);
+#pragma unroll
+    for (int i = 0; i < kQuarterTiles; ++i) {
+      fetch_tile<8>(hp.rk, kb + i * kTileBytes, t0 + i, t1 - 1, 0, fk);
+      fetch_tile<8>(hp.rv, vb + i * kTileBytes, t0 + i, t1 - 1, 0, fv);
+    }
+  }
+  RowsT rows;
+  rows.init(hp.q, geom.q_sr, lane, q0, seq, geom.seq_k, geom.coff, cq, cr);
+  if (t0 < t1) {
+    // This wave's own fetches have landed in LDS.
+    asm volatile("s_waitcnt vmcnt(0)" : : : "memory");
+    for (int t = t0; t < t1; ++t) {
+      float16_t S[2];
+      V8 P[2][2];
+      {
+        V8 ka[2][4];
+        rows.read_k(kb + (t - t0) * kTileBytes, ka);
+        rows.gemm1(ka, S);
+      }
+      rows.mask(t, S);
+      if (t == t0) rows.first_tile(S);
+      rows.softmax_checked(S, P);
+      {
+        V8 va[2][4];
+        rows.read_v(vb + (t - t0) * kTileBytes, va);
+        rows.gemm2(va, P);
+      }
+    }
+  }
+  // Merge tree through each sender's own (now idle) LDS.  A quarter with no
+  // visible key holds l = 0 and is skipped by the merge.
+  float* const part = reinterpret_cast<float*>(buf[w]);
+  asm volatile("s_waitcnt lgkmcnt(0)" : : : "memory");  // own LDS reads done
+  if (w & 1) rows.save_partial(part, lane);
+  __syncthreads();
+  if ((w & 1) == 0) rows.merge_partial(reinterpret_cast<const float*>(buf[w + 1]), lane);
+  asm volatile("s_waitcnt lgkmcnt(0)" : : : "memory");
+  if (w == 2) rows.save_partial(part, lane);
+  __syncthreads();
+  if (w != 0) return;
+  rows.merge_partial(reinterpret_cast<const float*>(buf[2]), lane);
+  rows.launder();
+  rows.store(hp.o, geom.o_sr, hp.lse);
+}
+
+struct QuarterLaunch {
+  template <bool C, bool S>
+  struct L {
+    static hipError_t run(const FwdArgs& a, const Geom& g, dim3 grid, int nqb, float cq, float cr,
+                          hipStream_t st) {
+      hipLaunchKernelGGL((fa2_fwd_quarter_kernel<C, S>), grid, dim3(256), 0, st,
+                         static_cast<const _Float16*>(a.q), static_cast<const _Float16*>(a.k),
+                         static_cast<const _Float16*>(a.v), static_cast<_Float16*>(a.o), g, nqb,
+                         cq, cr);
+      return hipSuccess;
+    }
+  };
+};
+
+}  // namespace
+
+// One 4-wave work-group per 32-row query block (grid B*H*ceil(N_q/32)).
+hipError_t launch_quarter(const FwdArgs& a, hipStream_t stream) {
+  if (!quarter_config_fits(a)) return hipErrorInvalidValue;
+  return dispatch<QuarterLaunch::L>(a, stream, 32);
+}
+
+}  // namespace fl

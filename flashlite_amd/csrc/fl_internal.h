@@ -51,7 +51,10 @@ constexpr int kSlotW4Config = 4;   // br128_bc64_w4_slot
 // fit one LDS buffer: needs N_k <= kStreamMaxKeys and row strides below
 // kStreamMaxRowStride elements (unit-relative 32-bit buffer offsets).
 constexpr int kStreamConfig = 5;   // br256_kv256_w8_stream
-constexpr int kNumFa2Configs = 6;
+// One 4-wave work-group per 32-row query block, each wave a quarter of at
+// most kQuarterMaxKeys keys (fp16, head_dim 64).
+constexpr int kQuarterConfig = 6;  // br32_kv512_w4_quarters
+constexpr int kNumFa2Configs = 7;
 extern const Fa2Config kFa2Configs[kNumFa2Configs];
 
 // Launches the FA2 kernel for configuration `cfg` on `stream`.  fp16 at
@@ -61,12 +64,15 @@ hipError_t launch_fa2(const FwdArgs& a, int cfg, hipStream_t stream);
 constexpr int kStreamMaxKeys = 256;
 constexpr int kStreamMaxRowStride = 1 << 22;
 bool stream_config_fits(const FwdArgs& a);
+constexpr int kQuarterMaxKeys = 512;
+inline bool quarter_config_fits(const FwdArgs& a) { return a.seq_k <= kQuarterMaxKeys; }
 
 // Per-schedule launchers behind launch_fa2 (one source file each).
 hipError_t launch_pipe(const FwdArgs& a, int cfg, hipStream_t stream);     // fa2_pipe.hip
 hipError_t launch_slot(const FwdArgs& a, int waves, hipStream_t stream);   // fa2_slot.hip
 hipError_t launch_slot_split(const FwdArgs& a, hipStream_t stream);        // fa2_slot.hip
 hipError_t launch_stream(const FwdArgs& a, hipStream_t stream);            // fa2_stream.hip
+hipError_t launch_quarter(const FwdArgs& a, hipStream_t stream);           // fa2_short.hip
 hipError_t launch_d128(const FwdArgs& a, int waves, hipStream_t stream);   // fa2_d128.hip
 
 // Split-KV ("flash-decoding"): `waves` (1, 2 or 4) waves of 32 query rows

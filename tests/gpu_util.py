@@ -17,10 +17,14 @@ SLOT_W4_CFG = capi.config_id("br128_bc64_w4_slot")
 SPLIT2_CFG = capi.config_id("br128_bc64_w4x2_slot")
 STREAM_CFG = capi.config_id("br256_kv256_w8_stream")
 STREAM_MAX_KEYS = 256
+QUARTER_CFG = capi.config_id("br32_kv512_w4_quarters")
+QUARTER_MAX_KEYS = 512
+# configuration -> the N_k limit it is built for (the others take any N_k)
+KEY_LIMITS = {STREAM_CFG: STREAM_MAX_KEYS, QUARTER_CFG: QUARTER_MAX_KEYS}
 
 
 def config_fits(config, n_k):
-    return config != STREAM_CFG or n_k <= STREAM_MAX_KEYS
+    return n_k <= KEY_LIMITS.get(config, n_k)
 
 
 def to_dev(x, dev):

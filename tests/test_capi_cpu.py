@@ -29,11 +29,11 @@ def test_library_loads_and_exports_header_symbols():
 
 
 def test_config_table():
-    assert capi.num_configs() == 6
-    names = [capi.config_name(i) for i in range(6)]
+    assert capi.num_configs() == 7
+    names = [capi.config_name(i) for i in range(7)]
     assert names == ["br32_bc64_w1", "br64_bc64_w2", "br128_bc64_w4x2_slot", "br256_bc64_w8_slot",
-                     "br128_bc64_w4_slot", "br256_kv256_w8_stream"]
-    assert capi.config_name(6) is None and capi.config_name(-1) is None
+                     "br128_bc64_w4_slot", "br256_kv256_w8_stream", "br32_kv512_w4_quarters"]
+    assert capi.config_name(7) is None and capi.config_name(-1) is None
     assert capi.config_id("br256_bc64_w8_slot") == 3
 
 
@@ -146,6 +146,11 @@ def test_bad_config():
     assert capi.fwd(_p(), config=-2) == capi.FL_ERR_BAD_CONFIG
     assert capi.fwd(_p(seq_q=256, seq_k=257), config=STREAM) == capi.FL_ERR_BAD_CONFIG
     assert "needs N_k <= 256" in capi.last_error()
+    quarter = capi.config_id("br32_kv512_w4_quarters")
+    assert capi.fwd(_p(seq_q=256, seq_k=513), config=quarter) == capi.FL_ERR_BAD_CONFIG
+    assert "needs N_k <= 512" in capi.last_error()
+    assert capi.fwd_ex(_ex(seq_k=4096), config=quarter) == capi.FL_ERR_BAD_CONFIG
+    assert "needs N_k <= 512" in capi.last_error()
 
 
 def test_empty_problems_are_noops():
@@ -166,7 +171,7 @@ def test_dispatcher_choices():
     sel = lambda **kw: capi.config_name(capi.select_config(_p(**kw)))  # noqa: E731
     W8, W4, SPLIT, STRM = ("br256_bc64_w8_slot", "br128_bc64_w4_slot", "br128_bc64_w4x2_slot",
                            "br256_kv256_w8_stream")
-    W1, W2 = "br32_bc64_w1", "br64_bc64_w2"
+    W1, W2, QTR = "br32_bc64_w1", "br64_bc64_w2", "br32_kv512_w4_quarters"
     # non-causal: 8-wave 256-row slot-scheduled groups when there is one per CU
     # and the key range is long
     assert sel(batch=2, heads=8, seq_q=4096) == W8      # 256 groups
@@ -185,11 +190,17 @@ def test_dispatcher_choices():
     assert sel(batch=1, heads=16, seq_q=16384, causal=True) == W4
     assert sel(batch=32, heads=32, seq_q=256, causal=True) == STRM   # streaming, any count
     assert sel(batch=1, heads=1, seq_q=128, causal=True) == STRM
-    assert sel(batch=1, heads=1, seq_q=257, causal=True) == W1     # N_k > 256
-    # small problems: smaller groups
-    assert sel(batch=2, heads=8, seq_q=512) == W4       # 64 groups of 128 rows
-    assert sel(batch=2, heads=4, seq_q=512) == W2       # 64 groups of 64 rows
-    assert sel(batch=1, heads=1, seq_q=257) == W1
+    # 256 < N_k <= 512 with at most one 32-row group per CU: key quarters
+    assert sel(batch=2, heads=8, seq_q=512) == QTR      # C1: 256 groups of 32 rows
+    assert sel(batch=2, heads=8, seq_q=512, causal=True) == QTR
+    assert sel(batch=1, heads=1, seq_q=257, causal=True) == QTR
+    assert sel(batch=1, heads=1, seq_q=257) == QTR
+    assert sel(batch=1, heads=1, seq_q=100, seq_k=512) == QTR
+    # more groups, or longer key ranges: 128-row or smaller groups
+    assert sel(batch=4, heads=8, seq_q=512) == W4       # 512 groups of 32 rows
+    assert sel(batch=2, heads=8, seq_q=513) == W4
+    assert sel(batch=2, heads=4, seq_q=600) == W2       # 80 groups of 64 rows
+    assert sel(batch=1, heads=1, seq_q=600) == W1
     assert capi.select_config(_p(head_dim=80)) == -1
 
 

@@ -56,7 +56,7 @@ RECT = [(1, 1), (1, 300), (5, 64), (37, 100), (100, 37), (64, 65), (200, 513), (
 def test_rectangular_each_config(cuda, config, nq, nk, causal):
     q, k, v = _qkv(1, 2, nq, nk, seed=nq * 7 + nk)
     if not config_fits(config, nk):
-        with pytest.raises(RuntimeError, match="needs N_k <= 256"):
+        with pytest.raises(RuntimeError, match="needs N_k <= "):
             _run(q, k, v, 0.125, causal, cuda, config=config, lse=True)
         return
     out, lse = _run(q, k, v, 0.125, causal, cuda, config=config, lse=True)

@@ -60,12 +60,14 @@ def test_wide_config_checks():
                 continue  # fp16 at D = 64 has every configuration
             slots = (capi.config_id("br256_bc64_w8_slot"), capi.config_id("br128_bc64_w4_slot"))
             stream_cfg = capi.config_id("br256_kv256_w8_stream")
+            quarter_cfg = capi.config_id("br32_kv512_w4_quarters")
             for cfg in range(capi.num_configs()):
-                if cfg in slots or cfg == stream_cfg:
+                if cfg in slots or cfg in (stream_cfg, quarter_cfg):
                     continue
                 assert fn(_ex(head_dim=d), config=cfg) == capi.FL_ERR_BAD_CONFIG
                 assert "not built" in capi.last_error() and who in capi.last_error()
             assert fn(_ex(head_dim=d), config=stream_cfg) == capi.FL_ERR_BAD_CONFIG
+            assert fn(_ex(head_dim=d), config=quarter_cfg) == capi.FL_ERR_BAD_CONFIG
         for d in (32, 96, 256):
             assert fn(_ex(head_dim=d)) == capi.FL_ERR_UNSUPPORTED
             assert "head_dim must be 64 or 128" in capi.last_error()
