@@ -20,19 +20,21 @@ namespace {
 // the row max tile by tile, so no second pass), then the quarters' O, m and
 // l merge through LDS at their larger m: 1 into 0 and 3 into 2, then 2 into
 // 0, which stores.  C1 then runs 1024 waves of 2 tiles instead of 256 waves
-// of 8.  LDS: 4 x 32 KiB, one work-group per CU.
-constexpr int kQuarterTiles = 2;                           // key tiles per wave
-constexpr int kQuarterWaveBytes = 2 * kQuarterTiles * kTileBytes;  // K | V, 32 KiB
+// of 8.  LDS: 4 x 32 KiB, one work-group per CU.  (Eight waves of one tile
+// each, two per SIMD and one more merge step, measured 7% slower on C1.)
+constexpr int kQuarterWaves = 4;
 
-template <bool CAUSAL, bool SCALED>
-__global__ void __launch_bounds__(256, 1)
+template <int NW, bool CAUSAL, bool SCALED>
+__global__ void __launch_bounds__(64 * NW, 1)
 fa2_fwd_quarter_kernel(const _Float16* Q, const _Float16* __restrict__ K,
                        const _Float16* __restrict__ V, _Float16* O, const Geom geom, int nqb,
                        float cq, float cr) {
   using RowsT = Rows<CAUSAL, SCALED, _Float16>;
   using V8 = typename RowsT::V8;
-  static_assert(4 * kQuarterTiles * kBc == kQuarterMaxKeys, "key range");
-  __shared__ __attribute__((aligned(16))) uint8_t buf[4][kQuarterWaveBytes];
+  constexpr int kQuarterTiles = kQuarterMaxKeys / kBc / NW;  // key tiles per wave
+  constexpr int kQuarterWaveBytes = 2 * kQuarterTiles * kTileBytes;
+  static_assert(NW * kQuarterTiles * kBc == kQuarterMaxKeys, "key range");
+  __shared__ __attribute__((aligned(16))) uint8_t buf[NW][kQuarterWaveBytes];
 
   const int lane = threadIdx.x & 63;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // key quarter
@@ -81,18 +83,18 @@ fa2_fwd_quarter_kernel(const _Float16* Q, const _Float16* __restrict__ K,
       }
     }
   }
-  // Merge tree through each sender's own (now idle) LDS.  A quarter with no
+  // Merge tree through each sender's own (now idle) LDS: at step s wave w
+  // with w % 2s == s hands its range to wave w - s.  A range with no
   // visible key holds l = 0 and is skipped by the merge.
   float* const part = reinterpret_cast<float*>(buf[w]);
-  asm volatile("s_waitcnt lgkmcnt(0)" : : : "memory");  // own LDS reads done
-  if (w & 1) rows.save_partial(part, lane);
-  __syncthreads();
-  if ((w & 1) == 0) rows.merge_partial(reinterpret_cast<const float*>(buf[w + 1]), lane);
-  asm volatile("s_waitcnt lgkmcnt(0)" : : : "memory");
-  if (w == 2) rows.save_partial(part, lane);
-  __syncthreads();
+#pragma unroll
+  for (int s = 1; s < NW; s *= 2) {
+    asm volatile("s_waitcnt lgkmcnt(0)" : : : "memory");  // own LDS reads done
+    if ((w & (2 * s - 1)) == s) rows.save_partial(part, lane);
+    __syncthreads();
+    if ((w & (2 * s - 1)) == 0) rows.merge_partial(reinterpret_cast<const float*>(buf[w + s]), lane);
+  }
   if (w != 0) return;
-  rows.merge_partial(reinterpret_cast<const float*>(buf[2]), lane);
   rows.launder();
   rows.store(hp.o, geom.o_sr, hp.lse);
 }
@@ -102,7 +104,8 @@ struct QuarterLaunch {
   struct L {
     static hipError_t run(const FwdArgs& a, const Geom& g, dim3 grid, int nqb, float cq, float cr,
                           hipStream_t st) {
-      hipLaunchKernelGGL((fa2_fwd_quarter_kernel<C, S>), grid, dim3(256), 0, st,
+      hipLaunchKernelGGL((fa2_fwd_quarter_kernel<kQuarterWaves, C, S>), grid,
+                         dim3(64 * kQuarterWaves), 0, st,
                          static_cast<const _Float16*>(a.q), static_cast<const _Float16*>(a.k),
                          static_cast<const _Float16*>(a.v), static_cast<_Float16*>(a.o), g, nqb,
                          cq, cr);
