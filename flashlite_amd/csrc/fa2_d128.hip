@@ -18,10 +18,21 @@ namespace {
 constexpr int kBc2 = 32;
 constexpr int kRowBytes2 = 2 * kD2;  // 256
 
+// LDS swizzles of 256-byte rows.  A row is one whole sweep of the 64 banks,
+// so unlike the 128-byte rows of D = 64 the row index does not move a read
+// to other banks: the swizzles must use all 4 bits of the 16-byte chunk
+// index.  K (ds_read_b128, 16 lanes = 16 rows per pass): chunk ^ (row % 16)
+// puts the 16 rows of a pass on 16 different chunks.  V (ds_read_b64_tr_b16:
+// 2 key-rows x 2 lane groups x 4 chunks x 2 halves per 32-lane pass): the
+// D = 64 pattern (row bits 0-1 on chunk bits 1-2) plus row bit 0 on chunk
+// bit 3.  Both are conflict-free for every lane pattern of read_k_op and
+// read_v_op (the D = 64 swizzles left 2-way conflicts on both).
+__device__ __forceinline__ int k_swz128(int row) { return row & 15; }
+__device__ __forceinline__ int v_swz128(int row) { return ((row & 3) << 1) | ((row & 1) << 3); }
+
 // DMA lane offsets for 256-byte rows: segment i of wave w is rows
 // 4(w kSegs + i) .. +3; lane l lands at byte 16 l of it, i.e. row l/16,
-// physical chunk l%16, which holds logical chunk (l%16) ^ swz(row) (the
-// swizzles flip the low 3 chunk bits only).
+// physical chunk l%16, which holds logical chunk (l%16) ^ swz(row).
 template <int kSegs, bool IS_V>
 __device__ __forceinline__ FetchOff<kSegs> fetch_offsets128(int wave, int lane, int row_bytes) {
   FetchOff<kSegs> f;
@@ -30,7 +41,7 @@ __device__ __forceinline__ FetchOff<kSegs> fetch_offsets128(int wave, int lane, 
     const int seg = wave * kSegs + i;
     const int row = 4 * seg + (lane >> 4);
     const int phys = lane & 15;
-    const int logical = phys ^ (IS_V ? v_swz(row) : k_swz(row));
+    const int logical = phys ^ (IS_V ? v_swz128(row) : k_swz128(row));
     f.lane[i] = row * row_bytes + 16 * logical;
     asm volatile("" : "+v"(f.lane[i]));
   }
@@ -97,15 +108,15 @@ struct Rows128 {
   }
   __device__ __forceinline__ V8 read_k_op(const uint8_t* kt, int st) const {
     const int ch = 2 * st + g;
-    return *reinterpret_cast<const V8*>(kt + col * kRowBytes2 + 16 * (ch ^ k_swz(col)));
+    return *reinterpret_cast<const V8*>(kt + col * kRowBytes2 + 16 * (ch ^ k_swz128(col)));
   }
   __device__ __forceinline__ V8 read_v_op(const uint8_t* vt, int db, int t) const {
     const int r1 = 16 * t + tr_row;
     const int r2 = r1 + 8;
     const int dcol = 32 * db + tr_col;
     const int ch = dcol >> 3, hb = ((dcol >> 2) & 1) * 8;
-    const V4 lo = lds_read_tr<V4>(vt + r1 * kRowBytes2 + 16 * (ch ^ v_swz(r1)) + hb);
-    const V4 hi = lds_read_tr<V4>(vt + r2 * kRowBytes2 + 16 * (ch ^ v_swz(r2)) + hb);
+    const V4 lo = lds_read_tr<V4>(vt + r1 * kRowBytes2 + 16 * (ch ^ v_swz128(r1)) + hb);
+    const V4 hi = lds_read_tr<V4>(vt + r2 * kRowBytes2 + 16 * (ch ^ v_swz128(r2)) + hb);
     return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
   }
   // Slot map: L even, GEMM1 head-dim step L/2 of the next tile (one chain,

@@ -136,7 +136,9 @@ torch::Tensor flash_attn_forward_flash2(torch::Tensor q, torch::Tensor k, torch:
 // N_k != N_q (bottom-right causal), optionally the fp32 log-sum-exp
 // [B, H, N_q], and split-KV for few query rows over many keys.  Returns
 // `out`, or (out, lse) with return_lse.  An omitted `out` is allocated with
-// q's layout (empty_like keeps dense strides).
+// q's layout (empty_like keeps dense strides); an omitted `lse` (with
+// return_lse) as a contiguous fp32 [B, H, N_q] tensor.  Passing both keeps
+// the call free of allocations (apart from a split-KV workspace, see below).
 // num_splits: 0 = the library's choice, 1 = one pass, n > 1 = n key chunks.
 // A split-KV call needs a workspace: `workspace` (any device tensor of
 // enough bytes, reused across calls for an allocation-free loop) or else
@@ -145,7 +147,8 @@ py::object flash_attn_forward_flash2_ex(torch::Tensor q, torch::Tensor k, torch:
                                         double sm_scale, bool is_causal,
                                         std::optional<torch::Tensor> out, bool return_lse,
                                         int64_t num_splits,
-                                        std::optional<torch::Tensor> workspace) {
+                                        std::optional<torch::Tensor> workspace,
+                                        std::optional<torch::Tensor> lse_out) {
   TORCH_CHECK(q.is_cuda() && k.is_cuda() && v.is_cuda(), "All tensors must be on CUDA");
   const auto dt = q.scalar_type();
   TORCH_CHECK((dt == torch::kHalf || dt == torch::kBFloat16) && k.scalar_type() == dt &&
@@ -178,7 +181,17 @@ py::object flash_attn_forward_flash2_ex(torch::Tensor q, torch::Tensor k, torch:
     out_tensor = torch::empty_like(q);
   }
   torch::Tensor lse;
-  if (return_lse)
+  const bool lse_given = lse_out.has_value() && lse_out.value().defined();
+  TORCH_CHECK(!lse_given || return_lse, "lse= needs return_lse=True");
+  if (lse_given) {
+    lse = lse_out.value();
+    TORCH_CHECK(lse.is_cuda() && lse.device() == q.device(),
+                "lse tensor must be on the same device as q");
+    TORCH_CHECK(lse.scalar_type() == torch::kFloat32, "lse tensor dtype must be float32");
+    TORCH_CHECK(lse.dim() == 3 && lse.size(0) == batch_size && lse.size(1) == num_heads &&
+                    lse.size(2) == q.size(2) && lse.is_contiguous(),
+                "lse tensor must be a contiguous [B, H, N_q] tensor");
+  } else if (return_lse)
     lse = torch::empty({batch_size, num_heads, q.size(2)},
                        q.options().dtype(torch::kFloat32).memory_format(torch::MemoryFormat::Contiguous));
 
@@ -239,7 +252,7 @@ PYBIND11_MODULE(flash_attn_wmma, m) {
         "N_k != N_q (bottom-right causal), optional log-sum-exp",
         py::arg("q"), py::arg("k"), py::arg("v"), py::arg("sm_scale") = 0.0,
         py::arg("is_causal") = false, py::arg("out") = py::none(), py::arg("return_lse") = false,
-        py::arg("num_splits") = 0, py::arg("workspace") = py::none());
+        py::arg("num_splits") = 0, py::arg("workspace") = py::none(), py::arg("lse") = py::none());
 
   m.def("splitkv_workspace_bytes",
         [](torch::Tensor q, torch::Tensor k, bool is_causal, int64_t num_splits) {

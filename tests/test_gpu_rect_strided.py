@@ -196,3 +196,33 @@ def test_lse_scales(cuda, scale, sm):
         mag = np.abs(ref_lse)
         assert mx <= LSE_MAX_ABS + 2.0 ** -11 * mag.max(), f"lse max-abs {mx:.3e}"
         assert mean <= LSE_MEAN_ABS + 2.0 ** -11 * mag.mean(), f"lse mean-abs {mean:.3e}"
+
+
+def test_binding_lse_out(cuda):
+    """forward_flash2_ex(..., return_lse=True, lse=buf) writes the log-sum-exp
+    into `buf` (no allocation) with the same values as an allocated one, and
+    rejects a wrong dtype, shape, layout or a missing return_lse."""
+    import torch
+
+    import flashlite_amd as fl
+
+    q16, k16, v16 = _qkv(2, 3, 200, 333, seed=14)
+    q, k, v = (to_dev(x, cuda) for x in (q16, k16, v16))
+    for causal in (False, True):
+        ref_o, ref_l = fl.forward_flash2_ex(q, k, v, 0.125, causal, return_lse=True)
+        out = torch.empty_like(q)
+        buf = torch.full((2, 3, 200), float("nan"), dtype=torch.float32, device=cuda)
+        got_o, got_l = fl.forward_flash2_ex(q, k, v, 0.125, causal, out=out, return_lse=True,
+                                            lse=buf)
+        torch.cuda.synchronize()
+        assert got_l.data_ptr() == buf.data_ptr() and got_o.data_ptr() == out.data_ptr()
+        assert torch.equal(got_l, ref_l) and torch.equal(got_o, ref_o)
+    bad = [(torch.empty((2, 3, 200), dtype=torch.float16, device=cuda), "float32"),
+           (torch.empty((2, 3, 199), dtype=torch.float32, device=cuda), r"\[B, H, N_q\]"),
+           (torch.empty((2, 200, 3), dtype=torch.float32, device=cuda).transpose(1, 2),
+            r"\[B, H, N_q\]")]
+    for t, msg in bad:
+        with pytest.raises(RuntimeError, match=msg):
+            fl.forward_flash2_ex(q, k, v, return_lse=True, lse=t)
+    with pytest.raises(RuntimeError, match="return_lse"):
+        fl.forward_flash2_ex(q, k, v, lse=torch.empty((2, 3, 200), device=cuda))
