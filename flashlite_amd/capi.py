@@ -31,8 +31,6 @@ EXPORTED = (
     "fl_attn_select_config",
     "fl_attn_fwd_f16_ex",
     "fl_attn_fwd_bf16_ex",
-    "fl_attn_fwd_workspace_bytes",
-    "fl_attn_fwd_f16_ws",
     "fl_attn_splitkv_workspace_bytes",
     "fl_attn_fwd_f16_splitkv",
     "fl_attn_fwd_f16_splitkv_noalloc",
@@ -110,11 +108,6 @@ def load(path: str = LIB_PATH) -> ctypes.CDLL:
     lib.fl_attn_fwd_bf16_ex.argtypes = [ctypes.POINTER(FlAttnParamsEx), ctypes.c_int32,
                                         ctypes.c_void_p]
     lib.fl_attn_fwd_bf16_ex.restype = ctypes.c_int
-    lib.fl_attn_fwd_workspace_bytes.argtypes = [ctypes.POINTER(FlAttnParamsEx)]
-    lib.fl_attn_fwd_workspace_bytes.restype = ctypes.c_int64
-    lib.fl_attn_fwd_f16_ws.argtypes = [ctypes.POINTER(FlAttnParamsEx), ctypes.c_void_p,
-                                       ctypes.c_int64, ctypes.c_void_p]
-    lib.fl_attn_fwd_f16_ws.restype = ctypes.c_int
     lib.fl_attn_splitkv_workspace_bytes.argtypes = [ctypes.POINTER(FlAttnParamsEx), ctypes.c_int32]
     lib.fl_attn_splitkv_workspace_bytes.restype = ctypes.c_int64
     lib.fl_attn_fwd_f16_splitkv.argtypes = [ctypes.POINTER(FlAttnParamsEx), ctypes.c_int32,
@@ -158,18 +151,6 @@ def fwd_ex(params: FlAttnParamsEx, stream: int = 0, config: int = -1) -> int:
 def fwd_bf16_ex(params: FlAttnParamsEx, stream: int = 0, config: int = -1) -> int:
     """``fl_attn_fwd_bf16_ex``; returns the status code."""
     return load().fl_attn_fwd_bf16_ex(ctypes.byref(params), config, stream or None)
-
-
-def fwd_workspace_bytes(params: FlAttnParamsEx) -> int:
-    """``fl_attn_fwd_workspace_bytes``: 0 = no workspace used, -1 = rejected."""
-    return load().fl_attn_fwd_workspace_bytes(ctypes.byref(params))
-
-
-def fwd_ws(params: FlAttnParamsEx, workspace: int, workspace_bytes: int, stream: int = 0) -> int:
-    """``fl_attn_fwd_f16_ws`` (zero-filled workspace, left zero-filled);
-    returns the status code."""
-    return load().fl_attn_fwd_f16_ws(ctypes.byref(params), workspace or None, workspace_bytes,
-                                     stream or None)
 
 
 def splitkv_workspace_bytes(params: FlAttnParamsEx, num_splits: int = 0) -> int:

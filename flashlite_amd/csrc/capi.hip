@@ -263,16 +263,6 @@ int select_any(const fl::FwdArgs& a) {
                                                            : fl::kSlotW4Config;
 }
 
-// The causal pair schedule (fl::launch_slot_pair) replaces the 128-row
-// slot configuration where its shape fits and its work-groups fill the CUs
-// in one round (two per CU); with more rounds the one-block-per-work-group
-// launch, dispatched heaviest first, balances as well by itself.
-bool use_pair(const fl::FwdArgs& a) {
-  constexpr int64_t kSlots = 2 * 256;
-  return fl::pair_fits(a) && select_fa2(a) == fl::kSlotW4Config &&
-         (int64_t)a.batch_heads * (a.seq / 128) <= kSlots;
-}
-
 int fwd_ex(const fl_attn_params_ex* p, int32_t config, void* stream, int dtype, const char* who) {
   fl::FwdArgs a;
   int rc = check_ex(p, &a, who, /*wide=*/true);
@@ -390,37 +380,6 @@ int fl_attn_fwd_f16_ex(const fl_attn_params_ex* p, int32_t config, void* stream)
 
 int fl_attn_fwd_bf16_ex(const fl_attn_params_ex* p, int32_t config, void* stream) {
   return fwd_ex(p, config, stream, fl::kDtypeBF16, "fl_attn_fwd_bf16_ex");
-}
-
-int64_t fl_attn_fwd_workspace_bytes(const fl_attn_params_ex* p) {
-  fl::FwdArgs a;
-  if (check_ex(p, &a, "fl_attn_fwd_workspace_bytes") != FL_OK) return -1;
-  return use_pair(a) ? fl::pair_workspace_bytes(a) : 0;
-}
-
-int fl_attn_fwd_f16_ws(const fl_attn_params_ex* p, void* workspace, int64_t workspace_bytes,
-                       void* stream) {
-  const char* who = "fl_attn_fwd_f16_ws";
-  fl::FwdArgs a;
-  int rc = check_ex(p, &a, who);
-  if (rc != FL_OK) return rc;
-  if (empty_problem(a)) return FL_OK;
-  rc = check_pointers(&p->base, &a, who, 16);
-  if (rc != FL_OK) return rc;
-  hipError_t e;
-  if (use_pair(a)) {
-    const int64_t need = fl::pair_workspace_bytes(a);
-    if (workspace == nullptr || workspace_bytes < need)
-      return fail(FL_ERR_INVALID_ARGUMENT, "%s: workspace of %lld bytes needed (got %lld%s)", who,
-                  (long long)need, (long long)workspace_bytes, workspace == nullptr ? ", NULL" : "");
-    if ((uintptr_t)workspace & 255)
-      return fail(FL_ERR_MISALIGNED, "%s: workspace must be 256-byte aligned", who);
-    e = fl::launch_slot_pair(a, workspace, static_cast<hipStream_t>(stream));
-  } else {
-    e = fl::launch_fa2(a, select_fa2(a), static_cast<hipStream_t>(stream));
-  }
-  if (e != hipSuccess) return fail(FL_ERR_LAUNCH, "%s: launch failed: %s", who, hipGetErrorString(e));
-  return FL_OK;
 }
 
 int64_t fl_attn_splitkv_workspace_bytes(const fl_attn_params_ex* p, int32_t num_splits) {

@@ -1,9 +1,7 @@
 // Diagnostic (not on the product path): the slot-scheduled kernels built
-// with per-wave timeline stamps.  Each wave's lane 0 writes 8 uint64 per
-// segment (one, or two for the second work-group of a causal pair) at
-// out[8 * (2 * (group * waves_per_group + wave) + segment)]:
+// with per-wave timeline stamps.  Each wave's lane 0 writes 8 uint64 at
+// out[8 * (group * waves_per_group + wave)]:
 //   [0..4] s_memrealtime at entry, first pass, loop start, loop end, store
-//          (for a pair segment: after the meeting, before the store)
 //   [5]    s_memrealtime after the wave's last store has completed
 //   [6]    s_memtime (shader clock) cycles spent in the loop
 //   [7]    iterations << 48 | XCC_ID << 32 | HW_ID
@@ -29,8 +27,7 @@ __device__ unsigned long long* g_fl_timeline;
     __builtin_amdgcn_s_waitcnt(0);                                                          \
     const unsigned long long t_exit = __builtin_amdgcn_s_memrealtime();                     \
     if ((lane) == 0) {                                                                      \
-      unsigned long long* d_ =                                                              \
-          g_fl_timeline + 8 * (2 * ((long long)blockIdx.x * (wpg) + (wave)) + seg);           \
+      unsigned long long* d_ = g_fl_timeline + 8 * ((long long)blockIdx.x * (wpg) + (wave)); \
       const unsigned hw_ = __builtin_amdgcn_s_getreg((31 << 11) | 4);  /* HW_ID */          \
       const unsigned xcc_ = __builtin_amdgcn_s_getreg((31 << 11) | 20); /* XCC_ID */        \
       d_[0] = t_entry;                                                                      \
@@ -48,30 +45,26 @@ __device__ unsigned long long* g_fl_timeline;
 // The instrumented copies get their own launcher names.
 #define launch_slot diag_timeline_launch_slot
 #define launch_slot_split diag_timeline_launch_slot_split
-#define launch_slot_pair diag_timeline_launch_slot_pair
 #include "fa2_slot.hip"
 #undef launch_slot
 #undef launch_slot_split
-#undef launch_slot_pair
 
 extern "C" {
 
 // Contiguous fp16 [B, H, N, 64] q, k, v, o; sm_scale 1/8.  mode 8 / 4: the
 // br256_bc64_w8_slot / br128_bc64_w4_slot configurations; 2: the key-range
-// split br128_bc64_w4x2_slot; 1: the causal pair schedule (N a multiple of
-// 256, `ws` its zero-filled workspace).  `out` holds `out_entries` uint64,
-// at least 16 per wave of the grid (B*H*ceil(N/256) groups of 8 waves for
-// mode 8, B*H*ceil(N/128) groups of 4 or 8 waves for modes 4, 2 and 1).
-// Returns a hipError_t.
+// split br128_bc64_w4x2_slot.  `out` holds `out_entries` uint64, at least 8
+// per wave of the grid (B*H*ceil(N/256) groups of 8 waves for mode 8,
+// B*H*ceil(N/128) groups of 4 or 8 waves for modes 4 and 2).  Returns a
+// hipError_t.
 int fl_diag_slot_timeline(int mode, int causal, const void* q, const void* k, const void* v,
                           void* o, int B, int H, int N, void* out, long long out_entries,
-                          void* stream, void* ws) {
-  if ((mode != 8 && mode != 4 && mode != 2 && mode != 1) || B < 1 || H < 1 || N < 1 ||
-      out == nullptr || (mode == 1 && (ws == nullptr || !causal || N % 256 != 0)))
+                          void* stream) {
+  if ((mode != 8 && mode != 4 && mode != 2) || B < 1 || H < 1 || N < 1 || out == nullptr)
     return (int)hipErrorInvalidValue;
   const long long rows = mode == 8 ? 256 : 128;
-  const long long waves = (mode == 4 || mode == 1) ? 4 : 8;
-  if (out_entries < 16 * waves * (long long)B * H * ((N + rows - 1) / rows))
+  const long long waves = mode == 4 ? 4 : 8;
+  if (out_entries < 8 * waves * (long long)B * H * ((N + rows - 1) / rows))
     return (int)hipErrorInvalidValue;
   hipError_t e = hipMemcpyToSymbol(HIP_SYMBOL(g_fl_timeline), &out, sizeof(out));
   if (e != hipSuccess) return (int)e;
@@ -94,9 +87,8 @@ int fl_diag_slot_timeline(int mode, int causal, const void* q, const void* k, co
   a.q_sh = a.k_sh = a.v_sh = a.o_sh = (int64_t)N * 64;
   a.q_sb = a.k_sb = a.v_sb = a.o_sb = (int64_t)H * N * 64;
   const auto st = static_cast<hipStream_t>(stream);
-  e = mode == 1   ? fl::diag_timeline_launch_slot_pair(a, ws, st)
-      : mode == 2 ? fl::diag_timeline_launch_slot_split(a, st)
-                  : fl::diag_timeline_launch_slot(a, mode, st);
+  e = mode == 2 ? fl::diag_timeline_launch_slot_split(a, st)
+                : fl::diag_timeline_launch_slot(a, mode, st);
   return (int)e;
 }
 

@@ -844,61 +844,6 @@ struct Rows {
       for (int r = 0; r < 16; ++r) o[db][r] = a0 * o[db][r] + a1 * part[(16 * db + r) * 64 + lane];
     m = mm;
   }
-  // The same exchange with another work-group through device memory
-  // (save_partial / merge_partial layout).  Every access is a relaxed
-  // device-scope atomic, coherent by itself across XCDs with no cache-wide
-  // write-back or invalidation; the caller orders the stores before its
-  // flag (by waiting for them) and the loads after it.  The merge fuses the
-  // lower key range's term, lo_scale * x_lo + (hi_scale * x_hi rounded), so
-  // the result has the same bits whichever work-group holds which range.
-  __device__ __forceinline__ void save_partial_coherent(float* part, int lane) const {
-    auto put = [&](int i, float x) {
-      __hip_atomic_store(part + i, x, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    };
-#pragma unroll
-    for (int db = 0; db < 2; ++db)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) put((16 * db + r) * 64 + lane, o[db][r]);
-    put(32 * 64 + lane, m);
-    put(33 * 64 + lane, l);
-  }
-  __device__ __forceinline__ void merge_partial_coherent(const float* part, int lane,
-                                                         bool self_lower) {
-    auto get = [&](int i) {
-      return __hip_atomic_load(part + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    };
-    float po[32];
-#pragma unroll
-    for (int i = 0; i < 32; ++i) po[i] = get(i * 64 + lane);
-    const float m1 = get(32 * 64 + lane), l1 = get(33 * 64 + lane);
-    const bool has0 = pair_sum(l) > 0.0f;
-    const bool has1 = pair_sum(l1) > 0.0f;
-    const float mm = has0 ? (has1 ? fmaxf(m, m1) : m) : m1;
-    const float k = SCALED ? cr : 1.0f;
-    const float a0 = has0 ? __builtin_amdgcn_exp2f(k * (m - mm)) : 0.0f;
-    const float a1 = has1 ? __builtin_amdgcn_exp2f(k * (m1 - mm)) : 0.0f;
-    auto mix = [&](float self, float other) {
-      return self_lower ? __builtin_fmaf(a0, self, a1 * other)
-                        : __builtin_fmaf(a1, other, a0 * self);
-    };
-    l = mix(l, l1);
-#pragma unroll
-    for (int db = 0; db < 2; ++db)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) o[db][r] = mix(o[db][r], po[16 * db + r]);
-    m = mm;
-  }
-  // NaN in O, m and l: the rows are written as NaN (a result that could not
-  // be completed is never passed off as a finite one).
-  __device__ __forceinline__ void poison() {
-    const float nan = __builtin_nanf("");
-#pragma unroll
-    for (int db = 0; db < 2; ++db)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) o[db][r] = nan;
-    m = nan;
-    l = nan;
-  }
   // Split-KV partial of the rows over one key chunk: O unnormalised
   // (relative to the stabiliser), the stabiliser in base-2 logit units
   // (m * cr) and the row sum, kPartStride floats per row.  A row with no key

@@ -21,117 +21,6 @@ namespace fl {
 namespace {
 
 // ---------------------------------------------------------------------------
-// Causal pair schedule (PAIR, configuration br128_bc64_w4_pair; causal,
-// N_q = N_k = 128 nqb, nqb even).  Block qb of a head sees n(qb) = 2qb + 2
-// key tiles, so blocks hi = nqb-1-p and lo = p (p < nqb/2) carry
-// T = n(hi) + n(lo) = 2 nqb + 2 tiles together.  Two work-groups share
-// each pair: member 0 walks the first h of the pair's T tiles (block hi's,
-// then block lo's), member 1 the rest, so at most one block is cut between
-// them.  With two co-resident work-groups per CU neither ever runs alone
-// at one wave per SIMD for long, which is
-// where the one-block-per-work-group causal launch loses its time (its
-// heaviest block's CU finishes last).  h is above T/2 (kPairNum / 128 of
-// T): the older of two work-groups on a CU issues first, so member 0 (the
-// older) progresses faster while both run.
-// The two members meet over the cut block in the caller's workspace, each
-// at the end of its walk: member 0 (whose walk ends with the lower range)
-// stores its O, m and l there (Rows::save_partial_coherent) and raises the
-// pair's flag; member 1 (whose walk ends with the upper range) waits for
-// the flag, merges and writes the block.  Member 0 never waits, and it is
-// dispatched first (pair_coords: the same XCD, an earlier position), so
-// member 1's wait always ends; it is also bounded in time (kPairWaitTicks
-// of the 100 MHz s_memrealtime clock), after which member 1 writes NaN to
-// the block instead of a wrong result.  Member 0 usually finishes first:
-// it is the older of the two work-groups on a CU and issues first.
-#ifndef FL_PAIR_NUM
-#define FL_PAIR_NUM 74
-#endif
-constexpr int kPairNum = FL_PAIR_NUM;
-constexpr int kPairPartFloats = 34 * 64;  // one wave: O (32 x 64), m, l
-constexpr unsigned long long kPairWaitTicks = 10000000;  // 100 ms
-
-// One segment of a pair member's walk: block qb, key tiles [tbeg, tend);
-// role 0 = the whole block, 1 / 2 = the lower / upper key range of the cut
-// block (always the walk's last segment).
-struct PairSeg {
-  int qb, tbeg, tend, role;
-};
-
-__device__ __forceinline__ int pair_cut(int nqb) {
-  const int t = 2 * nqb + 2;
-  return min(max(t * kPairNum / 128, 1), t - 1);
-}
-
-__device__ __forceinline__ int pair_nseg(int nqb, int p, int member) {
-  const int n_hi = 2 * (nqb - p), h = pair_cut(nqb);
-  return 1 + (member == 0 ? (h > n_hi) : (h < n_hi));
-}
-
-__device__ __forceinline__ PairSeg pair_seg(int nqb, int p, int member, int seg) {
-  const int hi = nqb - 1 - p, n_hi = 2 * hi + 2, n_lo = 2 * p + 2;
-  const int h = pair_cut(nqb);
-  if (member == 0)
-    return seg == 0 ? PairSeg{hi, 0, min(h, n_hi), h < n_hi ? 1 : 0} : PairSeg{p, 0, h - n_hi, 1};
-  if (h < n_hi) return seg == 0 ? PairSeg{p, 0, n_lo, 0} : PairSeg{hi, h, n_hi, 2};
-  return PairSeg{p, h - n_hi, n_lo, h > n_hi ? 2 : 0};
-}
-
-// Work-group -> (batch*head, pair p, member).  Whole heads per XCD (the
-// shapes the pair schedule takes): an XCD's first half of work-groups are
-// the members 0 of its pairs and the second half the members 1 in the same
-// order, so each member 0 is dispatched before its member 1 on the same
-// XCD, and a CU's two slots (filled in the same CU order, see wg_coords)
-// hold the two members of one pair.
-__device__ __forceinline__ void pair_coords(int nqb, int& bh, int& p, int& member) {
-  const int per = gridDim.x >> 3;
-  const int hx = per / nqb;  // whole heads per XCD
-  const int half = per >> 1;
-  const int i = blockIdx.x;
-  const int k = i >> 3;      // dispatch position within the XCD
-  member = k >= half ? 1 : 0;
-  const int r = k - member * half;
-  bh = (i & 7) * hx + r % hx;
-  p = r / hx;
-}
-
-// Member 0, at the end of its walk: the partials of the cut block, then the
-// flag.  Every access to the workspace is a relaxed device-scope atomic
-// (coherent by itself across XCDs, with no cache-wide write-back); the
-// partial stores are ordered before the flag by waiting for them.
-template <class R>
-__device__ __forceinline__ void pair_publish(unsigned* flag, float* part, int lane, const R& rows) {
-  rows.save_partial_coherent(part, lane);
-  __builtin_amdgcn_s_waitcnt(0);  // this wave's partial stores acknowledged ...
-  __syncthreads();                // ... and every wave's, before the flag
-  if (threadIdx.x == 0) __hip_atomic_store(flag, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-// Member 1, at the end of its walk: wait for the flag, clear it for the
-// next call, merge.  `seen` is an LDS word no wave reads or fetches into at
-// this point.
-template <class R>
-__device__ __forceinline__ void pair_merge(unsigned* flag, const float* part, int lane, R& rows,
-                                           int* seen) {
-  if (threadIdx.x == 0) {
-    const unsigned long long t0 = __builtin_amdgcn_s_memrealtime();
-    int ok = 0;
-    for (;;) {
-      if (__hip_atomic_load(flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0u) {
-        ok = 1;
-        break;
-      }
-      if (__builtin_amdgcn_s_memrealtime() - t0 > kPairWaitTicks) break;
-      __builtin_amdgcn_s_sleep(2);
-    }
-    __hip_atomic_store(flag, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    *seen = ok;
-  }
-  __syncthreads();  // the flag seen before any wave loads the partials
-  rows.merge_partial_coherent(part, lane, /*self_lower=*/false);
-  if (*seen == 0) rows.poison();
-}
-
-// ---------------------------------------------------------------------------
 // Slot-scheduled pipeline: W waves of 32 query rows, one key stream.
 //
 // Same work per iteration j as fa2_fwd_kernel (GEMM1, GEMM2 of tile j-1
@@ -169,12 +58,7 @@ __device__ __forceinline__ void pair_merge(unsigned* flag, const float* part, in
 // meets the same barriers.  This halves the longest key walk: a causal
 // work-group's time follows half its tiles, and heaviest-first dispatch of
 // one work-group per CU then balances the CUs.
-//
-// PAIR (4 waves, causal): the pair schedule above; a work-group runs one or
-// two segments (block, key-tile range) through the same pipeline, and
-// geom.part holds the pairs' flags (pair_flag_words) then the partials.
-template <int W, int FV, bool CAUSAL, bool SCALED, class T = _Float16, int SPLIT = 1,
-          bool PAIR = false>
+template <int W, int FV, bool CAUSAL, bool SCALED, class T = _Float16, int SPLIT = 1>
 __global__ void __launch_bounds__(64 * W * SPLIT, 2)  // <= 256 VGPRs: 2 waves per SIMD
 fa2_fwd_slot_kernel(const T* Q, const T* __restrict__ K, const T* __restrict__ V, T* O,
                     const Geom geom, int nqb, float cq, float cr) {
@@ -209,7 +93,6 @@ fa2_fwd_slot_kernel(const T* Q, const T* __restrict__ K, const T* __restrict__ V
   static_assert(kAhead % 2 == 0 && kAhead < 16, "read-ahead");
   static_assert(SPLIT == 1 || SPLIT == 2, "key-range split");
   static_assert(SPLIT == 1 || SPLIT * kRingBytes >= W * 34 * 64 * 4, "merge buffer");
-  static_assert(!PAIR || (CAUSAL && SPLIT == 1 && W == 4), "pair schedule: causal, 4 waves");
   __shared__ __attribute__((aligned(16))) uint8_t kring[SPLIT * kRingBytes];
   __shared__ __attribute__((aligned(16))) uint8_t vring[SPLIT * kRingBytes];
 
@@ -219,42 +102,23 @@ fa2_fwd_slot_kernel(const T* Q, const T* __restrict__ K, const T* __restrict__ V
   const int stream = wave / W;       // key-range half (0 unless SPLIT)
   const int rw = wave - stream * W;  // 32-row block within the work-group
   int bh, qb;
-  int pair = 0, member = 0;
-  if constexpr (PAIR)
-    pair_coords(nqb, bh, pair, member);
-  else
-    wg_coords<CAUSAL, kWgPerCu>(nqb, bh, qb);
+  wg_coords<CAUSAL, kWgPerCu>(nqb, bh, qb);
   const HeadPtrs<T> hp = head_ptrs(geom, bh, Q, K, V, O);
   const i32x4_t rk = hp.rk, rv = hp.rv;
   const FetchOff<kSegs> fk = fetch_offsets<kSegs, false>(rw, lane, 2 * geom.k_sr);
   const FetchOff<kSegs> fv = fetch_offsets<kSegs, true>(rw, lane, 2 * geom.v_sr);
   const int seq = geom.seq_q;
-  const StreamRings<kSlots> rings = {kring + stream * kRingBytes, vring + stream * kRingBytes};
-
-  const int nseg = PAIR ? pair_nseg(nqb, pair, member) : 1;
-  for (int seg = 0; seg < nseg; ++seg) {
-  int role = 0;  // PAIR: see PairSeg
-  int tbeg, tend, t0;
-  if constexpr (PAIR) {
-    const PairSeg sg = pair_seg(nqb, pair, member, seg);
-    qb = sg.qb;
-    role = sg.role;
-    tbeg = sg.tbeg;
-    tend = sg.tend;
-    t0 = tend - tbeg;
-  }
   const int q0 = qb * kBr;
+  const StreamRings<kSlots> rings = {kring + stream * kRingBytes, vring + stream * kRingBytes};
 
   int ntiles = max(1, (geom.seq_k + kBc - 1) / kBc);
   if (CAUSAL) ntiles = min(ntiles, causal_tiles(min(q0 + kBr, seq), geom.coff));
   // This stream's key tiles [tbeg, tend); iterations 0 .. t0 on tile tbeg + j
   // (the last one only drains GEMM2; with SPLIT the shorter stream's last
   // tile lies past the range and is masked).
-  if constexpr (!PAIR) {
-    t0 = SPLIT == 2 ? (ntiles + 1) / 2 : ntiles;
-    tbeg = stream == 0 ? 0 : t0;
-    tend = stream == 0 ? t0 : ntiles;
-  }
+  const int t0 = SPLIT == 2 ? (ntiles + 1) / 2 : ntiles;
+  const int tbeg = stream == 0 ? 0 : t0;
+  const int tend = stream == 0 ? t0 : ntiles;
   const int last = max(tend - 1, tbeg);  // fetch clamp
 
   // Prologue fetch groups -FK .. -1 (V tiles < 0 read as zeros through the
@@ -270,7 +134,7 @@ fa2_fwd_slot_kernel(const T* Q, const T* __restrict__ K, const T* __restrict__ V
   RowsT rows;
   rows.init(hp.q, geom.q_sr, lane, q0 + 32 * rw, seq, geom.seq_k, geom.coff, cq, cr);
   if constexpr (kMfmaSum) rows.init_msum(lane);
-  if ((SPLIT == 2 && stream == 0) || role == 1) rows.kv_lim = min(rows.kv_lim, tend * kBc);
+  if (SPLIT == 2 && stream == 0) rows.kv_lim = min(rows.kv_lim, tend * kBc);
 
   // Iterations j < jm need no mask on tiles tbeg + j and tbeg + j + 1.
   int tm = rows.kv_lim >> 6;
@@ -440,42 +304,20 @@ fa2_fwd_slot_kernel(const T* Q, const T* __restrict__ K, const T* __restrict__ V
     }
     rows.merge_partial(xchg, lane);
   }
-  bool owner = true;  // this work-group writes the block's output
-  if constexpr (PAIR) {
-    if (role != 0) {
-      const long long sb = (long long)bh * (nqb >> 1) + pair;
-      unsigned* flag = reinterpret_cast<unsigned*>(geom.part) + sb;
-      float* part = geom.part + pair_flag_words(geom.batch_heads, nqb) +
-                    (sb * W + rw) * kPairPartFloats;
-      if (role == 1) {
-        pair_publish(flag, part, lane, rows);
-        owner = false;
-      } else {
-        // a word of the idle K ring past the checked pass's flag
-        pair_merge(flag, part, lane, rows, reinterpret_cast<int*>(kring + kTileBytes) + 4);
-      }
-    }
-  }
+  rows.launder();
   FL_TL_STAMP(tl_store);
-  if (owner) {
-    rows.launder();
-    rows.store(hp.o, geom.o_sr, hp.lse);
-  }
+  rows.store(hp.o, geom.o_sr, hp.lse);
   FL_TL_RECORD(W * SPLIT, wave, lane, t0 + 1, tl_entry, tl_first, tl_loop, tl_loop_end, tl_store);
-  // PAIR: every wave is past its reads of the rings and their words before
-  // the next segment's prologue fetches into them.
-  if (PAIR && seg + 1 < nseg) __syncthreads();
-  }  // segments
 }
 
-template <int W, int FV, class T = _Float16, int SPLIT = 1, bool PAIR = false>
+template <int W, int FV, class T = _Float16, int SPLIT = 1>
 struct SlotLaunch {
   template <bool C, bool S>
   struct L {
     static hipError_t run(const FwdArgs& a, const Geom& g, dim3 grid, int nqb, float cq, float cr,
                           hipStream_t st) {
-      hipLaunchKernelGGL((fa2_fwd_slot_kernel<W, FV, C, S, T, SPLIT, PAIR>), grid,
-                         dim3(64 * W * SPLIT), 0, st,
+      hipLaunchKernelGGL((fa2_fwd_slot_kernel<W, FV, C, S, T, SPLIT>), grid, dim3(64 * W * SPLIT),
+                         0, st,
                          static_cast<const T*>(a.q), static_cast<const T*>(a.k),
                          static_cast<const T*>(a.v), static_cast<T*>(a.o), g, nqb, cq, cr);
       return hipSuccess;
@@ -496,23 +338,6 @@ hipError_t launch_slot(const FwdArgs& a, int waves, hipStream_t stream) {
     return bf ? dispatch<SlotLaunch<4, 3, __bf16>::L>(a, stream, 128)
               : dispatch<SlotLaunch<4, 3>::L>(a, stream, 128);
   return hipErrorInvalidValue;
-}
-
-// Causal pair schedule (pair_fits): 128-row groups of 4 waves, two per
-// CU, each half of a block pair; `workspace` as described at
-// pair_workspace_bytes.
-hipError_t launch_slot_pair(const FwdArgs& a, void* workspace, hipStream_t stream) {
-  if (!pair_fits(a) || workspace == nullptr) return hipErrorInvalidValue;
-  const int nqb = a.seq / 128;
-  Geom g = make_geom(a);
-  g.part = static_cast<float*>(workspace);
-  const dim3 grid((unsigned)(a.batch_heads * nqb));
-  const Scales sc(a);
-  using Pair = SlotLaunch<4, 3, _Float16, 1, true>;
-  const hipError_t e =
-      sc.scaled ? Pair::template L<true, true>::run(a, g, grid, nqb, sc.cq, sc.cr, stream)
-                : Pair::template L<true, false>::run(a, g, grid, nqb, sc.cq, sc.cr, stream);
-  return e != hipSuccess ? e : hipGetLastError();
 }
 
 // fp16: 128-row groups of 2 x 4 waves, the key range halved between them.

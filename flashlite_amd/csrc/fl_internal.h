@@ -67,27 +67,6 @@ bool stream_config_fits(const FwdArgs& a);
 constexpr int kQuarterMaxKeys = 512;
 inline bool quarter_config_fits(const FwdArgs& a) { return a.seq_k <= kQuarterMaxKeys; }
 
-// Causal pair schedule (fa2_slot.hip): 128-row blocks of 4 waves, each
-// work-group part of a (heavy, light) block pair, one block of the pair cut
-// between the pair's two work-groups, which merge through a workspace:
-// pair_flag_words flags (zero before the first launch, left zero by every
-// launch), then 4 * 34 * 64 floats per pair.  Causal, fp16, head_dim 64,
-// N_q = N_k a multiple of 256, B*H a multiple of 8 (whole heads per XCD).
-inline bool pair_fits(const FwdArgs& a) {
-  return a.causal && a.dtype == kDtypeF16 && a.head_dim == 64 && a.seq == a.seq_k &&
-         a.seq >= 256 && a.seq % 256 == 0 && a.batch_heads % 8 == 0 &&
-         (int64_t)a.batch_heads * (a.seq / 128) <= (int64_t)INT32_MAX;
-}
-__host__ __device__ inline int64_t pair_flag_words(int64_t batch_heads, int64_t nqb) {
-  return (batch_heads * (nqb / 2) + 63) / 64 * 64;  // one per pair, in 256-byte units
-}
-inline int64_t pair_workspace_bytes(const FwdArgs& a) {
-  const int64_t nqb = a.seq / 128;
-  const int64_t pairs = (int64_t)a.batch_heads * (nqb / 2);
-  return 4 * (pair_flag_words(a.batch_heads, nqb) + pairs * 4 * 34 * 64);
-}
-hipError_t launch_slot_pair(const FwdArgs& a, void* workspace, hipStream_t stream);
-
 // Per-schedule launchers behind launch_fa2 (one source file each).
 hipError_t launch_pipe(const FwdArgs& a, int cfg, hipStream_t stream);     // fa2_pipe.hip
 hipError_t launch_slot(const FwdArgs& a, int waves, hipStream_t stream);   // fa2_slot.hip

@@ -92,9 +92,6 @@ def main(argv=None):
     ap.add_argument("--cold-mib", type=int, default=0, metavar="M")
     ap.add_argument("--empty-kernel", type=int, nargs=2, metavar=("G", "W"), default=None)
     ap.add_argument("--timeline", type=int, default=0, metavar="MODE")
-    ap.add_argument("--ws", action="store_true",
-                    help="launch through fl_attn_fwd_f16_ws (the library's choice with a "
-                         "workspace: the causal pair schedule where it applies)")
     args = ap.parse_args(argv)
 
     import torch
@@ -154,19 +151,8 @@ def main(argv=None):
         p = capi.tensor_params(q, k, v, o, w.sm_scale, bool(args.causal))
         cfg = capi.select_config(p) if args.config < 0 else args.config
 
-    ws, ws_bytes = None, 0
-    if args.ws:
-        pex = capi.tensor_params_ex(q, k, v, o, w.sm_scale, bool(args.causal))
-        ws_bytes = capi.fwd_workspace_bytes(pex)
-        if ws_bytes < 0:
-            capi.check(capi.FL_ERR_INVALID_ARGUMENT)
-        ws = torch.zeros(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
-        cfg = -1
-
     def launch():
-        if args.ws:
-            rc = capi.fwd_ws(pex, ws.data_ptr(), ws_bytes, stream)
-        elif wide:
+        if wide:
             rc = fwd_ex(p, stream, cfg)
         else:
             rc = capi.naive(p, stream) if args.naive else capi.fwd(p, stream, cfg)
@@ -176,8 +162,6 @@ def main(argv=None):
     flops = (2.0 if args.causal else 4.0) * w.batch * w.heads * w.seq ** 2 * head_dim
     nbytes = 4 * w.batch * w.heads * w.seq * head_dim * q.element_size()
     name = "naive" if args.naive else ("auto" if cfg < 0 else capi.config_name(cfg))
-    if args.ws:
-        name = "ws:pair" if ws_bytes > 0 else "ws:auto"
     print(f"{w.name} {args.dtype} D={head_dim} causal={args.causal} {name}"
           f"{' cold' if args.cold_mib else ''}: {us:.2f} us/launch, "
           f"{flops / us / 1e6:.1f} TFLOP/s, {nbytes / us / 1e3:.1f} GB/s", flush=True)
@@ -288,7 +272,7 @@ def _timeline(args, torch):
     lib = _diag_lib()
     lib.fl_diag_slot_timeline.argtypes = ([ctypes.c_int] * 2 + [ctypes.c_void_p] * 4 +
                                           [ctypes.c_int] * 3 + [ctypes.c_void_p, ctypes.c_longlong,
-                                                                ctypes.c_void_p, ctypes.c_void_p])
+                                                                ctypes.c_void_p])
     lib.fl_diag_slot_timeline.restype = ctypes.c_int
     lib.fl_diag_wall_clock_khz.argtypes = [ctypes.c_int]
     lib.fl_diag_wall_clock_khz.restype = ctypes.c_int
@@ -296,30 +280,20 @@ def _timeline(args, torch):
     q, k, v = (torch.from_numpy(x).to(dev) for x in workload_inputs(w))
     o = torch.empty_like(q)
     mode = args.timeline
-    rows, wpg = (256, 8) if mode == 8 else (128, 4 if mode in (4, 1) else 8)
+    rows, wpg = (256, 8) if mode == 8 else (128, 4 if mode == 4 else 8)
     groups = w.batch * w.heads * ((w.seq + rows - 1) // rows)
-    # 8 words per wave and segment, two segments per wave
-    out = torch.zeros(groups * wpg * 16, dtype=torch.int64, device=dev)
-    ws = None
-    if mode == 1:
-        from flashlite_amd import capi
-
-        pex = capi.tensor_params_ex(q, k, v, o, w.sm_scale, True)
-        ws = torch.zeros(max(capi.fwd_workspace_bytes(pex), 256), dtype=torch.uint8, device=dev)
+    out = torch.zeros(groups * wpg * 8, dtype=torch.int64, device=dev)
     stream = torch.cuda.current_stream().cuda_stream
 
     def launch():
         rc = lib.fl_diag_slot_timeline(mode, args.causal, q.data_ptr(), k.data_ptr(), v.data_ptr(),
                                        o.data_ptr(), w.batch, w.heads, w.seq, out.data_ptr(),
-                                       out.numel(), stream, None if ws is None else ws.data_ptr())
+                                       out.numel(), stream)
         if rc != 0:
             raise RuntimeError(f"diagnostic launch failed: hipError {rc}")
 
     us = _time_launches(launch, args, torch)
-    full = out.cpu().numpy().reshape(groups, wpg, 2, 8).astype(np.int64)
-    if mode == 1:
-        return _timeline_pair(w, args, us, full, lib.fl_diag_wall_clock_khz(0))
-    d = full[:, :, 0, :].reshape(-1, 8)
+    d = out.cpu().numpy().reshape(-1, 8).astype(np.int64)
     d = d[d[:, 7] != 0]  # every wave that stamped
     tick_us = 1e3 / lib.fl_diag_wall_clock_khz(0)
     t = (d[:, :6] - d[:, 0].min()) * tick_us
@@ -359,58 +333,6 @@ def _timeline(args, torch):
         for key in sorted(per_cu, key=lambda c: -max(x[2] for x in per_cu[c]))[:3]:
             print("  latest CU: " + ", ".join(f"{n} it / loop {lt:.1f} us / exit {e:.1f} us"
                                               for n, lt, e in sorted(per_cu[key])))
-    return 0
-
-
-def _timeline_pair(w, args, us, full, khz):
-    """Timeline of the causal pair schedule: per member and segment, where
-    the work-group's time goes, and when each CU finishes."""
-    import collections
-
-    import numpy as np
-
-    tick_us = 1e3 / khz
-    stamped = full[:, :, :, 7] != 0
-    t0 = full[:, :, :, 0][stamped].min()
-    t = (full[:, :, :, :6] - t0) * tick_us  # [groups, waves, seg, 6]
-    groups = full.shape[0]
-    member = ((np.arange(groups) >> 3) >= (groups >> 3) // 2).astype(int)  # as pair_coords
-    xcc = (full[:, 0, 0, 7] >> 32) & 0xFF
-    hw = full[:, 0, 0, 7] & 0xFFFFFFFF
-    span = max(t[:, :, :, 5][stamped].max(), 0)
-    print(f"timeline {w.name} causal=1 br128_bc64_w4_pair: {us:.2f} us/launch over {args.iters} "
-          f"launches (events); last launch: span {span:.2f} us", flush=True)
-    pct = lambda x: (f"min {x.min():7.2f}  p50 {np.median(x):7.2f}  p90 "  # noqa: E731
-                     f"{np.percentile(x, 90):7.2f}  max {x.max():7.2f} us")
-    for m in (0, 1):
-        sel = member == m
-        for sg in (0, 1):
-            if not stamped[sel][:, :, sg].any():
-                continue
-            two = stamped[sel][:, 0, sg]  # groups of this member with this segment
-            x = t[sel][two][:, :, sg, :]  # [groups, waves, 6]
-            g = lambda i: x[:, :, i].max(axis=1)  # noqa: E731  latest wave of each group
-            print(f"  member {m} segment {sg} ({int(two.sum())} groups): start (first pass) "
-                  f"{pct(g(1))}")
-            print(f"    first pass -> loop start  {pct(g(2) - g(1))}")
-            print(f"    loop                      {pct(g(3) - g(2))}")
-            its = (full[sel][two][:, 0, sg, 7] >> 48).astype(np.float64)
-            cyc = full[sel][two][:, :, sg, 6].max(axis=1).astype(np.float64)
-            print(f"    per iteration: p50 {np.median((g(3) - g(2)) / its):.3f} us, "
-                  f"{np.median(cyc / its):.0f} cycles; loop clock p50 "
-                  f"{np.median(cyc / np.maximum(g(3) - g(2), 1e-9)) / 1e3:.3f} GHz")
-            print(f"    loop end -> after meeting {pct(g(4) - g(3))}")
-            print(f"    -> exit (store)           {pct(g(5) - g(4))}")
-        ends = t[sel][:, :, :, 5].max(axis=(1, 2))
-        print(f"  member {m} exits: {pct(ends)}")
-    per_cu = collections.defaultdict(list)
-    for gi in range(groups):
-        per_cu[int(xcc[gi]) * 256 + int((hw[gi] >> 8) & 0xFF)].append(
-            (int(member[gi]), float(t[gi, :, :, 5][stamped[gi]].max())))
-    ends = np.array([max(e for _, e in v) for v in per_cu.values()])
-    mix = collections.Counter(tuple(sorted(m for m, _ in v)) for v in per_cu.values())
-    print(f"  {len(per_cu)} CUs, members per CU {dict(mix)}; CU finish min {ends.min():.2f} "
-          f"p50 {np.median(ends):.2f} max {ends.max():.2f} us")
     return 0
 
 

@@ -158,33 +158,6 @@ int fl_attn_fwd_f16_splitkv(const fl_attn_params_ex* p, int32_t num_splits, void
                             int64_t workspace_bytes, void* stream);
 
 /*
- * The library's choice (as fl_attn_fwd_f16_ex with config -1, fp16 at
- * head_dim 64) when it may also use a workspace of the caller's.  For causal
- * attention with N_q = N_k a multiple of 256 whose 128-row query blocks fill
- * the GPU in one round (B*H*N/128 <= 512), it pairs the blocks: query blocks
- * hi = n-1-p and lo = p share two work-groups, one walking the first half of
- * block hi's keys, the other the rest of block hi and then block lo, and the
- * two halves of block hi merge through the workspace.  Every work-group then
- * carries the same work.  Elsewhere it runs the one-pass kernel and ignores
- * the workspace.
- *
- * fl_attn_fwd_workspace_bytes: the bytes that call needs (0: none; -1 on a
- * rejected argument).  The workspace must be 256-byte aligned and
- * zero-filled before its first use, and must not be modified by anything
- * else between calls: every call that returns FL_OK leaves it zero-filled
- * again.  Calls that may overlap (other streams, other host threads) need
- * workspaces of their own.  Results agree with fl_attn_fwd_f16_ex within
- * fp32 rounding (the merge adds two partial sums) and are the same bits on
- * every call.
- *
- * No counterpart in the reference, whose causal launch gives every query
- * block its own work-group (csrc/kernel_flash2.cu:786-835).
- */
-int64_t fl_attn_fwd_workspace_bytes(const fl_attn_params_ex* p);
-int fl_attn_fwd_f16_ws(const fl_attn_params_ex* p, void* workspace, int64_t workspace_bytes,
-                       void* stream);
-
-/*
  * fl_attn_fwd_f16_splitkv without a workspace argument and without any
  * allocation: the partial results go to a scratch array of
  * FL_ATTN_SCRATCH_BYTES (8 MiB) that the library holds in device memory on

@@ -267,48 +267,3 @@ def test_splitkv_workspace_checks():
     assert capi.fwd_splitkv(p, A + 0x400000, need - 4) == capi.FL_ERR_INVALID_ARGUMENT
     assert capi.fwd_splitkv(p, A + 0x400008, need) == capi.FL_ERR_MISALIGNED
     assert capi.load().fl_attn_fwd_f16_splitkv(None, 0, None, 0, None) == capi.FL_ERR_INVALID_ARGUMENT
-
-
-def test_pair_workspace_plan():
-    def bytes_for(batch, heads, n, causal=True, nk=None):
-        nk = n if nk is None else nk
-        base = _p(batch=batch, heads=heads, seq_q=n, seq_k=nk, causal=causal)
-        qs = (heads * n * 64, n * 64, 64)
-        ks = (heads * nk * 64, nk * 64, 64)
-        return capi.fwd_workspace_bytes(capi.make_params_ex(base, qs, ks, ks, qs))
-
-    def pair_bytes(bh, n):
-        pairs = bh * (n // 256)
-        flag_words = (pairs + 63) // 64 * 64
-        return 4 * (flag_words + pairs * 4 * 34 * 64)
-
-    # the headline causal shape: 512 work-groups of 128 rows, one round
-    assert bytes_for(2, 8, 4096) == pair_bytes(16, 4096)
-    assert bytes_for(2, 8, 1024) == pair_bytes(16, 1024)
-    assert bytes_for(1, 8, 1024) == pair_bytes(8, 1024)
-    # not paired: non-causal, N_q != N_k, N not a multiple of 256, short key
-    # ranges (quarter / stream kernels), more than one round of work-groups,
-    # too few work-groups for the 128-row configuration, B*H not a multiple
-    # of 8
-    assert bytes_for(1, 3, 4096) == 0
-    assert bytes_for(2, 8, 4096, causal=False) == 0
-    assert bytes_for(2, 8, 4096, nk=4352) == 0
-    assert bytes_for(2, 8, 4000) == 0
-    assert bytes_for(2, 8, 512) == 0
-    assert bytes_for(4, 8, 4096) == 0
-    assert bytes_for(1, 16, 16384) == 0
-    assert bytes_for(1, 2, 2048) == 0
-    assert bytes_for(2, -1, 4096) == -1
-
-
-def test_pair_workspace_checks_before_launch():
-    base = _p(batch=2, heads=8, seq_q=1024, seq_k=1024, causal=True)
-    c = (8 * 1024 * 64, 1024 * 64, 64)
-    p = capi.make_params_ex(base, c, c, c, c)
-    need = capi.fwd_workspace_bytes(p)
-    assert need > 0
-    assert capi.fwd_ws(p, 0, need) == capi.FL_ERR_INVALID_ARGUMENT
-    assert "workspace" in capi.last_error() and "NULL" in capi.last_error()
-    assert capi.fwd_ws(p, A + 0x4000000, need - 4) == capi.FL_ERR_INVALID_ARGUMENT
-    assert capi.fwd_ws(p, A + 0x4000010, need) == capi.FL_ERR_MISALIGNED
-    assert capi.load().fl_attn_fwd_f16_ws(None, None, 0, None) == capi.FL_ERR_INVALID_ARGUMENT
