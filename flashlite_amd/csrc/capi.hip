@@ -105,18 +105,20 @@ int check_pointers(const fl_attn_params* p, fl::FwdArgs* a, const char* who, uin
 }
 
 // Tile-configuration choice for 256 CUs (measured on MI355X, every
-// configuration computes the same result).  Non-causal: one 256-row group
-// of 8 waves per CU when there are enough of them and the key range is long
-// (N_k >= 4096; shorter ranges measured faster with 128-row groups); the
-// key-range-split 128-row group (8 waves, two key halves) when there are
-// very few groups; otherwise 128-row slot-scheduled groups of 4 waves, two
-// per CU, which also serve causal attention (groups of different lengths,
-// balanced by dispatch order).  Smaller problems fall back to smaller
-// groups.  Key ranges of at most 256 keys go to the streaming persistent
-// groups (measured at least as fast as every other configuration from 16
-// to 2048 units, both masks).  Replaces the reference's
-// `seq_len >= 2048 -> Br=128` rule (kernel_flash2.cu:786-789), which was
-// sized for 20 SMs.
+// configuration computes the same result).  Key ranges of at most 256 keys
+// go to the streaming persistent groups (measured at least as fast as every
+// other configuration from 16 to 2048 units, both masks), and of at most
+// 512 with at most one 32-row group per CU to the key quarters.  Long key
+// ranges (N_k >= 2048) with at most one 128-row group per CU take the
+// key-range-split group (8 waves, two per SIMD, each half walking half the
+// keys): 3-11% faster than the 4-wave groups there, both masks (and for
+// causal down to 64 groups; fewer fall back to smaller groups).  With more
+// groups, non-causal takes one 256-row group of 8 waves per CU; otherwise
+// 128-row slot-scheduled groups of 4 waves, two per CU, which also serve
+// causal attention (groups of different lengths, balanced by dispatch
+// order).  Smaller problems fall back to smaller groups.  Replaces the
+// reference's `seq_len >= 2048 -> Br=128` rule (kernel_flash2.cu:786-789),
+// which was sized for 20 SMs.
 int select_fa2(const fl::FwdArgs& a) {
   constexpr int64_t kCus = 256;
   auto wgs = [&](int64_t br) { return (a.seq + br - 1) / br * (int64_t)a.batch_heads; };
@@ -124,8 +126,9 @@ int select_fa2(const fl::FwdArgs& a) {
   // N_k <= 512 with few query blocks: quarter the key range (one 4-wave
   // work-group per 32 rows; a single round on the CUs).
   if (fl::quarter_config_fits(a) && wgs(32) <= kCus) return fl::kQuarterConfig;
-  if (!a.causal && a.seq_k >= 4096 && wgs(256) >= kCus) return fl::kSlotW8Config;
-  if (!a.causal && a.seq >= 2048 && wgs(128) < kCus / 2) return fl::kCfgSplit2;
+  if (a.seq_k >= 2048 && wgs(128) <= kCus && (!a.causal || wgs(128) >= kCus / 4))
+    return fl::kCfgSplit2;
+  if (!a.causal && a.seq_k >= 2048 && wgs(256) >= kCus / 2) return fl::kSlotW8Config;
   if (wgs(128) >= kCus / 4) return fl::kSlotW4Config;
   if (wgs(64) >= kCus / 4) return fl::kCfgW2;
   return fl::kCfgW1;

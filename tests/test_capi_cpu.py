@@ -172,22 +172,31 @@ def test_dispatcher_choices():
     W8, W4, SPLIT, STRM = ("br256_bc64_w8_slot", "br128_bc64_w4_slot", "br128_bc64_w4x2_slot",
                            "br256_kv256_w8_stream")
     W1, W2, QTR = "br32_bc64_w1", "br64_bc64_w2", "br32_kv512_w4_quarters"
-    # non-causal: 8-wave 256-row slot-scheduled groups when there is one per CU
-    # and the key range is long
+    # non-causal: 8-wave 256-row slot-scheduled groups when there are at
+    # least 128 and the key range is long
     assert sel(batch=2, heads=8, seq_q=4096) == W8      # 256 groups
     assert sel(batch=1, heads=16, seq_q=16384) == W8
+    assert sel(batch=2, heads=8, seq_q=2560) == W8      # 160 groups
+    assert sel(batch=4, heads=8, seq_q=2048) == W8
     # short key ranges (N_k <= 256): streaming groups
     assert sel(batch=32, heads=32, seq_q=256) == STRM     # 1024 units
     assert sel(batch=8, heads=32, seq_q=130) == STRM      # 256 units
     assert sel(batch=2, heads=8, seq_q=256) == STRM       # 16 units
     assert sel(batch=1, heads=1, seq_q=1000, seq_k=256) == STRM
-    assert sel(batch=2, heads=8, seq_q=2048) == W4
-    # very few groups at N >= 2048: split key range
+    # at most one 128-row group per CU over N_k >= 2048: split key range
+    assert sel(batch=2, heads=8, seq_q=2048) == SPLIT      # 256 groups of 128 rows
+    assert sel(batch=2, heads=8, seq_q=2048, causal=True) == SPLIT
+    assert sel(batch=1, heads=8, seq_q=4096, causal=True) == SPLIT
     assert sel(batch=1, heads=1, seq_q=4096) == SPLIT
     assert sel(batch=1, heads=3, seq_q=4096) == SPLIT      # 96 groups of 128 rows
+    assert sel(batch=1, heads=1, seq_q=1000, seq_k=4096) == SPLIT
+    assert sel(batch=2, heads=8, seq_q=1024) == W4         # N_k < 2048
+    assert sel(batch=4, heads=4, seq_q=1536, causal=True) == W4
     # causal: 128-row slot-scheduled groups balanced by dispatch order
     assert sel(batch=2, heads=8, seq_q=4096, causal=True) == W4
     assert sel(batch=1, heads=16, seq_q=16384, causal=True) == W4
+    assert sel(batch=3, heads=8, seq_q=2048, causal=True) == W4   # 384 groups
+    assert sel(batch=1, heads=1, seq_q=4096, causal=True) == W2   # 32 groups of 128 rows
     assert sel(batch=32, heads=32, seq_q=256, causal=True) == STRM   # streaming, any count
     assert sel(batch=1, heads=1, seq_q=128, causal=True) == STRM
     # 256 < N_k <= 512 with at most one 32-row group per CU: key quarters
