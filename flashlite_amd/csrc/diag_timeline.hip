@@ -12,6 +12,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cstdint>
 
 namespace {
@@ -48,6 +49,39 @@ __device__ unsigned long long* g_fl_timeline;
 #include "fa2_slot.hip"
 #undef launch_slot
 #undef launch_slot_split
+
+// The streaming kernel's marks: up to 64 s_memrealtime values per wave, kept
+// in two registers by lane (lane j holds mark j: no memory operation, so the
+// kernel's per-unit count of memory operations is unchanged) and written
+// once at the end: out[64 * (group * 8 + wave) + j], j = 0 at entry,
+// 1 + 3i / 2 + 3i / 3 + 3i for unit i past its barrier / after issuing the
+// next unit's loads / before its stores, 63 at exit.
+#define FL_ST_DECL() unsigned fl_st_lo = 0, fl_st_hi = 0
+#define FL_ST_MARK(index)                                                    \
+  do {                                                                       \
+    const unsigned long long t_ = __builtin_amdgcn_s_memrealtime();          \
+    const bool mine_ = (int)(threadIdx.x & 63) == (index);                   \
+    fl_st_lo = mine_ ? (unsigned)t_ : fl_st_lo;                              \
+    fl_st_hi = mine_ ? (unsigned)(t_ >> 32) : fl_st_hi;                      \
+  } while (0)
+#define FL_ST_FLUSH(wave, lane, count)                                                  \
+  do {                                                                                  \
+    __builtin_amdgcn_s_waitcnt(0);                                                      \
+    FL_ST_MARK(63);                                                                     \
+    if ((lane) < (count) || (lane) == 63)                                               \
+      g_fl_timeline[64 * ((long long)blockIdx.x * 8 + (wave)) + (lane)] =               \
+          ((unsigned long long)fl_st_hi << 32) | fl_st_lo;                              \
+  } while (0)
+namespace fl {
+namespace {
+bool diag_stream_fits(const FwdArgs& a) { return a.seq_k <= kStreamMaxKeys; }
+}  // namespace
+}  // namespace fl
+#define launch_stream diag_timeline_launch_stream
+#define stream_config_fits diag_stream_fits
+#include "fa2_stream.hip"
+#undef launch_stream
+#undef stream_config_fits
 
 extern "C" {
 
@@ -90,6 +124,37 @@ int fl_diag_slot_timeline(int mode, int causal, const void* q, const void* k, co
   e = mode == 2 ? fl::diag_timeline_launch_slot_split(a, st)
                 : fl::diag_timeline_launch_slot(a, mode, st);
   return (int)e;
+}
+
+// The streaming kernel (br256_kv256_w8_stream; contiguous fp16 [B, H, N, 64],
+// N <= 256, sm_scale 1/8) with its per-wave marks; `out` holds at least
+// 64 * 8 * min(B*H*ceil(N/256), 256) uint64.  Returns a hipError_t.
+int fl_diag_stream_timeline(int causal, const void* q, const void* k, const void* v, void* o,
+                            int B, int H, int N, void* out, long long out_entries, void* stream) {
+  if (B < 1 || H < 1 || N < 1 || N > 256 || out == nullptr) return (int)hipErrorInvalidValue;
+  const long long groups = std::min<long long>((long long)B * H, 256);
+  if (out_entries < 64 * 8 * groups) return (int)hipErrorInvalidValue;
+  hipError_t e = hipMemcpyToSymbol(HIP_SYMBOL(g_fl_timeline), &out, sizeof(out));
+  if (e != hipSuccess) return (int)e;
+  fl::FwdArgs a{};
+  a.q = q;
+  a.k = k;
+  a.v = v;
+  a.o = o;
+  a.lse = nullptr;
+  a.batch_heads = B * H;
+  a.heads = H;
+  a.seq = N;
+  a.seq_k = N;
+  a.head_dim = 64;
+  a.scale_log2 = (float)(0.125 * 1.4426950408889634);
+  a.negate = 0;
+  a.causal = causal;
+  a.dtype = fl::kDtypeF16;
+  a.q_sr = a.k_sr = a.v_sr = a.o_sr = 64;
+  a.q_sh = a.k_sh = a.v_sh = a.o_sh = (int64_t)N * 64;
+  a.q_sb = a.k_sb = a.v_sb = a.o_sb = (int64_t)H * N * 64;
+  return (int)fl::diag_timeline_launch_stream(a, static_cast<hipStream_t>(stream));
 }
 
 }  // extern "C"

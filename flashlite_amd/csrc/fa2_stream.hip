@@ -4,6 +4,15 @@
 
 #include "fa2_common.h"
 
+// Per-wave timeline marks (kernel entry; per unit: past its barrier, loads of
+// the next unit issued, stores issued), compiled only into the diagnostic
+// library (diag_timeline.hip); empty in the product.
+#ifndef FL_ST_MARK
+#define FL_ST_DECL()
+#define FL_ST_MARK(index)
+#define FL_ST_FLUSH(wave, lane, count)
+#endif
+
 namespace fl {
 
 namespace {
@@ -16,8 +25,13 @@ namespace {
 // buffers: after the barrier that publishes unit i, each wave reads its Q
 // rows, then issues unit i+1's K/V fetches (into the buffer unit i-1 used)
 // and its own next Q rows (into the 4 KiB it just read), then computes unit
-// i and stores it.  Per-wave memory operations per unit are fixed (8 K/V
-// and 4 Q fetches, 5 stores; out-of-range rows are dropped by the buffer
+// i and stores it.  Causal units with all 256 rows: waves 0-3 (1-2 key tiles
+// each) issue the fetches of their SIMD-mates w+4 (3-4 tiles) as well, after
+// a barrier that has every wave's Q rows read; a DMA instruction waits at
+// issue while the memory pipeline is backed up (2-7 us for a unit's loads),
+// and the mates' longer walks then start at once.  Per-wave memory
+// operations per unit are fixed (8 K/V and 4 Q fetches, or 16 + 8 and none
+// when sharing; 5 stores last; out-of-range rows are dropped by the buffer
 // bounds, never branched around), so "unit i's loads have landed" is
 // exactly vmcnt <= 5: only unit i-1's stores may still be in flight.  With
 // one short unit per work-group, the start-up latency of every unit (Q and
@@ -40,7 +54,13 @@ __device__ __forceinline__ void wait_vm_barrier() {
   __builtin_amdgcn_sched_barrier(0);
 }
 
-template <bool CAUSAL, bool SCALED, class T = _Float16>
+// SPREAD (at least 4 units per work-group over 4 key tiles): the next
+// unit's K/V fetches go out one tile pair per tile step of the current
+// unit's compute (the rest after it) instead of all before it, so a wave's
+// compute starts without waiting for their issue.  Measured 4-6% faster on
+// B32 H32 N256 and slower where a work-group has one or two short units,
+// where the extra code in the steps costs more than it hides.
+template <bool CAUSAL, bool SCALED, class T = _Float16, bool SPREAD = false>
 __global__ void __launch_bounds__(512, 2)  // <= 256 VGPRs: 8 waves, two per SIMD
 fa2_fwd_stream_kernel(const T* Q, const T* __restrict__ K, const T* __restrict__ V, T* O,
                       const Geom geom, int nqb, int units, float cq, float cr) {
@@ -50,6 +70,7 @@ fa2_fwd_stream_kernel(const T* Q, const T* __restrict__ K, const T* __restrict__
   __shared__ __attribute__((aligned(16))) uint8_t buf[2][2 * kStreamHalf];  // [unit parity][K | V]
   __shared__ __attribute__((aligned(16))) uint8_t qbuf[8 * 4096];            // 32 Q rows per wave
 
+  FL_ST_DECL();
   const int lane = threadIdx.x & 63;
   const int rw = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int g = lane >> 5, col = lane & 31;
@@ -64,25 +85,42 @@ fa2_fwd_stream_kernel(const T* Q, const T* __restrict__ K, const T* __restrict__
   const int blk = CAUSAL && rw >= 4 ? 11 - rw : rw;
 
   // Unit u's K/V tiles 0..3 into buffer b (rows >= N_k read as zeros) and
-  // this wave's 32 Q rows into its 4 KiB of qbuf (rows >= N_q read as
-  // zeros), all by LDS DMA; chunks swizzled as K tiles are.
-  int qoff[4];
+  // 32 Q rows into a wave's 4 KiB of qbuf (rows >= N_q read as zeros), all
+  // by LDS DMA; chunks swizzled as K tiles are.  Wave w fetches segment w
+  // (rows 8w..8w+7) of every tile and its own Q rows; with `mate`, also
+  // those of wave w+4.
+  auto q_offsets = [&](int b_blk, int (&off)[4]) __attribute__((always_inline)) {
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int lrow = 8 * i + (lane >> 3);
-    qoff[i] = (32 * blk + lrow) * qrow_bytes + 16 * ((lane & 7) ^ k_swz(lrow));
-    asm volatile("" : "+v"(qoff[i]));
+    for (int i = 0; i < 4; ++i) {
+      const int lrow = 8 * i + (lane >> 3);
+      off[i] = (32 * b_blk + lrow) * qrow_bytes + 16 * ((lane & 7) ^ k_swz(lrow));
+      asm volatile("" : "+v"(off[i]));
+    }
+  };
+  int qoff[4];
+  q_offsets(blk, qoff);
+  // Causal units whose mates' blocks (rows 128-255) all hold rows.
+  constexpr bool kShare = CAUSAL;
+  const bool share = kShare && seq > kStreamBr - 32;
+  int qoff2[4];  // wave w+4's Q rows and tile segments (waves 0-3)
+  FetchOff<1> fk2 = fk, fv2 = fv;
+  if constexpr (kShare) {
+    q_offsets(11 - (rw + 4), qoff2);
+    fk2 = fetch_offsets<1, false>(rw + 4, lane, 2 * geom.k_sr);
+    fv2 = fetch_offsets<1, true>(rw + 4, lane, 2 * geom.v_sr);
   }
   uint8_t* const qdst = qbuf + 4096 * rw;
-  auto issue_loads = [&](int u, int b) __attribute__((always_inline)) {
-    const int bh = u / nqb, qb = u - bh * nqb;
-    const HeadPtrs<T> hp = head_ptrs<T>(geom, bh, Q, K, V, O);
-#pragma unroll
-    for (int t = 0; t < kStreamTiles; ++t) {
-      fetch_tile<1>(hp.rk, buf[b] + t * kTileBytes, t, kStreamTiles - 1, rw, fk);
-      fetch_tile<1>(hp.rv, buf[b] + kStreamHalf + t * kTileBytes, t, kStreamTiles - 1, rw, fv);
+  auto issue_kv = [&](const HeadPtrs<T>& hp, int b, int t, bool mate) __attribute__((always_inline)) {
+    fetch_tile<1>(hp.rk, buf[b] + t * kTileBytes, t, kStreamTiles - 1, rw, fk);
+    fetch_tile<1>(hp.rv, buf[b] + kStreamHalf + t * kTileBytes, t, kStreamTiles - 1, rw, fv);
+    if (kShare && mate) {
+      fetch_tile<1>(hp.rk, buf[b] + t * kTileBytes, t, kStreamTiles - 1, rw + 4, fk2);
+      fetch_tile<1>(hp.rv, buf[b] + kStreamHalf + t * kTileBytes, t, kStreamTiles - 1, rw + 4,
+                    fv2);
     }
-    const int q0 = qb * kStreamBr;
+  };
+  auto issue_q = [&](const HeadPtrs<T>& hp, int u, bool mate) __attribute__((always_inline)) {
+    const int q0 = (u - (u / nqb) * nqb) * kStreamBr;
     const int valid = min(kStreamBr, seq - q0);
     const i32x4_t rq =
         buffer_rsrc(hp.q + (long long)q0 * geom.q_sr, (valid - 1) * qrow_bytes + kRowBytes);
@@ -92,12 +130,27 @@ fa2_fwd_stream_kernel(const T* Q, const T* __restrict__ K, const T* __restrict__
       asm volatile("buffer_load_dwordx4 %0, %1, 0 offen lds" : : "v"(qoff[i]), "s"(rq),
                    "{m0}"(lds_base));
     }
+    if (kShare && mate) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const uint32_t lds_base = (uint32_t)(uintptr_t)(qdst + 4 * 4096 + 1024 * i);
+        asm volatile("buffer_load_dwordx4 %0, %1, 0 offen lds" : : "v"(qoff2[i]), "s"(rq),
+                     "{m0}"(lds_base));
+      }
+    }
+  };
+  auto issue_loads = [&](int u, int b, bool mate) __attribute__((always_inline)) {
+    const HeadPtrs<T> hp = head_ptrs<T>(geom, u / nqb, Q, K, V, O);
+#pragma unroll
+    for (int t = 0; t < kStreamTiles; ++t) issue_kv(hp, b, t, mate);
+    issue_q(hp, u, mate);
   };
 
   const int G = gridDim.x;
   // Unit u in buffer b; its loads have landed and every wave is done with
   // the other buffer.
-  auto unit = [&](int u, int b) __attribute__((always_inline)) {
+  auto unit = [&](int u, int b, int ui) __attribute__((always_inline)) {
+    (void)ui;  // the unit's index within this work-group (timeline marks)
     const int bh = u / nqb, qb = u - bh * nqb;
     const int q0 = qb * kStreamBr;
     const int qw = q0 + 32 * blk;
@@ -112,9 +165,29 @@ fa2_fwd_stream_kernel(const T* Q, const T* __restrict__ K, const T* __restrict__
       rows.set_q(raw, cq);
     }
     rows.reset();
-    // This wave's Q reads are done before its DMA refills the same rows.
+    // This wave's Q reads are done before its DMA refills the same rows
+    // (when sharing: every wave's, before waves 0-3 refill their mates').
     asm volatile("s_waitcnt lgkmcnt(0)" : : : "memory");
-    if (u + G < units) issue_loads(u + G, b ^ 1);
+    const bool more = u + G < units;
+    if (share && more) __syncthreads();
+    const bool fetcher = more && (!share || rw < 4);
+    // SPREAD: the next unit's Q rows now, its K/V tile pairs one per tile
+    // step below and the rest after the steps.
+    const HeadPtrs<T> hn = head_ptrs<T>(geom, SPREAD && more ? (u + G) / nqb : 0, Q, K, V, O);
+    int kv_sent = SPREAD && fetcher ? 0 : kStreamTiles;
+    auto kv_next = [&]() __attribute__((always_inline)) {
+      if (SPREAD && kv_sent < kStreamTiles) {
+        issue_kv(hn, b ^ 1, kv_sent, share);
+        ++kv_sent;
+      }
+    };
+    if (fetcher) {
+      if constexpr (SPREAD)
+        issue_q(hn, u + G, share);
+      else
+        issue_loads(u + G, b ^ 1, share);
+    }
+    FL_ST_MARK(2 + 3 * ui);
 
     int nt = ntiles;
     if (CAUSAL) nt = min(nt, causal_tiles(min(qw + 32, seq), geom.coff));
@@ -143,6 +216,7 @@ fa2_fwd_stream_kernel(const T* Q, const T* __restrict__ K, const T* __restrict__
         rows.mask(0, S0);
         rows.first_tile(S0);
         auto step = [&](int t, float16_t (&S)[2], float16_t (&Sn)[2]) __attribute__((always_inline)) {
+          if constexpr (SPREAD) kv_next();
           V8 ka[2][4];
           rows.read_k(kb + (t + 1) * kTileBytes, ka);
           if (t > 0) {
@@ -178,6 +252,7 @@ fa2_fwd_stream_kernel(const T* Q, const T* __restrict__ K, const T* __restrict__
       if (checked) {
         rows.reset();
         for (int t = 0; t < nt; ++t) {
+          if constexpr (SPREAD) kv_next();
           float16_t S[2];
           V8 P[2][2];
           {
@@ -196,6 +271,8 @@ fa2_fwd_stream_kernel(const T* Q, const T* __restrict__ K, const T* __restrict__
         }
       }
     }
+    if constexpr (SPREAD)
+      while (kv_sent < kStreamTiles) kv_next();
     const int valid = min(kStreamBr, seq - q0);
     const int b_ = bh / geom.heads, h_ = bh - b_ * geom.heads;
     T* oh = O + (b_ * geom.o_sb + h_ * geom.o_sh) + (long long)q0 * geom.o_sr;
@@ -204,29 +281,31 @@ fa2_fwd_stream_kernel(const T* Q, const T* __restrict__ K, const T* __restrict__
     float* lh = geom.lse ? geom.lse + (long long)bh * seq + q0 : geom.lse;
     const __amdgpu_buffer_rsrc_t rl =
         __builtin_amdgcn_make_buffer_rsrc((void*)lh, 0, geom.lse ? 4 * valid : 0, 0x00020000);
+    FL_ST_MARK(3 + 3 * ui);
     rows.store_rsrc(ro, q0, 2 * geom.o_sr, rl);
   };
   // The first unit is peeled off: its wait also covers the launch's first
   // loads, and every later one has exactly one unit's stores behind it.
+  FL_ST_MARK(0);
   int u = blockIdx.x;
-  issue_loads(u, 0);
+  issue_loads(u, 0, false);
   wait_vm_barrier<0>();
-  unit(u, 0);
+  FL_ST_MARK(1);
+  unit(u, 0, 0);
   u += G;
-  for (int i = 1; u < units; ++i, u += G) {
+  int i = 1;
+  for (; u < units; ++i, u += G) {
     wait_vm_barrier<kStores>();  // only unit i-1's stores may be in flight
-    unit(u, i & 1);
+    FL_ST_MARK(1 + 3 * i);
+    unit(u, i & 1, i);
   }
+  FL_ST_FLUSH(rw, lane, 1 + 3 * i);
 }
 
 // Streaming short-key kernel: one persistent work-group per CU (its two
 // 64 KiB buffers take 128 KiB of the CU's 160 KiB), at most one per unit.
-template <class T>
-hipError_t launch_stream_t(const FwdArgs& a, hipStream_t st) {
-  constexpr int kCus = 256;
-  const int nqb = (a.seq + kStreamBr - 1) / kStreamBr;
-  const int units = nqb * a.batch_heads;
-  const dim3 grid((unsigned)min(units, kCus));
+template <class T, bool SPREAD>
+hipError_t launch_stream_v(const FwdArgs& a, hipStream_t st, dim3 grid, int nqb, int units) {
   const Scales sc(a);
   const Geom g = make_geom(a);
   const T *q = static_cast<const T*>(a.q), *k = static_cast<const T*>(a.k),
@@ -234,16 +313,28 @@ hipError_t launch_stream_t(const FwdArgs& a, hipStream_t st) {
   T* o = static_cast<T*>(a.o);
   if (a.causal) {
     if (sc.scaled)
-      hipLaunchKernelGGL((fa2_fwd_stream_kernel<true, true, T>), grid, dim3(512), 0, st, q, k, v, o, g, nqb, units, sc.cq, sc.cr);
+      hipLaunchKernelGGL((fa2_fwd_stream_kernel<true, true, T, SPREAD>), grid, dim3(512), 0, st, q, k, v, o, g, nqb, units, sc.cq, sc.cr);
     else
-      hipLaunchKernelGGL((fa2_fwd_stream_kernel<true, false, T>), grid, dim3(512), 0, st, q, k, v, o, g, nqb, units, sc.cq, sc.cr);
+      hipLaunchKernelGGL((fa2_fwd_stream_kernel<true, false, T, SPREAD>), grid, dim3(512), 0, st, q, k, v, o, g, nqb, units, sc.cq, sc.cr);
   } else {
     if (sc.scaled)
-      hipLaunchKernelGGL((fa2_fwd_stream_kernel<false, true, T>), grid, dim3(512), 0, st, q, k, v, o, g, nqb, units, sc.cq, sc.cr);
+      hipLaunchKernelGGL((fa2_fwd_stream_kernel<false, true, T, SPREAD>), grid, dim3(512), 0, st, q, k, v, o, g, nqb, units, sc.cq, sc.cr);
     else
-      hipLaunchKernelGGL((fa2_fwd_stream_kernel<false, false, T>), grid, dim3(512), 0, st, q, k, v, o, g, nqb, units, sc.cq, sc.cr);
+      hipLaunchKernelGGL((fa2_fwd_stream_kernel<false, false, T, SPREAD>), grid, dim3(512), 0, st, q, k, v, o, g, nqb, units, sc.cq, sc.cr);
   }
   return hipGetLastError();
+}
+
+template <class T>
+hipError_t launch_stream_t(const FwdArgs& a, hipStream_t st) {
+  constexpr int kCus = 256;
+  const int nqb = (a.seq + kStreamBr - 1) / kStreamBr;
+  const int units = nqb * a.batch_heads;
+  const dim3 grid((unsigned)min(units, kCus));
+  // at least 4 units per work-group, every one over 4 key tiles
+  const bool spread = units >= 4 * kCus && a.seq_k > 3 * kBc;
+  return spread ? launch_stream_v<T, true>(a, st, grid, nqb, units)
+                : launch_stream_v<T, false>(a, st, grid, nqb, units);
 }
 
 }  // namespace

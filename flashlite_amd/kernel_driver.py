@@ -92,6 +92,8 @@ def main(argv=None):
     ap.add_argument("--cold-mib", type=int, default=0, metavar="M")
     ap.add_argument("--empty-kernel", type=int, nargs=2, metavar=("G", "W"), default=None)
     ap.add_argument("--timeline", type=int, default=0, metavar="MODE")
+    ap.add_argument("--stream-timeline", action="store_true",
+                    help="per-unit marks of the streaming kernel (N <= 256)")
     args = ap.parse_args(argv)
 
     import torch
@@ -102,6 +104,8 @@ def main(argv=None):
         return _empty(args, torch)
     if args.timeline:
         return _timeline(args, torch)
+    if args.stream_timeline:
+        return _stream_timeline(args, torch)
     if args.decode:
         return _decode(args, torch)
 
@@ -333,6 +337,65 @@ def _timeline(args, torch):
         for key in sorted(per_cu, key=lambda c: -max(x[2] for x in per_cu[c]))[:3]:
             print("  latest CU: " + ", ".join(f"{n} it / loop {lt:.1f} us / exit {e:.1f} us"
                                               for n, lt, e in sorted(per_cu[key])))
+    return 0
+
+
+def _stream_timeline(args, torch):
+    """Where the streaming kernel's time goes: per unit of each work-group,
+    the wait at its barrier (its loads landing), the issue of the next
+    unit's loads and its compute."""
+    import ctypes
+
+    import numpy as np
+
+    from flashlite_amd.workloads import WORKLOADS, Workload, workload_inputs
+
+    w = WORKLOADS[args.workload]
+    if args.shape:
+        b, h, n = args.shape
+        w = Workload(f"B{b}H{h}N{n}", b, h, n, 64, (False, True), 1)
+    lib = _diag_lib()
+    lib.fl_diag_stream_timeline.argtypes = ([ctypes.c_int] + [ctypes.c_void_p] * 4 +
+                                            [ctypes.c_int] * 3 +
+                                            [ctypes.c_void_p, ctypes.c_longlong, ctypes.c_void_p])
+    lib.fl_diag_stream_timeline.restype = ctypes.c_int
+    lib.fl_diag_wall_clock_khz.argtypes = [ctypes.c_int]
+    lib.fl_diag_wall_clock_khz.restype = ctypes.c_int
+    dev = torch.device("cuda:0")
+    q, k, v = (torch.from_numpy(x).to(dev) for x in workload_inputs(w))
+    o = torch.empty_like(q)
+    groups = min(w.batch * w.heads * ((w.seq + 255) // 256), 256)
+    out = torch.zeros(groups * 8 * 64, dtype=torch.int64, device=dev)
+    stream = torch.cuda.current_stream().cuda_stream
+
+    def launch():
+        rc = lib.fl_diag_stream_timeline(args.causal, q.data_ptr(), k.data_ptr(), v.data_ptr(),
+                                         o.data_ptr(), w.batch, w.heads, w.seq, out.data_ptr(),
+                                         out.numel(), stream)
+        if rc != 0:
+            raise RuntimeError(f"diagnostic launch failed: hipError {rc}")
+
+    us = _time_launches(launch, args, torch)
+    d = out.cpu().numpy().reshape(groups, 8, 64).astype(np.int64)
+    tick_us = 1e3 / lib.fl_diag_wall_clock_khz(0)
+    t = (d - d[:, :, 0].min()) * tick_us
+    units = (np.count_nonzero(d[0, 0, 1:63]) - 1) // 3 + 1 if d[0, 0, 1] else 0
+    pct = lambda x: (f"p50 {np.median(x):6.2f}  p90 {np.percentile(x, 90):6.2f}  "  # noqa: E731
+                     f"max {x.max():6.2f} us")
+    print(f"stream timeline {w.name} causal={args.causal}: {us:.2f} us/launch over {args.iters} "
+          f"launches (events); last launch: {groups} groups x 8 waves, {units} units each, span "
+          f"{t[:, :, 63].max():.2f} us", flush=True)
+    print(f"  entry -> first unit's loads landed  {pct(t[:, :, 1] - t[:, :, 0])}")
+    for i in range(units):
+        start = t[:, :, 1 + 3 * i].max(axis=1)  # barrier passed (all waves)
+        issued = t[:, :, 2 + 3 * i].max(axis=1)
+        stored = t[:, :, 3 + 3 * i].max(axis=1)
+        line = f"  unit {i}: starts {pct(start)}; issue {pct(issued - start)}; compute {pct(stored - issued)}"
+        if i > 0:
+            prev = t[:, :, 3 * i].max(axis=1)
+            line += f"; wait for loads {pct(start - prev)}"
+        print(line)
+    print(f"  last stores issued -> exit  {pct(t[:, :, 63].max(axis=1) - t[:, :, 3 * units].max(axis=1))}")
     return 0
 
 
