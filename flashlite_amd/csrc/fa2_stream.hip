@@ -156,6 +156,11 @@ fa2_fwd_stream_kernel(const T* Q, const T* __restrict__ K, const T* __restrict__
     const int qw = q0 + 32 * blk;
     RowsT rows;
     rows.place(lane, qw, seq, geom.seq_k, geom.coff, cr);
+    // Opaque per unit: with N_q <= 256 every unit has the same rows, and the
+    // masks and addresses derived from them would otherwise be hoisted out
+    // of the unit loop and kept live (spilled) across it.
+    rows.launder();
+    asm volatile("" : "+v"(rows.my_d), "+v"(rows.qd), "+v"(rows.kv_lim), "+v"(rows.qw));
     {
       u32x4_t raw[4];
 #pragma unroll
