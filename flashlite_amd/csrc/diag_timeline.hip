@@ -82,6 +82,9 @@ bool diag_stream_fits(const FwdArgs& a) { return a.seq_k <= kStreamMaxKeys; }
 #include "fa2_stream.hip"
 #undef launch_stream
 #undef stream_config_fits
+#define launch_quarter diag_timeline_launch_quarter
+#include "fa2_short.hip"
+#undef launch_quarter
 
 extern "C" {
 
@@ -155,6 +158,37 @@ int fl_diag_stream_timeline(int causal, const void* q, const void* k, const void
   a.q_sh = a.k_sh = a.v_sh = a.o_sh = (int64_t)N * 64;
   a.q_sb = a.k_sb = a.v_sb = a.o_sb = (int64_t)H * N * 64;
   return (int)fl::diag_timeline_launch_stream(a, static_cast<hipStream_t>(stream));
+}
+
+// The key-quarter kernel (br32_kv512_w4_quarters; contiguous fp16
+// [B, H, N, 64], N <= 512, sm_scale 1/8) with per-wave marks (0 entry, 1
+// loads issued, 2 loads landed, 3 tiles done, 4 merged, 63 exit, as for the
+// streaming kernel); `out` holds at least 64 * 8 * B*H*ceil(N/32) uint64.
+int fl_diag_quarter_timeline(int causal, const void* q, const void* k, const void* v, void* o,
+                             int B, int H, int N, void* out, long long out_entries, void* stream) {
+  if (B < 1 || H < 1 || N < 1 || N > 512 || out == nullptr) return (int)hipErrorInvalidValue;
+  if (out_entries < 64 * 8 * (long long)B * H * ((N + 31) / 32)) return (int)hipErrorInvalidValue;
+  hipError_t e = hipMemcpyToSymbol(HIP_SYMBOL(g_fl_timeline), &out, sizeof(out));
+  if (e != hipSuccess) return (int)e;
+  fl::FwdArgs a{};
+  a.q = q;
+  a.k = k;
+  a.v = v;
+  a.o = o;
+  a.lse = nullptr;
+  a.batch_heads = B * H;
+  a.heads = H;
+  a.seq = N;
+  a.seq_k = N;
+  a.head_dim = 64;
+  a.scale_log2 = (float)(0.125 * 1.4426950408889634);
+  a.negate = 0;
+  a.causal = causal;
+  a.dtype = fl::kDtypeF16;
+  a.q_sr = a.k_sr = a.v_sr = a.o_sr = 64;
+  a.q_sh = a.k_sh = a.v_sh = a.o_sh = (int64_t)N * 64;
+  a.q_sb = a.k_sb = a.v_sb = a.o_sb = (int64_t)H * N * 64;
+  return (int)fl::diag_timeline_launch_quarter(a, static_cast<hipStream_t>(stream));
 }
 
 }  // extern "C"

@@ -3,6 +3,15 @@
 
 #include "fa2_common.h"
 
+// Per-wave timeline marks (entry, loads issued, loads landed, tiles done,
+// merged, exit), compiled only into the diagnostic library
+// (diag_timeline.hip); empty in the product.
+#ifndef FL_ST_MARK
+#define FL_ST_DECL()
+#define FL_ST_MARK(index)
+#define FL_ST_FLUSH(wave, lane, count)
+#endif
+
 namespace fl {
 
 namespace {
@@ -15,11 +24,12 @@ namespace {
 // wave w the key tiles [2w, 2w+2): a quarter of at most 512 keys.  Each wave
 // fetches its own two K and two V tiles into its own 32 KiB of LDS by DMA
 // and reads nothing another wave wrote, so no barrier precedes the compute;
-// Q goes straight to registers, its load overlapping the fetches.  Each
-// wave runs its tiles through the checked softmax (the stabiliser follows
-// the row max tile by tile, so no second pass), then the quarters' O, m and
-// l merge through LDS at their larger m: 1 into 0 and 3 into 2, then 2 into
-// 0, which stores.  C1 then runs 1024 waves of 2 tiles instead of 256 waves
+// Q goes straight to registers, its loads issued first so their latency
+// overlaps the fetches.  Each wave runs its tiles through the checked
+// softmax (the stabiliser follows the row max tile by tile, so no second
+// pass; the second tile's GEMM1 goes out before the first tile's softmax),
+// then the quarters' O, m and l merge through LDS in 16-byte chunks at
+// their larger m: 1 into 0 and 3 into 2, then 2 into 0, which stores.  C1 then runs 1024 waves of 2 tiles instead of 256 waves
 // of 8.  LDS: 4 x 32 KiB, one work-group per CU.  (Eight waves of one tile
 // each, two per SIMD and one more merge step, measured 7% slower on C1.)
 constexpr int kQuarterWaves = 4;
@@ -36,6 +46,8 @@ fa2_fwd_quarter_kernel(const _Float16* Q, const _Float16* __restrict__ K,
   static_assert(NW * kQuarterTiles * kBc == kQuarterMaxKeys, "key range");
   __shared__ __attribute__((aligned(16))) uint8_t buf[NW][kQuarterWaveBytes];
 
+  FL_ST_DECL();
+  FL_ST_MARK(0);
   const int lane = threadIdx.x & 63;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // key quarter
   const int bh = blockIdx.x / nqb, qb = blockIdx.x - bh * nqb;
@@ -49,6 +61,16 @@ fa2_fwd_quarter_kernel(const _Float16* Q, const _Float16* __restrict__ K,
   uint8_t* const kb = buf[w];
   uint8_t* const vb = buf[w] + kQuarterTiles * kTileBytes;
 
+  // Q rows first, straight to registers: their latency then overlaps the
+  // issue of the tile fetches below (which waits while the memory pipeline
+  // is backed up).
+  const int my_q = q0 + (lane & 31), g = lane >> 5;
+  u32x4_t qraw[4];
+#pragma unroll
+  for (int s = 0; s < 4; ++s)
+    qraw[s] = my_q < seq ? *reinterpret_cast<const u32x4_t*>(hp.q + (long long)my_q * geom.q_sr +
+                                                            16 * s + 8 * g)
+                         : (u32x4_t){0u, 0u, 0u, 0u};
   // This wave's K and V tiles, whole (8 segments each); rows >= N_k read
   // as zeros through the buffer bound.
   if (t0 < t1) {
@@ -61,42 +83,68 @@ fa2_fwd_quarter_kernel(const _Float16* Q, const _Float16* __restrict__ K,
     }
   }
   RowsT rows;
-  rows.init(hp.q, geom.q_sr, lane, q0, seq, geom.seq_k, geom.coff, cq, cr);
+  rows.place(lane, q0, seq, geom.seq_k, geom.coff, cr);
+  rows.set_q(qraw, cq);
+  rows.reset();
+  FL_ST_MARK(1);
   if (t0 < t1) {
     // This wave's own fetches have landed in LDS.
     asm volatile("s_waitcnt vmcnt(0)" : : : "memory");
-    for (int t = t0; t < t1; ++t) {
-      float16_t S[2];
-      V8 P[2][2];
-      {
-        V8 ka[2][4];
-        rows.read_k(kb + (t - t0) * kTileBytes, ka);
-        rows.gemm1(ka, S);
-      }
-      rows.mask(t, S);
-      if (t == t0) rows.first_tile(S);
-      rows.softmax_checked(S, P);
-      {
-        V8 va[2][4];
-        rows.read_v(vb + (t - t0) * kTileBytes, va);
-        rows.gemm2(va, P);
-      }
+    FL_ST_MARK(2);
+    // Tile t0 sets the stabiliser to its exact row max, so its p are at most
+    // 1 and its checked softmax never moves m: tile t0+1's GEMM1 can go out
+    // before that softmax, against the same m.
+    static_assert(kQuarterTiles == 2, "two tiles per wave");
+    float16_t S0[2], S1[2];
+    V8 P[2][2];
+    {
+      V8 ka[2][4];
+      rows.read_k(kb, ka);
+      rows.gemm1(ka, S0);
+    }
+    rows.mask(t0, S0);
+    rows.first_tile(S0);
+    const bool two = t0 + 1 < t1;
+    if (two) {
+      V8 ka[2][4];
+      rows.read_k(kb + kTileBytes, ka);
+      rows.gemm1(ka, S1);
+    }
+    rows.softmax_checked(S0, P);
+    {
+      V8 va[2][4];
+      rows.read_v(vb, va);
+      rows.gemm2(va, P);
+    }
+    if (two) {
+      rows.mask(t0 + 1, S1);
+      rows.softmax_checked(S1, P);
+      V8 va[2][4];
+      rows.read_v(vb + kTileBytes, va);
+      rows.gemm2(va, P);
     }
   }
+  FL_ST_MARK(3);
   // Merge tree through each sender's own (now idle) LDS: at step s wave w
   // with w % 2s == s hands its range to wave w - s.  A range with no
   // visible key holds l = 0 and is skipped by the merge.
-  float* const part = reinterpret_cast<float*>(buf[w]);
+  float4* const part = reinterpret_cast<float4*>(buf[w]);
 #pragma unroll
   for (int s = 1; s < NW; s *= 2) {
     asm volatile("s_waitcnt lgkmcnt(0)" : : : "memory");  // own LDS reads done
-    if ((w & (2 * s - 1)) == s) rows.save_partial(part, lane);
+    if ((w & (2 * s - 1)) == s) rows.save_partial4(part, lane);
     __syncthreads();
-    if ((w & (2 * s - 1)) == 0) rows.merge_partial(reinterpret_cast<const float*>(buf[w + s]), lane);
+    if ((w & (2 * s - 1)) == 0)
+      rows.merge_partial4(reinterpret_cast<const float4*>(buf[w + s]), lane);
   }
-  if (w != 0) return;
+  FL_ST_MARK(4);
+  if (w != 0) {
+    FL_ST_FLUSH(w, lane, 5);
+    return;
+  }
   rows.launder();
   rows.store(hp.o, geom.o_sr, hp.lse);
+  FL_ST_FLUSH(w, lane, 5);
 }
 
 struct QuarterLaunch {

@@ -94,6 +94,8 @@ def main(argv=None):
     ap.add_argument("--timeline", type=int, default=0, metavar="MODE")
     ap.add_argument("--stream-timeline", action="store_true",
                     help="per-unit marks of the streaming kernel (N <= 256)")
+    ap.add_argument("--quarter-timeline", action="store_true",
+                    help="per-wave marks of the key-quarter kernel (N <= 512)")
     args = ap.parse_args(argv)
 
     import torch
@@ -106,6 +108,8 @@ def main(argv=None):
         return _timeline(args, torch)
     if args.stream_timeline:
         return _stream_timeline(args, torch)
+    if args.quarter_timeline:
+        return _quarter_timeline(args, torch)
     if args.decode:
         return _decode(args, torch)
 
@@ -396,6 +400,60 @@ def _stream_timeline(args, torch):
             line += f"; wait for loads {pct(start - prev)}"
         print(line)
     print(f"  last stores issued -> exit  {pct(t[:, :, 63].max(axis=1) - t[:, :, 3 * units].max(axis=1))}")
+    return 0
+
+
+def _quarter_timeline(args, torch):
+    """Where the key-quarter kernel's time goes: per wave, its loads' issue
+    and landing, its two tiles, the merge tree and the store."""
+    import ctypes
+
+    import numpy as np
+
+    from flashlite_amd.workloads import WORKLOADS, Workload, workload_inputs
+
+    w = WORKLOADS[args.workload]
+    if args.shape:
+        b, h, n = args.shape
+        w = Workload(f"B{b}H{h}N{n}", b, h, n, 64, (False, True), 1)
+    lib = _diag_lib()
+    lib.fl_diag_quarter_timeline.argtypes = ([ctypes.c_int] + [ctypes.c_void_p] * 4 +
+                                             [ctypes.c_int] * 3 +
+                                             [ctypes.c_void_p, ctypes.c_longlong, ctypes.c_void_p])
+    lib.fl_diag_quarter_timeline.restype = ctypes.c_int
+    lib.fl_diag_wall_clock_khz.argtypes = [ctypes.c_int]
+    lib.fl_diag_wall_clock_khz.restype = ctypes.c_int
+    dev = torch.device("cuda:0")
+    q, k, v = (torch.from_numpy(x).to(dev) for x in workload_inputs(w))
+    o = torch.empty_like(q)
+    groups = w.batch * w.heads * ((w.seq + 31) // 32)
+    out = torch.zeros(groups * 8 * 64, dtype=torch.int64, device=dev)
+    stream = torch.cuda.current_stream().cuda_stream
+
+    def launch():
+        rc = lib.fl_diag_quarter_timeline(args.causal, q.data_ptr(), k.data_ptr(), v.data_ptr(),
+                                          o.data_ptr(), w.batch, w.heads, w.seq, out.data_ptr(),
+                                          out.numel(), stream)
+        if rc != 0:
+            raise RuntimeError(f"diagnostic launch failed: hipError {rc}")
+
+    us = _time_launches(launch, args, torch)
+    d = out.cpu().numpy().reshape(groups, 8, 64)[:, :4, :].astype(np.int64)
+    tick_us = 1e3 / lib.fl_diag_wall_clock_khz(0)
+    t = (d - d[:, :, 0].min()) * tick_us
+    pct = lambda x: (f"p50 {np.median(x):6.2f}  p90 {np.percentile(x, 90):6.2f}  "  # noqa: E731
+                     f"max {x.max():6.2f} us")
+    print(f"quarter timeline {w.name} causal={args.causal}: {us:.2f} us/launch over {args.iters} "
+          f"launches (events); last launch: {groups} groups x 4 waves, span "
+          f"{t[:, :, 63].max():.2f} us", flush=True)
+    busy = d[:, :, 2] != 0  # waves with key tiles
+    print(f"  entry (after the first)          {pct(t[:, :, 0].ravel())}")
+    print(f"  entry -> loads issued, Q loaded  {pct((t[:, :, 1] - t[:, :, 0]).ravel())}")
+    print(f"  -> loads landed                  {pct((t[:, :, 2] - t[:, :, 1])[busy])}")
+    print(f"  -> tiles done                    {pct((t[:, :, 3] - t[:, :, 2])[busy])}")
+    print(f"  -> merged                        {pct((t[:, :, 4] - t[:, :, 3]).ravel())}")
+    print(f"  -> exit (wave 0: the store)      {pct(t[:, 0, 63] - t[:, 0, 4])}")
+    print(f"  group span (first entry -> wave 0 exit) {pct(t[:, 0, 63] - t[:, :, 0].min(axis=1))}")
     return 0
 
 
