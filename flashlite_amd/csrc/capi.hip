@@ -109,11 +109,14 @@ int check_pointers(const fl_attn_params* p, fl::FwdArgs* a, const char* who, uin
 // go to the streaming persistent groups (measured at least as fast as every
 // other configuration from 16 to 2048 units, both masks), and of at most
 // 512 with at most one 32-row group per CU to the key quarters.  Long key
-// ranges (N_k >= 2048) with at most one 128-row group per CU take the
-// key-range-split group (8 waves, two per SIMD, each half walking half the
-// keys): 3-11% faster than the 4-wave groups there, both masks (and for
-// causal down to 64 groups; fewer fall back to smaller groups).  With more
-// groups, non-causal takes one 256-row group of 8 waves per CU; otherwise
+// ranges with at most one 128-row group per CU take the key-range-split
+// group (8 waves, two per SIMD, each half walking half the keys): causal
+// from N_k 2048 (64 groups up; fewer fall back to smaller groups), 7-11%
+// faster than the 4-wave groups; non-causal from N_k 4096, or 2048 with
+// fewer than 128 groups, 5-10% faster (at N_k 2048 with 128-256 groups the
+// two measured within 3% either way).  With more than 128 groups of 256
+// rows over N_k >= 2048, non-causal takes one 256-row group of 8 waves per
+// CU; otherwise
 // 128-row slot-scheduled groups of 4 waves, two per CU, which also serve
 // causal attention (groups of different lengths, balanced by dispatch
 // order).  Smaller problems fall back to smaller groups.  Replaces the
@@ -126,9 +129,10 @@ int select_fa2(const fl::FwdArgs& a) {
   // N_k <= 512 with few query blocks: quarter the key range (one 4-wave
   // work-group per 32 rows; a single round on the CUs).
   if (fl::quarter_config_fits(a) && wgs(32) <= kCus) return fl::kQuarterConfig;
-  if (a.seq_k >= 2048 && wgs(128) <= kCus && (!a.causal || wgs(128) >= kCus / 4))
+  const bool one_round = a.seq_k >= 2048 && wgs(128) <= kCus;
+  if (one_round && (a.causal ? wgs(128) >= kCus / 4 : a.seq_k >= 4096 || wgs(128) < kCus / 2))
     return fl::kCfgSplit2;
-  if (!a.causal && a.seq_k >= 2048 && wgs(256) >= kCus / 2) return fl::kSlotW8Config;
+  if (!a.causal && a.seq_k >= 2048 && wgs(256) > kCus / 2) return fl::kSlotW8Config;
   if (wgs(128) >= kCus / 4) return fl::kSlotW4Config;
   if (wgs(64) >= kCus / 4) return fl::kCfgW2;
   return fl::kCfgW1;

@@ -172,8 +172,8 @@ def test_dispatcher_choices():
     W8, W4, SPLIT, STRM = ("br256_bc64_w8_slot", "br128_bc64_w4_slot", "br128_bc64_w4x2_slot",
                            "br256_kv256_w8_stream")
     W1, W2, QTR = "br32_bc64_w1", "br64_bc64_w2", "br32_kv512_w4_quarters"
-    # non-causal: 8-wave 256-row slot-scheduled groups when there are at
-    # least 128 and the key range is long
+    # non-causal: 8-wave 256-row slot-scheduled groups when there are more
+    # than 128 and the key range is long
     assert sel(batch=2, heads=8, seq_q=4096) == W8      # 256 groups
     assert sel(batch=1, heads=16, seq_q=16384) == W8
     assert sel(batch=2, heads=8, seq_q=2560) == W8      # 160 groups
@@ -183,9 +183,12 @@ def test_dispatcher_choices():
     assert sel(batch=8, heads=32, seq_q=130) == STRM      # 256 units
     assert sel(batch=2, heads=8, seq_q=256) == STRM       # 16 units
     assert sel(batch=1, heads=1, seq_q=1000, seq_k=256) == STRM
-    # at most one 128-row group per CU over N_k >= 2048: split key range
-    assert sel(batch=2, heads=8, seq_q=2048) == SPLIT      # 256 groups of 128 rows
+    # at most one 128-row group per CU over long key ranges: split key range
+    # (non-causal from N_k 4096, or with fewer than 128 groups)
+    assert sel(batch=2, heads=8, seq_q=2048) == W4         # 256 groups of 128 rows
     assert sel(batch=2, heads=8, seq_q=2048, causal=True) == SPLIT
+    assert sel(batch=1, heads=8, seq_q=4096) == SPLIT
+    assert sel(batch=1, heads=4, seq_q=2048) == SPLIT      # 64 groups
     assert sel(batch=1, heads=8, seq_q=4096, causal=True) == SPLIT
     assert sel(batch=1, heads=1, seq_q=4096) == SPLIT
     assert sel(batch=1, heads=3, seq_q=4096) == SPLIT      # 96 groups of 128 rows
