@@ -18,7 +18,7 @@ import pytest
 
 from flashlite_amd import capi
 from flashlite_amd.workloads import WORKLOADS, make_qkv, workload_inputs
-from gpu_util import SLOT_W4_CFG, STREAM_CFG, assert_close_oracle, run_capi, to_dev
+from gpu_util import SLOT_W4_CFG, STREAM_CFG, assert_close_oracle, run_capi, sample_rows, to_dev
 from oracle import attention_fp32, attention_lse, error_stats
 
 pytestmark = pytest.mark.gpu
@@ -53,6 +53,30 @@ SHAPES = [
     (2, 2, 513, 129),      # N_q > N_k, rows with no visible key when causal
     (64, 48, 96, 160),     # 3072 units: 12 per work-group, both buffers reused many times
 ]
+
+
+# The kernel's instances and modes by shape: the next unit's K/V fetches
+# spread over the tile steps (at least 4 units per work-group, N_k > 192),
+# or all issued first; causal waves 0-3 fetching for waves 4-7 (N_q > 224).
+# Sampled rows keep the CPU oracle short at 512-1024 heads.
+MODES = [
+    (32, 32, 250, 250),    # 1024 units: spread, and causal sharing
+    (32, 32, 200, 200),    # 1024 units: spread, no sharing
+    (8, 64, 256, 256),     # 512 units: all first, causal sharing
+    (16, 32, 225, 225),    # 512 units: sharing from N_q 225 on
+]
+
+
+@pytest.mark.parametrize("b,h,nq,nk", MODES)
+@pytest.mark.parametrize("causal", [False, True])
+def test_fetch_modes(cuda, b, h, nq, nk, causal):
+    rs = np.random.RandomState(b * 100 + h + nq)
+    mk = lambda n: rs.standard_normal((b, h, n, 64)).astype(np.float32).astype(np.float16)  # noqa: E731
+    q, k, v = mk(nq), mk(nk), mk(nk)
+    out, _ = _run_ex(q, k, v, 0.125, causal, cuda)
+    assert np.isfinite(out).all(), "unwritten outputs"
+    rows = sample_rows(nq, count=48, seed=nq)
+    assert_close_oracle(out, q, k, v, 0.125, causal, rows=rows)
 
 
 @pytest.mark.parametrize("b,h,nq,nk", SHAPES)
