@@ -108,9 +108,14 @@ int check_pointers(const fl_attn_params* p, fl::FwdArgs* a, const char* who, uin
 // configuration computes the same result).  Key ranges of at most 256 keys
 // go to the streaming persistent groups (measured at least as fast as every
 // other configuration from 16 to 2048 units, both masks), and of at most
-// 512 with at most one 32-row group per CU to the key quarters.  Long key
-// ranges with at most one 128-row group per CU take the key-range-split
-// group (8 waves, two per SIMD, each half walking half the keys): causal
+// 512 with at most one 32-row group per CU to the key quarters.  Past 576
+// keys, 64 to 256 groups of 64 rows take the key-range split on 64-row
+// groups (2 x 2 waves, one per SIMD, each pair walking half the keys): one
+// group on every CU where the 128-row groups leave CUs idle, 1-13% faster
+// than every other configuration (N_k 640-16384; at N_k 513 the 128-row
+// groups were 2.5% faster, and with more than 256 groups a second round
+// costs 27-70%).  Other long key ranges with at most one 128-row group per
+// CU take the key-range-split group of 8 waves (two per SIMD): causal
 // from N_k 2048 (64 groups up; fewer fall back to smaller groups), 7-11%
 // faster than the 4-wave groups; non-causal from N_k 4096, or 2048 with
 // fewer than 128 groups, 5-10% faster (at N_k 2048 with 128-256 groups the
@@ -129,6 +134,9 @@ int select_fa2(const fl::FwdArgs& a) {
   // N_k <= 512 with few query blocks: quarter the key range (one 4-wave
   // work-group per 32 rows; a single round on the CUs).
   if (fl::quarter_config_fits(a) && wgs(32) <= kCus) return fl::kQuarterConfig;
+  // Past 576 keys, 64 to 256 groups of 64 rows: the key-range split on
+  // 64-row groups (2 x 2 waves), one group per CU in a single round.
+  if (a.seq_k > 576 && wgs(64) <= kCus && wgs(64) >= kCus / 4) return fl::kCfgSplit2W2;
   const bool one_round = a.seq_k >= 2048 && wgs(128) <= kCus;
   if (one_round && (a.causal ? wgs(128) >= kCus / 4 : a.seq_k >= 4096 || wgs(128) < kCus / 2))
     return fl::kCfgSplit2;

@@ -124,7 +124,7 @@ int fl_diag_slot_timeline(int mode, int causal, const void* q, const void* k, co
   a.q_sh = a.k_sh = a.v_sh = a.o_sh = (int64_t)N * 64;
   a.q_sb = a.k_sb = a.v_sb = a.o_sb = (int64_t)H * N * 64;
   const auto st = static_cast<hipStream_t>(stream);
-  e = mode == 2 ? fl::diag_timeline_launch_slot_split(a, st)
+  e = mode == 2 ? fl::diag_timeline_launch_slot_split(a, 4, st)
                 : fl::diag_timeline_launch_slot(a, mode, st);
   return (int)e;
 }

@@ -15,6 +15,7 @@ const Fa2Config kFa2Configs[kNumFa2Configs] = {
     {4, "br128_bc64_w4_slot"},
     {8, "br256_kv256_w8_stream"},
     {4, "br32_kv512_w4_quarters"},
+    {4, "br64_bc64_w2x2_slot"},
 };
 
 bool stream_config_fits(const FwdArgs& a) {
@@ -37,7 +38,8 @@ hipError_t launch_fa2(const FwdArgs& a, int cfg, hipStream_t stream) {
   switch (cfg) {
     case kCfgW1:
     case kCfgW2: return launch_pipe(a, cfg, stream);
-    case kCfgSplit2: return launch_slot_split(a, stream);
+    case kCfgSplit2: return launch_slot_split(a, 4, stream);
+    case kCfgSplit2W2: return launch_slot_split(a, 2, stream);
     case kSlotW8Config: return launch_slot(a, 8, stream);
     case kSlotW4Config: return launch_slot(a, 4, stream);
     case kStreamConfig: return launch_stream(a, stream);

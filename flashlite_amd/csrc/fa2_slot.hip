@@ -49,17 +49,23 @@ namespace {
 // sums a few p.  Blocks whose first pass saw a tile sum out of the
 // fp16-safe range are recomputed by a plain one-tile-per-step checked pass.
 //
-// SPLIT = 2 (configuration br128_bc64_w4x2_slot): 2W waves, two per SIMD,
-// hold the same 32W query rows; waves 0..W-1 (stream 0) walk the first
-// ceil(n/2) of the block's n key tiles and waves W..2W-1 (stream 1) the rest,
-// each stream through its own rings, and the halves merge through LDS at
-// the end (Rows::save_partial / merge_partial).  Both streams run the same
-// iterations (the shorter one ends on a fully masked tile), so every wave
-// meets the same barriers.  This halves the longest key walk: a causal
-// work-group's time follows half its tiles, and heaviest-first dispatch of
-// one work-group per CU then balances the CUs.
+// SPLIT = 2 (configurations br128_bc64_w4x2_slot, W = 4, and
+// br64_bc64_w2x2_slot, W = 2): 2W waves hold the same 32W query rows (W = 4:
+// two waves per SIMD; W = 2: one per SIMD, and twice as many groups for the
+// same problem, so up to 256 CUs get one each in a single round); waves
+// 0..W-1 (stream 0) walk the first ceil(n/2) of the block's n key tiles and
+// waves W..2W-1 (stream 1) the rest, each stream through its own rings,
+// and the halves merge through LDS at the end (Rows::save_partial /
+// merge_partial).  Both streams run the same iterations (the shorter one
+// ends on a fully masked tile), so every wave meets the same barriers.
+// This halves the longest key walk: a causal work-group's time follows half
+// its tiles, and heaviest-first dispatch of one work-group per CU then
+// balances the CUs.
 template <int W, int FV, bool CAUSAL, bool SCALED, class T = _Float16, int SPLIT = 1>
-__global__ void __launch_bounds__(64 * W * SPLIT, 2)  // <= 256 VGPRs: 2 waves per SIMD
+// Register budget for 2 waves per SIMD (<= 256 VGPRs).  W = 2 with SPLIT
+// holds 160 KiB of LDS, so one work-group (one wave per SIMD) per CU: the
+// compiler reports that target as missed; that code is the measured one.
+__global__ void __launch_bounds__(64 * W * SPLIT, 2)
 fa2_fwd_slot_kernel(const T* Q, const T* __restrict__ K, const T* __restrict__ V, T* O,
                     const Geom geom, int nqb, float cq, float cr) {
   using RowsT = Rows<CAUSAL, SCALED, T>;
@@ -340,10 +346,13 @@ hipError_t launch_slot(const FwdArgs& a, int waves, hipStream_t stream) {
   return hipErrorInvalidValue;
 }
 
-// fp16: 128-row groups of 2 x 4 waves, the key range halved between them.
-hipError_t launch_slot_split(const FwdArgs& a, hipStream_t stream) {
+// fp16: groups of 2 x `waves` waves (4: 128 rows, 2: 64 rows), the key
+// range halved between them.
+hipError_t launch_slot_split(const FwdArgs& a, int waves, hipStream_t stream) {
   if (a.dtype != kDtypeF16) return hipErrorInvalidValue;
-  return dispatch<SlotLaunch<4, SLOT_SPLIT_FV, _Float16, 2>::L>(a, stream, 128);
+  if (waves == 4) return dispatch<SlotLaunch<4, SLOT_SPLIT_FV, _Float16, 2>::L>(a, stream, 128);
+  if (waves == 2) return dispatch<SlotLaunch<2, SLOT_SPLIT_FV, _Float16, 2>::L>(a, stream, 64);
+  return hipErrorInvalidValue;
 }
 
 }  // namespace fl

@@ -54,7 +54,8 @@ constexpr int kStreamConfig = 5;   // br256_kv256_w8_stream
 // One 4-wave work-group per 32-row query block, each wave a quarter of at
 // most kQuarterMaxKeys keys (fp16, head_dim 64).
 constexpr int kQuarterConfig = 6;  // br32_kv512_w4_quarters
-constexpr int kNumFa2Configs = 7;
+constexpr int kCfgSplit2W2 = 7;     // br64_bc64_w2x2_slot: 2 x 2 waves, key range halved
+constexpr int kNumFa2Configs = 8;
 extern const Fa2Config kFa2Configs[kNumFa2Configs];
 
 // Launches the FA2 kernel for configuration `cfg` on `stream`.  fp16 at
@@ -70,7 +71,7 @@ inline bool quarter_config_fits(const FwdArgs& a) { return a.seq_k <= kQuarterMa
 // Per-schedule launchers behind launch_fa2 (one source file each).
 hipError_t launch_pipe(const FwdArgs& a, int cfg, hipStream_t stream);     // fa2_pipe.hip
 hipError_t launch_slot(const FwdArgs& a, int waves, hipStream_t stream);   // fa2_slot.hip
-hipError_t launch_slot_split(const FwdArgs& a, hipStream_t stream);        // fa2_slot.hip
+hipError_t launch_slot_split(const FwdArgs& a, int waves, hipStream_t stream);  // fa2_slot.hip
 hipError_t launch_stream(const FwdArgs& a, hipStream_t stream);            // fa2_stream.hip
 hipError_t launch_quarter(const FwdArgs& a, hipStream_t stream);           // fa2_short.hip
 hipError_t launch_d128(const FwdArgs& a, int waves, hipStream_t stream);   // fa2_d128.hip

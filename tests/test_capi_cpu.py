@@ -29,11 +29,12 @@ def test_library_loads_and_exports_header_symbols():
 
 
 def test_config_table():
-    assert capi.num_configs() == 7
-    names = [capi.config_name(i) for i in range(7)]
+    assert capi.num_configs() == 8
+    names = [capi.config_name(i) for i in range(8)]
     assert names == ["br32_bc64_w1", "br64_bc64_w2", "br128_bc64_w4x2_slot", "br256_bc64_w8_slot",
-                     "br128_bc64_w4_slot", "br256_kv256_w8_stream", "br32_kv512_w4_quarters"]
-    assert capi.config_name(7) is None and capi.config_name(-1) is None
+                     "br128_bc64_w4_slot", "br256_kv256_w8_stream", "br32_kv512_w4_quarters",
+                     "br64_bc64_w2x2_slot"]
+    assert capi.config_name(8) is None and capi.config_name(-1) is None
     assert capi.config_id("br256_bc64_w8_slot") == 3
 
 
@@ -172,6 +173,7 @@ def test_dispatcher_choices():
     W8, W4, SPLIT, STRM = ("br256_bc64_w8_slot", "br128_bc64_w4_slot", "br128_bc64_w4x2_slot",
                            "br256_kv256_w8_stream")
     W1, W2, QTR = "br32_bc64_w1", "br64_bc64_w2", "br32_kv512_w4_quarters"
+    SPLIT64 = "br64_bc64_w2x2_slot"
     # non-causal: 8-wave 256-row slot-scheduled groups when there are more
     # than 128 and the key range is long
     assert sel(batch=2, heads=8, seq_q=4096) == W8      # 256 groups
@@ -188,18 +190,28 @@ def test_dispatcher_choices():
     assert sel(batch=2, heads=8, seq_q=2048) == W4         # 256 groups of 128 rows
     assert sel(batch=2, heads=8, seq_q=2048, causal=True) == SPLIT
     assert sel(batch=1, heads=8, seq_q=4096) == SPLIT
-    assert sel(batch=1, heads=4, seq_q=2048) == SPLIT      # 64 groups
+    assert sel(batch=1, heads=1, seq_q=2048) == SPLIT      # 16 groups
     assert sel(batch=1, heads=8, seq_q=4096, causal=True) == SPLIT
-    assert sel(batch=1, heads=1, seq_q=4096) == SPLIT
-    assert sel(batch=1, heads=3, seq_q=4096) == SPLIT      # 96 groups of 128 rows
+    assert sel(batch=1, heads=1, seq_q=1024, seq_k=4096) == SPLIT
+    assert sel(batch=1, heads=1, seq_q=2048, seq_k=8192) == SPLIT   # 16 groups of 128 rows
     assert sel(batch=1, heads=1, seq_q=1000, seq_k=4096) == SPLIT
-    assert sel(batch=2, heads=8, seq_q=1024) == W4         # N_k < 2048
+    # past 512 keys with 128-256 groups of 64 rows: the split on 64-row groups
+    assert sel(batch=2, heads=8, seq_q=1024) == SPLIT64    # 256 groups of 64 rows
+    assert sel(batch=2, heads=8, seq_q=1024, causal=True) == SPLIT64
+    assert sel(batch=1, heads=8, seq_q=2048) == SPLIT64
+    assert sel(batch=1, heads=4, seq_q=4096, causal=True) == SPLIT64
+    assert sel(batch=1, heads=8, seq_q=1024) == SPLIT64    # 128 groups
+    assert sel(batch=1, heads=1, seq_q=4096) == SPLIT64    # 64 groups
+    assert sel(batch=1, heads=1, seq_q=4096, causal=True) == SPLIT64
+    assert sel(batch=2, heads=8, seq_q=640) == SPLIT64
+    assert sel(batch=2, heads=8, seq_q=513) == W4          # N_k <= 576: 128-row groups
+    assert sel(batch=1, heads=1, seq_q=2048, causal=True) == W1    # 32 groups of 64 rows
+    assert sel(batch=3, heads=8, seq_q=1024) == W4         # 384 groups of 64 rows
     assert sel(batch=4, heads=4, seq_q=1536, causal=True) == W4
     # causal: 128-row slot-scheduled groups balanced by dispatch order
     assert sel(batch=2, heads=8, seq_q=4096, causal=True) == W4
     assert sel(batch=1, heads=16, seq_q=16384, causal=True) == W4
     assert sel(batch=3, heads=8, seq_q=2048, causal=True) == W4   # 384 groups
-    assert sel(batch=1, heads=1, seq_q=4096, causal=True) == W2   # 32 groups of 128 rows
     assert sel(batch=32, heads=32, seq_q=256, causal=True) == STRM   # streaming, any count
     assert sel(batch=1, heads=1, seq_q=128, causal=True) == STRM
     # 256 < N_k <= 512 with at most one 32-row group per CU: key quarters
@@ -210,8 +222,7 @@ def test_dispatcher_choices():
     assert sel(batch=1, heads=1, seq_q=100, seq_k=512) == QTR
     # more groups, or longer key ranges: 128-row or smaller groups
     assert sel(batch=4, heads=8, seq_q=512) == W4       # 512 groups of 32 rows
-    assert sel(batch=2, heads=8, seq_q=513) == W4
-    assert sel(batch=2, heads=4, seq_q=600) == W2       # 80 groups of 64 rows
+    assert sel(batch=2, heads=4, seq_q=576) == W2       # 72 groups of 64 rows
     assert sel(batch=1, heads=1, seq_q=600) == W1
     assert capi.select_config(_p(head_dim=80)) == -1
 

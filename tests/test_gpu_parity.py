@@ -12,22 +12,23 @@ import pytest
 
 from flashlite_amd import capi
 from flashlite_amd.workloads import WORKLOADS, make_qkv, workload_inputs
-from gpu_util import (SLOT_W4_CFG, SLOT_W8_CFG, SPLIT2_CFG, assert_close_oracle, config_fits,
-                      redo_expected, run_capi, sample_rows, to_dev)
+from gpu_util import (SLOT_W4_CFG, SLOT_W8_CFG, SPLIT2_CFG, SPLIT2W2_CFG, assert_close_oracle,
+                      config_fits, redo_expected, run_capi, sample_rows, to_dev)
 from oracle import error_stats
 
 pytestmark = pytest.mark.gpu
 
 GOLDEN = os.path.join(os.path.dirname(__file__), "golden")
-NCFG = 7  # tile configurations exported by the library
-SPLIT_CFGS = [SPLIT2_CFG]  # the key-range-split configuration
+NCFG = 8  # tile configurations exported by the library
+SPLIT_CFGS = [SPLIT2_CFG, SPLIT2W2_CFG]  # the key-range-split configurations
 
 
 def test_num_configs():
     assert capi.num_configs() == NCFG
     assert [capi.config_name(i) for i in range(NCFG)] == [
         "br32_bc64_w1", "br64_bc64_w2", "br128_bc64_w4x2_slot", "br256_bc64_w8_slot",
-        "br128_bc64_w4_slot", "br256_kv256_w8_stream", "br32_kv512_w4_quarters"]
+        "br128_bc64_w4_slot", "br256_kv256_w8_stream", "br32_kv512_w4_quarters",
+        "br64_bc64_w2x2_slot"]
 
 
 @pytest.mark.parametrize("config", list(range(NCFG)))
