@@ -33,6 +33,8 @@ hipError_t launch_fa2(const FwdArgs& a, int cfg, hipStream_t stream) {
   if (a.dtype == kDtypeBF16) {
     if (cfg == kSlotW8Config) return launch_slot(a, 8, stream);
     if (cfg == kSlotW4Config) return launch_slot(a, 4, stream);
+    if (cfg == kCfgSplit2) return launch_slot_split(a, 4, stream);
+    if (cfg == kCfgSplit2W2) return launch_slot_split(a, 2, stream);
     return hipErrorInvalidValue;
   }
   switch (cfg) {

@@ -346,12 +346,16 @@ hipError_t launch_slot(const FwdArgs& a, int waves, hipStream_t stream) {
   return hipErrorInvalidValue;
 }
 
-// fp16: groups of 2 x `waves` waves (4: 128 rows, 2: 64 rows), the key
-// range halved between them.
+// fp16 or bf16 by a.dtype: groups of 2 x `waves` waves (4: 128 rows, 2: 64
+// rows), the key range halved between them.
 hipError_t launch_slot_split(const FwdArgs& a, int waves, hipStream_t stream) {
-  if (a.dtype != kDtypeF16) return hipErrorInvalidValue;
-  if (waves == 4) return dispatch<SlotLaunch<4, SLOT_SPLIT_FV, _Float16, 2>::L>(a, stream, 128);
-  if (waves == 2) return dispatch<SlotLaunch<2, SLOT_SPLIT_FV, _Float16, 2>::L>(a, stream, 64);
+  const bool bf = a.dtype == kDtypeBF16;
+  if (waves == 4)
+    return bf ? dispatch<SlotLaunch<4, SLOT_SPLIT_FV, __bf16, 2>::L>(a, stream, 128)
+              : dispatch<SlotLaunch<4, SLOT_SPLIT_FV, _Float16, 2>::L>(a, stream, 128);
+  if (waves == 2)
+    return bf ? dispatch<SlotLaunch<2, SLOT_SPLIT_FV, __bf16, 2>::L>(a, stream, 64)
+              : dispatch<SlotLaunch<2, SLOT_SPLIT_FV, _Float16, 2>::L>(a, stream, 64);
   return hipErrorInvalidValue;
 }
 

@@ -24,7 +24,8 @@ import numpy as np
 import pytest
 
 from flashlite_amd import capi
-from gpu_util import MAX_ABS, MEAN_ABS, SLOT_W4_CFG, SLOT_W8_CFG, half_ulp, sample_rows
+from gpu_util import (MAX_ABS, MEAN_ABS, SLOT_W4_CFG, SLOT_W8_CFG, SPLIT2_CFG, SPLIT2W2_CFG,
+                      half_ulp, sample_rows)
 from oracle import attention_fp32, attention_lse, error_stats
 
 pytestmark = pytest.mark.gpu
@@ -180,6 +181,28 @@ def test_strided_bit_exact(cuda, kind, d, causal):
     for views in (bnhd, padded):
         out, _ = _run(kind, q, k, v, 0.125, causal, cuda, views=views)
         assert np.array_equal(out, base), views.__name__
+
+
+@pytest.mark.parametrize("config", [SPLIT2_CFG, SPLIT2W2_CFG])
+@pytest.mark.parametrize("causal", [False, True])
+def test_bf16_key_range_splits(cuda, config, causal):
+    """bf16 at D = 64 on both key-range splits (128- and 64-row groups):
+    ragged lengths, every output row of B1 H4 N1024, and a peaked scale whose
+    row sums leave the first pass's range (the checked pass)."""
+    for n in RAGGED:
+        q, k, v = _inputs("bf16", 2, 3, n, n, 64, seed=3000 + n)
+        out, _ = _run("bf16", q, k, v, 0.0, causal, cuda, config=config)
+        _check("bf16", out, attention_fp32(q, k, v, 0.0, causal), f"N={n}")
+    q, k, v = _inputs("bf16", 1, 4, 1024, 1024, 64, seed=41)
+    out, _ = _run("bf16", q, k, v, 0.125, causal, cuda, config=config)
+    _check("bf16", out, attention_fp32(q, k, v, 0.125, causal), "B1 H4 N1024")
+    q, k, v = _inputs("bf16", 1, 2, 700, 700, 64, seed=43, qk_scale=3.0)
+    out, _ = _run("bf16", q, k, v, 1.0, causal, cuda, config=config)
+    ref = attention_fp32(q, k, v, 1.0, causal)
+    mx_tol, mean_tol = _tol("bf16")
+    assert np.isfinite(out).all()
+    assert error_stats(out, ref)[1] <= mean_tol
+    assert (np.abs(out.astype(np.float64) - ref) <= mx_tol + half_ulp(ref, 7)).all()
 
 
 @pytest.mark.parametrize("kind,d", WIDE)

@@ -61,8 +61,13 @@ def test_wide_config_checks():
             slots = (capi.config_id("br256_bc64_w8_slot"), capi.config_id("br128_bc64_w4_slot"))
             stream_cfg = capi.config_id("br256_kv256_w8_stream")
             quarter_cfg = capi.config_id("br32_kv512_w4_quarters")
+            # bf16 at D = 64 also has both key-range splits
+            splits = (capi.config_id("br128_bc64_w4x2_slot"), capi.config_id("br64_bc64_w2x2_slot"))
             for cfg in range(capi.num_configs()):
                 if cfg in slots or cfg in (stream_cfg, quarter_cfg):
+                    continue
+                if d == 64 and cfg in splits:
+                    assert fn(_ex(head_dim=d), config=cfg) != capi.FL_ERR_BAD_CONFIG
                     continue
                 assert fn(_ex(head_dim=d), config=cfg) == capi.FL_ERR_BAD_CONFIG
                 assert "not built" in capi.last_error() and who in capi.last_error()
