@@ -225,10 +225,14 @@ int check_ex(const fl_attn_params_ex* p, fl::FwdArgs* a, const char* who, bool w
 // The library's choice (requested <= 0), from decode sweeps on MI355X
 // (B2 H8 and B1 H16 with N_q 1-16 over 4k-64k keys, B32 H32 over 4k): with
 // at most 128 query rows and fewer query-row groups than CUs, cut each key
-// range so that the groups times chunks cover the 256 CUs once, keeping at
-// least 4 key tiles per chunk (more chunks measured slower: per-work-group
-// start-up); with more single-wave groups (N_q <= 32), chunks of 8 tiles up
-// to 8 chunks when the range is long (>= 32 tiles).  Otherwise one pass.
+// range so that the groups times chunks cover the 256 CUs twice with
+// single-wave groups (N_q <= 32; 2-11% faster than once, measured) and once
+// with 2- and 4-wave groups (twice: +1% and +25%), keeping at least 4 key
+// tiles per chunk (shorter chunks measured slower: per-work-group start-up);
+// with more single-wave groups, chunks of 8 tiles up to 8 chunks when the
+// range is long (>= 32 tiles).  Otherwise one pass.  Single-wave plans then
+// stay within 512 x 32 rows of partials (4.5 MB), inside the static scratch
+// of the allocation-free entry point.
 struct KvPlan {
   int waves, nsplit;
   int64_t bytes;
@@ -249,7 +253,8 @@ KvPlan plan_kvsplit(const fl::FwdArgs& a, int32_t requested) {
   } else if (a.seq > 128) {
     n = 0;  // long query ranges: the one-pass kernel's groups fill the GPU
   } else if (groups < kCus) {
-    n = std::min<int64_t>({(kCus + groups - 1) / groups, tiles / 4, kMaxSplits});
+    const int64_t cover = (p.waves == 1 ? 2 : 1) * kCus;
+    n = std::min<int64_t>({(cover + groups - 1) / groups, tiles / 4, kMaxSplits});
   } else {
     n = (a.seq <= 32 && tiles >= 32) ? std::min<int64_t>(8, tiles / 8) : 0;
   }

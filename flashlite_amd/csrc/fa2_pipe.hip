@@ -209,9 +209,20 @@ fa2_fwd_kernel(const _Float16* Q, const _Float16* __restrict__ K,
 // row (O unnormalised at stabiliser m_s, row sum l_s) at their largest m:
 //   O = sum_s 2^(m_s - M) O_s / sum_s 2^(m_s - M) l_s,
 // and writes O (fp16, lane = head dim) and, when asked, the log-sum-exp.
+// Lane j holds m and l of chunks j, j + 64, ...; its weight w_j goes to the
+// whole wave by readlane, and each batch of 8 chunks issues its 8 O loads
+// before the first multiply, so the row costs a few memory round trips
+// rather than one per chunk.  A chunk with no visible key stored m = -inf
+// and l = 0: weight 0, skipped by a select, not a branch.
 __device__ __forceinline__ float wave_max64(float x) {
 #pragma unroll
   for (int m = 32; m >= 1; m >>= 1) x = fmaxf(x, __shfl_xor(x, m, 64));
+  return x;
+}
+
+__device__ __forceinline__ float wave_sum64(float x) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) x += __shfl_xor(x, m, 64);
   return x;
 }
 
@@ -223,18 +234,37 @@ splitkv_combine_kernel(_Float16* O, const Geom geom) {
   const int bh = row_id / geom.seq_q, row = row_id - bh * geom.seq_q;
   const long long split_stride = (long long)geom.batch_heads * geom.seq_q * kPartStride;
   const float* p0 = geom.part + (long long)row_id * kPartStride;
+  const int ns = geom.nsplit;
   float mx = ninf();
-  for (int s = lane; s < geom.nsplit; s += 64) mx = fmaxf(mx, p0[s * split_stride + 64]);
+  for (int s = lane; s < ns; s += 64) mx = fmaxf(mx, p0[s * split_stride + 64]);
   mx = wave_max64(mx);
-  float acc = 0.0f, lsum = 0.0f;
-  for (int s = 0; s < geom.nsplit; ++s) {
-    const float* ps = p0 + s * split_stride;
-    const float m = ps[64];
-    if (m == ninf()) continue;  // no key of this chunk is visible to the row
-    const float w = __builtin_amdgcn_exp2f(m - mx);
-    lsum += w * ps[65];
-    acc += w * ps[lane];
+  float acc = 0.0f, lpart = 0.0f;
+  for (int s0 = 0; s0 < ns; s0 += 64) {
+    float w = 0.0f;
+    if (s0 + lane < ns) {
+      const float* ps = p0 + (s0 + lane) * split_stride;
+      const float m = ps[64];
+      w = m == ninf() ? 0.0f : __builtin_amdgcn_exp2f(m - mx);
+      lpart += w * ps[65];
+    }
+    // Chunk s0 + j's weight, from lane j; a weight of 0 skips the chunk.
+    auto fold = [&](int j, float oj) __attribute__((always_inline)) {
+      const float wj = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), j));
+      acc += wj == 0.0f ? 0.0f : wj * oj;
+    };
+    const int cnt = min(64, ns - s0);
+    const float* pb = p0 + (long long)s0 * split_stride + lane;
+    int j = 0;
+    for (; j + 8 <= cnt; j += 8) {
+      float o[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) o[u] = pb[(j + u) * split_stride];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) fold(j + u, o[u]);
+    }
+    for (; j < cnt; ++j) fold(j, pb[j * split_stride]);
   }
+  const float lsum = wave_sum64(lpart);
   const int b = bh / geom.heads, h = bh - b * geom.heads;
   _Float16* orow = O + (b * geom.o_sb + h * geom.o_sh) + (long long)row * geom.o_sr;
   orow[lane] = (_Float16)(lsum > 0.0f ? acc / lsum : 0.0f);

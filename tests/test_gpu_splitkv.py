@@ -40,8 +40,10 @@ def _run_split(tq, tk, tv, sm_scale, causal, splits, lse=True, o_fill=float("nan
     return o, ls, need
 
 
+# (2, 9000) with 1000 requested: 141 chunks, more than one wave's 64 lanes
+# in the combine
 SHAPES = [(1, 4096), (1, 1000), (4, 777), (32, 4096), (33, 2048), (100, 3000), (1, 64),
-          (100, 130)]
+          (100, 130), (2, 9000)]
 
 
 @pytest.mark.parametrize("nq,nk", SHAPES)
