@@ -108,7 +108,9 @@ int check_pointers(const fl_attn_params* p, fl::FwdArgs* a, const char* who, uin
 // configuration computes the same result).  Key ranges of at most 256 keys
 // go to the streaming persistent groups (measured at least as fast as every
 // other configuration from 16 to 2048 units, both masks), and of at most
-// 512 with at most one 32-row group per CU to the key quarters.  Past 576
+// 512 with at most 512 blocks of 32 rows to the key quarters (one block per
+// group up to 256 blocks, two beyond: 4-18% faster than the 128-row groups
+// from 320 to 512 blocks).  Past 576
 // keys, 64 to 256 groups of 64 rows take the key-range split on 64-row
 // groups (2 x 2 waves, one per SIMD, each pair walking half the keys): one
 // group on every CU where the 128-row groups leave CUs idle, 1-13% faster
@@ -131,9 +133,9 @@ int select_fa2(const fl::FwdArgs& a) {
   constexpr int64_t kCus = 256;
   auto wgs = [&](int64_t br) { return (a.seq + br - 1) / br * (int64_t)a.batch_heads; };
   if (fl::stream_config_fits(a)) return fl::kStreamConfig;  // br256_kv256_w8_stream
-  // N_k <= 512 with few query blocks: quarter the key range (one 4-wave
-  // work-group per 32 rows; a single round on the CUs).
-  if (fl::quarter_config_fits(a) && wgs(32) <= kCus) return fl::kQuarterConfig;
+  // N_k <= 512 with few query blocks: quarter the key range (4-wave groups
+  // of 32 rows, or 8-wave groups of 64 past 256 blocks; a single round).
+  if (fl::quarter_config_fits(a) && wgs(32) <= 2 * kCus) return fl::kQuarterConfig;
   // Past 576 keys, 64 to 256 groups of 64 rows: the key-range split on
   // 64-row groups (2 x 2 waves), one group per CU in a single round.
   if (a.seq_k > 576 && wgs(64) <= kCus && wgs(64) >= kCus / 4) return fl::kCfgSplit2W2;

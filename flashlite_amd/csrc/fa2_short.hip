@@ -33,10 +33,19 @@ namespace {
 // waves of 2 tiles instead of 256 waves of 8.  LDS: 4 x 32 KiB, one
 // work-group per CU.  (Eight waves of one tile each, two per SIMD, measured
 // 7% slower on C1.)
+//
+// RB = 2 (more than 256 blocks of 32 rows, up to 512): a work-group of 8
+// waves owns two 32-row blocks, wave 4 rb + q taking row block rb and key
+// quarter q.  The two waves of a quarter fetch half of its tiles each into
+// the quarter's 32 KiB and read all of it, so a barrier publishes the tiles;
+// two more order the merge (every quarter's K/V read before any partial
+// overwrites it; partials written before wave 0 of each row block folds
+// them in).  Up to 512 blocks then still run in one round, two waves per
+// SIMD.
 constexpr int kQuarterWaves = 4;
 
-template <int NW, bool CAUSAL, bool SCALED>
-__global__ void __launch_bounds__(64 * NW, 1)
+template <int NW, int RB, bool CAUSAL, bool SCALED>
+__global__ void __launch_bounds__(64 * NW * RB, 1)
 fa2_fwd_quarter_kernel(const _Float16* Q, const _Float16* __restrict__ K,
                        const _Float16* __restrict__ V, _Float16* O, const Geom geom, int nqb,
                        float cq, float cr) {
@@ -45,52 +54,63 @@ fa2_fwd_quarter_kernel(const _Float16* Q, const _Float16* __restrict__ K,
   constexpr int kQuarterTiles = kQuarterMaxKeys / kBc / NW;  // key tiles per wave
   constexpr int kQuarterWaveBytes = 2 * kQuarterTiles * kTileBytes;
   static_assert(NW * kQuarterTiles * kBc == kQuarterMaxKeys, "key range");
+  static_assert(RB == 1 || RB == 2, "row blocks per group");
+  static_assert(RB * (9 * 64) * 16 <= kQuarterWaveBytes, "partials fit a quarter's LDS");
+  constexpr int kSegs = 8 / RB;  // 1 KiB segments of a tile each wave of a quarter fetches
   __shared__ __attribute__((aligned(16))) uint8_t buf[NW][kQuarterWaveBytes];
 
   FL_ST_DECL();
   FL_ST_MARK(0);
   const int lane = threadIdx.x & 63;
-  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // key quarter
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int kq = RB == 1 ? w : w % NW;  // key quarter
+  const int rb = RB == 1 ? 0 : w / NW;  // 32-row block within the group
   const int bh = blockIdx.x / nqb, qb = blockIdx.x - bh * nqb;
   const HeadPtrs<_Float16> hp = head_ptrs(geom, bh, Q, K, V, O);
   const int seq = geom.seq_q;
-  const int q0 = 32 * qb;
+  const int q0 = 32 * RB * qb;  // the group's first row
   int ntiles = (geom.seq_k + kBc - 1) / kBc;
-  if (CAUSAL) ntiles = min(ntiles, causal_tiles(min(q0 + 32, seq), geom.coff));
-  const int t0 = kQuarterTiles * w;
+  if (CAUSAL) ntiles = min(ntiles, causal_tiles(min(q0 + 32 * RB, seq), geom.coff));
+  const int t0 = kQuarterTiles * kq;
   const int t1 = min(t0 + kQuarterTiles, ntiles);
-  uint8_t* const kb = buf[w];
-  uint8_t* const vb = buf[w] + kQuarterTiles * kTileBytes;
+  uint8_t* const kb = buf[kq];
+  uint8_t* const vb = buf[kq] + kQuarterTiles * kTileBytes;
 
   // Q rows first, straight to registers: their latency then overlaps the
   // issue of the tile fetches below (which waits while the memory pipeline
   // is backed up).
-  const int my_q = q0 + (lane & 31), g = lane >> 5;
+  const int qr = q0 + 32 * rb;  // this wave's rows
+  const int my_q = qr + (lane & 31), g = lane >> 5;
   u32x4_t qraw[4];
 #pragma unroll
   for (int s = 0; s < 4; ++s)
     qraw[s] = my_q < seq ? *reinterpret_cast<const u32x4_t*>(hp.q + (long long)my_q * geom.q_sr +
                                                             16 * s + 8 * g)
                          : (u32x4_t){0u, 0u, 0u, 0u};
-  // This wave's K and V tiles, whole (8 segments each); rows >= N_k read
-  // as zeros through the buffer bound.
+  // This quarter's K and V tiles (this wave's kSegs segments of each);
+  // rows >= N_k read as zeros through the buffer bound.
   if (t0 < t1) {
-    const FetchOff<8> fk = fetch_offsets<8, false>(0, lane, 2 * geom.k_sr);
-    const FetchOff<8> fv = fetch_offsets<8, true>(0, lane, 2 * geom.v_sr);
+    const FetchOff<kSegs> fk = fetch_offsets<kSegs, false>(rb, lane, 2 * geom.k_sr);
+    const FetchOff<kSegs> fv = fetch_offsets<kSegs, true>(rb, lane, 2 * geom.v_sr);
 #pragma unroll
     for (int i = 0; i < kQuarterTiles; ++i) {
-      fetch_tile<8>(hp.rk, kb + i * kTileBytes, t0 + i, t1 - 1, 0, fk);
-      fetch_tile<8>(hp.rv, vb + i * kTileBytes, t0 + i, t1 - 1, 0, fv);
+      fetch_tile<kSegs>(hp.rk, kb + i * kTileBytes, t0 + i, t1 - 1, rb, fk);
+      fetch_tile<kSegs>(hp.rv, vb + i * kTileBytes, t0 + i, t1 - 1, rb, fv);
     }
   }
   RowsT rows;
-  rows.place(lane, q0, seq, geom.seq_k, geom.coff, cr);
+  rows.place(lane, qr, seq, geom.seq_k, geom.coff, cr);
   rows.set_q(qraw, cq);
   rows.reset();
   FL_ST_MARK(1);
-  if (t0 < t1) {
-    // This wave's own fetches have landed in LDS.
+  // This wave's own fetches have landed in LDS; with RB = 2 a barrier
+  // (taken by every wave) publishes the other half of each tile.
+  if constexpr (RB > 1) {
     asm volatile("s_waitcnt vmcnt(0)" : : : "memory");
+    __syncthreads();
+  }
+  if (t0 < t1) {
+    if constexpr (RB == 1) asm volatile("s_waitcnt vmcnt(0)" : : : "memory");
     FL_ST_MARK(2);
     // Tile t0 sets the stabiliser to its exact row max, so its p are at most
     // 1 and its checked softmax never moves m: tile t0+1's GEMM1 can go out
@@ -126,22 +146,23 @@ fa2_fwd_quarter_kernel(const _Float16* Q, const _Float16* __restrict__ K,
     }
   }
   FL_ST_MARK(3);
-  // Merge through each sender's own (now idle) LDS: waves 1..NW-1 store
-  // their partials at once and, after one barrier, wave 0 merges them in
+  // Merge through each quarter's (now idle) LDS: quarters 1..NW-1 store
+  // their partials at once and, after one barrier, quarter 0 merges them in
   // order (measured 5% faster on C1 than a two-step tree, which took a
-  // second barrier).  A range with no visible key holds l = 0 and is
-  // skipped by the merge.
-  float4* const part = reinterpret_cast<float4*>(buf[w]);
+  // second barrier).  Row block rb's partials sit 9 KiB in.  A range with
+  // no visible key holds l = 0 and is skipped by the merge.
+  float4* const part = reinterpret_cast<float4*>(buf[kq]) + rb * (9 * 64);
   asm volatile("s_waitcnt lgkmcnt(0)" : : : "memory");  // own LDS reads done
-  if (w != 0) rows.save_partial4(part, lane);
+  if constexpr (RB > 1) __syncthreads();  // and the other row block's
+  if (kq != 0) rows.save_partial4(part, lane);
   __syncthreads();
-  if (w == 0) {
+  if (kq == 0) {
 #pragma unroll
     for (int s = 1; s < NW; ++s)
-      rows.merge_partial4(reinterpret_cast<const float4*>(buf[s]), lane);
+      rows.merge_partial4(reinterpret_cast<const float4*>(buf[s]) + rb * (9 * 64), lane);
   }
   FL_ST_MARK(4);
-  if (w != 0) {
+  if (kq != 0) {
     FL_ST_FLUSH(w, lane, 5);
     return;
   }
@@ -150,13 +171,14 @@ fa2_fwd_quarter_kernel(const _Float16* Q, const _Float16* __restrict__ K,
   FL_ST_FLUSH(w, lane, 5);
 }
 
+template <int RB>
 struct QuarterLaunch {
   template <bool C, bool S>
   struct L {
     static hipError_t run(const FwdArgs& a, const Geom& g, dim3 grid, int nqb, float cq, float cr,
                           hipStream_t st) {
-      hipLaunchKernelGGL((fa2_fwd_quarter_kernel<kQuarterWaves, C, S>), grid,
-                         dim3(64 * kQuarterWaves), 0, st,
+      hipLaunchKernelGGL((fa2_fwd_quarter_kernel<kQuarterWaves, RB, C, S>), grid,
+                         dim3(64 * kQuarterWaves * RB), 0, st,
                          static_cast<const _Float16*>(a.q), static_cast<const _Float16*>(a.k),
                          static_cast<const _Float16*>(a.v), static_cast<_Float16*>(a.o), g, nqb,
                          cq, cr);
@@ -167,10 +189,13 @@ struct QuarterLaunch {
 
 }  // namespace
 
-// One 4-wave work-group per 32-row query block (grid B*H*ceil(N_q/32)).
+// One 4-wave work-group per 32-row query block (grid B*H*ceil(N_q/32)) up
+// to 256 of them; beyond that one 8-wave work-group per 64 rows.
 hipError_t launch_quarter(const FwdArgs& a, hipStream_t stream) {
   if (!quarter_config_fits(a)) return hipErrorInvalidValue;
-  return dispatch<QuarterLaunch::L>(a, stream, 32);
+  const int64_t blocks32 = (a.seq + 31) / 32 * (int64_t)a.batch_heads;
+  if (blocks32 > kQuarterOneBlockGroups) return dispatch<QuarterLaunch<2>::L>(a, stream, 64);
+  return dispatch<QuarterLaunch<1>::L>(a, stream, 32);
 }
 
 }  // namespace fl

@@ -67,6 +67,9 @@ constexpr int kStreamMaxKeys = 256;
 constexpr int kStreamMaxRowStride = 1 << 22;
 bool stream_config_fits(const FwdArgs& a);
 constexpr int kQuarterMaxKeys = 512;
+// Up to this many 32-row blocks the key-quarter groups hold one block each;
+// beyond it two (8 waves).
+constexpr int64_t kQuarterOneBlockGroups = 256;
 inline bool quarter_config_fits(const FwdArgs& a) { return a.seq_k <= kQuarterMaxKeys; }
 
 // Per-schedule launchers behind launch_fa2 (one source file each).

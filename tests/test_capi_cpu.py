@@ -214,14 +214,16 @@ def test_dispatcher_choices():
     assert sel(batch=3, heads=8, seq_q=2048, causal=True) == W4   # 384 groups
     assert sel(batch=32, heads=32, seq_q=256, causal=True) == STRM   # streaming, any count
     assert sel(batch=1, heads=1, seq_q=128, causal=True) == STRM
-    # 256 < N_k <= 512 with at most one 32-row group per CU: key quarters
+    # 256 < N_k <= 512 with at most 512 blocks of 32 rows: key quarters
     assert sel(batch=2, heads=8, seq_q=512) == QTR      # C1: 256 groups of 32 rows
     assert sel(batch=2, heads=8, seq_q=512, causal=True) == QTR
     assert sel(batch=1, heads=1, seq_q=257, causal=True) == QTR
     assert sel(batch=1, heads=1, seq_q=257) == QTR
     assert sel(batch=1, heads=1, seq_q=100, seq_k=512) == QTR
     # more groups, or longer key ranges: 128-row or smaller groups
-    assert sel(batch=4, heads=8, seq_q=512) == W4       # 512 groups of 32 rows
+    assert sel(batch=4, heads=8, seq_q=512) == QTR      # 512 blocks: 8-wave groups of 64 rows
+    assert sel(batch=4, heads=8, seq_q=320, causal=True) == QTR
+    assert sel(batch=8, heads=8, seq_q=512) == W4       # 1024 blocks of 32 rows
     assert sel(batch=2, heads=4, seq_q=576) == W2       # 72 groups of 64 rows
     assert sel(batch=1, heads=1, seq_q=600) == W1
     assert capi.select_config(_p(head_dim=80)) == -1

@@ -88,6 +88,27 @@ def test_c4_many_small_heads(cuda):
     assert_close_oracle(out, q, k, v, w.sm_scale, True)
 
 
+# More than 256 blocks of 32 query rows: the key-quarter kernel runs 8-wave
+# groups of two row blocks (a ragged last group, N_q != N_k both ways).
+QUARTER_RB2 = [(4, 8, 512, 512), (5, 7, 300, 300), (4, 20, 130, 400), (3, 11, 400, 130)]
+
+
+@pytest.mark.parametrize("b,h,nq,nk", QUARTER_RB2)
+@pytest.mark.parametrize("causal", [False, True])
+def test_quarter_two_row_blocks(cuda, b, h, nq, nk, causal):
+    assert b * h * ((nq + 31) // 32) > 256
+    rs = np.random.RandomState(b * 1000 + h * 10 + nq + nk)
+    mk = lambda n: rs.standard_normal((b, h, n, 64)).astype(np.float32).astype(np.float16)  # noqa: E731
+    q, k, v = mk(nq), mk(nk), mk(nk)
+    cfg = capi.config_id("br32_kv512_w4_quarters")
+    print(f"quarter RB2 B{b} H{h} Nq{nq} Nk{nk} causal={causal}", flush=True)
+    out = run_capi(q, k, v, 0.125, causal, cuda, config=cfg)
+    assert_close_oracle(out, q, k, v, 0.125, causal)
+    # peaked scores take the checked softmax in every quarter
+    out = run_capi(q, k, v, 3.0, causal, cuda, config=cfg)
+    assert_close_oracle(out, q, k, v, 3.0, causal, peaked=True)
+
+
 RAGGED = [1, 2, 3, 17, 31, 32, 33, 63, 64, 65, 100, 127, 128, 129, 191, 255, 256, 257, 300, 513]
 
 
