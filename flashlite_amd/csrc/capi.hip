@@ -271,24 +271,26 @@ KvPlan plan_kvsplit(const fl::FwdArgs& a, int32_t requested) {
 }
 
 // fp16 at head_dim 64 has every tile configuration; bf16 at head_dim 64
-// the two slot-scheduled ones and the two key-range splits; head_dim 128
-// the two slot-scheduled ones.
+// all but the two pipelined ones; head_dim 128 the two slot-scheduled ones.
 bool narrow_configs(const fl::FwdArgs& a) {
   return a.dtype != fl::kDtypeF16 || a.head_dim != 64;
 }
 
 bool config_built(const fl::FwdArgs& a, int cfg) {
   if (!narrow_configs(a) || cfg == fl::kSlotW8Config || cfg == fl::kSlotW4Config) return true;
-  return a.head_dim == 64 && (cfg == fl::kCfgSplit2 || cfg == fl::kCfgSplit2W2);
+  return a.head_dim == 64 && cfg != fl::kCfgW1 && cfg != fl::kCfgW2;
 }
 
-// bf16 at head_dim 64 follows the fp16 dispatcher where it picks a key-range
-// split; otherwise (and at head_dim 128) one of the slot-scheduled groups.
+// bf16 at head_dim 64 follows the fp16 dispatcher where it picks the
+// streaming kernel, the key quarters or a key-range split; otherwise (and at
+// head_dim 128) one of the slot-scheduled groups.
 int select_any(const fl::FwdArgs& a) {
   if (!narrow_configs(a)) return select_fa2(a);
   if (a.head_dim == 64) {
     const int c = select_fa2(a);
-    if (c == fl::kCfgSplit2 || c == fl::kCfgSplit2W2) return c;
+    if (c == fl::kCfgSplit2 || c == fl::kCfgSplit2W2 || c == fl::kStreamConfig ||
+        c == fl::kQuarterConfig)
+      return c;
   }
   constexpr int64_t kCus = 256;
   const int64_t wgs256 = (a.seq + 255) / 256 * (int64_t)a.batch_heads;
@@ -309,7 +311,7 @@ int fwd_ex(const fl_attn_params_ex* p, int32_t config, void* stream, int dtype, 
                 "%s: config %d is not built for %s at head_dim %d (use -1, %d or %d%s)", who,
                 (int)config, dtype == fl::kDtypeBF16 ? "bf16" : "fp16", a.head_dim,
                 fl::kSlotW8Config, fl::kSlotW4Config,
-                a.head_dim == 64 ? ", or a key-range split, 2 or 7" : "");
+                a.head_dim == 64 ? ", 2, 5, 6 or 7" : "");
   if (config == fl::kStreamConfig && !fl::stream_config_fits(a))
     return fail(FL_ERR_BAD_CONFIG, "%s: config %d needs N_k <= %d and row strides below 2^22 "
                 "(got N_k %d)", who, (int)config, fl::kStreamMaxKeys, a.seq_k);

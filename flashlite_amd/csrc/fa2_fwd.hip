@@ -35,6 +35,8 @@ hipError_t launch_fa2(const FwdArgs& a, int cfg, hipStream_t stream) {
     if (cfg == kSlotW4Config) return launch_slot(a, 4, stream);
     if (cfg == kCfgSplit2) return launch_slot_split(a, 4, stream);
     if (cfg == kCfgSplit2W2) return launch_slot_split(a, 2, stream);
+    if (cfg == kStreamConfig) return launch_stream(a, stream);
+    if (cfg == kQuarterConfig) return launch_quarter(a, stream);
     return hipErrorInvalidValue;
   }
   switch (cfg) {

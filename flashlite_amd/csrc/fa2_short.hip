@@ -44,12 +44,11 @@ namespace {
 // SIMD.
 constexpr int kQuarterWaves = 4;
 
-template <int NW, int RB, bool CAUSAL, bool SCALED>
+template <int NW, int RB, bool CAUSAL, bool SCALED, class T>
 __global__ void __launch_bounds__(64 * NW * RB, 1)
-fa2_fwd_quarter_kernel(const _Float16* Q, const _Float16* __restrict__ K,
-                       const _Float16* __restrict__ V, _Float16* O, const Geom geom, int nqb,
-                       float cq, float cr) {
-  using RowsT = Rows<CAUSAL, SCALED, _Float16>;
+fa2_fwd_quarter_kernel(const T* Q, const T* __restrict__ K, const T* __restrict__ V, T* O,
+                       const Geom geom, int nqb, float cq, float cr) {
+  using RowsT = Rows<CAUSAL, SCALED, T>;
   using V8 = typename RowsT::V8;
   constexpr int kQuarterTiles = kQuarterMaxKeys / kBc / NW;  // key tiles per wave
   constexpr int kQuarterWaveBytes = 2 * kQuarterTiles * kTileBytes;
@@ -66,7 +65,7 @@ fa2_fwd_quarter_kernel(const _Float16* Q, const _Float16* __restrict__ K,
   const int kq = RB == 1 ? w : w % NW;  // key quarter
   const int rb = RB == 1 ? 0 : w / NW;  // 32-row block within the group
   const int bh = blockIdx.x / nqb, qb = blockIdx.x - bh * nqb;
-  const HeadPtrs<_Float16> hp = head_ptrs(geom, bh, Q, K, V, O);
+  const HeadPtrs<T> hp = head_ptrs<T>(geom, bh, Q, K, V, O);
   const int seq = geom.seq_q;
   const int q0 = 32 * RB * qb;  // the group's first row
   int ntiles = (geom.seq_k + kBc - 1) / kBc;
@@ -171,31 +170,38 @@ fa2_fwd_quarter_kernel(const _Float16* Q, const _Float16* __restrict__ K,
   FL_ST_FLUSH(w, lane, 5);
 }
 
-template <int RB>
+template <int RB, class T>
 struct QuarterLaunch {
   template <bool C, bool S>
   struct L {
     static hipError_t run(const FwdArgs& a, const Geom& g, dim3 grid, int nqb, float cq, float cr,
                           hipStream_t st) {
-      hipLaunchKernelGGL((fa2_fwd_quarter_kernel<kQuarterWaves, RB, C, S>), grid,
-                         dim3(64 * kQuarterWaves * RB), 0, st,
-                         static_cast<const _Float16*>(a.q), static_cast<const _Float16*>(a.k),
-                         static_cast<const _Float16*>(a.v), static_cast<_Float16*>(a.o), g, nqb,
-                         cq, cr);
+      hipLaunchKernelGGL((fa2_fwd_quarter_kernel<kQuarterWaves, RB, C, S, T>), grid,
+                         dim3(64 * kQuarterWaves * RB), 0, st, static_cast<const T*>(a.q),
+                         static_cast<const T*>(a.k), static_cast<const T*>(a.v),
+                         static_cast<T*>(a.o), g, nqb, cq, cr);
       return hipSuccess;
     }
   };
 };
 
+template <class T>
+hipError_t launch_quarter_t(const FwdArgs& a, hipStream_t stream) {
+  const int64_t blocks32 = (a.seq + 31) / 32 * (int64_t)a.batch_heads;
+  if (blocks32 > kQuarterOneBlockGroups)
+    return dispatch<QuarterLaunch<2, T>::template L>(a, stream, 64);
+  return dispatch<QuarterLaunch<1, T>::template L>(a, stream, 32);
+}
+
 }  // namespace
 
-// One 4-wave work-group per 32-row query block (grid B*H*ceil(N_q/32)) up
-// to 256 of them; beyond that one 8-wave work-group per 64 rows.
+// fp16 or bf16 by a.dtype: one 4-wave work-group per 32-row query block
+// (grid B*H*ceil(N_q/32)) up to 256 of them; beyond that one 8-wave
+// work-group per 64 rows.
 hipError_t launch_quarter(const FwdArgs& a, hipStream_t stream) {
   if (!quarter_config_fits(a)) return hipErrorInvalidValue;
-  const int64_t blocks32 = (a.seq + 31) / 32 * (int64_t)a.batch_heads;
-  if (blocks32 > kQuarterOneBlockGroups) return dispatch<QuarterLaunch<2>::L>(a, stream, 64);
-  return dispatch<QuarterLaunch<1>::L>(a, stream, 32);
+  return a.dtype == kDtypeBF16 ? launch_quarter_t<__bf16>(a, stream)
+                               : launch_quarter_t<_Float16>(a, stream);
 }
 
 }  // namespace fl

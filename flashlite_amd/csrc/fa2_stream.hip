@@ -344,8 +344,11 @@ hipError_t launch_stream_t(const FwdArgs& a, hipStream_t st) {
 
 }  // namespace
 
+// fp16 or bf16 by a.dtype.
 hipError_t launch_stream(const FwdArgs& a, hipStream_t stream) {
-  return stream_config_fits(a) ? launch_stream_t<_Float16>(a, stream) : hipErrorInvalidValue;
+  if (!stream_config_fits(a)) return hipErrorInvalidValue;
+  return a.dtype == kDtypeBF16 ? launch_stream_t<__bf16>(a, stream)
+                               : launch_stream_t<_Float16>(a, stream);
 }
 
 }  // namespace fl

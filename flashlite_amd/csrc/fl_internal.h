@@ -59,9 +59,9 @@ constexpr int kNumFa2Configs = 8;
 extern const Fa2Config kFa2Configs[kNumFa2Configs];
 
 // Launches the FA2 kernel for configuration `cfg` on `stream`.  fp16 at
-// head_dim 64 has every configuration; bf16 at head_dim 64 the
-// slot-scheduled ones (kSlotW8Config, kSlotW4Config) and the key-range
-// splits (kCfgSplit2, kCfgSplit2W2); head_dim 128 the slot-scheduled ones.
+// head_dim 64 has every configuration; bf16 at head_dim 64 all but the
+// pipelined ones (kCfgW1, kCfgW2); head_dim 128 the slot-scheduled ones
+// (kSlotW8Config, kSlotW4Config).
 hipError_t launch_fa2(const FwdArgs& a, int cfg, hipStream_t stream);
 constexpr int kStreamMaxKeys = 256;
 constexpr int kStreamMaxRowStride = 1 << 22;

@@ -24,8 +24,8 @@ import numpy as np
 import pytest
 
 from flashlite_amd import capi
-from gpu_util import (MAX_ABS, MEAN_ABS, SLOT_W4_CFG, SLOT_W8_CFG, SPLIT2_CFG, SPLIT2W2_CFG,
-                      half_ulp, sample_rows)
+from gpu_util import (MAX_ABS, MEAN_ABS, QUARTER_CFG, SLOT_W4_CFG, SLOT_W8_CFG, SPLIT2_CFG,
+                      SPLIT2W2_CFG, STREAM_CFG, half_ulp, sample_rows)
 from oracle import attention_fp32, attention_lse, error_stats
 
 pytestmark = pytest.mark.gpu
@@ -197,6 +197,40 @@ def test_bf16_key_range_splits(cuda, config, causal):
     out, _ = _run("bf16", q, k, v, 0.125, causal, cuda, config=config)
     _check("bf16", out, attention_fp32(q, k, v, 0.125, causal), "B1 H4 N1024")
     q, k, v = _inputs("bf16", 1, 2, 700, 700, 64, seed=43, qk_scale=3.0)
+    out, _ = _run("bf16", q, k, v, 1.0, causal, cuda, config=config)
+    ref = attention_fp32(q, k, v, 1.0, causal)
+    mx_tol, mean_tol = _tol("bf16")
+    assert np.isfinite(out).all()
+    assert error_stats(out, ref)[1] <= mean_tol
+    assert (np.abs(out.astype(np.float64) - ref) <= mx_tol + half_ulp(ref, 7)).all()
+
+
+@pytest.mark.parametrize("config", [STREAM_CFG, QUARTER_CFG])
+@pytest.mark.parametrize("causal", [False, True])
+def test_bf16_short_key_kernels(cuda, config, causal):
+    """bf16 at D = 64 on the streaming (N_k <= 256) and key-quarter (N_k <=
+    512) kernels: ragged lengths, N_k != N_q with the log-sum-exp, many heads
+    (several units per streaming group; two-block key-quarter groups) and a
+    peaked scale."""
+    limit = 256 if config == STREAM_CFG else 512
+    for n in [x for x in RAGGED if x <= limit]:
+        q, k, v = _inputs("bf16", 2, 3, n, n, 64, seed=4000 + n)
+        out, _ = _run("bf16", q, k, v, 0.0, causal, cuda, config=config)
+        _check("bf16", out, attention_fp32(q, k, v, 0.0, causal), f"N={n}")
+    for nq, nk in [(37, 100), (100, 37), (300, limit), (limit, 130)]:
+        q, k, v = _inputs("bf16", 1, 2, nq, nk, 64, seed=nq * 7 + nk)
+        out, lse = _run("bf16", q, k, v, 0.125, causal, cuda, config=config, lse=True)
+        _check("bf16", out, attention_fp32(q, k, v, 0.125, causal), f"{nq}x{nk}")
+        ref_lse = attention_lse(q, k, 0.125, causal)
+        fin = np.isfinite(ref_lse)
+        assert np.array_equal(fin, np.isfinite(lse)), f"{nq}x{nk}: lse -inf pattern"
+        mx, mean = error_stats(lse[fin], ref_lse[fin]) if fin.any() else (0.0, 0.0)
+        assert mx <= LSE_MAX_ABS and mean <= LSE_MEAN_ABS["bf16"], f"{nq}x{nk}: lse {mx:.3e}"
+    b, h, n = (32, 32, 256) if config == STREAM_CFG else (4, 8, 512)
+    q, k, v = _inputs("bf16", b, h, n, n, 64, seed=7)
+    out, _ = _run("bf16", q, k, v, 0.125, causal, cuda, config=config)
+    _check("bf16", out, attention_fp32(q, k, v, 0.125, causal), f"B{b} H{h} N{n}")
+    q, k, v = _inputs("bf16", 1, 2, 200, 200, 64, seed=43, qk_scale=3.0)
     out, _ = _run("bf16", q, k, v, 1.0, causal, cuda, config=config)
     ref = attention_fp32(q, k, v, 1.0, causal)
     mx_tol, mean_tol = _tol("bf16")

@@ -61,7 +61,8 @@ def test_wide_config_checks():
             slots = (capi.config_id("br256_bc64_w8_slot"), capi.config_id("br128_bc64_w4_slot"))
             stream_cfg = capi.config_id("br256_kv256_w8_stream")
             quarter_cfg = capi.config_id("br32_kv512_w4_quarters")
-            # bf16 at D = 64 also has both key-range splits
+            # bf16 at D = 64 also has both key-range splits (and the streaming and
+            # key-quarter kernels, checked below)
             splits = (capi.config_id("br128_bc64_w4x2_slot"), capi.config_id("br64_bc64_w2x2_slot"))
             for cfg in range(capi.num_configs()):
                 if cfg in slots or cfg in (stream_cfg, quarter_cfg):
@@ -71,8 +72,11 @@ def test_wide_config_checks():
                     continue
                 assert fn(_ex(head_dim=d), config=cfg) == capi.FL_ERR_BAD_CONFIG
                 assert "not built" in capi.last_error() and who in capi.last_error()
+            # N_k 4096: past both short-key kernels' limits (not built at D = 128)
             assert fn(_ex(head_dim=d), config=stream_cfg) == capi.FL_ERR_BAD_CONFIG
             assert fn(_ex(head_dim=d), config=quarter_cfg) == capi.FL_ERR_BAD_CONFIG
+            if d == 64:
+                assert "needs N_k" in capi.last_error()
         for d in (32, 96, 256):
             assert fn(_ex(head_dim=d)) == capi.FL_ERR_UNSUPPORTED
             assert "head_dim must be 64 or 128" in capi.last_error()
