@@ -148,8 +148,9 @@ fa2_fwd_quarter_kernel(const T* Q, const T* __restrict__ K, const T* __restrict_
   // Merge through each quarter's (now idle) LDS: quarters 1..NW-1 store
   // their partials at once and, after one barrier, quarter 0 merges them in
   // order (measured 5% faster on C1 than a two-step tree, which took a
-  // second barrier).  Row block rb's partials sit 9 KiB in.  A range with
-  // no visible key holds l = 0 and is skipped by the merge.
+  // second barrier).  Row block rb's partials start rb x 9 KiB into the
+  // quarter's buffer.  A range with no visible key holds l = 0 and is
+  // skipped by the merge.
   float4* const part = reinterpret_cast<float4*>(buf[kq]) + rb * (9 * 64);
   asm volatile("s_waitcnt lgkmcnt(0)" : : : "memory");  // own LDS reads done
   if constexpr (RB > 1) __syncthreads();  // and the other row block's
