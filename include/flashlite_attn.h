@@ -75,8 +75,9 @@ int fl_attn_fwd_f16(const fl_attn_params* p, void* stream);
  * the reference's two hard-wired launch branches (Br=64 / Br=128,
  * csrc/kernel_flash2.cu:789-835); used by sweeps and by tests that check
  * every configuration against the oracle.  Configuration 5
- * (br256_kv256_w8_stream) takes N_k <= 256 only and returns
- * FL_ERR_BAD_CONFIG otherwise.
+ * (br256_kv256_w8_stream) takes N_k <= 256 only and configuration 6
+ * (br32_kv512_w4_quarters) N_k <= 512 only; they return FL_ERR_BAD_CONFIG
+ * otherwise.
  */
 int fl_attn_fwd_f16_cfg(const fl_attn_params* p, int32_t config, void* stream);
 
@@ -122,9 +123,10 @@ int fl_attn_fwd_f16_ex(const fl_attn_params_ex* p, int32_t config, void* stream)
 
 /*
  * bf16 q, k, v and o (same layouts, strides, lse and head_dims as
- * fl_attn_fwd_f16_ex; `config` -1, 3 or 4).  Q enters the MFMA unscaled and
- * the fp32 scores are scaled by sm_scale*log2(e); P is rounded to bf16
- * before the PV product and the row sums are fp32.
+ * fl_attn_fwd_f16_ex; `config` -1 or, at head_dim 64, any configuration but
+ * the pipelined 0 and 1, at head_dim 128 3 or 4).  Q enters the MFMA
+ * unscaled and the fp32 scores are scaled by sm_scale*log2(e); P is rounded
+ * to bf16 before the PV product and the row sums are fp32.
  *
  * No counterpart in the reference, which accepts fp16 only
  * (csrc/kernel_flash2.cu:745-747).
