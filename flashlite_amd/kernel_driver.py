@@ -17,7 +17,8 @@ scales the HBM byte counters (FETCH_SIZE / WRITE_SIZE) of a profile.
 ``--dtype bf16`` and/or ``--head-dim 128`` run the workload's shape at that
 element type / head dim through ``fl_attn_fwd_bf16_ex`` or
 ``fl_attn_fwd_f16_ex`` (seeded inputs from ``make_qkv`` / ``make_qkv_bf16``;
-``--config`` -1, 3 or 4).
+``--config`` -1 or what the entry point accepts: at head_dim 128 3 or 4, bf16 at
+head_dim 64 any configuration but 0 and 1).
 
 ``--cold-mib M`` (workloads and ``--decode``) reads and writes an M MiB
 buffer before every launch, evicting the inputs from the L2 caches and the
