@@ -235,8 +235,14 @@ int check_ex(const fl_attn_params_ex* p, fl::FwdArgs* a, const char* who, bool w
 // range is long (>= 32 tiles).  Otherwise one pass.  Single-wave plans then
 // stay within 512 x 32 rows of partials (4.5 MB), inside the static scratch
 // of the allocation-free entry point.
+//
+// Single-wave groups whose chunks fit the key-quarter kernel (at most 8
+// tiles) in one round of its 4-wave work-groups (at most 256) run there
+// (`quarter`): the library's choice cuts such ranges into chunks of 8 tiles
+// when that fits, and a requested chunk count takes it when it does.
 struct KvPlan {
   int waves, nsplit;
+  bool quarter;
   int64_t bytes;
 };
 constexpr int kMaxSplits = 256;
@@ -246,6 +252,7 @@ KvPlan plan_kvsplit(const fl::FwdArgs& a, int32_t requested) {
   constexpr int64_t kCus = 256;
   KvPlan p;
   p.waves = a.seq <= 32 ? 1 : (a.seq <= 64 ? 2 : 4);
+  p.quarter = false;
   const int64_t nqb = (a.seq + 32 * p.waves - 1) / (32 * p.waves);
   const int64_t tiles = std::max<int64_t>(1, (a.seq_k + 63) / 64);
   const int64_t groups = nqb * a.batch_heads;
@@ -260,6 +267,15 @@ KvPlan plan_kvsplit(const fl::FwdArgs& a, int32_t requested) {
   } else {
     n = (a.seq <= 32 && tiles >= 32) ? std::min<int64_t>(8, tiles / 8) : 0;
   }
+  if (p.waves == 1 && requested <= 0 && groups < kCus) {
+    const int64_t nq = (tiles + 7) / 8;  // chunks of at most 8 tiles
+    if (nq >= 2 && groups * nq <= kCus) {
+      n = nq;
+      p.quarter = true;
+    }
+  } else if (p.waves == 1 && requested > 0) {
+    p.quarter = (tiles + n - 1) / n <= 8 && groups * n <= kCus;
+  }
   if (requested <= 0 && n < 2) n = 0;
   // the chunk kernel's grid (64 * waves lanes per group) must stay below 2^32 lanes
   const int64_t grid_cap = ((int64_t)UINT32_MAX / (64 * p.waves)) / (nqb * a.batch_heads);
@@ -268,6 +284,13 @@ KvPlan plan_kvsplit(const fl::FwdArgs& a, int32_t requested) {
   p.nsplit = (int)n;
   p.bytes = n * (int64_t)a.batch_heads * a.seq * kPartFloats * (int64_t)sizeof(float);
   return p;
+}
+
+// The chunk kernel the plan names (key quarters or the pipelined kernel),
+// then the combine kernel.
+hipError_t run_kvsplit(const fl::FwdArgs& a, const KvPlan& plan, float* part, hipStream_t st) {
+  return plan.quarter ? fl::launch_kvsplit_quarter(a, part, plan.nsplit, st)
+                      : fl::launch_kvsplit(a, plan.waves, part, plan.nsplit, st);
 }
 
 // fp16 at head_dim 64 has every tile configuration; bf16 at head_dim 64
@@ -445,8 +468,7 @@ int fl_attn_fwd_f16_splitkv(const fl_attn_params_ex* p, int32_t num_splits, void
                   workspace == nullptr ? ", NULL" : "");
     if ((uintptr_t)workspace & 15)
       return fail(FL_ERR_MISALIGNED, "%s: workspace must be 16-byte aligned", who);
-    e = fl::launch_kvsplit(a, plan.waves, static_cast<float*>(workspace), plan.nsplit,
-                           static_cast<hipStream_t>(stream));
+    e = run_kvsplit(a, plan, static_cast<float*>(workspace), static_cast<hipStream_t>(stream));
   }
   if (e != hipSuccess) return fail(FL_ERR_LAUNCH, "%s: launch failed: %s", who, hipGetErrorString(e));
   return FL_OK;
@@ -472,8 +494,7 @@ int fl_attn_fwd_f16_splitkv_noalloc(const fl_attn_params_ex* p, int32_t num_spli
     void* s = nullptr;
     rc = scratch_for_current_device(&s, who);
     if (rc != FL_OK) return rc;
-    e = fl::launch_kvsplit(a, plan.waves, static_cast<float*>(s), plan.nsplit,
-                           static_cast<hipStream_t>(stream));
+    e = run_kvsplit(a, plan, static_cast<float*>(s), static_cast<hipStream_t>(stream));
   }
   if (e != hipSuccess) return fail(FL_ERR_LAUNCH, "%s: launch failed: %s", who, hipGetErrorString(e));
   return FL_OK;

@@ -83,7 +83,9 @@ bool diag_stream_fits(const FwdArgs& a) { return a.seq_k <= kStreamMaxKeys; }
 #undef launch_stream
 #undef stream_config_fits
 #define launch_quarter diag_timeline_launch_quarter
+#define FL_QUARTER_NO_SPLITKV
 #include "fa2_short.hip"
+#undef FL_QUARTER_NO_SPLITKV
 #undef launch_quarter
 
 extern "C" {

@@ -314,15 +314,24 @@ hipError_t launch_kvsplit_w(const FwdArgs& a, float* part, int nsplit, hipStream
     else
       hipLaunchKernelGGL((fa2_fwd_kernel<W, D, false, false, true>), grid, block, 0, st, q, k, v, o, g, nqb, sc.cq, sc.cr);
   }
-  hipError_t e = hipGetLastError();
+  const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  const int rows = a.batch_heads * a.seq;
-  hipLaunchKernelGGL(splitkv_combine_kernel, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, st, o,
-                     g);
-  return hipGetLastError();
+  return launch_splitkv_combine(a, part, nsplit, st);
 }
 
 }  // namespace
+
+// The combine kernel over `nsplit` chunk partials in `part`: one wave per
+// query row, 4 rows per work-group.
+hipError_t launch_splitkv_combine(const FwdArgs& a, float* part, int nsplit, hipStream_t st) {
+  Geom g = make_geom(a);
+  g.part = part;
+  g.nsplit = nsplit;
+  const int rows = a.batch_heads * a.seq;
+  hipLaunchKernelGGL(splitkv_combine_kernel, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, st,
+                     static_cast<_Float16*>(a.o), g);
+  return hipGetLastError();
+}
 
 hipError_t launch_pipe(const FwdArgs& a, int cfg, hipStream_t stream) {
   switch (cfg) {

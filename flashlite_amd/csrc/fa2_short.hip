@@ -42,9 +42,16 @@ namespace {
 // overwrites it; partials written before wave 0 of each row block folds
 // them in).  Up to 512 blocks then still run in one round, two waves per
 // SIMD.
+//
+// KVSPLIT (split-KV chunks of at most 8 tiles, RB = 1): work-group i takes
+// key chunk i % nsplit of its query block, the waves a quarter of the
+// chunk each, and wave 0 writes the merged partial (O unnormalised, m, l)
+// that splitkv_combine_kernel folds together, as the one-wave chunks of
+// the pipelined kernel do.  A decode step's chunk is then a 2-tile chain
+// per wave instead of an up-to-8-tile one.
 constexpr int kQuarterWaves = 4;
 
-template <int NW, int RB, bool CAUSAL, bool SCALED, class T>
+template <int NW, int RB, bool CAUSAL, bool SCALED, class T, bool KVSPLIT = false>
 __global__ void __launch_bounds__(64 * NW * RB, 1)
 fa2_fwd_quarter_kernel(const T* Q, const T* __restrict__ K, const T* __restrict__ V, T* O,
                        const Geom geom, int nqb, float cq, float cr) {
@@ -54,6 +61,7 @@ fa2_fwd_quarter_kernel(const T* Q, const T* __restrict__ K, const T* __restrict_
   constexpr int kQuarterWaveBytes = 2 * kQuarterTiles * kTileBytes;
   static_assert(NW * kQuarterTiles * kBc == kQuarterMaxKeys, "key range");
   static_assert(RB == 1 || RB == 2, "row blocks per group");
+  static_assert(!KVSPLIT || RB == 1, "split-KV chunks hold one row block");
   static_assert(RB * (9 * 64) * 16 <= kQuarterWaveBytes, "partials fit a quarter's LDS");
   constexpr int kSegs = 8 / RB;  // 1 KiB segments of a tile each wave of a quarter fetches
   __shared__ __attribute__((aligned(16))) uint8_t buf[NW][kQuarterWaveBytes];
@@ -64,14 +72,32 @@ fa2_fwd_quarter_kernel(const T* Q, const T* __restrict__ K, const T* __restrict_
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int kq = RB == 1 ? w : w % NW;  // key quarter
   const int rb = RB == 1 ? 0 : w / NW;  // 32-row block within the group
-  const int bh = blockIdx.x / nqb, qb = blockIdx.x - bh * nqb;
+  int bh, qb, chunk = 0;
+  if constexpr (KVSPLIT) {
+    const int r = blockIdx.x / geom.nsplit;
+    chunk = blockIdx.x - r * geom.nsplit;
+    bh = r / nqb;
+    qb = r - bh * nqb;
+  } else {
+    bh = blockIdx.x / nqb;
+    qb = blockIdx.x - bh * nqb;
+  }
   const HeadPtrs<T> hp = head_ptrs<T>(geom, bh, Q, K, V, O);
   const int seq = geom.seq_q;
   const int q0 = 32 * RB * qb;  // the group's first row
-  int ntiles = (geom.seq_k + kBc - 1) / kBc;
+  const int all_tiles = (geom.seq_k + kBc - 1) / kBc;
+  int ntiles = all_tiles;
   if (CAUSAL) ntiles = min(ntiles, causal_tiles(min(q0 + 32 * RB, seq), geom.coff));
-  const int t0 = kQuarterTiles * kq;
-  const int t1 = min(t0 + kQuarterTiles, ntiles);
+  // The group's key tiles [cbeg, cend): all of them, or its split-KV chunk
+  // (the same cut as the pipelined kernel's chunks).
+  int cbeg = 0, cend = ntiles;
+  if constexpr (KVSPLIT) {
+    const int per = (max(all_tiles, 1) + geom.nsplit - 1) / geom.nsplit;
+    cbeg = chunk * per;
+    cend = min(ntiles, cbeg + per);
+  }
+  const int t0 = cbeg + kQuarterTiles * kq;
+  const int t1 = min(t0 + kQuarterTiles, cend);
   uint8_t* const kb = buf[kq];
   uint8_t* const vb = buf[kq] + kQuarterTiles * kTileBytes;
 
@@ -167,7 +193,10 @@ fa2_fwd_quarter_kernel(const T* Q, const T* __restrict__ K, const T* __restrict_
     return;
   }
   rows.launder();
-  rows.store(hp.o, geom.o_sr, hp.lse);
+  if constexpr (KVSPLIT)
+    rows.store_partial(geom.part + (long long)(chunk * geom.batch_heads + bh) * seq * kPartStride);
+  else
+    rows.store(hp.o, geom.o_sr, hp.lse);
   FL_ST_FLUSH(w, lane, 5);
 }
 
@@ -204,5 +233,46 @@ hipError_t launch_quarter(const FwdArgs& a, hipStream_t stream) {
   return a.dtype == kDtypeBF16 ? launch_quarter_t<__bf16>(a, stream)
                                : launch_quarter_t<_Float16>(a, stream);
 }
+
+#ifndef FL_QUARTER_NO_SPLITKV
+// Split-KV with key-quarter chunks (fp16): grid B*H*ceil(N_q/32)*nsplit
+// 4-wave work-groups, every chunk at most kQuarterMaxKeys keys, then the
+// combine kernel on the same stream.
+hipError_t launch_kvsplit_quarter(const FwdArgs& a, float* part, int nsplit, hipStream_t st) {
+  const int all_tiles = a.seq_k > 0 ? (a.seq_k + kBc - 1) / kBc : 1;
+  if (a.dtype != kDtypeF16 || nsplit < 1 ||
+      (all_tiles + nsplit - 1) / nsplit * kBc > kQuarterMaxKeys)
+    return hipErrorInvalidValue;
+  const int nqb = (a.seq + 31) / 32;
+  const Scales sc(a);
+  Geom g = make_geom(a);
+  g.part = part;
+  g.nsplit = nsplit;
+  const dim3 grid((unsigned)(nqb * a.batch_heads * nsplit));
+  const dim3 block(64 * kQuarterWaves);
+  const _Float16 *q = static_cast<const _Float16*>(a.q), *k = static_cast<const _Float16*>(a.k),
+                 *v = static_cast<const _Float16*>(a.v);
+  _Float16* o = static_cast<_Float16*>(a.o);
+  constexpr int NW = kQuarterWaves;
+  if (a.causal) {
+    if (sc.scaled)
+      hipLaunchKernelGGL((fa2_fwd_quarter_kernel<NW, 1, true, true, _Float16, true>), grid, block,
+                         0, st, q, k, v, o, g, nqb, sc.cq, sc.cr);
+    else
+      hipLaunchKernelGGL((fa2_fwd_quarter_kernel<NW, 1, true, false, _Float16, true>), grid,
+                         block, 0, st, q, k, v, o, g, nqb, sc.cq, sc.cr);
+  } else {
+    if (sc.scaled)
+      hipLaunchKernelGGL((fa2_fwd_quarter_kernel<NW, 1, false, true, _Float16, true>), grid,
+                         block, 0, st, q, k, v, o, g, nqb, sc.cq, sc.cr);
+    else
+      hipLaunchKernelGGL((fa2_fwd_quarter_kernel<NW, 1, false, false, _Float16, true>), grid,
+                         block, 0, st, q, k, v, o, g, nqb, sc.cq, sc.cr);
+  }
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  return launch_splitkv_combine(a, part, nsplit, st);
+}
+#endif
 
 }  // namespace fl

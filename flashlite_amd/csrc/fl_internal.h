@@ -86,6 +86,12 @@ hipError_t launch_d128(const FwdArgs& a, int waves, hipStream_t stream);   // fa
 // then merged by a second kernel on the same stream.
 hipError_t launch_kvsplit(const FwdArgs& a, int waves, float* part, int nsplit,
                           hipStream_t stream);
+// The same with single-wave query blocks (N_q <= 32) in key-quarter chunks
+// of at most kQuarterMaxKeys keys: 4 waves per chunk (fa2_short.hip).
+hipError_t launch_kvsplit_quarter(const FwdArgs& a, float* part, int nsplit, hipStream_t stream);
+// The combine kernel alone (fa2_pipe.hip): merges the nsplit partials in
+// `part` into O (and the log-sum-exp when a.lse is set).
+hipError_t launch_splitkv_combine(const FwdArgs& a, float* part, int nsplit, hipStream_t stream);
 
 // Largest seq the naive kernel can stage in LDS for this head_dim.
 int64_t naive_max_seq(int64_t head_dim);

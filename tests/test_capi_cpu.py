@@ -258,9 +258,10 @@ def test_splitkv_plan():
         return capi.splitkv_workspace_bytes(capi.make_params_ex(base, qs, ks, ks, qs), splits)
 
     # decode step B2 H8, one query over 4096 keys: 16 one-wave groups would
-    # leave most CUs idle; one-wave chunks cover the 256 CUs twice, of at
-    # least 4 tiles (multi-wave chunks: once)
-    assert bytes_for(1, 4096, 0) == 16 * 16 * 1 * 68 * 4
+    # leave most CUs idle; key-quarter chunks of 8 tiles when they fit one
+    # round (16 x 8 groups of 4 waves), else one-wave chunks covering the
+    # 256 CUs twice, of at least 4 tiles (multi-wave chunks: once)
+    assert bytes_for(1, 4096, 0) == 8 * 16 * 1 * 68 * 4
     assert bytes_for(1, 1 << 16, 0) == 32 * 16 * 1 * 68 * 4
     # fewer than 8 tiles: at most tiles / 4 chunks, and no split below 2
     assert bytes_for(1, 512, 0) == 2 * 16 * 1 * 68 * 4
@@ -275,7 +276,8 @@ def test_splitkv_plan():
     assert bytes_for(129, 1 << 16, 0) == 0
     assert bytes_for(128, 1 << 16, 0) == 16 * 16 * 128 * 68 * 4
     assert bytes_for(64, 8192, 0, batch=4) == 8 * 32 * 64 * 68 * 4
-    assert bytes_for(1, 4096, 0, batch=4) == 16 * 32 * 1 * 68 * 4
+    assert bytes_for(1, 4096, 0, batch=4) == 8 * 32 * 1 * 68 * 4      # 256 quarter groups
+    assert bytes_for(1, 4096, 0, batch=8) == 8 * 64 * 1 * 68 * 4      # one-wave chunks: 512 / 64
     # forced: as asked, clamped to the number of 64-key tiles
     assert bytes_for(4096, 4096, 5) == 5 * 16 * 4096 * 68 * 4
     assert bytes_for(3, 130, 100) == 3 * 16 * 3 * 68 * 4

@@ -96,7 +96,7 @@ def test_splitkv_auto_choice(cuda):
     q16, k16, v16 = _qkv(2, 8, 1, 4096, seed=1)
     tq, tk, tv = (to_dev(x, cuda) for x in (q16, k16, v16))
     _, _, need = _run_split(tq, tk, tv, 0.125, False, 0)
-    assert need == 16 * 16 * 68 * 4
+    assert need == 8 * 16 * 68 * 4  # 8 key-quarter chunks of 8 tiles
 
 
 def test_splitkv_strided_and_deterministic(cuda):
