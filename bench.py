@@ -167,7 +167,8 @@ def main():
     args = parse()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (got --gpus {args.gpus}); the "
-              "path shards over (batch, head) with no communication, see DESIGN.md.",
+              "path shards over (batch, head) with no communication, so one GPU's share "
+              "runs the same kernel at the same shape per GPU.",
               file=sys.stderr)
         sys.exit(2)
 
