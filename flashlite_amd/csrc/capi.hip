@@ -104,7 +104,8 @@ int check_pointers(const fl_attn_params* p, fl::FwdArgs* a, const char* who, uin
   return FL_OK;
 }
 
-// Tile-configuration choice for 256 CUs (measured on MI355X, every
+// Tile-configuration choice for the device's CUs (fl::device_cus(): 256 on
+// an MI355X seen whole, where the rules below were measured; every
 // configuration computes the same result).  Key ranges of at most 256 keys
 // go to the streaming persistent groups (measured at least as fast as every
 // other configuration from 16 to 2048 units, both masks), and of at most
@@ -130,21 +131,21 @@ int check_pointers(const fl_attn_params* p, fl::FwdArgs* a, const char* who, uin
 // reference's `seq_len >= 2048 -> Br=128` rule (kernel_flash2.cu:786-789),
 // which was sized for 20 SMs.
 int select_fa2(const fl::FwdArgs& a) {
-  constexpr int64_t kCus = 256;
+  const int64_t cus = fl::device_cus();
   auto wgs = [&](int64_t br) { return (a.seq + br - 1) / br * (int64_t)a.batch_heads; };
   if (fl::stream_config_fits(a)) return fl::kStreamConfig;  // br256_kv256_w8_stream
   // N_k <= 512 with few query blocks: quarter the key range (4-wave groups
   // of 32 rows, or 8-wave groups of 64 past 256 blocks; a single round).
-  if (fl::quarter_config_fits(a) && wgs(32) <= 2 * kCus) return fl::kQuarterConfig;
+  if (fl::quarter_config_fits(a) && wgs(32) <= 2 * cus) return fl::kQuarterConfig;
   // Past 576 keys, 64 to 256 groups of 64 rows: the key-range split on
   // 64-row groups (2 x 2 waves), one group per CU in a single round.
-  if (a.seq_k > 576 && wgs(64) <= kCus && wgs(64) >= kCus / 4) return fl::kCfgSplit2W2;
-  const bool one_round = a.seq_k >= 2048 && wgs(128) <= kCus;
-  if (one_round && (a.causal ? wgs(128) >= kCus / 4 : a.seq_k >= 4096 || wgs(128) < kCus / 2))
+  if (a.seq_k > 576 && wgs(64) <= cus && wgs(64) >= cus / 4) return fl::kCfgSplit2W2;
+  const bool one_round = a.seq_k >= 2048 && wgs(128) <= cus;
+  if (one_round && (a.causal ? wgs(128) >= cus / 4 : a.seq_k >= 4096 || wgs(128) < cus / 2))
     return fl::kCfgSplit2;
-  if (!a.causal && a.seq_k >= 2048 && wgs(256) > kCus / 2) return fl::kSlotW8Config;
-  if (wgs(128) >= kCus / 4) return fl::kSlotW4Config;
-  if (wgs(64) >= kCus / 4) return fl::kCfgW2;
+  if (!a.causal && a.seq_k >= 2048 && wgs(256) > cus / 2) return fl::kSlotW8Config;
+  if (wgs(128) >= cus / 4) return fl::kSlotW4Config;
+  if (wgs(64) >= cus / 4) return fl::kCfgW2;
   return fl::kCfgW1;
 }
 
@@ -227,7 +228,7 @@ int check_ex(const fl_attn_params_ex* p, fl::FwdArgs* a, const char* who, bool w
 // The library's choice (requested <= 0), from decode sweeps on MI355X
 // (B2 H8 and B1 H16 with N_q 1-16 over 4k-64k keys, B32 H32 over 4k): with
 // at most 128 query rows and fewer query-row groups than CUs, cut each key
-// range so that the groups times chunks cover the 256 CUs twice with
+// range so that the groups times chunks cover the CUs twice with
 // single-wave groups (N_q <= 32; 2-11% faster than once, measured) and once
 // with 2- and 4-wave groups (twice: +1% and +25%), keeping at least 4 key
 // tiles per chunk (shorter chunks measured slower: per-work-group start-up);
@@ -249,7 +250,7 @@ constexpr int kMaxSplits = 256;
 constexpr int64_t kPartFloats = 68;  // per row: O[64], m, l, 2 pad
 
 KvPlan plan_kvsplit(const fl::FwdArgs& a, int32_t requested) {
-  constexpr int64_t kCus = 256;
+  const int64_t cus = fl::device_cus();
   KvPlan p;
   p.waves = a.seq <= 32 ? 1 : (a.seq <= 64 ? 2 : 4);
   p.quarter = false;
@@ -261,20 +262,20 @@ KvPlan plan_kvsplit(const fl::FwdArgs& a, int32_t requested) {
     n = std::min<int64_t>({(int64_t)requested, tiles, kMaxSplits});
   } else if (a.seq > 128) {
     n = 0;  // long query ranges: the one-pass kernel's groups fill the GPU
-  } else if (groups < kCus) {
-    const int64_t cover = (p.waves == 1 ? 2 : 1) * kCus;
+  } else if (groups < cus) {
+    const int64_t cover = (p.waves == 1 ? 2 : 1) * cus;
     n = std::min<int64_t>({(cover + groups - 1) / groups, tiles / 4, kMaxSplits});
   } else {
     n = (a.seq <= 32 && tiles >= 32) ? std::min<int64_t>(8, tiles / 8) : 0;
   }
-  if (p.waves == 1 && requested <= 0 && groups < kCus) {
+  if (p.waves == 1 && requested <= 0 && groups < cus) {
     const int64_t nq = (tiles + 7) / 8;  // chunks of at most 8 tiles
-    if (nq >= 2 && groups * nq <= kCus) {
+    if (nq >= 2 && groups * nq <= cus) {
       n = nq;
       p.quarter = true;
     }
   } else if (p.waves == 1 && requested > 0) {
-    p.quarter = (tiles + n - 1) / n <= 8 && groups * n <= kCus;
+    p.quarter = (tiles + n - 1) / n <= 8 && groups * n <= cus;
   }
   if (requested <= 0 && n < 2) n = 0;
   // the chunk kernel's grid (64 * waves lanes per group) must stay below 2^32 lanes
@@ -315,9 +316,9 @@ int select_any(const fl::FwdArgs& a) {
         c == fl::kQuarterConfig)
       return c;
   }
-  constexpr int64_t kCus = 256;
+  const int64_t cus = fl::device_cus();
   const int64_t wgs256 = (a.seq + 255) / 256 * (int64_t)a.batch_heads;
-  return (!a.causal && a.seq_k >= 4096 && wgs256 >= kCus) ? fl::kSlotW8Config
+  return (!a.causal && a.seq_k >= 4096 && wgs256 >= cus) ? fl::kSlotW8Config
                                                            : fl::kSlotW4Config;
 }
 

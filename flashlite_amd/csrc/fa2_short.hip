@@ -218,7 +218,7 @@ struct QuarterLaunch {
 template <class T>
 hipError_t launch_quarter_t(const FwdArgs& a, hipStream_t stream) {
   const int64_t blocks32 = (a.seq + 31) / 32 * (int64_t)a.batch_heads;
-  if (blocks32 > kQuarterOneBlockGroups)
+  if (blocks32 > device_cus())
     return dispatch<QuarterLaunch<2, T>::template L>(a, stream, 64);
   return dispatch<QuarterLaunch<1, T>::template L>(a, stream, 32);
 }
@@ -226,7 +226,7 @@ hipError_t launch_quarter_t(const FwdArgs& a, hipStream_t stream) {
 }  // namespace
 
 // fp16 or bf16 by a.dtype: one 4-wave work-group per 32-row query block
-// (grid B*H*ceil(N_q/32)) up to 256 of them; beyond that one 8-wave
+// (grid B*H*ceil(N_q/32)) up to one per CU; beyond that one 8-wave
 // work-group per 64 rows.
 hipError_t launch_quarter(const FwdArgs& a, hipStream_t stream) {
   if (!quarter_config_fits(a)) return hipErrorInvalidValue;

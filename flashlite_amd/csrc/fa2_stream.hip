@@ -332,12 +332,12 @@ hipError_t launch_stream_v(const FwdArgs& a, hipStream_t st, dim3 grid, int nqb,
 
 template <class T>
 hipError_t launch_stream_t(const FwdArgs& a, hipStream_t st) {
-  constexpr int kCus = 256;
+  const int cus = device_cus();
   const int nqb = (a.seq + kStreamBr - 1) / kStreamBr;
   const int units = nqb * a.batch_heads;
-  const dim3 grid((unsigned)min(units, kCus));
+  const dim3 grid((unsigned)min(units, cus));
   // at least 4 units per work-group, every one over 4 key tiles
-  const bool spread = units >= 4 * kCus && a.seq_k > 3 * kBc;
+  const bool spread = units >= 4 * cus && a.seq_k > 3 * kBc;
   return spread ? launch_stream_v<T, true>(a, st, grid, nqb, units)
                 : launch_stream_v<T, false>(a, st, grid, nqb, units);
 }

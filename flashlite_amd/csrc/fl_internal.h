@@ -67,9 +67,26 @@ constexpr int kStreamMaxKeys = 256;
 constexpr int kStreamMaxRowStride = 1 << 22;
 bool stream_config_fits(const FwdArgs& a);
 constexpr int kQuarterMaxKeys = 512;
-// Up to this many 32-row blocks the key-quarter groups hold one block each;
-// beyond it two (8 waves).
-constexpr int64_t kQuarterOneBlockGroups = 256;
+// Compute units of the current device: 256 on an MI355X seen whole, fewer
+// when the GPU is partitioned into several devices.  The dispatch rules
+// that plan for one round of work-groups on the CUs use it.  Looked up once
+// per device (hipDeviceAttributeMultiprocessorCount); 256 when no device is
+// visible (host-only callers of the dispatcher, such as its CPU tests).
+constexpr int kMi355xCus = 256;
+inline int device_cus() {
+  constexpr int kMaxDevices = 64;
+  static int cached[kMaxDevices];  // 0: not looked up yet
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return kMi355xCus;
+  int c = __atomic_load_n(&cached[dev], __ATOMIC_RELAXED);
+  if (c <= 0) {
+    if (hipDeviceGetAttribute(&c, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        c <= 0)
+      c = kMi355xCus;
+    __atomic_store_n(&cached[dev], c, __ATOMIC_RELAXED);
+  }
+  return c;
+}
 inline bool quarter_config_fits(const FwdArgs& a) { return a.seq_k <= kQuarterMaxKeys; }
 
 // Per-schedule launchers behind launch_fa2 (one source file each).
