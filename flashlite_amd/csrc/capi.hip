@@ -112,12 +112,12 @@ int check_pointers(const fl_attn_params* p, fl::FwdArgs* a, const char* who, uin
 // 512 with at most 512 blocks of 32 rows to the key quarters (one block per
 // group up to 256 blocks, two beyond: 4-18% faster than the 128-row groups
 // from 320 to 512 blocks).  Past 576
-// keys, 64 to 256 groups of 64 rows take the key-range split on 64-row
+// keys, up to 256 groups of 64 rows take the key-range split on 64-row
 // groups (2 x 2 waves, one per SIMD, each pair walking half the keys): one
-// group on every CU where the 128-row groups leave CUs idle, 1-13% faster
-// than every other configuration (N_k 640-16384; at N_k 513 the 128-row
-// groups were 2.5% faster, and with more than 256 groups a second round
-// costs 27-70%).  Other long key ranges with at most one 128-row group per
+// group per CU where the 128-row groups leave CUs idle, 1-28% faster than
+// every other configuration from 16 to 256 groups (N_k 640-16384, fp16 and
+// bf16; at N_k 513 the 128-row groups were 2.5% faster, and with more than
+// 256 groups a second round costs 27-70%).  Other long key ranges with at most one 128-row group per
 // CU take the key-range-split group of 8 waves (two per SIMD): causal
 // from N_k 2048 (64 groups up; fewer fall back to smaller groups), 7-11%
 // faster than the 4-wave groups; non-causal from N_k 4096, or 2048 with
@@ -137,9 +137,9 @@ int select_fa2(const fl::FwdArgs& a) {
   // N_k <= 512 with few query blocks: quarter the key range (4-wave groups
   // of 32 rows, or 8-wave groups of 64 past 256 blocks; a single round).
   if (fl::quarter_config_fits(a) && wgs(32) <= 2 * cus) return fl::kQuarterConfig;
-  // Past 576 keys, 64 to 256 groups of 64 rows: the key-range split on
-  // 64-row groups (2 x 2 waves), one group per CU in a single round.
-  if (a.seq_k > 576 && wgs(64) <= cus && wgs(64) >= cus / 4) return fl::kCfgSplit2W2;
+  // Past 576 keys, at most one group of 64 rows per CU: the key-range split
+  // on 64-row groups (2 x 2 waves) in a single round.
+  if (a.seq_k > 576 && wgs(64) <= cus) return fl::kCfgSplit2W2;
   const bool one_round = a.seq_k >= 2048 && wgs(128) <= cus;
   if (one_round && (a.causal ? wgs(128) >= cus / 4 : a.seq_k >= 4096 || wgs(128) < cus / 2))
     return fl::kCfgSplit2;

@@ -190,11 +190,11 @@ def test_dispatcher_choices():
     assert sel(batch=2, heads=8, seq_q=2048) == W4         # 256 groups of 128 rows
     assert sel(batch=2, heads=8, seq_q=2048, causal=True) == SPLIT
     assert sel(batch=1, heads=8, seq_q=4096) == SPLIT
-    assert sel(batch=1, heads=1, seq_q=2048) == SPLIT      # 16 groups
+    assert sel(batch=1, heads=1, seq_q=2048) == SPLIT64    # 32 groups of 64 rows
     assert sel(batch=1, heads=8, seq_q=4096, causal=True) == SPLIT
-    assert sel(batch=1, heads=1, seq_q=1024, seq_k=4096) == SPLIT
-    assert sel(batch=1, heads=1, seq_q=2048, seq_k=8192) == SPLIT   # 16 groups of 128 rows
-    assert sel(batch=1, heads=1, seq_q=1000, seq_k=4096) == SPLIT
+    assert sel(batch=1, heads=1, seq_q=1024, seq_k=4096) == SPLIT64
+    assert sel(batch=1, heads=1, seq_q=2048, seq_k=8192) == SPLIT64
+    assert sel(batch=1, heads=1, seq_q=1000, seq_k=4096) == SPLIT64
     # past 512 keys with 128-256 groups of 64 rows: the split on 64-row groups
     assert sel(batch=2, heads=8, seq_q=1024) == SPLIT64    # 256 groups of 64 rows
     assert sel(batch=2, heads=8, seq_q=1024, causal=True) == SPLIT64
@@ -205,7 +205,7 @@ def test_dispatcher_choices():
     assert sel(batch=1, heads=1, seq_q=4096, causal=True) == SPLIT64
     assert sel(batch=2, heads=8, seq_q=640) == SPLIT64
     assert sel(batch=2, heads=8, seq_q=513) == W4          # N_k <= 576: 128-row groups
-    assert sel(batch=1, heads=1, seq_q=2048, causal=True) == W1    # 32 groups of 64 rows
+    assert sel(batch=1, heads=1, seq_q=2048, causal=True) == SPLIT64
     assert sel(batch=3, heads=8, seq_q=1024) == W4         # 384 groups of 64 rows
     assert sel(batch=4, heads=4, seq_q=1536, causal=True) == W4
     # causal: 128-row slot-scheduled groups balanced by dispatch order
@@ -225,7 +225,8 @@ def test_dispatcher_choices():
     assert sel(batch=4, heads=8, seq_q=320, causal=True) == QTR
     assert sel(batch=8, heads=8, seq_q=512) == W4       # 1024 blocks of 32 rows
     assert sel(batch=2, heads=4, seq_q=576) == W2       # 72 groups of 64 rows
-    assert sel(batch=1, heads=1, seq_q=600) == W1
+    assert sel(batch=1, heads=1, seq_q=600) == SPLIT64     # 10 groups of 64 rows
+    assert sel(batch=1, heads=1, seq_q=576) == W1          # N_k <= 576: small groups
     assert capi.select_config(_p(head_dim=80)) == -1
 
 
