@@ -130,6 +130,58 @@ def sustained_mfma():
     return flops / us / 1e6, ghz
 
 
+def gemm_ceiling(steps=50):
+    """The reference's ceiling (README.md:30-31): a dense fp16 4096^3 matrix
+    product on the same GPU (torch.matmul, hipBLASLt on ROCm), N(0,1) inputs,
+    timed back to back with HIP events after warm-up.  Returns TFLOP/s."""
+    import torch
+
+    g = torch.Generator(device="cuda:0").manual_seed(0)
+    n = 4096
+    a = torch.randn((n, n), device="cuda:0", generator=g).half()
+    b = torch.randn((n, n), device="cuda:0", generator=g).half()
+    c = torch.empty((n, n), device="cuda:0", dtype=torch.float16)
+    for _ in range(10):
+        torch.matmul(a, b, out=c)
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(steps):
+        torch.matmul(a, b, out=c)
+    end.record()
+    torch.cuda.synchronize()
+    us = start.elapsed_time(end) * 1e3 / steps
+    return 2.0 * n ** 3 / us / 1e6
+
+
+def physical_cores(cpus):
+    """Physical cores (distinct (package, core) pairs of /proc/cpuinfo) among
+    the logical CPUs `cpus`, and on the whole host; (None, None) if unknown."""
+    pairs, pkg, core, cpu = {}, None, None, None
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in list(f) + ["\n"]:
+                if not line.strip():
+                    if cpu is not None:
+                        pairs[cpu] = (pkg, core)
+                    pkg = core = cpu = None
+                    continue
+                key, _, val = line.partition(":")
+                key = key.strip()
+                if key == "processor":
+                    cpu = int(val)
+                elif key == "physical id":
+                    pkg = val.strip()
+                elif key == "core id":
+                    core = val.strip()
+    except OSError:
+        return None, None
+    if not pairs or any(v[1] is None for v in pairs.values()):
+        return None, None
+    used = {pairs[c] for c in cpus if c in pairs}
+    return len(used), len(set(pairs.values()))
+
+
 def cpu_baseline_leg(q16, k16, v16, gpu_out, sm_scale, seconds):
     """PyTorch-CPU SDPA in fp32 on the same inputs: full calls repeated for
     about `seconds` of CPU work per mask (median call time), and the parity
@@ -160,7 +212,7 @@ def cpu_baseline_leg(q16, k16, v16, gpu_out, sm_scale, seconds):
                     break
     except OSError:
         pass
-    return res, torch.get_num_threads(), os.cpu_count(), cpu_model
+    return res, torch.get_num_threads(), cpu_model
 
 
 def main():
@@ -209,10 +261,12 @@ def main():
     achieved = nc["flops"] / (nc["kern_ms"] * 1e-3) / 1e12
     io_bytes = 4 * w.batch * w.heads * w.seq * w.head_dim * 2
 
-    traffic = None
+    traffic = traffic_causal = None
     if os.path.exists(TRAFFIC_FILE):
         with open(TRAFFIC_FILE) as f:
-            traffic = json.load(f).get("noncausal_bytes_per_launch")
+            tj = json.load(f)
+        traffic = tj.get("noncausal_bytes_per_launch")
+        traffic_causal = tj.get("causal_bytes_per_launch")
 
     line = {
         "metric": METRIC,
@@ -249,7 +303,9 @@ def main():
             "frac": round(achieved / MFMA_PEAK_TFLOPS, 4),
             "peak_note": "published dense fp16 MFMA peak of MI355X (2.4 GHz)",
             "traffic": traffic,
+            "traffic_causal": traffic_causal,
             "kernel_avg_us": round(nc["kern_ms"] * 1e3, 3),
+            "causal_kernel_avg_us": round(ca["kern_ms"] * 1e3, 3),
             "algorithmic_flops_per_launch": nc["flops"],
             "algorithmic_bytes_per_launch": io_bytes,
         },
@@ -269,19 +325,37 @@ def main():
                    "timed region",
         }
 
+    # The reference's own framing: the kernel's share of a dense GEMM on the
+    # same device (its 96.2% is FlashLite's TFLOP/s over cuBLAS 4096^3).
+    gemm = gemm_ceiling()
+    ca_kernel = ca["flops"] / (ca["kern_ms"] * 1e-3) / 1e12
+    line["roofline"]["gemm_ceiling"] = {
+        "tflops": round(gemm, 1),
+        "frac": round(achieved / gemm, 4),
+        "causal_frac": round(ca_kernel / gemm, 4),
+        "how": "torch.matmul fp16 4096x4096x4096 (hipBLASLt), N(0,1) inputs, 50 back-to-back "
+               "calls timed with HIP events after the timed region",
+    }
+
     if not args.no_cpu:
-        res, threads, ncpu, model = cpu_baseline_leg(q16, k16, v16, gpu_out, w.sm_scale,
-                                                     args.cpu_seconds)
+        res, threads, model = cpu_baseline_leg(q16, k16, v16, gpu_out, w.sm_scale,
+                                               args.cpu_seconds)
+        cpus = sorted(os.sched_getaffinity(0))
+        phys_used, phys_host = physical_cores(cpus)
         t_nc, mx_nc, mean_nc, n_nc = res[False]
         t_c, mx_c, mean_c, n_c = res[True]
         line["cpu_baseline"] = {
             "value": round(nc["flops"] / t_nc / 1e12, 5),
             "unit": "TFLOP/s",
             "cores": threads,
+            "physical_cores": phys_used,
+            "logical_cpus": len(cpus),
             "kind": "port",
             "sample": (f"full {HEADLINE} calls, torch-CPU scaled_dot_product_attention fp32, "
                        f"median of {n_nc} non-causal ({n_c} causal) calls (~{args.cpu_seconds:.0f} s "
-                       f"of CPU work per mask) after 1 warm-up; host {model} ({ncpu} logical CPUs)"),
+                       f"of CPU work per mask) after 1 warm-up, {threads} threads on {len(cpus)} "
+                       f"logical CPUs = {phys_used} physical cores of this process's affinity "
+                       f"(host: {model}, {phys_host} physical cores)"),
             "latency_s": round(t_nc, 4),
             "causal_latency_s": round(t_c, 4),
         }

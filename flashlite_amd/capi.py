@@ -34,6 +34,8 @@ EXPORTED = (
     "fl_attn_splitkv_workspace_bytes",
     "fl_attn_fwd_f16_splitkv",
     "fl_attn_fwd_f16_splitkv_noalloc",
+    "fl_attn_splitkv_noalloc_bytes",
+    "fl_attn_config_id",
 )
 
 SCRATCH_BYTES = 8 << 20  # FL_ATTN_SCRATCH_BYTES
@@ -116,6 +118,10 @@ def load(path: str = LIB_PATH) -> ctypes.CDLL:
     lib.fl_attn_fwd_f16_splitkv_noalloc.argtypes = [ctypes.POINTER(FlAttnParamsEx), ctypes.c_int32,
                                                     ctypes.c_void_p]
     lib.fl_attn_fwd_f16_splitkv_noalloc.restype = ctypes.c_int
+    lib.fl_attn_splitkv_noalloc_bytes.argtypes = [ctypes.POINTER(FlAttnParamsEx), ctypes.c_int32]
+    lib.fl_attn_splitkv_noalloc_bytes.restype = ctypes.c_int64
+    lib.fl_attn_config_id.argtypes = [ctypes.c_char_p]
+    lib.fl_attn_config_id.restype = ctypes.c_int
     _lib = lib
     return lib
 
@@ -165,6 +171,12 @@ def fwd_splitkv(params: FlAttnParamsEx, workspace: int, workspace_bytes: int, st
                                           workspace_bytes, stream or None)
 
 
+def splitkv_noalloc_bytes(params: FlAttnParamsEx, num_splits: int = 0) -> int:
+    """``fl_attn_splitkv_noalloc_bytes``: scratch bytes the allocation-free
+    call uses (0 = one pass, -1 = rejected)."""
+    return load().fl_attn_splitkv_noalloc_bytes(ctypes.byref(params), num_splits)
+
+
 def fwd_splitkv_noalloc(params: FlAttnParamsEx, stream: int = 0, num_splits: int = 0) -> int:
     """``fl_attn_fwd_f16_splitkv_noalloc`` (partials in the library's scratch
     array); returns the status code."""
@@ -202,11 +214,12 @@ def config_name(cfg: int) -> str | None:
 
 
 def config_id(name: str) -> int:
-    """Index of the tile configuration called `name` (KeyError if none)."""
-    for i in range(num_configs()):
-        if config_name(i) == name:
-            return i
-    raise KeyError(name)
+    """``fl_attn_config_id``: index of the tile configuration called `name`
+    (KeyError if none)."""
+    i = load().fl_attn_config_id(name.encode())
+    if i < 0:
+        raise KeyError(name)
+    return i
 
 
 def select_config(params: FlAttnParams) -> int:

@@ -15,6 +15,7 @@
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
+#include <cstring>
 #include <cstdint>
 #include <mutex>
 
@@ -233,9 +234,11 @@ int check_ex(const fl_attn_params_ex* p, fl::FwdArgs* a, const char* who, bool w
 // with 2- and 4-wave groups (twice: +1% and +25%), keeping at least 4 key
 // tiles per chunk (shorter chunks measured slower: per-work-group start-up);
 // with more single-wave groups, chunks of 8 tiles up to 8 chunks when the
-// range is long (>= 32 tiles).  Otherwise one pass.  Single-wave plans then
-// stay within 512 x 32 rows of partials (4.5 MB), inside the static scratch
-// of the allocation-free entry point.
+// range is long (>= 32 tiles).  Otherwise one pass.  The partials grow with
+// B*H: with at least as many groups as CUs the 8-chunk rule alone needs
+// 8 x B*H x 32 rows (71 MB at B32 H32), so the allocation-free entry point
+// plans with plan_kvsplit_capped, which lowers the library's chunk count to
+// what its static scratch holds.
 //
 // Single-wave groups whose chunks fit the key-quarter kernel (at most 8
 // tiles) in one round of its 4-wave work-groups (at most 256) run there
@@ -284,6 +287,30 @@ KvPlan plan_kvsplit(const fl::FwdArgs& a, int32_t requested) {
   if (n < 1) n = 0;
   p.nsplit = (int)n;
   p.bytes = n * (int64_t)a.batch_heads * a.seq * kPartFloats * (int64_t)sizeof(float);
+  return p;
+}
+
+// The plan of the allocation-free entry point, whose partials must fit
+// `limit` bytes.  A requested chunk count is kept as asked (the caller then
+// gets FL_ERR_UNSUPPORTED when it does not fit).  The library's own choice
+// is lowered to the most chunks that fit, or to one pass when fewer than two
+// do; fewer chunks are longer, so a key-quarter plan whose chunks would pass
+// 8 tiles moves to the pipelined chunk kernel.
+KvPlan plan_kvsplit_capped(const fl::FwdArgs& a, int32_t requested, int64_t limit) {
+  KvPlan p = plan_kvsplit(a, requested);
+  if (requested > 0 || p.nsplit == 0 || p.bytes <= limit) return p;
+  const int64_t per_chunk = p.bytes / p.nsplit;
+  const int64_t n = limit / per_chunk;
+  if (n < 2) {
+    p.nsplit = 0;
+    p.quarter = false;
+    p.bytes = 0;
+    return p;
+  }
+  const int64_t tiles = std::max<int64_t>(1, (a.seq_k + 63) / 64);
+  p.nsplit = (int)n;
+  p.bytes = n * per_chunk;
+  if (p.quarter && (tiles + n - 1) / n > 8) p.quarter = false;
   return p;
 }
 
@@ -401,6 +428,13 @@ const char* fl_attn_config_name(int32_t config) {
   return fl::kFa2Configs[config].name;
 }
 
+int fl_attn_config_id(const char* name) {
+  if (name == nullptr) return -1;
+  for (int i = 0; i < fl::kNumFa2Configs; ++i)
+    if (std::strcmp(name, fl::kFa2Configs[i].name) == 0) return i;
+  return -1;
+}
+
 int fl_attn_select_config(const fl_attn_params* p) {
   fl::FwdArgs a;
   if (check_fa2(p, &a) != FL_OK) return -1;
@@ -449,6 +483,13 @@ int64_t fl_attn_splitkv_workspace_bytes(const fl_attn_params_ex* p, int32_t num_
   return plan.nsplit == 0 ? 0 : plan.bytes;
 }
 
+int64_t fl_attn_splitkv_noalloc_bytes(const fl_attn_params_ex* p, int32_t num_splits) {
+  fl::FwdArgs a;
+  if (check_ex(p, &a, "fl_attn_splitkv_noalloc_bytes") != FL_OK) return -1;
+  const KvPlan plan = plan_kvsplit_capped(a, num_splits, FL_ATTN_SCRATCH_BYTES);
+  return plan.nsplit == 0 ? 0 : plan.bytes;
+}
+
 int fl_attn_fwd_f16_splitkv(const fl_attn_params_ex* p, int32_t num_splits, void* workspace,
                             int64_t workspace_bytes, void* stream) {
   const char* who = "fl_attn_fwd_f16_splitkv";
@@ -483,7 +524,7 @@ int fl_attn_fwd_f16_splitkv_noalloc(const fl_attn_params_ex* p, int32_t num_spli
   if (empty_problem(a)) return FL_OK;
   rc = check_pointers(&p->base, &a, who, 16);
   if (rc != FL_OK) return rc;
-  const KvPlan plan = plan_kvsplit(a, num_splits);
+  const KvPlan plan = plan_kvsplit_capped(a, num_splits, FL_ATTN_SCRATCH_BYTES);
   if (plan.nsplit != 0 && plan.bytes > (int64_t)FL_ATTN_SCRATCH_BYTES)
     return fail(FL_ERR_UNSUPPORTED, "%s: %d key chunks need %lld bytes of scratch, above the "
                 "%lld-byte limit (use fl_attn_fwd_f16_splitkv with a workspace)", who, plan.nsplit,

@@ -208,6 +208,9 @@ int fl_diag_mfma_mix(int groups, int waves, int rounds, int mode, int lds_bytes,
   if (groups < 1 || waves < 1 || waves > 16 || rounds < 1 || mode < 0 || mode > 12 ||
       lds_bytes < 0 || lds_bytes > 160 * 1024 || out == nullptr || sink == nullptr)
     return (int)hipErrorInvalidValue;
+  // Modes 9-12 read lane*16 + offset:512 bytes of dynamic LDS (up to
+  // 1.5 KiB): refuse a smaller allocation.
+  if (mode >= 9 && lds_bytes < 2048) return (int)hipErrorInvalidValue;
   const void* fns[13] = {
       (const void*)mfma_mix_kernel<0>,  (const void*)mfma_mix_kernel<1>,
       (const void*)mfma_mix_kernel<2>,  (const void*)mfma_mix_kernel<3>,

@@ -178,6 +178,7 @@ struct Geom {
   long long q_sb, q_sh, k_sb, k_sh, v_sb, v_sh, o_sb, o_sh;
   int q_sr, k_sr, v_sr, o_sr;
   int heads, seq_q, seq_k, coff;
+  int xcds, cus_per_xcd;  // the device's XCDs and CUs per XCD (wg_coords)
   float* lse;  // [B*H][N_q] or null
   // split-KV launches: partial results [nsplit][B*H][N_q][kPartStride]
   float* part;
@@ -251,38 +252,39 @@ __device__ __forceinline__ void static_for(std::integer_sequence<int, I...>, F&&
   (f(Ic<I>{}), ...);
 }
 
-// Work-group -> (batch*head, query block).  Work-groups are dealt to the 8
-// XCDs round-robin; remap so that the query blocks of a head land on the
-// same XCD (shared K/V in its L2).  Causal work-groups differ in length, so
-// each XCD is fed heaviest first (heads interleaved).  Measured dispatch on
-// gfx950: an XCD fills its 32 CUs in a fixed order with its first 32
-// work-groups; with two co-resident work-groups per CU its next 32 fill the
+// Work-group -> (batch*head, query block).  Work-groups are dealt to the
+// device's XCDs round-robin (`xcds`, 8 on an MI355X seen whole); remap so
+// that the query blocks of a head land on the same XCD (shared K/V in its
+// L2).  Causal work-groups differ in length, so each XCD is fed heaviest
+// first (heads interleaved).  Measured dispatch on gfx950: an XCD fills its
+// CUs (`cpx` of them, 32 on an MI355X) in a fixed order with its first cpx
+// work-groups; with two co-resident work-groups per CU its next cpx fill the
 // second slots of the same CUs in the same order; after that each goes to
-// whichever CU frees first.  So with kSlotsPerCu == 2 the second 32 are
+// whichever CU frees first.  So with kSlotsPerCu == 2 the second cpx are
 // taken in reverse (CU j pairs the j-th heaviest block with the j-th
-// lightest of the first 64), and every later position keeps the
-// longest-processing-time order.
+// lightest of the first 2 cpx), and every later position keeps the
+// longest-processing-time order.  With one XCD the remap is the identity
+// and only the causal order remains.
 template <bool CAUSAL, int kSlotsPerCu>
-__device__ __forceinline__ void wg_coords(int nqb, int& bh, int& qb) {
-  constexpr int kCusPerXcd = 32;
+__device__ __forceinline__ void wg_coords(int nqb, int xcds, int cpx, int& bh, int& qb) {
   const int total = gridDim.x;
   const int i = blockIdx.x;
-  const int per = total >> 3;
-  if ((total & 7) != 0) {
+  const int per = total / xcds;
+  const int x = i % xcds;  // the XCD this work-group runs on
+  const int k = i / xcds;  // its dispatch position within the XCD
+  if (per * xcds != total) {
     bh = i / nqb;
     qb = i - bh * nqb;
   } else if (!CAUSAL || per % nqb != 0) {
-    const int lin = (i & 7) * per + (i >> 3);
+    const int lin = x * per + k;
     bh = lin / nqb;
     qb = lin - bh * nqb;
   } else {
     const int hx = per / nqb;  // whole heads per XCD
-    const int k = i >> 3;      // dispatch position within the XCD
-    constexpr int first = kCusPerXcd * kSlotsPerCu;
+    const int first = cpx * kSlotsPerCu;
     int r = k;                 // work rank, 0 = heaviest
-    if (kSlotsPerCu == 2 && per >= first && k >= kCusPerXcd && k < first)
-      r = first - 1 - (k - kCusPerXcd);
-    bh = (i & 7) * hx + r % hx;
+    if (kSlotsPerCu == 2 && per >= first && k >= cpx && k < first) r = first - 1 - (k - cpx);
+    bh = x * hx + r % hx;
     qb = r / hx;
   }
   if (CAUSAL) qb = nqb - 1 - qb;
@@ -1019,6 +1021,8 @@ inline Geom make_geom(const FwdArgs& a) {
   g.seq_q = a.seq;
   g.seq_k = a.seq_k;
   g.coff = a.seq_k - a.seq;
+  g.xcds = device_xcds();
+  g.cus_per_xcd = device_cus() / g.xcds;
   g.lse = a.lse;
   g.part = nullptr;
   g.nsplit = 1;

@@ -280,7 +280,7 @@ fa2_fwd_d128_kernel(const T* Q, const T* __restrict__ K, const T* __restrict__ V
   const int lane = threadIdx.x & 63;
   const int rw = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   int bh, qb;
-  wg_coords<CAUSAL, kWgPerCu>(nqb, bh, qb);
+  wg_coords<CAUSAL, kWgPerCu>(nqb, geom.xcds, geom.cus_per_xcd, bh, qb);
   const HeadPtrs<T> hp = head_ptrs<T, kRowBytes2>(geom, bh, Q, K, V, O);
   const i32x4_t rk = hp.rk, rv = hp.rv;
   const FetchOff<kSegs> fk = fetch_offsets128<kSegs, false>(rw, lane, 2 * geom.k_sr);

@@ -37,7 +37,7 @@ fa2_fwd_kernel(const _Float16* Q, const _Float16* __restrict__ K,
     bh = r / nqb;
     qb = r - bh * nqb;
   } else {
-    wg_coords<CAUSAL, W == 4 ? 2 : 1>(nqb, bh, qb);
+    wg_coords<CAUSAL, W == 4 ? 2 : 1>(nqb, geom.xcds, geom.cus_per_xcd, bh, qb);
   }
   const HeadPtrs hp = head_ptrs(geom, bh, Q, K, V, O);
   const i32x4_t rk = hp.rk, rv = hp.rv;

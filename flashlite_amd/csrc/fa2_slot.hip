@@ -105,7 +105,7 @@ fa2_fwd_slot_kernel(const T* Q, const T* __restrict__ K, const T* __restrict__ V
   const int stream = wave / W;       // key-range half (0 unless SPLIT)
   const int rw = wave - stream * W;  // 32-row block within the work-group
   int bh, qb;
-  wg_coords<CAUSAL, kWgPerCu>(nqb, bh, qb);
+  wg_coords<CAUSAL, kWgPerCu>(nqb, geom.xcds, geom.cus_per_xcd, bh, qb);
   const HeadPtrs<T> hp = head_ptrs(geom, bh, Q, K, V, O);
   const i32x4_t rk = hp.rk, rv = hp.rv;
   const FetchOff<kSegs> fk = fetch_offsets<kSegs, false>(rw, lane, 2 * geom.k_sr);

@@ -87,6 +87,26 @@ inline int device_cus() {
   }
   return c;
 }
+// XCDs of the current device (8 on an MI355X seen whole; 1 per partition
+// when it is split into single-XCD devices), looked up once per device
+// (hipDeviceAttributeNumberOfXccs).  The work-group remap that keeps a head
+// on one XCD (wg_coords) follows it; a count that does not divide the CUs,
+// or a failed lookup, gives 1 (no remap).  8 when no device is visible.
+constexpr int kMi355xXcds = 8;
+inline int device_xcds() {
+  constexpr int kMaxDevices = 64;
+  static int cached[kMaxDevices];  // 0: not looked up yet
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return kMi355xXcds;
+  int x = __atomic_load_n(&cached[dev], __ATOMIC_RELAXED);
+  if (x <= 0) {
+    if (hipDeviceGetAttribute(&x, hipDeviceAttributeNumberOfXccs, dev) != hipSuccess || x <= 0 ||
+        device_cus() % x != 0)
+      x = 1;
+    __atomic_store_n(&cached[dev], x, __ATOMIC_RELAXED);
+  }
+  return x;
+}
 inline bool quarter_config_fits(const FwdArgs& a) { return a.seq_k <= kQuarterMaxKeys; }
 
 // Per-schedule launchers behind launch_fa2 (one source file each).

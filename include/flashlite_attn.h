@@ -163,11 +163,17 @@ int fl_attn_fwd_f16_splitkv(const fl_attn_params_ex* p, int32_t num_splits, void
  * fl_attn_fwd_f16_splitkv without a workspace argument and without any
  * allocation: the partial results go to a scratch array of
  * FL_ATTN_SCRATCH_BYTES (8 MiB) that the library holds in device memory on
- * every GPU it runs on, until the process ends.  Same parameters, plan
- * (num_splits as for fl_attn_fwd_f16_splitkv) and results, bit for bit.
- * A plan that needs more scratch than the limit (see
- * fl_attn_splitkv_workspace_bytes) returns FL_ERR_UNSUPPORTED and launches
- * nothing; a plan with no split runs the one-pass kernel.  Launches on the
+ * every GPU it runs on, until the process ends.  Same parameters and
+ * results as fl_attn_fwd_f16_splitkv, bit for bit, for the same chunk
+ * count.  num_splits > 0 is taken as asked; a count whose partials exceed
+ * the limit returns FL_ERR_UNSUPPORTED and launches nothing.
+ * num_splits <= 0 lets the library choose as for fl_attn_fwd_f16_splitkv,
+ * lowered to the most chunks whose partials fit the limit, or to one pass
+ * (no scratch) when fewer than two fit: the library's own choice never
+ * fails for lack of scratch.  fl_attn_splitkv_noalloc_bytes returns the
+ * scratch bytes a call with the same `p` and `num_splits` uses (0 for one
+ * pass, -1 if `p` is rejected; above FL_ATTN_SCRATCH_BYTES only for a
+ * requested count that will be refused).  Launches on the
  * current device, into `stream`, which must belong to it.  Every call on a
  * GPU shares that GPU's array (each call writes every partial it reads, so
  * nothing has to start at zero): calls that may overlap on one GPU -- other
@@ -179,6 +185,7 @@ int fl_attn_fwd_f16_splitkv(const fl_attn_params_ex* p, int32_t num_splits, void
  */
 #define FL_ATTN_SCRATCH_BYTES (8 << 20)
 int fl_attn_fwd_f16_splitkv_noalloc(const fl_attn_params_ex* p, int32_t num_splits, void* stream);
+int64_t fl_attn_splitkv_noalloc_bytes(const fl_attn_params_ex* p, int32_t num_splits);
 
 /*
  * Un-fused baseline: one work-group per query row, scores staged in LDS.
@@ -196,6 +203,11 @@ const char* fl_attn_last_error(void);
  * rule is the fixed `seq_len >= 2048` test at csrc/kernel_flash2.cu:789). */
 int fl_attn_num_configs(void);
 const char* fl_attn_config_name(int32_t config);
+/* The id of the configuration named `name` (as fl_attn_config_name returns
+ * it), or -1 if no configuration has that name.  Ids can change between
+ * versions of the library; names do not, so a caller that forces a
+ * configuration should look its id up by name. */
+int fl_attn_config_id(const char* name);
 /* Returns the configuration fl_attn_fwd_f16 would launch for `p`, or -1 if
  * `p` is rejected (the reason is in fl_attn_last_error()). */
 int fl_attn_select_config(const fl_attn_params* p);

@@ -147,6 +147,31 @@ def test_flash2_out_reused_many_times(cuda):
 
 
 @pytest.mark.gpu
+def test_c4_out_buffer_reused_100_times(cuda):
+    # BASELINE's C4 as defined: B32 H32 N256 causal through the out-buffer
+    # interface, one preallocated output reused over 100 calls
+    # (benchmarks/benchmark_throughput.py:141-147); then every row against
+    # the oracle, and the 100th result equal to the first bit for bit
+    from flashlite_amd.workloads import WORKLOADS, workload_inputs
+    from gpu_util import assert_close_oracle
+
+    w = WORKLOADS["C4_many_B32H32N256"]
+    q16, k16, v16 = workload_inputs(w)
+    q, k, v = (torch.from_numpy(x).to(cuda) for x in (q16, k16, v16))
+    buf = torch.full_like(q, float("nan"))
+    first = None
+    for i in range(100):
+        got = flash_attn_wmma.forward_flash2(q, k, v, w.sm_scale, True, out=buf)
+        assert got.data_ptr() == buf.data_ptr()
+        if i == 0:
+            first = buf.clone()
+    torch.cuda.synchronize(cuda)
+    assert torch.equal(buf, first)
+    mx, mean = assert_close_oracle(buf.cpu().numpy(), q16, k16, v16, w.sm_scale, True)
+    print(f"C4 after 100 calls, every row: max-abs {mx:.2e} mean-abs {mean:.2e}")
+
+
+@pytest.mark.gpu
 def test_naive_via_binding(cuda):
     from oracle import attention_fp32, error_stats
     from flashlite_amd.workloads import make_qkv

@@ -298,3 +298,78 @@ def test_splitkv_workspace_checks():
     assert capi.fwd_splitkv(p, A + 0x400000, need - 4) == capi.FL_ERR_INVALID_ARGUMENT
     assert capi.fwd_splitkv(p, A + 0x400008, need) == capi.FL_ERR_MISALIGNED
     assert capi.load().fl_attn_fwd_f16_splitkv(None, 0, None, 0, None) == capi.FL_ERR_INVALID_ARGUMENT
+
+
+def _ex_shape(batch, heads, nq, nk, causal=False):
+    base = _p(batch=batch, heads=heads, seq_q=nq, seq_k=nk, causal=causal)
+    qs = (heads * nq * 64, nq * 64, 64)
+    ks = (heads * nk * 64, nk * 64, 64)
+    return capi.make_params_ex(base, qs, ks, ks, qs)
+
+
+def test_noalloc_plan_fits_the_scratch_array():
+    """Every plan the library chooses for the allocation-free entry point fits
+    its static scratch (num_splits <= 0 never fails for lack of scratch): the
+    chunk count is lowered to what fits, or the call runs one pass."""
+    per_row = 68 * 4
+    checked = 0
+    for batch, heads in ((1, 1), (1, 16), (2, 8), (4, 8), (8, 16), (32, 32), (64, 64)):
+        for nq in (1, 2, 16, 32, 33, 64, 65, 100, 128, 129, 1024):
+            for nk in (64, 192, 512, 1000, 4096, 8192, 65536, 1 << 20):
+                for causal in (False, True):
+                    p = _ex_shape(batch, heads, nq, nk, causal)
+                    ws = capi.splitkv_workspace_bytes(p, 0)
+                    na = capi.splitkv_noalloc_bytes(p, 0)
+                    assert 0 <= na <= capi.SCRATCH_BYTES, (batch, heads, nq, nk, ws, na)
+                    assert na % (batch * heads * nq * per_row) == 0
+                    if ws <= capi.SCRATCH_BYTES:
+                        assert na == ws  # the cap changes only plans that do not fit
+                    else:
+                        # the most chunks that fit, and never a single chunk
+                        per_chunk = batch * heads * nq * per_row
+                        fit = capi.SCRATCH_BYTES // per_chunk
+                        assert na == (fit * per_chunk if fit >= 2 else 0)
+                    checked += 1
+    assert checked > 1000
+
+
+def test_noalloc_plan_of_reported_shapes():
+    # B8 H16, 128 query rows over 65536 keys: 2 chunks of 128 x 128 rows need
+    # 8,912,896 bytes, above the 8 MiB array, and one chunk is no split
+    p = _ex_shape(8, 16, 128, 65536)
+    assert capi.splitkv_workspace_bytes(p, 0) == 8912896
+    assert capi.splitkv_noalloc_bytes(p, 0) == 0
+    # B32 H32, 32 query rows over 4096 keys: 8 chunks (71 MB) with a
+    # workspace; one 8.9 MB chunk does not fit either, so one pass
+    p = _ex_shape(32, 32, 32, 4096)
+    assert capi.splitkv_workspace_bytes(p, 0) == 8 * 1024 * 32 * 68 * 4
+    assert capi.splitkv_noalloc_bytes(p, 0) == 0
+    # B32 H32 decode (one query row): 8 chunks of 1024 rows fit
+    p = _ex_shape(32, 32, 1, 4096)
+    assert capi.splitkv_noalloc_bytes(p, 0) == capi.splitkv_workspace_bytes(p, 0) == 8 * 1024 * 272
+    # B16 H64, 16 rows over 65536 keys: 8 chunks (35.7 MB) with a workspace;
+    # one 4.5 MB chunk fits, two do not, so one pass
+    p = _ex_shape(16, 64, 16, 65536)
+    ws = capi.splitkv_workspace_bytes(p, 0)
+    assert ws == 8 * 1024 * 16 * 272 and ws > capi.SCRATCH_BYTES
+    assert capi.splitkv_noalloc_bytes(p, 0) == 0
+    # B4 H64, 16 rows over 65536 keys: 8 chunks of 256 x 16 rows (8.9 MB),
+    # lowered to the 7 that fit
+    p = _ex_shape(4, 64, 16, 65536)
+    assert capi.splitkv_workspace_bytes(p, 0) == 8 * 256 * 16 * 272
+    assert capi.splitkv_noalloc_bytes(p, 0) == 7 * 256 * 16 * 272
+    # a requested count is kept as asked, even when it will be refused
+    p = _ex_shape(4, 16, 256, 4096)
+    assert capi.splitkv_noalloc_bytes(p, 16) == capi.splitkv_workspace_bytes(p, 16) \
+        == 16 * 64 * 256 * 272
+    assert capi.splitkv_noalloc_bytes(_ex_shape(1, -1, 1, 4096), 0) == -1
+
+
+def test_config_id_lookup():
+    for i in range(capi.num_configs()):
+        assert capi.load().fl_attn_config_id(capi.config_name(i).encode()) == i
+    assert capi.load().fl_attn_config_id(b"br128_bc64_w4_slot") == 4
+    assert capi.load().fl_attn_config_id(b"no_such_config") == -1
+    assert capi.load().fl_attn_config_id(None) == -1
+    with pytest.raises(KeyError):
+        capi.config_id("no_such_config")

@@ -21,7 +21,9 @@ pytestmark = pytest.mark.gpu
 
 # (B, H, N_q, N_k, causal, num_splits): the first uses about half the array
 # (8 chunks x 32 heads x 64 rows x 272 bytes = 4.5 MB), the second far less.
-CALLS = [(4, 8, 64, 8192, False, 0), (1, 4, 1, 1000, True, 3)]
+# The first asks for its 8 chunks explicitly: the library's own plan depends
+# on the device's CU count and would run one pass on a partitioned GPU.
+CALLS = [(4, 8, 64, 8192, False, 8), (1, 4, 1, 1000, True, 3)]
 
 
 def _qkv(b, h, nq, nk, seed):
@@ -79,3 +81,103 @@ def test_noalloc_rejects_oversized_plan(cuda):
     assert "scratch" in capi.last_error()
     torch.cuda.synchronize(cuda)
     assert bool((o == 7.0).all()), "a rejected call launched work"
+
+
+# The library's own plan (num_splits = 0) lowered to fit the array:
+# (B, H, N_q, N_k, chunks with a workspace, chunks without). B4 H16 N_q 128
+# over 1024 keys plans 4 chunks of 64 groups (8.9 MB) and runs 3; B8 H16
+# N_q 128 over 4096 keys plans 2 chunks (8.9 MB) and runs one pass; B4 H64
+# N_q 16 over 4096 keys plans 8 one-wave chunks (8.9 MB) and runs 7.
+CAPPED = [(4, 16, 128, 1024, 4, 3), (8, 16, 128, 4096, 2, 0), (4, 64, 16, 4096, 8, 7)]
+
+
+@pytest.mark.parametrize("b,h,nq,nk,ws_chunks,na_chunks", CAPPED)
+def test_noalloc_library_plan_is_capped(cuda, b, h, nq, nk, ws_chunks, na_chunks):
+    import torch
+
+    print(f"capped plan: B{b} H{h} Nq{nq} Nk{nk}", flush=True)
+    if _cus(cuda) != 256:
+        pytest.skip("the plans below are the whole MI355X's (256 CUs)")
+    q16, k16, v16 = _qkv(b, h, nq, nk, seed=7)
+    tq, tk, tv = (to_dev(x, cuda) for x in (q16, k16, v16))
+    o = torch.full_like(tq, float("nan"))
+    ls = torch.full(tq.shape[:3], float("nan"), dtype=torch.float32, device=cuda)
+    p = capi.tensor_params_ex(tq, tk, tv, o, 0.125, False, lse=ls)
+    per_chunk = b * h * nq * 68 * 4
+    assert capi.splitkv_workspace_bytes(p, 0) == ws_chunks * per_chunk > capi.SCRATCH_BYTES
+    assert capi.splitkv_noalloc_bytes(p, 0) == na_chunks * per_chunk
+    stream = torch.cuda.current_stream(cuda).cuda_stream
+    capi.check(capi.fwd_splitkv_noalloc(p, stream, 0))
+    torch.cuda.synchronize(cuda)
+    # the same plan through the other entry points, bit for bit
+    o2 = torch.full_like(tq, float("nan"))
+    l2 = torch.full(tq.shape[:3], float("nan"), dtype=torch.float32, device=cuda)
+    p2 = capi.tensor_params_ex(tq, tk, tv, o2, 0.125, False, lse=l2)
+    if na_chunks == 0:
+        capi.check(capi.fwd_ex(p2, stream))
+    else:
+        need = capi.splitkv_workspace_bytes(p2, na_chunks)
+        assert need == na_chunks * per_chunk
+        ws = torch.full((need // 4,), float("nan"), dtype=torch.float32, device=cuda)
+        capi.check(capi.fwd_splitkv(p2, ws.data_ptr(), need, stream, na_chunks))
+    torch.cuda.synchronize(cuda)
+    assert torch.equal(o, o2) and torch.equal(ls, l2)
+    hs = slice(0, 2)  # two heads of the first batch against the oracle
+    assert_close_oracle(o[:1, hs].float().cpu().numpy(), q16[:1, hs], k16[:1, hs], v16[:1, hs],
+                        0.125, False)
+
+
+def _cus(dev):
+    import torch
+
+    return torch.cuda.get_device_properties(dev).multi_processor_count
+
+
+def test_noalloc_under_graph_capture(cuda):
+    """One eager call (the first call per device looks the scratch address
+    up), then two allocation-free calls captured in a HIP graph and replayed
+    several times, with eager work and synchronisation between replays:
+    every replay equals the eager outputs bit for bit."""
+    import torch
+
+    shapes = [(2, 8, 1, 4096, True, 8), (4, 8, 32, 2048, False, 4)]
+    data, eager = [], []
+    stream = torch.cuda.Stream(cuda)
+    for i, (b, h, nq, nk, causal, splits) in enumerate(shapes):
+        print(f"graph call {i}: B{b} H{h} Nq{nq} Nk{nk} causal={causal} splits={splits}",
+              flush=True)
+        q16, k16, v16 = _qkv(b, h, nq, nk, seed=40 + i)
+        tq, tk, tv = (to_dev(x, cuda) for x in (q16, k16, v16))
+        o = torch.full_like(tq, float("nan"))
+        ls = torch.full(tq.shape[:3], float("nan"), dtype=torch.float32, device=cuda)
+        p = capi.tensor_params_ex(tq, tk, tv, o, 0.125, causal, lse=ls)
+        assert 0 < capi.splitkv_noalloc_bytes(p, splits) <= capi.SCRATCH_BYTES
+        with torch.cuda.stream(stream):
+            capi.check(capi.fwd_splitkv_noalloc(p, stream.cuda_stream, splits))
+        stream.synchronize()
+        eager.append((o.clone(), ls.clone()))
+        o.fill_(float("nan"))
+        ls.fill_(float("nan"))
+        # the params hold raw addresses: keep the tensors alive for the graph
+        # (torch.cuda.graph empties the caching allocator on entry, which
+        # would unmap the memory of tensors that are no longer referenced)
+        data.append((p, o, ls, splits, (q16, k16, v16, causal), (tq, tk, tv)))
+    torch.cuda.synchronize(cuda)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        for p, _, _, splits, _, _ in data:
+            capi.check(capi.fwd_splitkv_noalloc(p, stream.cuda_stream, splits))
+    for rep in range(3):
+        for _, o, ls, _, _, _ in data:
+            o.fill_(float("nan"))
+            ls.fill_(float("nan"))
+        junk = torch.randn(1 << 20, device=cuda) * 2.0  # eager work between replays
+        torch.cuda.synchronize(cuda)
+        graph.replay()
+        torch.cuda.synchronize(cuda)
+        assert bool(torch.isfinite(junk).all())
+        for i, (_, o, ls, _, _, _) in enumerate(data):
+            assert torch.equal(o, eager[i][0]), f"replay {rep}, call {i}: O differs from eager"
+            assert torch.equal(ls, eager[i][1]), f"replay {rep}, call {i}: lse differs from eager"
+    q16, k16, v16, causal = data[0][4]
+    assert_close_oracle(data[0][1].float().cpu().numpy(), q16, k16, v16, 0.125, causal)
