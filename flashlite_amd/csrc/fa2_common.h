@@ -214,6 +214,18 @@ __device__ __forceinline__ HeadPtrs<T> head_ptrs(const Geom& g, int bh, const T*
   return p;
 }
 
+// K and V resources of head `bh` that end after row `rows` (at most N_k):
+// loads of later rows return zeros without reaching memory, so fetches past
+// a walk's last tile cost no L2 or HBM traffic.
+template <class T, int kRowB = kRowBytes>
+__device__ __forceinline__ void kv_rsrc_rows(const Geom& g, int bh, const T* K, const T* V,
+                                             int rows, i32x4_t& rk, i32x4_t& rv) {
+  const int b = bh / g.heads, h = bh - b * g.heads;
+  const int n = min(rows, g.seq_k);
+  rk = buffer_rsrc(K + (b * g.k_sb + h * g.k_sh), n > 0 ? (n - 1) * (2 * g.k_sr) + kRowB : 0);
+  rv = buffer_rsrc(V + (b * g.v_sb + h * g.v_sh), n > 0 ? (n - 1) * (2 * g.v_sr) + kRowB : 0);
+}
+
 // Key tiles a causal block of query rows [q0, q_end) needs: through the
 // diagonal of its last row (at least one, fully masked when no row of the
 // block sees a key).
@@ -318,6 +330,26 @@ __device__ __forceinline__ FetchOff<kSegs> fetch_offsets(int wave, int lane, int
   }
   f.tile_bytes = kBc * row_bytes;
   return f;
+}
+
+// The same through a resource that ends at the walk's last row
+// (kv_rsrc_rows), with tiles clamped to `tzero`, the first tile wholly past
+// that row: a fetch past the walk lands as zeros with no memory traffic,
+// where fetch_tile re-reads the last tile.  (Rows are at least 128 bytes
+// apart, so tile tzero starts at or past the resource's end; the C ABI's
+// N_k limit keeps its offset below 2^31.)
+template <int kSegs>
+__device__ __forceinline__ void fetch_tile_z(const i32x4_t& rs, const uint8_t* slot, int t,
+                                             int tzero, int wave, const FetchOff<kSegs>& f) {
+  t = min(t, tzero);
+  const int tb = t * f.tile_bytes;
+#pragma unroll
+  for (int i = 0; i < kSegs; ++i) {
+    const int seg = wave * kSegs + i;
+    const int voff = tb + f.lane[i];
+    const uint32_t lds_base = (uint32_t)(uintptr_t)(slot + 1024 * seg);
+    asm volatile("buffer_load_dwordx4 %0, %1, 0 offen lds" : : "v"(voff), "s"(rs), "{m0}"(lds_base));
+  }
 }
 
 template <int kSegs>

@@ -107,7 +107,6 @@ fa2_fwd_slot_kernel(const T* Q, const T* __restrict__ K, const T* __restrict__ V
   int bh, qb;
   wg_coords<CAUSAL, kWgPerCu>(nqb, geom.xcds, geom.cus_per_xcd, bh, qb);
   const HeadPtrs<T> hp = head_ptrs(geom, bh, Q, K, V, O);
-  const i32x4_t rk = hp.rk, rv = hp.rv;
   const FetchOff<kSegs> fk = fetch_offsets<kSegs, false>(rw, lane, 2 * geom.k_sr);
   const FetchOff<kSegs> fv = fetch_offsets<kSegs, true>(rw, lane, 2 * geom.v_sr);
   const int seq = geom.seq_q;
@@ -122,17 +121,29 @@ fa2_fwd_slot_kernel(const T* Q, const T* __restrict__ K, const T* __restrict__ V
   const int t0 = SPLIT == 2 ? (ntiles + 1) / 2 : ntiles;
   const int tbeg = stream == 0 ? 0 : t0;
   const int tend = stream == 0 ? t0 : ntiles;
-  const int last = max(tend - 1, tbeg);  // fetch clamp
+  const int last = max(tend - 1, tbeg);  // fetch clamp of the checked pass
+  // K and V end with this stream's range: fetches past it (the pipeline's
+  // look-ahead near the end of the walk) land as zeros with no traffic.
+  i32x4_t rk, rv;
+  kv_rsrc_rows(geom, bh, K, V, tend * kBc, rk, rv);
+  const int tzero = tend;
+  // Tiles of the range this wave's rows need (through their causal
+  // diagonal; none for a wave wholly past the last query row), at least
+  // one: iteration nw drains the wave's GEMM2, later ones only fetch and
+  // meet the barrier.
+  int nw = tend - tbeg;
+  if (CAUSAL) nw = min(nw, causal_tiles(min(q0 + 32 * rw + 32, seq), geom.coff) - tbeg);
+  if (q0 + 32 * rw >= seq) nw = 1;
+  nw = max(nw, 1);
 
-  // Prologue fetch groups -FK .. -1 (V tiles < 0 read as zeros through the
-  // buffer bound, which also zeroes the slot GEMM2(-1) reads under P = 0),
+  // Prologue fetch groups -FK .. -1: K tiles 0 .. FK-1 and V tiles
+  // 0 .. FV-1 of the range (iteration 0 has no GEMM2, so no tile -1),
   // issued before the Q loads so the two latencies overlap.
   static_for(std::make_integer_sequence<int, FK>{}, [&](auto i) __attribute__((always_inline)) {
     constexpr int G = decltype(i)::value - FK;
-    // (tile tbeg - 1 of stream 1 is a real tile: the zeroed P of
-    // iteration 0 keeps it out of O)
-    fetch_tile<kSegs>(rk, rings.kslot(Ic<G + FK>{}), tbeg + G + FK, last, rw, fk);
-    fetch_tile<kSegs>(rv, rings.vslot(Ic<G + FV>{}), tbeg + G + FV, last, rw, fv);
+    fetch_tile_z<kSegs>(rk, rings.kslot(Ic<G + FK>{}), tbeg + G + FK, tzero, rw, fk);
+    if constexpr (G + FV >= 0)
+      fetch_tile_z<kSegs>(rv, rings.vslot(Ic<G + FV>{}), tbeg + G + FV, tzero, rw, fv);
   });
   RowsT rows;
   rows.init(hp.q, geom.q_sr, lane, q0 + 32 * rw, seq, geom.seq_k, geom.coff, cq, cr);
@@ -149,13 +160,8 @@ fa2_fwd_slot_kernel(const T* Q, const T* __restrict__ K, const T* __restrict__ V
   sync_ring_ahead<(FK - 1) * kDmaPerIter, 0>();  // K(0)
   float16_t S[2];
   V8 P0[2][2], P1[2][2];
-#pragma unroll
-  for (int a = 0; a < 2; ++a)
-#pragma unroll
-    for (int b = 0; b < 2; ++b) P1[a][b] = (V8){0, 0, 0, 0, 0, 0, 0, 0};
   {
-    // S(tbeg) with the exact row max; iteration 0 recomputes block 1
-    // against it.
+    // S(tbeg) with the exact row max; iteration 0 exponentiates it.
     V8 ka[2][4];
     rows.read_k(rings.kslot(Ic<0>{}), ka);
     rows.gemm1(ka, S);
@@ -163,27 +169,41 @@ fa2_fwd_slot_kernel(const T* Q, const T* __restrict__ K, const T* __restrict__ V
   rows.mask(tbeg, S);
   rows.first_tile(S);
   sync_ring_ahead<(FV - 1) * kDmaPerIter, 0>();  // K(1), V(0)
+  // Operands of the next iteration's first kAhead slots (iteration 0 reads
+  // its own: its first slots carry no MFMA).
   V8 ahead[kAhead];
-  static_for(std::make_integer_sequence<int, kAhead>{}, [&](auto a) __attribute__((always_inline)) {
-    constexpr int L = decltype(a)::value;
-    ahead[L] = rows.template read_slot<L>(rings.kslot(Ic<0>{}), rings.kslot(Ic<1>{}),
-                                          rings.vslot(Ic<-1>{}));
-  });
 
   uint64_t out_of_range = 0;
+  // Iteration kinds (bits): a full iteration j runs GEMM1 of tile j block 1
+  // (even slots 0-6) and of tile j+1 block 0 (even slots 8-14), GEMM2 of
+  // tile j-1 (odd slots) and the softmax of tile j.  kFirst (j = 0): tile
+  // 0's scores come from the first pass and there is no tile -1, so no
+  // block-1 GEMM1 and no GEMM2.  kLast (the wave's last tile): no GEMM1 of
+  // the tile after it.  kDrain (j = nw): GEMM2 of the wave's last tile
+  // only.  Skipped MFMAs skip their operand reads too.
+  constexpr int kFull = 0, kFirst = 1, kLast = 2, kDrain = 4;
+  constexpr auto runs = [](int kind, int L) {
+    if (L & 1) return (kind & kFirst) == 0;
+    if (kind & kDrain) return false;
+    return L < 8 ? (kind & kFirst) == 0 : (kind & kLast) == 0;
+  };
   // Iteration j at unrolled position I (ring slots static): fetch K(j+FK)
   // and V(j+FV); 16 slots; the range check of tile j's sum; on MASKED
   // iterations, mask block 1 of tile j (after slot 7, before its
   // exponentials) and block 0 of tile j+1; publish K(j+2), V(j+1).
-  auto iteration = [&](auto i, int j, V8 (&P)[2][2], const V8 (&Pp)[2][2],
-                       auto masked) __attribute__((always_inline)) {
+  auto iteration = [&](auto i, int j, V8 (&P)[2][2], const V8 (&Pp)[2][2], auto masked,
+                       auto kind) __attribute__((always_inline)) {
     constexpr int I = decltype(i)::value;
     constexpr bool kMasked = decltype(masked)::value;
-    fetch_tile<kSegs>(rk, rings.kslot(Ic<I + FK>{}), tbeg + j + FK, last, rw, fk);
-    fetch_tile<kSegs>(rv, rings.vslot(Ic<I + FV>{}), tbeg + j + FV, last, rw, fv);
+    constexpr int Kd = decltype(kind)::value;
+    constexpr bool kSoftmax = (Kd & kDrain) == 0;
+    fetch_tile_z<kSegs>(rk, rings.kslot(Ic<I + FK>{}), tbeg + j + FK, tzero, rw, fk);
+    fetch_tile_z<kSegs>(rv, rings.vslot(Ic<I + FV>{}), tbeg + j + FV, tzero, rw, fv);
     V8 op[16];
+    if constexpr ((Kd & kFirst) == 0) {
 #pragma unroll
-    for (int a = 0; a < kAhead; ++a) op[a] = ahead[a];
+      for (int a = 0; a < kAhead; ++a) op[a] = ahead[a];
+    }
     half2_t tree[14];
     float sum[4];
     // SCALED: each slot scales the next slot's pair, so a slot's
@@ -193,27 +213,35 @@ fa2_fwd_slot_kernel(const T* Q, const T* __restrict__ K, const T* __restrict__ V
       constexpr int L = decltype(sl)::value;
       // The MFMA goes first (fenced): its operand's wait then never covers
       // the read issued in the same slot.
-      rows.template mfma_slot<L, kMfmaSum>(op[L], S, Pp);
+      if constexpr (runs(Kd, L)) rows.template mfma_slot<L, kMfmaSum>(op[L], S, Pp);
       __builtin_amdgcn_sched_barrier(0);
-      if constexpr (L + kAhead < 16)
-        op[L + kAhead] = rows.template read_slot<L + kAhead>(
-            rings.kslot(Ic<I>{}), rings.kslot(Ic<I + 1>{}), rings.vslot(Ic<I - 1>{}));
-      else
+      if constexpr (L + kAhead < 16) {
+        if constexpr (runs(Kd, L + kAhead))
+          op[L + kAhead] = rows.template read_slot<L + kAhead>(
+              rings.kslot(Ic<I>{}), rings.kslot(Ic<I + 1>{}), rings.vslot(Ic<I - 1>{}));
+      } else if constexpr (kSoftmax && (Kd & kLast) == 0) {
         ahead[L + kAhead - 16] = rows.template read_slot<L + kAhead - 16>(
             rings.kslot(Ic<I + 1>{}), rings.kslot(Ic<I + 2>{}), rings.vslot(Ic<I>{}));
-      if constexpr (L == 0) rows.template scale_pair<0>(S, xs[0]);
-      const float epair = rows.template exp_pair<L>(xs[L & 1], P);
-      if constexpr (kMfmaSum)
-        ;
-      else if constexpr (kTree && !kMasked)
-        RowsT::template sum_slot<L>(P, tree);
-      else
-        RowsT::template sum_pair_f32<L>(epair, sum);
-      if constexpr (kMasked && L == 7) rows.template mask_block<1>(tbeg + j, S[1]);
-      if constexpr (L < 15) rows.template scale_pair<L + 1>(S, xs[(L + 1) & 1]);
+      } else if constexpr (kSoftmax && (L + kAhead - 16) % 2 == 1) {
+        // the wave's last tile: its drain needs only V (odd slots)
+        ahead[L + kAhead - 16] = rows.template read_slot<L + kAhead - 16>(
+            rings.kslot(Ic<I + 1>{}), rings.kslot(Ic<I + 2>{}), rings.vslot(Ic<I>{}));
+      }
+      if constexpr (kSoftmax) {
+        if constexpr (L == 0) rows.template scale_pair<0>(S, xs[0]);
+        const float epair = rows.template exp_pair<L>(xs[L & 1], P);
+        if constexpr (kMfmaSum)
+          ;
+        else if constexpr (kTree && !kMasked)
+          RowsT::template sum_slot<L>(P, tree);
+        else
+          RowsT::template sum_pair_f32<L>(epair, sum);
+        if constexpr (kMasked && L == 7) rows.template mask_block<1>(tbeg + j, S[1]);
+        if constexpr (L < 15) rows.template scale_pair<L + 1>(S, xs[(L + 1) & 1]);
+      }
       __builtin_amdgcn_sched_barrier(0);
     });
-    if constexpr (!kMfmaSum) {
+    if constexpr (!kMfmaSum && kSoftmax) {
       float tot;
       if constexpr (kTree && !kMasked)
         tot = RowsT::sum_root(tree);
@@ -222,26 +250,68 @@ fa2_fwd_slot_kernel(const T* Q, const T* __restrict__ K, const T* __restrict__ V
       rows.l += tot;
       out_of_range |= __builtin_amdgcn_ballot_w64(!(tot <= kSumLimit));
     }
-    if constexpr (kMasked) rows.template mask_block<0>(tbeg + j + 1, S[0]);
-    sync_ring_ahead<(FV - 1) * kDmaPerIter, kTailReads>();
+    if constexpr (kMasked && (Kd & (kLast | kDrain)) == 0)
+      rows.template mask_block<0>(tbeg + j + 1, S[0]);
+    if constexpr (kSoftmax)
+      sync_ring_ahead<(FV - 1) * kDmaPerIter, kTailReads - ((Kd & kLast) ? kAhead / 2 : 0)>();
+    else
+      sync_ring_ahead<(FV - 1) * kDmaPerIter, 0>();
   };
-  auto group = [&](int j0, auto masked) __attribute__((always_inline)) {
+  auto group = [&](int j0, auto masked, auto first) __attribute__((always_inline)) {
     static_for(std::make_integer_sequence<int, kUnroll>{}, [&](auto i) __attribute__((always_inline)) {
       constexpr int I = decltype(i)::value;
       const int j = j0 + I;
-      if (!decltype(masked)::value || j <= t0) {
-        if constexpr (I % 2 == 0)
-          iteration(i, j, P0, P1, masked);
-        else
-          iteration(i, j, P1, P0, masked);
-      }
+      auto& P = I % 2 == 0 ? P0 : P1;
+      auto& Pp = I % 2 == 0 ? P1 : P0;
+      if constexpr (decltype(first)::value && I == 0)
+        iteration(i, j, P, Pp, masked, Ic<kFirst>{});
+      else if (!decltype(masked)::value || j < nw - 1)
+        iteration(i, j, P, Pp, masked, Ic<kFull>{});
     });
+  };
+  // The wave's last tile (j = nw - 1, at unrolled position I) and its drain.
+  auto tail = [&](auto i) __attribute__((always_inline)) {
+    constexpr int I = decltype(i)::value;
+    auto& P = I % 2 == 0 ? P0 : P1;
+    auto& Pp = I % 2 == 0 ? P1 : P0;
+    if constexpr (I == 0) {
+      if (nw == 1)
+        iteration(i, 0, P, Pp, Ic<true>{}, Ic<kFirst | kLast>{});
+      else
+        iteration(i, nw - 1, P, Pp, Ic<true>{}, Ic<kLast>{});
+    } else {
+      iteration(i, nw - 1, P, Pp, Ic<true>{}, Ic<kLast>{});
+    }
+    iteration(Ic<I + 1>{}, nw, Pp, P, Ic<true>{}, Ic<kDrain>{});
   };
   FL_TL_STAMP(tl_loop);
   {
-    int j0 = 0;
-    for (; j0 + kUnroll <= jm; j0 += kUnroll) group(j0, Ic<false>{});
-    for (; j0 <= t0; j0 += kUnroll) group(j0, Ic<true>{});
+    // iterations 0 .. nw - 2 in unrolled groups: unmasked while every tile
+    // is below the diagonal and the range end (j < jm <= nw - 1), then
+    // masked; then the wave's last tile and its drain
+    if (nw >= 2) {
+      int j0 = kUnroll;
+      if (kUnroll <= jm) {
+        group(0, Ic<false>{}, Ic<true>{});
+        for (; j0 + kUnroll <= jm; j0 += kUnroll) group(j0, Ic<false>{}, Ic<false>{});
+      } else {
+        group(0, Ic<true>{}, Ic<true>{});
+      }
+      for (; j0 < nw - 1; j0 += kUnroll) group(j0, Ic<true>{}, Ic<false>{});
+    }
+    static_for(std::make_integer_sequence<int, kUnroll>{}, [&](auto i) __attribute__((always_inline)) {
+      if ((nw - 1) % kUnroll == decltype(i)::value) tail(i);
+    });
+    // Past its drain (iterations nw + 1 .. t0, when other waves of the
+    // work-group need more tiles) a wave only fetches its share of the
+    // tiles and meets the barrier.
+    for (int j = nw + 1; j <= t0; ++j) {
+      fetch_tile_z<kSegs>(rk, rings.k + kTileBytes * ((j + FK) % kSlots), tbeg + j + FK, tzero, rw,
+                          fk);
+      fetch_tile_z<kSegs>(rv, rings.v + kTileBytes * ((j + FV) % kSlots), tbeg + j + FV, tzero, rw,
+                          fv);
+      sync_ring_ahead<(FV - 1) * kDmaPerIter, 0>();
+    }
   }
   FL_TL_STAMP(tl_loop_end);
   if constexpr (kMfmaSum) {
