@@ -352,6 +352,19 @@ __device__ __forceinline__ void fetch_tile_z(const i32x4_t& rs, const uint8_t* s
   }
 }
 
+// DMA of the 32 query rows [q, q + 32) of a head (rows >= N_q read as
+// zeros) into `qblk`, laid out as the first half of a K tile (Rows::
+// set_q_lds reads it): 4 fetches of 1 KiB per wave, counted by vmcnt.
+template <class T>
+__device__ __forceinline__ void fetch_q_block(const T* Qh, int q_sr, int q, int seq,
+                                              uint8_t* qblk, int lane) {
+  const int rows = min(32, seq - q);
+  const i32x4_t rq = buffer_rsrc(Qh + (long long)(rows > 0 ? q : 0) * q_sr,
+                                 rows > 0 ? (rows - 1) * (2 * q_sr) + kRowBytes : 0);
+  const FetchOff<4> fq = fetch_offsets<4, false>(0, lane, 2 * q_sr);
+  fetch_tile_z<4>(rq, qblk, 0, 1, 0, fq);
+}
+
 template <int kSegs>
 __device__ __forceinline__ void fetch_tile(const i32x4_t& rs, const uint8_t* slot, int t,
                                            int last_tile, int wave, const FetchOff<kSegs>& f) {
@@ -408,26 +421,40 @@ struct Rows {
     const int tr_x = trj & 3;
     tr_col = 16 * (trG & 1) + 4 * (((tr_x & 1) << 1) | (tr_x >> 1));
   }
+  // cq = +-1 applied to a 16-bit float: exact, as a flip of the sign bits
+  // (two elements per dword).
+  __device__ __forceinline__ static uint32_t sign_mask(float cq) {
+    return cq < 0.0f ? 0x80008000u : 0u;
+  }
+  __device__ __forceinline__ static V8 signed_q(const u32x4_t& raw, uint32_t m) {
+    return __builtin_bit_cast(V8, raw ^ (u32x4_t){m, m, m, m});
+  }
   // Q'^T from the raw 16-byte chunks Q[my_q][16s + 8g .. +7] (s = 0..3).
   __device__ __forceinline__ void set_q(const u32x4_t (&raw)[4], float cq) {
+    const uint32_t m = sign_mask(cq);
 #pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      const V8 x = __builtin_bit_cast(V8, raw[s]);
+    for (int s = 0; s < 4; ++s) qf[s] = signed_q(raw[s], m);
+  }
+  // The same from a 32-row Q block staged in LDS like the first half of a K
+  // tile (row r's chunk c at physical chunk c ^ k_swz(r)): the B operand
+  // chunks are read_k_op's reads of that block.
+  __device__ __forceinline__ void set_q_lds(const uint8_t* qblk, float cq) {
+    const uint32_t m = sign_mask(cq);
 #pragma unroll
-      for (int e = 0; e < 8; ++e) qf[s][e] = (T)((float)x[e] * cq);
-    }
+    for (int s = 0; s < 4; ++s)
+      qf[s] = signed_q(__builtin_bit_cast(u32x4_t, read_k_op(qblk, 0, s)), m);
   }
   __device__ __forceinline__ void init(const T* Qh, int q_sr, int lane, int qw_, int seq_,
                                        int seq_k, int coff, float cq, float cr_) {
     place(lane, qw_, seq_, seq_k, coff, cr_);
-    // Q'^T: lane holds cq * Q[my_q][16s + 8g .. +7] for s = 0..3, in fp16.
+    // Q'^T: lane holds cq * Q[my_q][16s + 8g .. +7] for s = 0..3.
+    const uint32_t sm = sign_mask(cq);
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
       if (my_q < seq) {
-        const V8 raw =
-            *reinterpret_cast<const V8*>(Qh + (long long)my_q * q_sr + 16 * s + 8 * g);
-#pragma unroll
-        for (int e = 0; e < 8; ++e) qf[s][e] = (T)((float)raw[e] * cq);
+        const u32x4_t raw =
+            *reinterpret_cast<const u32x4_t*>(Qh + (long long)my_q * q_sr + 16 * s + 8 * g);
+        qf[s] = signed_q(raw, sm);
       } else {
         qf[s] = (V8){0, 0, 0, 0, 0, 0, 0, 0};
       }
@@ -442,6 +469,21 @@ struct Rows {
     l = 0.0f;
   }
 
+  // The state after init with Q'^T read from a 32-row block staged in LDS
+  // (set_q_lds).
+  __device__ __forceinline__ void init_lds(const uint8_t* qblk, int lane, int qw_, int seq_,
+                                           int seq_k, int coff, float cq, float cr_) {
+    place(lane, qw_, seq_, seq_k, coff, cr_);
+    set_q_lds(qblk, cq);
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      o[0][r] = 0.0f;
+      o[1][r] = 0.0f;
+      bias[r] = 0.0f;
+    }
+    m = 0.0f;
+    l = 0.0f;
+  }
   // Makes the per-lane index fields opaque, so addresses derived from them
   // are recomputed after this point instead of being kept live (and, under
   // register pressure, spilled) from an earlier use.

@@ -65,6 +65,8 @@ fa2_fwd_quarter_kernel(const T* Q, const T* __restrict__ K, const T* __restrict_
   static_assert(RB * (9 * 64) * 16 <= kQuarterWaveBytes, "partials fit a quarter's LDS");
   constexpr int kSegs = 8 / RB;  // 1 KiB segments of a tile each wave of a quarter fetches
   __shared__ __attribute__((aligned(16))) uint8_t buf[NW][kQuarterWaveBytes];
+  // each wave's 32 query rows (4 KiB)
+  __shared__ __attribute__((aligned(16))) uint8_t qbuf[NW * RB][32 * kRowBytes];
 
   FL_ST_DECL();
   FL_ST_MARK(0);
@@ -100,71 +102,106 @@ fa2_fwd_quarter_kernel(const T* Q, const T* __restrict__ K, const T* __restrict_
   const int t1 = min(t0 + kQuarterTiles, cend);
   uint8_t* const kb = buf[kq];
   uint8_t* const vb = buf[kq] + kQuarterTiles * kTileBytes;
+  uint8_t* const qblk = qbuf[w];
 
-  // Q rows first, straight to registers: their latency then overlaps the
-  // issue of the tile fetches below (which waits while the memory pipeline
-  // is backed up).
+  // This wave's 32 query rows come by DMA like a K half-tile (rows >= N_q
+  // read as zeros through the resource's bound), then its quarter's tiles
+  // in the order they are used: K, K, V, V.  Each wave waits for one piece
+  // at a time (the DMA is invisible to the compiler's own counting, so the
+  // waits are explicit) and starts computing as soon as K of the first tile
+  // has landed.  Tiles past the quarter land as zeros with no traffic.
   const int qr = q0 + 32 * rb;  // this wave's rows
-  const int my_q = qr + (lane & 31), g = lane >> 5;
-  u32x4_t qraw[4];
-#pragma unroll
-  for (int s = 0; s < 4; ++s)
-    qraw[s] = my_q < seq ? *reinterpret_cast<const u32x4_t*>(hp.q + (long long)my_q * geom.q_sr +
-                                                            16 * s + 8 * g)
-                         : (u32x4_t){0u, 0u, 0u, 0u};
-  // This quarter's K and V tiles (this wave's kSegs segments of each);
-  // rows >= N_k read as zeros through the buffer bound.
-  if (t0 < t1) {
+  {
+    const int qrows = min(32, seq - qr);
+    const i32x4_t rq = buffer_rsrc(hp.q + (long long)(qrows > 0 ? qr : 0) * geom.q_sr,
+                                   qrows > 0 ? (qrows - 1) * (2 * geom.q_sr) + kRowBytes : 0);
+    const FetchOff<4> fq = fetch_offsets<4, false>(0, lane, 2 * geom.q_sr);
+    fetch_tile_z<4>(rq, qblk, 0, 1, 0, fq);
+  }
+  i32x4_t rk, rv;
+  kv_rsrc_rows(geom, bh, K, V, t1 * kBc, rk, rv);
+  const bool any = t0 < t1;
+  if (any) {
     const FetchOff<kSegs> fk = fetch_offsets<kSegs, false>(rb, lane, 2 * geom.k_sr);
     const FetchOff<kSegs> fv = fetch_offsets<kSegs, true>(rb, lane, 2 * geom.v_sr);
 #pragma unroll
-    for (int i = 0; i < kQuarterTiles; ++i) {
-      fetch_tile<kSegs>(hp.rk, kb + i * kTileBytes, t0 + i, t1 - 1, rb, fk);
-      fetch_tile<kSegs>(hp.rv, vb + i * kTileBytes, t0 + i, t1 - 1, rb, fv);
-    }
+    for (int i = 0; i < kQuarterTiles; ++i)
+      fetch_tile_z<kSegs>(rk, kb + i * kTileBytes, t0 + i, t1, rb, fk);
+#pragma unroll
+    for (int i = 0; i < kQuarterTiles; ++i)
+      fetch_tile_z<kSegs>(rv, vb + i * kTileBytes, t0 + i, t1, rb, fv);
   }
   RowsT rows;
   rows.place(lane, qr, seq, geom.seq_k, geom.coff, cr);
-  rows.set_q(qraw, cq);
   rows.reset();
+  // Outstanding fetches of this wave, oldest first: Q (4), then when `any`
+  // K(t0), K(t0+1), V(t0), V(t0+1) (kSegs each).
+  static_assert(kQuarterTiles == 2, "two tiles per wave");
+  constexpr int kT = kSegs;
+  if (any) {
+    asm volatile("s_waitcnt vmcnt(%0)" : : "n"(4 * kT) : "memory");
+  } else {
+    asm volatile("s_waitcnt vmcnt(0)" : : : "memory");
+  }
+  rows.set_q_lds(qblk, cq);
   FL_ST_MARK(1);
-  // This wave's own fetches have landed in LDS; with RB = 2 a barrier
-  // (taken by every wave) publishes the other half of each tile.
   if constexpr (RB > 1) {
+    // the other wave of each quarter fetched half of every tile: one
+    // barrier publishes them all (taken by every wave)
     asm volatile("s_waitcnt vmcnt(0)" : : : "memory");
     __syncthreads();
   }
-  if (t0 < t1) {
-    if constexpr (RB == 1) asm volatile("s_waitcnt vmcnt(0)" : : : "memory");
+  if (any) {
     FL_ST_MARK(2);
-    // Tile t0 sets the stabiliser to its exact row max, so its p are at most
-    // 1 and its checked softmax never moves m: tile t0+1's GEMM1 can go out
-    // before that softmax, against the same m.
-    static_assert(kQuarterTiles == 2, "two tiles per wave");
+    // Both tiles' scores against one stabiliser, the exact row max over
+    // them: every p is then at most 1 and the row sum at most 128, so the
+    // softmax needs no range check.  A row with no visible key gets m = 0
+    // and p = 0.
+    const bool two = t0 + 1 < t1;
     float16_t S0[2], S1[2];
     V8 P[2][2];
+    if constexpr (RB == 1) asm volatile("s_waitcnt vmcnt(%0)" : : "n"(3 * kT) : "memory");
     {
       V8 ka[2][4];
       rows.read_k(kb, ka);
       rows.gemm1(ka, S0);
     }
-    rows.mask(t0, S0);
-    rows.first_tile(S0);
-    const bool two = t0 + 1 < t1;
-    if (two) {
+    if constexpr (RB == 1) asm volatile("s_waitcnt vmcnt(%0)" : : "n"(2 * kT) : "memory");
+    {
       V8 ka[2][4];
       rows.read_k(kb + kTileBytes, ka);
       rows.gemm1(ka, S1);
     }
-    rows.softmax_checked(S0, P);
+    rows.mask(t0, S0);
+    if (two) rows.mask(t0 + 1, S1);
+    {
+      float mx = ninf();
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) mx = fmaxf(mx, S0[h][r]);
+      if (two) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) mx = fmaxf(mx, S1[h][r]);
+      }
+      mx = pair_max(mx);
+      mx = mx == ninf() ? 0.0f : mx;
+      RowsT::sub(S0, mx);
+      if (two) RowsT::sub(S1, mx);
+      rows.set_m(mx);
+    }
+    rows.l = rows.exponentiate(S0, P);
+    if constexpr (RB == 1) asm volatile("s_waitcnt vmcnt(%0)" : : "n"(kT) : "memory");
     {
       V8 va[2][4];
       rows.read_v(vb, va);
       rows.gemm2(va, P);
     }
     if (two) {
-      rows.mask(t0 + 1, S1);
-      rows.softmax_checked(S1, P);
+      rows.l += rows.exponentiate(S1, P);
+      if constexpr (RB == 1) asm volatile("s_waitcnt vmcnt(0)" : : : "memory");
       V8 va[2][4];
       rows.read_v(vb + kTileBytes, va);
       rows.gemm2(va, P);

@@ -87,10 +87,11 @@ fa2_fwd_slot_kernel(const T* Q, const T* __restrict__ K, const T* __restrict__ V
   // LDS reads of the first kAhead slots (K slots: 1, V slots: 2).
   constexpr int kTailReads = kAhead + kAhead / 2;
   constexpr int kRingBytes = kSlots * kTileBytes;
-  // Two work-groups share a CU when both rings fit its 160 KiB and the
-  // waves fit two per SIMD (<= 4 waves each).
+  constexpr int kQBytes = W * SPLIT * 32 * kRowBytes;  // each wave's 32 query rows
+  // Two work-groups share a CU when both rings and Q blocks fit its 160 KiB
+  // and the waves fit two per SIMD (<= 4 waves each).
   constexpr int kWgPerCu =
-      (W * SPLIT <= 4 && 2 * 2 * SPLIT * kRingBytes <= 160 * 1024) ? 2 : 1;
+      (W * SPLIT <= 4 && 2 * (2 * SPLIT * kRingBytes + kQBytes) <= 160 * 1024) ? 2 : 1;
   static_assert(kSegs * W == 8, "tile split");
   static_assert(FV >= 2 && FV <= 6, "fetch distance");
   static_assert(kAhead % 2 == 0 && kAhead < 16, "read-ahead");
@@ -98,6 +99,7 @@ fa2_fwd_slot_kernel(const T* Q, const T* __restrict__ K, const T* __restrict__ V
   static_assert(SPLIT == 1 || SPLIT * kRingBytes >= W * 34 * 64 * 4, "merge buffer");
   __shared__ __attribute__((aligned(16))) uint8_t kring[SPLIT * kRingBytes];
   __shared__ __attribute__((aligned(16))) uint8_t vring[SPLIT * kRingBytes];
+  __shared__ __attribute__((aligned(16))) uint8_t qbuf[kQBytes];
 
   FL_TL_STAMP(tl_entry);
   const int lane = threadIdx.x & 63;
@@ -136,9 +138,14 @@ fa2_fwd_slot_kernel(const T* Q, const T* __restrict__ K, const T* __restrict__ V
   if (q0 + 32 * rw >= seq) nw = 1;
   nw = max(nw, 1);
 
-  // Prologue fetch groups -FK .. -1: K tiles 0 .. FK-1 and V tiles
-  // 0 .. FV-1 of the range (iteration 0 has no GEMM2, so no tile -1),
-  // issued before the Q loads so the two latencies overlap.
+  // This wave's 32 query rows by DMA into its Q block (first, so they
+  // land first), then the prologue fetch groups -FK .. -1: K tiles
+  // 0 .. FK-1 and V tiles 0 .. FV-1 of the range (iteration 0 has no
+  // GEMM2, so no tile -1).  Q goes through LDS rather than straight to
+  // registers: the compiler cannot see these DMA operations, so a plain
+  // load of Q would wait for every one of them, one Q chunk at a time.
+  uint8_t* const qblk = qbuf + wave * 32 * kRowBytes;
+  fetch_q_block(hp.q, geom.q_sr, q0 + 32 * rw, seq, qblk, lane);
   static_for(std::make_integer_sequence<int, FK>{}, [&](auto i) __attribute__((always_inline)) {
     constexpr int G = decltype(i)::value - FK;
     fetch_tile_z<kSegs>(rk, rings.kslot(Ic<G + FK>{}), tbeg + G + FK, tzero, rw, fk);
@@ -146,18 +153,17 @@ fa2_fwd_slot_kernel(const T* Q, const T* __restrict__ K, const T* __restrict__ V
       fetch_tile_z<kSegs>(rv, rings.vslot(Ic<G + FV>{}), tbeg + G + FV, tzero, rw, fv);
   });
   RowsT rows;
-  rows.init(hp.q, geom.q_sr, lane, q0 + 32 * rw, seq, geom.seq_k, geom.coff, cq, cr);
+
+  // ---- first pass ----
+  FL_TL_STAMP(tl_first);
+  sync_ring_ahead<(FK - 1) * kDmaPerIter, 0>();  // Q, K(0)
+  rows.init_lds(qblk, lane, q0 + 32 * rw, seq, geom.seq_k, geom.coff, cq, cr);
   if constexpr (kMfmaSum) rows.init_msum(lane);
   if (SPLIT == 2 && stream == 0) rows.kv_lim = min(rows.kv_lim, tend * kBc);
-
   // Iterations j < jm need no mask on tiles tbeg + j and tbeg + j + 1.
   int tm = rows.kv_lim >> 6;
   if (CAUSAL) tm = min(tm, (rows.qd + 1) >> 6);
   const int jm = max(0, tm - tbeg - 1);
-
-  // ---- first pass ----
-  FL_TL_STAMP(tl_first);
-  sync_ring_ahead<(FK - 1) * kDmaPerIter, 0>();  // K(0)
   float16_t S[2];
   V8 P0[2][2], P1[2][2];
   {

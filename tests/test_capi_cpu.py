@@ -208,8 +208,14 @@ def test_dispatcher_choices():
     assert sel(batch=1, heads=1, seq_q=2048, causal=True) == SPLIT64
     assert sel(batch=3, heads=8, seq_q=1024) == W4         # 384 groups of 64 rows
     assert sel(batch=4, heads=4, seq_q=1536, causal=True) == W4
-    # causal: 128-row slot-scheduled groups balanced by dispatch order
-    assert sel(batch=2, heads=8, seq_q=4096, causal=True) == W4
+    # causal from N_k 4096 with 257-512 groups of 128 rows: the split in two
+    # rounds; beyond, and at N_k 2048, 128-row slot-scheduled groups
+    # balanced by dispatch order
+    assert sel(batch=2, heads=8, seq_q=4096, causal=True) == SPLIT
+    assert sel(batch=1, heads=8, seq_q=8192, causal=True) == SPLIT
+    assert sel(batch=4, heads=8, seq_q=4096, causal=True) == W4
+    assert sel(batch=2, heads=16, seq_q=2048, causal=True) == W4
+    assert sel(batch=2, heads=8, seq_q=4096) == W8
     assert sel(batch=1, heads=16, seq_q=16384, causal=True) == W4
     assert sel(batch=3, heads=8, seq_q=2048, causal=True) == W4   # 384 groups
     assert sel(batch=32, heads=32, seq_q=256, causal=True) == STRM   # streaming, any count
