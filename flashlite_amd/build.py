@@ -136,9 +136,13 @@ def build_extension(verbose: bool = False) -> str:
 
 
 def build(verbose: bool = False):
-    lib = build_library(verbose)
-    ext = build_extension(verbose)
-    build_diag_library(verbose)
+    # The diagnostic library compiles its own copy of the slot kernels:
+    # build it beside the product library instead of after it.
+    with ThreadPoolExecutor(max_workers=2) as pool:
+        diag = pool.submit(build_diag_library, verbose)
+        lib = build_library(verbose)
+        ext = build_extension(verbose)
+        diag.result()
     return lib, ext
 
 

@@ -122,9 +122,8 @@ int check_pointers(const fl_attn_params* p, fl::FwdArgs* a, const char* who, uin
 // CU take the key-range-split group of 8 waves (two per SIMD): causal
 // from N_k 2048 (64 groups up; fewer fall back to smaller groups), 7-11%
 // faster than the 4-wave groups, and from N_k 4096 up to two such rounds
-// (2-7% faster); non-causal from N_k 4096, or 2048 with
-// fewer than 128 groups, 5-10% faster (at N_k 2048 with 128-256 groups the
-// two measured within 3% either way).  With more than 128 groups of 256
+// (2-7% faster); non-causal from N_k 2048, 4-5% faster (B2 H8 N2048 22.8
+// against 23.9 us, B1 H8 N4096 39.5 against 41.1).  With more than 128 groups of 256
 // rows over N_k >= 2048, non-causal takes one 256-row group of 8 waves per
 // CU; otherwise
 // 128-row slot-scheduled groups of 4 waves, two per CU, which also serve
@@ -143,8 +142,7 @@ int select_fa2(const fl::FwdArgs& a) {
   // on 64-row groups (2 x 2 waves) in a single round.
   if (a.seq_k > 576 && wgs(64) <= cus) return fl::kCfgSplit2W2;
   const bool one_round = a.seq_k >= 2048 && wgs(128) <= cus;
-  if (one_round && (a.causal ? wgs(128) >= cus / 4 : a.seq_k >= 4096 || wgs(128) < cus / 2))
-    return fl::kCfgSplit2;
+  if (one_round && (!a.causal || wgs(128) >= cus / 4)) return fl::kCfgSplit2;
   // Causal over at least 4096 keys with up to two rounds of the split
   // groups: the split's halved walk beats the 4-wave groups' lone heavy
   // blocks (B2 H8 N4096 48.8 against 50.5 us, B1 H8 N8192 78.9 against

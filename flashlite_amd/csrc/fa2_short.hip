@@ -121,28 +121,37 @@ fa2_fwd_quarter_kernel(const T* Q, const T* __restrict__ K, const T* __restrict_
   i32x4_t rk, rv;
   kv_rsrc_rows(geom, bh, K, V, t1 * kBc, rk, rv);
   const bool any = t0 < t1;
-  if (any) {
-    const FetchOff<kSegs> fk = fetch_offsets<kSegs, false>(rb, lane, 2 * geom.k_sr);
-    const FetchOff<kSegs> fv = fetch_offsets<kSegs, true>(rb, lane, 2 * geom.v_sr);
+  const FetchOff<kSegs> fk = fetch_offsets<kSegs, false>(rb, lane, 2 * geom.k_sr);
+  const FetchOff<kSegs> fv = fetch_offsets<kSegs, true>(rb, lane, 2 * geom.v_sr);
+  auto fetch_k = [&]() __attribute__((always_inline)) {
 #pragma unroll
     for (int i = 0; i < kQuarterTiles; ++i)
       fetch_tile_z<kSegs>(rk, kb + i * kTileBytes, t0 + i, t1, rb, fk);
+  };
+  auto fetch_v = [&]() __attribute__((always_inline)) {
 #pragma unroll
     for (int i = 0; i < kQuarterTiles; ++i)
       fetch_tile_z<kSegs>(rv, vb + i * kTileBytes, t0 + i, t1, rb, fv);
-  }
+  };
+  // RB = 1: Q and K go out first and V after the first tile's scores: a
+  // DMA instruction waits at issue while the CU's memory pipeline is backed
+  // up, so issuing V before any compute would hold every wave behind all
+  // of its CU's loads.  Outstanding fetches of the wave, oldest first:
+  // Q (4), K(t0), K(t0+1), then V(t0), V(t0+1) (kSegs each).  RB = 2 issues
+  // everything at once: a barrier publishes the tiles either way.
+  static_assert(kQuarterTiles == 2, "two tiles per wave");
+  constexpr int kT = kSegs;
+  if (any) fetch_k();
+  if (RB > 1 && any) fetch_v();
   RowsT rows;
   rows.place(lane, qr, seq, geom.seq_k, geom.coff, cr);
   rows.reset();
-  // Outstanding fetches of this wave, oldest first: Q (4), then when `any`
-  // K(t0), K(t0+1), V(t0), V(t0+1) (kSegs each).
-  static_assert(kQuarterTiles == 2, "two tiles per wave");
-  constexpr int kT = kSegs;
-  if (any) {
+  if (any && RB == 1)
+    asm volatile("s_waitcnt vmcnt(%0)" : : "n"(2 * kT) : "memory");
+  else if (any)
     asm volatile("s_waitcnt vmcnt(%0)" : : "n"(4 * kT) : "memory");
-  } else {
+  else
     asm volatile("s_waitcnt vmcnt(0)" : : : "memory");
-  }
   rows.set_q_lds(qblk, cq);
   FL_ST_MARK(1);
   if constexpr (RB > 1) {
@@ -160,13 +169,16 @@ fa2_fwd_quarter_kernel(const T* Q, const T* __restrict__ K, const T* __restrict_
     const bool two = t0 + 1 < t1;
     float16_t S0[2], S1[2];
     V8 P[2][2];
-    if constexpr (RB == 1) asm volatile("s_waitcnt vmcnt(%0)" : : "n"(3 * kT) : "memory");
+    if constexpr (RB == 1) asm volatile("s_waitcnt vmcnt(%0)" : : "n"(kT) : "memory");
     {
       V8 ka[2][4];
       rows.read_k(kb, ka);
       rows.gemm1(ka, S0);
     }
-    if constexpr (RB == 1) asm volatile("s_waitcnt vmcnt(%0)" : : "n"(2 * kT) : "memory");
+    if constexpr (RB == 1) {
+      fetch_v();
+      asm volatile("s_waitcnt vmcnt(%0)" : : "n"(2 * kT) : "memory");
+    }
     {
       V8 ka[2][4];
       rows.read_k(kb + kTileBytes, ka);
@@ -215,7 +227,9 @@ fa2_fwd_quarter_kernel(const T* Q, const T* __restrict__ K, const T* __restrict_
   // quarter's buffer.  A range with no visible key holds l = 0 and is
   // skipped by the merge.
   float4* const part = reinterpret_cast<float4*>(buf[kq]) + rb * (9 * 64);
-  asm volatile("s_waitcnt lgkmcnt(0)" : : : "memory");  // own LDS reads done
+  // own LDS reads done, and every fetch landed (a one-tile quarter's zero
+  // tiles too: nothing may still write this LDS once the group ends)
+  asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" : : : "memory");
   if constexpr (RB > 1) __syncthreads();  // and the other row block's
   if (kq != 0) rows.save_partial4(part, lane);
   __syncthreads();

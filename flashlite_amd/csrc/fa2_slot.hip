@@ -144,19 +144,25 @@ fa2_fwd_slot_kernel(const T* Q, const T* __restrict__ K, const T* __restrict__ V
   // GEMM2, so no tile -1).  Q goes through LDS rather than straight to
   // registers: the compiler cannot see these DMA operations, so a plain
   // load of Q would wait for every one of them, one Q chunk at a time.
+  // Groups -FK and -FK+1 go out before the first pass, the rest after its
+  // GEMM1: a DMA instruction waits at issue while the CU's memory pipeline
+  // is backed up, so the first pass would otherwise wait behind all of
+  // them.  (The loop's waits count only the newest FV - 1 groups.)
   uint8_t* const qblk = qbuf + wave * 32 * kRowBytes;
   fetch_q_block(hp.q, geom.q_sr, q0 + 32 * rw, seq, qblk, lane);
-  static_for(std::make_integer_sequence<int, FK>{}, [&](auto i) __attribute__((always_inline)) {
+  auto prologue_group = [&](auto i) __attribute__((always_inline)) {
     constexpr int G = decltype(i)::value - FK;
     fetch_tile_z<kSegs>(rk, rings.kslot(Ic<G + FK>{}), tbeg + G + FK, tzero, rw, fk);
     if constexpr (G + FV >= 0)
       fetch_tile_z<kSegs>(rv, rings.vslot(Ic<G + FV>{}), tbeg + G + FV, tzero, rw, fv);
-  });
+  };
+  prologue_group(Ic<0>{});
+  prologue_group(Ic<1>{});
   RowsT rows;
 
   // ---- first pass ----
   FL_TL_STAMP(tl_first);
-  sync_ring_ahead<(FK - 1) * kDmaPerIter, 0>();  // Q, K(0)
+  sync_ring_ahead<kDmaPerIter, 0>();  // Q, K(0)
   rows.init_lds(qblk, lane, q0 + 32 * rw, seq, geom.seq_k, geom.coff, cq, cr);
   if constexpr (kMfmaSum) rows.init_msum(lane);
   if (SPLIT == 2 && stream == 0) rows.kv_lim = min(rows.kv_lim, tend * kBc);
@@ -172,6 +178,9 @@ fa2_fwd_slot_kernel(const T* Q, const T* __restrict__ K, const T* __restrict__ V
     rows.read_k(rings.kslot(Ic<0>{}), ka);
     rows.gemm1(ka, S);
   }
+  static_for(std::make_integer_sequence<int, FK - 2>{}, [&](auto i) __attribute__((always_inline)) {
+    prologue_group(Ic<decltype(i)::value + 2>{});
+  });
   rows.mask(tbeg, S);
   rows.first_tile(S);
   sync_ring_ahead<(FV - 1) * kDmaPerIter, 0>();  // K(1), V(0)
