@@ -143,11 +143,13 @@ int select_fa2(const fl::FwdArgs& a) {
   if (a.seq_k > 576 && wgs(64) <= cus) return fl::kCfgSplit2W2;
   const bool one_round = a.seq_k >= 2048 && wgs(128) <= cus;
   if (one_round && (!a.causal || wgs(128) >= cus / 4)) return fl::kCfgSplit2;
-  // Causal over at least 4096 keys with up to two rounds of the split
-  // groups: the split's halved walk beats the 4-wave groups' lone heavy
-  // blocks (B2 H8 N4096 48.8 against 50.5 us, B1 H8 N8192 78.9 against
-  // 84.3); from 1024 groups, or at N_k 2048, the 4-wave groups win.
-  if (a.causal && a.seq_k >= 4096 && wgs(128) <= 2 * cus) return fl::kCfgSplit2;
+  // Causal over at least 4096 keys with more than one 128-row block but at
+  // most one block pair per CU: the block pairs (one round of equal
+  // work-groups, each key range halved), 2-10% faster than the 4-wave
+  // groups and the one-block split (B2 H8 N4096 48.3 against 50.1 and 53.7
+  // us, B1 H16 N4096 43.2 against 45.5 and 45.0, B1 H8 N8192 77.3 against
+  // 85.2 and 79.6); past one pair per CU the 4-wave groups win.
+  if (a.causal && a.seq_k >= 4096 && wgs(128) <= 2 * cus) return fl::kCfgPair;
   if (!a.causal && a.seq_k >= 2048 && wgs(256) > cus / 2) return fl::kSlotW8Config;
   if (wgs(128) >= cus / 4) return fl::kSlotW4Config;
   if (wgs(64) >= cus / 4) return fl::kCfgW2;
@@ -343,7 +345,7 @@ int select_any(const fl::FwdArgs& a) {
   if (!narrow_configs(a)) return select_fa2(a);
   if (a.head_dim == 64) {
     const int c = select_fa2(a);
-    if (c == fl::kCfgSplit2 || c == fl::kCfgSplit2W2 || c == fl::kStreamConfig ||
+    if (c == fl::kCfgSplit2 || c == fl::kCfgSplit2W2 || c == fl::kCfgPair || c == fl::kStreamConfig ||
         c == fl::kQuarterConfig)
       return c;
   }
@@ -366,7 +368,7 @@ int fwd_ex(const fl_attn_params_ex* p, int32_t config, void* stream, int dtype, 
                 "%s: config %d is not built for %s at head_dim %d (use -1, %d or %d%s)", who,
                 (int)config, dtype == fl::kDtypeBF16 ? "bf16" : "fp16", a.head_dim,
                 fl::kSlotW8Config, fl::kSlotW4Config,
-                a.head_dim == 64 ? ", 2, 5, 6 or 7" : "");
+                a.head_dim == 64 ? ", 2, 5, 6, 7 or 8" : "");
   if (config == fl::kStreamConfig && !fl::stream_config_fits(a))
     return fail(FL_ERR_BAD_CONFIG, "%s: config %d needs N_k <= %d and row strides below 2^22 "
                 "(got N_k %d)", who, (int)config, fl::kStreamMaxKeys, a.seq_k);

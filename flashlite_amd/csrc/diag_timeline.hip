@@ -46,9 +46,11 @@ __device__ unsigned long long* g_fl_timeline;
 // The instrumented copies get their own launcher names.
 #define launch_slot diag_timeline_launch_slot
 #define launch_slot_split diag_timeline_launch_slot_split
+#define launch_slot_pair diag_timeline_launch_slot_pair
 #include "fa2_slot.hip"
 #undef launch_slot
 #undef launch_slot_split
+#undef launch_slot_pair
 
 // The streaming kernel's marks: up to 64 s_memrealtime values per wave, kept
 // in two registers by lane (lane j holds mark j: no memory operation, so the
@@ -99,7 +101,8 @@ extern "C" {
 int fl_diag_slot_timeline(int mode, int causal, const void* q, const void* k, const void* v,
                           void* o, int B, int H, int N, void* out, long long out_entries,
                           void* stream) {
-  if ((mode != 8 && mode != 4 && mode != 2) || B < 1 || H < 1 || N < 1 || out == nullptr)
+  if ((mode != 8 && mode != 4 && mode != 2 && mode != 9) || B < 1 || H < 1 || N < 1 ||
+      out == nullptr)
     return (int)hipErrorInvalidValue;
   const long long rows = mode == 8 ? 256 : 128;
   const long long waves = mode == 4 ? 4 : 8;
@@ -126,8 +129,9 @@ int fl_diag_slot_timeline(int mode, int causal, const void* q, const void* k, co
   a.q_sh = a.k_sh = a.v_sh = a.o_sh = (int64_t)N * 64;
   a.q_sb = a.k_sb = a.v_sb = a.o_sb = (int64_t)H * N * 64;
   const auto st = static_cast<hipStream_t>(stream);
-  e = mode == 2 ? fl::diag_timeline_launch_slot_split(a, 4, st)
-                : fl::diag_timeline_launch_slot(a, mode, st);
+  e = mode == 2   ? fl::diag_timeline_launch_slot_split(a, 4, st)
+      : mode == 9 ? fl::diag_timeline_launch_slot_pair(a, st)
+                  : fl::diag_timeline_launch_slot(a, mode, st);
   return (int)e;
 }
 

@@ -302,6 +302,19 @@ __device__ __forceinline__ void wg_coords(int nqb, int xcds, int cpx, int& bh, i
   if (CAUSAL) qb = nqb - 1 - qb;
 }
 
+// Work-group -> (batch*head, block pair p) of the pair schedule: pairs
+// p = 0 .. ceil(nqb/2) - 1 of a head, dealt so that a head's pairs run on
+// one XCD (shared K/V in its L2) when the work-groups divide evenly.
+__device__ __forceinline__ void pair_coords(int nqb, int xcds, int& bh, int& p) {
+  const int np = (nqb + 1) / 2;
+  const int total = gridDim.x;
+  const int i = blockIdx.x;
+  const int per = total / xcds;
+  const int lin = per * xcds == total ? (i % xcds) * per + i / xcds : i;
+  bh = lin / np;
+  p = lin - bh * np;
+}
+
 // Asynchronous fetch of tile t (clamped to the last tile the work-group
 // needs) straight into LDS with buffer_load_dwordx4 ... lds: each wave moves
 // `kSegs` 1 KiB segments (8 rows); lane i of a segment lands at byte 16*i,

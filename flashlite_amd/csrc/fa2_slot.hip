@@ -58,7 +58,16 @@ namespace {
 // This halves the longest key walk: a causal work-group's time follows half
 // its tiles, and heaviest-first dispatch of one work-group per CU then
 // balances the CUs.
-template <int W, int FV, bool CAUSAL, bool SCALED, class T = _Float16, int SPLIT = 1>
+//
+// PAIR (SPLIT = 2, configuration br128_bc64_w4x2_pair): a work-group walks
+// two 128-row blocks of a head one after the other, p and nqb-1-p (the
+// heavier first), each with its key range split between the streams.
+// Under the causal mask the two need about the same tiles as any other pair
+// (2 nqb + 2 at N_q = N_k), so one round of work-groups, one per CU,
+// carries equal work: no lone heavy block at the end (the 4-wave groups'
+// tail) and no second round of start-ups (the one-block split's).
+template <int W, int FV, bool CAUSAL, bool SCALED, class T = _Float16, int SPLIT = 1,
+          bool PAIR = false>
 // Register budget for 2 waves per SIMD (<= 256 VGPRs).  W = 2 with SPLIT
 // holds 128 KiB of LDS, so one work-group (one wave per SIMD) per CU: the
 // compiler reports that target as missed; that code is the measured one.
@@ -97,6 +106,7 @@ fa2_fwd_slot_kernel(const T* Q, const T* __restrict__ K, const T* __restrict__ V
   static_assert(kAhead % 2 == 0 && kAhead < 16, "read-ahead");
   static_assert(SPLIT == 1 || SPLIT == 2, "key-range split");
   static_assert(SPLIT == 1 || SPLIT * kRingBytes >= W * 34 * 64 * 4, "merge buffer");
+  static_assert(!PAIR || SPLIT == 2, "block pairs: key-range split groups");
   __shared__ __attribute__((aligned(16))) uint8_t kring[SPLIT * kRingBytes];
   __shared__ __attribute__((aligned(16))) uint8_t vring[SPLIT * kRingBytes];
   __shared__ __attribute__((aligned(16))) uint8_t qbuf[kQBytes];
@@ -106,14 +116,23 @@ fa2_fwd_slot_kernel(const T* Q, const T* __restrict__ K, const T* __restrict__ V
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int stream = wave / W;       // key-range half (0 unless SPLIT)
   const int rw = wave - stream * W;  // 32-row block within the work-group
-  int bh, qb;
-  wg_coords<CAUSAL, kWgPerCu>(nqb, geom.xcds, geom.cus_per_xcd, bh, qb);
+  int bh, qb, qb2 = 0, nblk = 1;
+  if constexpr (PAIR) {
+    int pr;
+    pair_coords(nqb, geom.xcds, bh, pr);
+    qb = nqb - 1 - pr;
+    qb2 = pr;
+    nblk = qb2 < qb ? 2 : 1;  // the middle block of an odd count walks alone
+  } else {
+    wg_coords<CAUSAL, kWgPerCu>(nqb, geom.xcds, geom.cus_per_xcd, bh, qb);
+  }
   const HeadPtrs<T> hp = head_ptrs(geom, bh, Q, K, V, O);
   const FetchOff<kSegs> fk = fetch_offsets<kSegs, false>(rw, lane, 2 * geom.k_sr);
   const FetchOff<kSegs> fv = fetch_offsets<kSegs, true>(rw, lane, 2 * geom.v_sr);
   const int seq = geom.seq_q;
-  const int q0 = qb * kBr;
   const StreamRings<kSlots> rings = {kring + stream * kRingBytes, vring + stream * kRingBytes};
+  for (int bi = 0; bi < nblk; ++bi) {
+  const int q0 = (bi == 0 ? qb : qb2) * kBr;
 
   int ntiles = max(1, (geom.seq_k + kBc - 1) / kBc);
   if (CAUSAL) ntiles = min(ntiles, causal_tiles(min(q0 + kBr, seq), geom.coff));
@@ -384,28 +403,29 @@ fa2_fwd_slot_kernel(const T* Q, const T* __restrict__ K, const T* __restrict__ V
     float* xchg = reinterpret_cast<float*>(kring) + rw * (34 * 64);
     if (stream == 1) rows.save_partial(xchg, lane);
     __syncthreads();
-    if (stream == 1) {
-      FL_TL_STAMP(tl_store);
-      FL_TL_RECORD(W * SPLIT, wave, lane, t0 + 1, tl_entry, tl_first, tl_loop, tl_loop_end,
-                   tl_store);
-      return;
-    }
-    rows.merge_partial(xchg, lane);
+    if (stream == 0) rows.merge_partial(xchg, lane);
   }
-  rows.launder();
   FL_TL_STAMP(tl_store);
-  rows.store(hp.o, geom.o_sr, hp.lse);
+  if (SPLIT == 1 || stream == 0) {
+    rows.launder();
+    rows.store(hp.o, geom.o_sr, hp.lse);
+  }
   FL_TL_RECORD(W * SPLIT, wave, lane, t0 + 1, tl_entry, tl_first, tl_loop, tl_loop_end, tl_store);
+  // PAIR: every wave past its reads of the rings (the merge's included)
+  // before the next block's prologue fetches into them.
+  if (PAIR && bi + 1 < nblk) __syncthreads();
+  }  // blocks
 }
 
-template <int W, int FV, class T = _Float16, int SPLIT = 1>
+template <int W, int FV, class T = _Float16, int SPLIT = 1, bool PAIR = false>
 struct SlotLaunch {
   template <bool C, bool S>
   struct L {
     static hipError_t run(const FwdArgs& a, const Geom& g, dim3 grid, int nqb, float cq, float cr,
                           hipStream_t st) {
-      hipLaunchKernelGGL((fa2_fwd_slot_kernel<W, FV, C, S, T, SPLIT>), grid, dim3(64 * W * SPLIT),
-                         0, st,
+      if constexpr (PAIR) grid = dim3((unsigned)(a.batch_heads * ((nqb + 1) / 2)));
+      hipLaunchKernelGGL((fa2_fwd_slot_kernel<W, FV, C, S, T, SPLIT, PAIR>), grid,
+                         dim3(64 * W * SPLIT), 0, st,
                          static_cast<const T*>(a.q), static_cast<const T*>(a.k),
                          static_cast<const T*>(a.v), static_cast<T*>(a.o), g, nqb, cq, cr);
       return hipSuccess;
@@ -435,6 +455,15 @@ hipError_t launch_slot(const FwdArgs& a, int waves, hipStream_t stream) {
 // dispatcher sends to them; their walks are short, so the shorter prologue
 // matters more than the deeper pipeline.
 constexpr int kSplitFv = 2;
+
+// fp16 or bf16 by a.dtype: groups of 2 x 4 waves walking a pair of 128-row
+// blocks of a head, p and nqb-1-p, each with its key range halved between
+// the streams (grid B*H*ceil(nqb/2)).
+hipError_t launch_slot_pair(const FwdArgs& a, hipStream_t stream) {
+  const bool bf = a.dtype == kDtypeBF16;
+  return bf ? dispatch<SlotLaunch<4, kSplitFv, __bf16, 2, true>::L>(a, stream, 128)
+            : dispatch<SlotLaunch<4, kSplitFv, _Float16, 2, true>::L>(a, stream, 128);
+}
 
 // fp16 or bf16 by a.dtype: groups of 2 x `waves` waves (4: 128 rows, 2: 64
 // rows), the key range halved between them.

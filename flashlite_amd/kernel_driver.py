@@ -25,8 +25,9 @@ buffer before every launch, evicting the inputs from the L2 caches and the
 256 MiB Infinity Cache (M > 256), and times each launch alone with its own
 HIP event pair; the mean over ``--iters`` launches is printed.
 
-``--timeline MODE`` (MODE 8, 4 or 2: br256_bc64_w8_slot, br128_bc64_w4_slot
-or br128_bc64_w4x2_slot; fp16 D = 64 workloads or ``--shape``, ``--causal``)
+``--timeline MODE`` (MODE 8, 4, 2 or 9: br256_bc64_w8_slot, br128_bc64_w4_slot,
+br128_bc64_w4x2_slot or br128_bc64_w4x2_pair; fp16 D = 64 workloads or
+``--shape``, ``--causal``)
 runs the diagnostic build of the slot kernels whose waves stamp their entry,
 loop start and end, and exit (``fl_diag_slot_timeline``), launched
 ``--iters`` times back to back, and summarises the last launch: launch span,
@@ -311,7 +312,8 @@ def _timeline(args, torch):
     hw = d[:, 7] & 0xFFFFFFFF
     loop = t[:, 3] - t[:, 2]
     clk = d[:, 6] / np.maximum(loop, 1e-9) / 1e3  # GHz
-    names = {8: "br256_bc64_w8_slot", 4: "br128_bc64_w4_slot", 2: "br128_bc64_w4x2_slot"}
+    names = {8: "br256_bc64_w8_slot", 4: "br128_bc64_w4_slot", 2: "br128_bc64_w4x2_slot",
+             9: "br128_bc64_w4x2_pair"}
     print(f"timeline {w.name} causal={args.causal} {names[mode]}: {us:.2f} us/launch over "
           f"{args.iters} launches (events); last launch: {len(d)} waves, span "
           f"{t[:, 5].max():.2f} us (first entry to last exit), start skew {t[:, 0].max():.2f} us",

@@ -29,12 +29,13 @@ def test_library_loads_and_exports_header_symbols():
 
 
 def test_config_table():
-    assert capi.num_configs() == 8
-    names = [capi.config_name(i) for i in range(8)]
+    assert capi.num_configs() == 9
+    names = [capi.config_name(i) for i in range(9)]
+    # ids are stable: a new configuration is appended, never inserted
     assert names == ["br32_bc64_w1", "br64_bc64_w2", "br128_bc64_w4x2_slot", "br256_bc64_w8_slot",
                      "br128_bc64_w4_slot", "br256_kv256_w8_stream", "br32_kv512_w4_quarters",
-                     "br64_bc64_w2x2_slot"]
-    assert capi.config_name(8) is None and capi.config_name(-1) is None
+                     "br64_bc64_w2x2_slot", "br128_bc64_w4x2_pair"]
+    assert capi.config_name(9) is None and capi.config_name(-1) is None
     assert capi.config_id("br256_bc64_w8_slot") == 3
 
 
@@ -173,6 +174,7 @@ def test_dispatcher_choices():
     W8, W4, SPLIT, STRM = ("br256_bc64_w8_slot", "br128_bc64_w4_slot", "br128_bc64_w4x2_slot",
                            "br256_kv256_w8_stream")
     W1, W2, QTR = "br32_bc64_w1", "br64_bc64_w2", "br32_kv512_w4_quarters"
+    PAIR = "br128_bc64_w4x2_pair"
     SPLIT64 = "br64_bc64_w2x2_slot"
     # non-causal: 8-wave 256-row slot-scheduled groups when there are more
     # than 128 and the key range is long
@@ -187,7 +189,7 @@ def test_dispatcher_choices():
     assert sel(batch=1, heads=1, seq_q=1000, seq_k=256) == STRM
     # at most one 128-row group per CU over long key ranges: split key range
     # (non-causal from N_k 4096, or with fewer than 128 groups)
-    assert sel(batch=2, heads=8, seq_q=2048) == W4         # 256 groups of 128 rows
+    assert sel(batch=2, heads=8, seq_q=2048) == SPLIT      # 256 groups of 128 rows
     assert sel(batch=2, heads=8, seq_q=2048, causal=True) == SPLIT
     assert sel(batch=1, heads=8, seq_q=4096) == SPLIT
     assert sel(batch=1, heads=1, seq_q=2048) == SPLIT64    # 32 groups of 64 rows
@@ -211,8 +213,8 @@ def test_dispatcher_choices():
     # causal from N_k 4096 with 257-512 groups of 128 rows: the split in two
     # rounds; beyond, and at N_k 2048, 128-row slot-scheduled groups
     # balanced by dispatch order
-    assert sel(batch=2, heads=8, seq_q=4096, causal=True) == SPLIT
-    assert sel(batch=1, heads=8, seq_q=8192, causal=True) == SPLIT
+    assert sel(batch=2, heads=8, seq_q=4096, causal=True) == PAIR
+    assert sel(batch=1, heads=8, seq_q=8192, causal=True) == PAIR
     assert sel(batch=4, heads=8, seq_q=4096, causal=True) == W4
     assert sel(batch=2, heads=16, seq_q=2048, causal=True) == W4
     assert sel(batch=2, heads=8, seq_q=4096) == W8

@@ -12,15 +12,16 @@ import pytest
 
 from flashlite_amd import capi
 from flashlite_amd.workloads import WORKLOADS, make_qkv, workload_inputs
-from gpu_util import (SLOT_W4_CFG, SLOT_W8_CFG, SPLIT2_CFG, SPLIT2W2_CFG, assert_close_oracle,
+from gpu_util import (PAIR_CFG, SLOT_W4_CFG, SLOT_W8_CFG, SPLIT2_CFG, SPLIT2W2_CFG,
+                      assert_close_oracle,
                       config_fits, redo_expected, run_capi, to_dev)
 from oracle import attention_fp32, error_stats
 
 pytestmark = pytest.mark.gpu
 
 GOLDEN = os.path.join(os.path.dirname(__file__), "golden")
-NCFG = 8  # tile configurations exported by the library
-SPLIT_CFGS = [SPLIT2_CFG, SPLIT2W2_CFG]  # the key-range-split configurations
+NCFG = 9  # tile configurations exported by the library
+SPLIT_CFGS = [SPLIT2_CFG, SPLIT2W2_CFG, PAIR_CFG]  # the key-range-split configurations
 
 
 def test_num_configs():
@@ -28,7 +29,7 @@ def test_num_configs():
     assert [capi.config_name(i) for i in range(NCFG)] == [
         "br32_bc64_w1", "br64_bc64_w2", "br128_bc64_w4x2_slot", "br256_bc64_w8_slot",
         "br128_bc64_w4_slot", "br256_kv256_w8_stream", "br32_kv512_w4_quarters",
-        "br64_bc64_w2x2_slot"]
+        "br64_bc64_w2x2_slot", "br128_bc64_w4x2_pair"]
 
 
 @pytest.mark.parametrize("config", list(range(NCFG)))
@@ -250,3 +251,24 @@ def test_naive_matches_flash2(cuda):
         a = run_capi(q, k, v, 0.125, causal, cuda, naive=True)
         b = run_capi(q, k, v, 0.125, causal, cuda)
         assert error_stats(a, b)[0] < 2e-3
+
+
+# The block-pair schedule (a work-group walks blocks p and nqb-1-p): even and
+# odd block counts (an odd count leaves the middle block alone), ragged
+# last blocks, N_k != N_q both ways (bottom-right diagonal), every row.
+PAIR_SHAPES = [(2, 8, 4096, 4096), (1, 3, 640, 640), (2, 2, 1000, 1000), (1, 4, 384, 1500),
+               (1, 2, 1500, 384), (3, 5, 129, 129)]
+
+
+@pytest.mark.parametrize("b,h,nq,nk", PAIR_SHAPES)
+@pytest.mark.parametrize("causal", [False, True])
+def test_pair_schedule(cuda, b, h, nq, nk, causal):
+    rs = np.random.RandomState(b * 7919 + h * 104729 + nq * 31 + nk)
+    mk = lambda n: rs.standard_normal((b, h, n, 64)).astype(np.float32).astype(np.float16)  # noqa: E731
+    q, k, v = mk(nq), mk(nk), mk(nk)
+    print(f"pair schedule B{b} H{h} Nq{nq} Nk{nk} causal={causal}", flush=True)
+    out = run_capi(q, k, v, 0.125, causal, cuda, config=PAIR_CFG)
+    assert_close_oracle(out, q, k, v, 0.125, causal)
+    # peaked scores send blocks to the checked pass in both blocks of a pair
+    out = run_capi(q, k, v, 3.0, causal, cuda, config=PAIR_CFG)
+    assert_close_oracle(out, q, k, v, 3.0, causal, peaked=True)
