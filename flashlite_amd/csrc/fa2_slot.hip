@@ -105,7 +105,7 @@ fa2_fwd_slot_kernel(const T* Q, const T* __restrict__ K, const T* __restrict__ V
   static_assert(FV >= 2 && FV <= 6, "fetch distance");
   static_assert(kAhead % 2 == 0 && kAhead < 16, "read-ahead");
   static_assert(SPLIT == 1 || SPLIT == 2, "key-range split");
-  static_assert(SPLIT == 1 || SPLIT * kRingBytes >= W * 34 * 64 * 4, "merge buffer");
+  static_assert(SPLIT == 1 || SPLIT * kRingBytes - 16 >= W * 34 * 64 * 4, "merge buffer");
   static_assert(!PAIR || SPLIT == 2, "block pairs: key-range split groups");
   __shared__ __attribute__((aligned(16))) uint8_t kring[SPLIT * kRingBytes];
   __shared__ __attribute__((aligned(16))) uint8_t vring[SPLIT * kRingBytes];
@@ -131,22 +131,38 @@ fa2_fwd_slot_kernel(const T* Q, const T* __restrict__ K, const T* __restrict__ V
   const FetchOff<kSegs> fv = fetch_offsets<kSegs, true>(rw, lane, 2 * geom.v_sr);
   const int seq = geom.seq_q;
   const StreamRings<kSlots> rings = {kring + stream * kRingBytes, vring + stream * kRingBytes};
-  for (int bi = 0; bi < nblk; ++bi) {
-  const int q0 = (bi == 0 ? qb : qb2) * kBr;
-
-  int ntiles = max(1, (geom.seq_k + kBc - 1) / kBc);
-  if (CAUSAL) ntiles = min(ntiles, causal_tiles(min(q0 + kBr, seq), geom.coff));
-  // This stream's key tiles [tbeg, tend); iterations 0 .. t0 on tile tbeg + j
-  // (the last one only drains GEMM2; with SPLIT the shorter stream's last
-  // tile lies past the range and is masked).
-  const int t0 = SPLIT == 2 ? (ntiles + 1) / 2 : ntiles;
-  const int tbeg = stream == 0 ? 0 : t0;
-  const int tend = stream == 0 ? t0 : ntiles;
+  // The walk of block bi: its first query row, and this stream's key tiles
+  // [tbeg, tend); iterations 0 .. t0 on tile tbeg + j (the last one only
+  // drains GEMM2; with SPLIT the shorter stream's last tile lies past the
+  // range and is masked).  K and V end with the stream's range: fetches
+  // past it (the pipeline's look-ahead near the end of the walk) land as
+  // zeros with no traffic.
+  struct Walk {
+    int q0, t0, tbeg, tend;
+    i32x4_t rk, rv;
+  };
+  auto walk_of = [&](int bi) __attribute__((always_inline)) {
+    Walk w;
+    w.q0 = (bi == 0 ? qb : qb2) * kBr;
+    int ntiles = max(1, (geom.seq_k + kBc - 1) / kBc);
+    if (CAUSAL) ntiles = min(ntiles, causal_tiles(min(w.q0 + kBr, seq), geom.coff));
+    w.t0 = SPLIT == 2 ? (ntiles + 1) / 2 : ntiles;
+    w.tbeg = stream == 0 ? 0 : w.t0;
+    w.tend = stream == 0 ? w.t0 : ntiles;
+    kv_rsrc_rows(geom, bh, K, V, w.tend * kBc, w.rk, w.rv);
+    return w;
+  };
+  uint8_t* const qblk = qbuf + wave * 32 * kRowBytes;
+  // PAIR: the next block's Q and first two K tiles, fetched during this
+  // block's merge and store.
+  bool prefetched = false;
+  // One block's walk (inlined once, or twice for a pair: a loop around the
+  // body pushes the register allocator into spills).
+  auto run_block = [&](const int bi) __attribute__((always_inline)) {
+  const Walk wk = walk_of(bi);
+  const int q0 = wk.q0, t0 = wk.t0, tbeg = wk.tbeg, tend = wk.tend;
+  const i32x4_t rk = wk.rk, rv = wk.rv;
   const int last = max(tend - 1, tbeg);  // fetch clamp of the checked pass
-  // K and V end with this stream's range: fetches past it (the pipeline's
-  // look-ahead near the end of the walk) land as zeros with no traffic.
-  i32x4_t rk, rv;
-  kv_rsrc_rows(geom, bh, K, V, tend * kBc, rk, rv);
   const int tzero = tend;
   // Tiles of the range this wave's rows need (through their causal
   // diagonal; none for a wave wholly past the last query row), at least
@@ -167,16 +183,21 @@ fa2_fwd_slot_kernel(const T* Q, const T* __restrict__ K, const T* __restrict__ V
   // GEMM1: a DMA instruction waits at issue while the CU's memory pipeline
   // is backed up, so the first pass would otherwise wait behind all of
   // them.  (The loop's waits count only the newest FV - 1 groups.)
-  uint8_t* const qblk = qbuf + wave * 32 * kRowBytes;
-  fetch_q_block(hp.q, geom.q_sr, q0 + 32 * rw, seq, qblk, lane);
   auto prologue_group = [&](auto i) __attribute__((always_inline)) {
     constexpr int G = decltype(i)::value - FK;
     fetch_tile_z<kSegs>(rk, rings.kslot(Ic<G + FK>{}), tbeg + G + FK, tzero, rw, fk);
     if constexpr (G + FV >= 0)
       fetch_tile_z<kSegs>(rv, rings.vslot(Ic<G + FV>{}), tbeg + G + FV, tzero, rw, fv);
   };
-  prologue_group(Ic<0>{});
-  prologue_group(Ic<1>{});
+  if (!PAIR || !prefetched) {
+    fetch_q_block(hp.q, geom.q_sr, q0 + 32 * rw, seq, qblk, lane);
+    prologue_group(Ic<0>{});
+    prologue_group(Ic<1>{});
+  } else {
+    // Q, K(0) and K(1) came during the previous block: V(0) completes group
+    // -FK+1, so the waits below count the same fetches
+    fetch_tile_z<kSegs>(rv, rings.vslot(Ic<0>{}), tbeg, tzero, rw, fv);
+  }
   RowsT rows;
 
   // ---- first pass ----
@@ -358,13 +379,14 @@ fa2_fwd_slot_kernel(const T* Q, const T* __restrict__ K, const T* __restrict__ V
   }
 
   // ---- checked pass, when any wave saw a tile sum out of range ----
-  // The work-group's flag lives in stream 0's K ring slot 1, which the
-  // checked pass never refills (the rings are idle here: every wave has
-  // drained its fetches and reads before the first barrier).  No extra
-  // LDS, so two 64 KiB work-groups still fit one CU.  Both streams read the
-  // one flag, so every wave takes the same barriers.
+  // The work-group's flag lives in the last 16 bytes of the V rings, which
+  // neither the checked pass (slot 0) nor the streams' exchange (the first
+  // 35 KiB) touches (the rings are idle here: every wave has drained its
+  // fetches and reads before the first barrier).  No extra LDS, so two
+  // 4-wave work-groups still fit one CU.  Both streams read the one flag,
+  // so every wave takes the same barriers.
   __builtin_amdgcn_s_waitcnt(0);
-  int* redo = reinterpret_cast<int*>(kring + kTileBytes);
+  int* redo = reinterpret_cast<int*>(vring + SPLIT * kRingBytes - 16);
   __syncthreads();
   if (threadIdx.x == 0) *redo = 0;
   __syncthreads();
@@ -396,11 +418,23 @@ fa2_fwd_slot_kernel(const T* Q, const T* __restrict__ K, const T* __restrict__ V
       sync_ring_ahead<0, 0>();  // every wave's reads done before the next fetch
     }
   }
+  if (PAIR && bi + 1 < nblk) {
+    // Every wave is past its reads of the rings and of its Q block (the
+    // flag's barriers, or the checked pass's last one): the next block's Q
+    // and first two K tiles go out now, to land during the merge and store.
+    const Walk nx = walk_of(bi + 1);
+    fetch_q_block(hp.q, geom.q_sr, nx.q0 + 32 * rw, seq, qblk, lane);
+    fetch_tile_z<kSegs>(nx.rk, rings.kslot(Ic<0>{}), nx.tbeg, nx.tend, rw, fk);
+    fetch_tile_z<kSegs>(nx.rk, rings.kslot(Ic<1>{}), nx.tbeg + 1, nx.tend, rw, fk);
+    prefetched = true;
+  }
   if constexpr (SPLIT == 2) {
-    // Stream 1 hands its O, m, l to stream 0 through the (idle) rings.
-    __builtin_amdgcn_s_waitcnt(0);
+    // Stream 1 hands its O, m, l to stream 0 through the (idle) V rings.
+    // (Only LDS needs to settle: the fetches still in flight, the next
+    // block's, write the K rings and Q blocks.)
+    asm volatile("s_waitcnt lgkmcnt(0)" : : : "memory");
     __syncthreads();
-    float* xchg = reinterpret_cast<float*>(kring) + rw * (34 * 64);
+    float* xchg = reinterpret_cast<float*>(vring) + rw * (34 * 64);
     if (stream == 1) rows.save_partial(xchg, lane);
     __syncthreads();
     if (stream == 0) rows.merge_partial(xchg, lane);
@@ -414,7 +448,11 @@ fa2_fwd_slot_kernel(const T* Q, const T* __restrict__ K, const T* __restrict__ V
   // PAIR: every wave past its reads of the rings (the merge's included)
   // before the next block's prologue fetches into them.
   if (PAIR && bi + 1 < nblk) __syncthreads();
-  }  // blocks
+  };  // run_block
+  run_block(0);
+  if constexpr (PAIR) {
+    if (nblk > 1) run_block(1);
+  }
 }
 
 template <int W, int FV, class T = _Float16, int SPLIT = 1, bool PAIR = false>
