@@ -94,9 +94,11 @@ extern "C" {
 
 // Contiguous fp16 [B, H, N, 64] q, k, v, o; sm_scale 1/8.  mode 8 / 4: the
 // br256_bc64_w8_slot / br128_bc64_w4_slot configurations; 2: the key-range
-// split br128_bc64_w4x2_slot.  `out` holds `out_entries` uint64, at least 8
-// per wave of the grid (B*H*ceil(N/256) groups of 8 waves for mode 8,
-// B*H*ceil(N/128) groups of 4 or 8 waves for modes 4 and 2).  Returns a
+// split br128_bc64_w4x2_slot; 9: the block pairs br128_bc64_w4x2_pair.
+// `out` holds `out_entries` uint64, at least 8 per wave record of the grid
+// (B*H*ceil(N/256) groups of 8 waves for mode 8, B*H*ceil(N/128) groups of
+// 4 or 8 waves for modes 4 and 2, B*H*ceil(ceil(N/128)/2) groups of 8 waves
+// with one record per wave and block, 16 per group, for mode 9).  Returns a
 // hipError_t.
 int fl_diag_slot_timeline(int mode, int causal, const void* q, const void* k, const void* v,
                           void* o, int B, int H, int N, void* out, long long out_entries,
@@ -105,9 +107,10 @@ int fl_diag_slot_timeline(int mode, int causal, const void* q, const void* k, co
       out == nullptr)
     return (int)hipErrorInvalidValue;
   const long long rows = mode == 8 ? 256 : 128;
-  const long long waves = mode == 4 ? 4 : 8;
-  if (out_entries < 8 * waves * (long long)B * H * ((N + rows - 1) / rows))
-    return (int)hipErrorInvalidValue;
+  const long long blocks = (N + rows - 1) / rows;
+  const long long groups = (long long)B * H * (mode == 9 ? (blocks + 1) / 2 : blocks);
+  const long long records = mode == 4 ? 4 : mode == 9 ? 16 : 8;
+  if (out_entries < 8 * records * groups) return (int)hipErrorInvalidValue;
   hipError_t e = hipMemcpyToSymbol(HIP_SYMBOL(g_fl_timeline), &out, sizeof(out));
   if (e != hipSuccess) return (int)e;
   fl::FwdArgs a{};

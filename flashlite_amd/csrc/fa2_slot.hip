@@ -1,6 +1,7 @@
-// Slot-scheduled schedule (configurations br256_bc64_w8_slot and
-// br128_bc64_w4_slot), fp16 and bf16 at head_dim 64.  Shared building
-// blocks: fa2_common.h.
+// Slot-scheduled schedule (configurations br256_bc64_w8_slot,
+// br128_bc64_w4_slot, the key-range splits br128_bc64_w4x2_slot and
+// br64_bc64_w2x2_slot, and the block pairs br128_bc64_w4x2_pair), fp16 and
+// bf16 at head_dim 64.  Shared building blocks: fa2_common.h.
 
 #include "fa2_common.h"
 
@@ -159,6 +160,7 @@ fa2_fwd_slot_kernel(const T* Q, const T* __restrict__ K, const T* __restrict__ V
   // One block's walk (inlined once, or twice for a pair: a loop around the
   // body pushes the register allocator into spills).
   auto run_block = [&](const int bi) __attribute__((always_inline)) {
+  FL_TL_STAMP(tl_block);
   const Walk wk = walk_of(bi);
   const int q0 = wk.q0, t0 = wk.t0, tbeg = wk.tbeg, tend = wk.tend;
   const i32x4_t rk = wk.rk, rv = wk.rv;
@@ -444,7 +446,9 @@ fa2_fwd_slot_kernel(const T* Q, const T* __restrict__ K, const T* __restrict__ V
     rows.launder();
     rows.store(hp.o, geom.o_sr, hp.lse);
   }
-  FL_TL_RECORD(W * SPLIT, wave, lane, t0 + 1, tl_entry, tl_first, tl_loop, tl_loop_end, tl_store);
+  // (a pair records each block: wave + 8 bi of 16 records per work-group)
+  FL_TL_RECORD(PAIR ? 2 * W * SPLIT : W * SPLIT, wave + bi * W * SPLIT, lane, t0 + 1,
+               (bi == 0 ? tl_entry : tl_block), tl_first, tl_loop, tl_loop_end, tl_store);
   // PAIR: every wave past its reads of the rings (the merge's included)
   // before the next block's prologue fetches into them.
   if (PAIR && bi + 1 < nblk) __syncthreads();

@@ -291,7 +291,10 @@ def _timeline(args, torch):
     o = torch.empty_like(q)
     mode = args.timeline
     rows, wpg = (256, 8) if mode == 8 else (128, 4 if mode == 4 else 8)
-    groups = w.batch * w.heads * ((w.seq + rows - 1) // rows)
+    blocks = (w.seq + rows - 1) // rows
+    groups = w.batch * w.heads * blocks
+    if mode == 9:  # one group per block pair, one record per wave and block
+        groups, wpg = w.batch * w.heads * ((blocks + 1) // 2), 16
     out = torch.zeros(groups * wpg * 8, dtype=torch.int64, device=dev)
     stream = torch.cuda.current_stream().cuda_stream
 
@@ -304,7 +307,9 @@ def _timeline(args, torch):
 
     us = _time_launches(launch, args, torch)
     d = out.cpu().numpy().reshape(-1, 8).astype(np.int64)
-    d = d[d[:, 7] != 0]  # every wave that stamped
+    blk = (np.arange(len(d)) % wpg) // 8 if mode == 9 else np.zeros(len(d), np.int64)
+    keep = d[:, 7] != 0  # every wave (and block) that stamped
+    d, blk = d[keep], blk[keep]
     tick_us = 1e3 / lib.fl_diag_wall_clock_khz(0)
     t = (d[:, :6] - d[:, 0].min()) * tick_us
     iters = d[:, 7] >> 48
@@ -315,14 +320,22 @@ def _timeline(args, torch):
     names = {8: "br256_bc64_w8_slot", 4: "br128_bc64_w4_slot", 2: "br128_bc64_w4x2_slot",
              9: "br128_bc64_w4x2_pair"}
     print(f"timeline {w.name} causal={args.causal} {names[mode]}: {us:.2f} us/launch over "
-          f"{args.iters} launches (events); last launch: {len(d)} waves, span "
+          f"{args.iters} launches (events); last launch: {len(d)} wave records, span "
           f"{t[:, 5].max():.2f} us (first entry to last exit), start skew {t[:, 0].max():.2f} us",
           flush=True)
     pct = lambda x: (f"min {x.min():7.2f}  p50 {np.median(x):7.2f}  p90 "  # noqa: E731
                      f"{np.percentile(x, 90):7.2f}  max {x.max():7.2f} us")
-    print(f"  entry -> loop start (prologue)  {pct(t[:, 2] - t[:, 0])}")
-    print(f"  loop                            {pct(loop)}")
-    print(f"  loop end -> exit (epilogue)     {pct(t[:, 5] - t[:, 3])}")
+    for b in sorted(set(blk.tolist())):
+        m = blk == b
+        if mode == 9:
+            print(f"  block {b} of each pair ({'the heavier, first' if b == 0 else 'the lighter'}; "
+                  f"times from {'the group entry' if b == 0 else 'its own start'}):")
+        print(f"  entry -> loop start (prologue)  {pct(t[m, 2] - t[m, 0])}")
+        print(f"  loop                            {pct(loop[m])}")
+        print(f"  loop end -> exit (epilogue)     {pct(t[m, 5] - t[m, 3])}")
+        it = iters[m]
+        print(f"  iterations p50 {np.median(it):.0f} (min {it.min()}, max {it.max()}); loop time "
+              f"per iteration p50 {np.median(loop[m] / it) * 1e3:.0f} ns")
     print(f"  loop cycles per iteration p50 {np.median(d[:, 6] / iters):.0f}; loop clock "
           f"min {clk.min():.3f} p50 {np.median(clk):.3f} max {clk.max():.3f} GHz")
     for x in range(8):
@@ -336,7 +349,9 @@ def _timeline(args, torch):
         per_cu = collections.defaultdict(list)
         for g in range(len(d) // wpg):
             sl = slice(g * wpg, (g + 1) * wpg)
-            per_cu[cu_key[sl][0]].append((int(iters[sl].max()), float(loop[sl].max()),
+            bs = [blk[sl] == b for b in sorted(set(blk[sl].tolist()))]  # a pair's two blocks
+            per_cu[cu_key[sl][0]].append((int(sum(iters[sl][m].max() for m in bs)),
+                                          float(sum(loop[sl][m].max() for m in bs)),
                                           float(t[sl, 5].max())))
         ends = np.array([max(x[2] for x in v) for v in per_cu.values()])
         print(f"  {len(per_cu)} CUs; CU finish min {ends.min():.2f} p50 {np.median(ends):.2f} "
