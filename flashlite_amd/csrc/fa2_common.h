@@ -610,6 +610,13 @@ struct Rows {
       if constexpr (MS && db == 1) lacc = E::mfma16(sel, pp[t >> 1][t & 1], lacc);
     }
   }
+  // One GEMM2 MFMA outside the slot map: O[db] += V^T(key step t) . P (with
+  // MS, key step t's row sums ride with db = 1, as in mfma_slot).
+  template <int DB, int TS, bool MS = false>
+  __device__ __forceinline__ void gemm2_step(const V8& a, const V8 (&pp)[2][2]) {
+    o[DB] = E::mfma(a, pp[TS >> 1][TS & 1], o[DB]);
+    if constexpr (MS && DB == 1) lacc = E::mfma16(sel, pp[TS >> 1][TS & 1], lacc);
+  }
   // Row sums on the matrix core.  The 16x16x32 MFMA takes a 32x32x16 P^T
   // B operand (lane l: query l%32, keys 8(l/32) .. +7 of a 16-key step) as
   // B16[k = 8(l/16) + e][n = l%16], i.e. query n + 16h (h = bit 4 of l) at

@@ -53,8 +53,8 @@ namespace {
 // same problem, so up to 256 CUs get one each in a single round); waves
 // 0..W-1 (stream 0) walk the first ceil(n/2) of the block's n key tiles and
 // waves W..2W-1 (stream 1) the rest, each stream through its own rings,
-// and the halves merge through LDS at the end (Rows::save_partial /
-// merge_partial).  Both streams run the same iterations (the shorter one
+// and the halves merge through LDS at the end (Rows::save_partial4 /
+// merge_partial4).  Both streams run the same iterations (the shorter one
 // ends on a fully masked tile), so every wave meets the same barriers.
 // This halves the longest key walk: a causal work-group's time follows half
 // its tiles, and heaviest-first dispatch of one work-group per CU then
@@ -106,7 +106,14 @@ fa2_fwd_slot_kernel(const T* Q, const T* __restrict__ K, const T* __restrict__ V
   static_assert(FV >= 2 && FV <= 6, "fetch distance");
   static_assert(kAhead % 2 == 0 && kAhead < 16, "read-ahead");
   static_assert(SPLIT == 1 || SPLIT == 2, "key-range split");
-  static_assert(SPLIT == 1 || SPLIT * kRingBytes - 16 >= W * 34 * 64 * 4, "merge buffer");
+  // The streams' exchange: stream 1's wave rw leaves its O, m, l (9 KiB)
+  // in V ring slots 1 .. kSlots-1 of stream rw / ceil(W/2), clear of slot 0
+  // (a block pair's next V(0) lands there meanwhile) and of the flag in the
+  // last 16 bytes.
+  constexpr int kXchgBytes = 9 * 64 * 16;
+  constexpr int kXchgPerRing = (W + 1) / 2;
+  static_assert(SPLIT == 1 || (kSlots - 1) * kTileBytes - 16 >= kXchgPerRing * kXchgBytes,
+                "merge buffer");
   static_assert(!PAIR || SPLIT == 2, "block pairs: key-range split groups");
   __shared__ __attribute__((aligned(16))) uint8_t kring[SPLIT * kRingBytes];
   __shared__ __attribute__((aligned(16))) uint8_t vring[SPLIT * kRingBytes];
@@ -133,9 +140,8 @@ fa2_fwd_slot_kernel(const T* Q, const T* __restrict__ K, const T* __restrict__ V
   const int seq = geom.seq_q;
   const StreamRings<kSlots> rings = {kring + stream * kRingBytes, vring + stream * kRingBytes};
   // The walk of block bi: its first query row, and this stream's key tiles
-  // [tbeg, tend); iterations 0 .. t0 on tile tbeg + j (the last one only
-  // drains GEMM2; with SPLIT the shorter stream's last tile lies past the
-  // range and is masked).  K and V end with the stream's range: fetches
+  // [tbeg, tend); iterations 0 .. t0 - 1 on tile tbeg + j (with SPLIT the
+  // shorter stream's last tile lies past the range and is masked).  K and V end with the stream's range: fetches
   // past it (the pipeline's look-ahead near the end of the walk) land as
   // zeros with no traffic.
   struct Walk {
@@ -168,7 +174,7 @@ fa2_fwd_slot_kernel(const T* Q, const T* __restrict__ K, const T* __restrict__ V
   const int tzero = tend;
   // Tiles of the range this wave's rows need (through their causal
   // diagonal; none for a wave wholly past the last query row), at least
-  // one: iteration nw drains the wave's GEMM2, later ones only fetch and
+  // one: iteration nw - 1 ends the wave's GEMM2, later ones only fetch and
   // meet the barrier.
   int nw = tend - tbeg;
   if (CAUSAL) nw = min(nw, causal_tiles(min(q0 + 32 * rw + 32, seq), geom.coff) - tbeg);
@@ -191,14 +197,13 @@ fa2_fwd_slot_kernel(const T* Q, const T* __restrict__ K, const T* __restrict__ V
     if constexpr (G + FV >= 0)
       fetch_tile_z<kSegs>(rv, rings.vslot(Ic<G + FV>{}), tbeg + G + FV, tzero, rw, fv);
   };
+  // (A block pair's second block had Q and groups -FK, -FK+1 (K(0), K(1),
+  // V(0)) fetched during the first block's merge, in the same order, so
+  // the waits below count the same fetches.)
   if (!PAIR || !prefetched) {
     fetch_q_block(hp.q, geom.q_sr, q0 + 32 * rw, seq, qblk, lane);
     prologue_group(Ic<0>{});
     prologue_group(Ic<1>{});
-  } else {
-    // Q, K(0) and K(1) came during the previous block: V(0) completes group
-    // -FK+1, so the waits below count the same fetches
-    fetch_tile_z<kSegs>(rv, rings.vslot(Ic<0>{}), tbeg, tzero, rw, fv);
   }
   RowsT rows;
 
@@ -235,15 +240,22 @@ fa2_fwd_slot_kernel(const T* Q, const T* __restrict__ K, const T* __restrict__ V
   // (even slots 0-6) and of tile j+1 block 0 (even slots 8-14), GEMM2 of
   // tile j-1 (odd slots) and the softmax of tile j.  kFirst (j = 0): tile
   // 0's scores come from the first pass and there is no tile -1, so no
-  // block-1 GEMM1 and no GEMM2.  kLast (the wave's last tile): no GEMM1 of
-  // the tile after it.  kDrain (j = nw): GEMM2 of the wave's last tile
-  // only.  Skipped MFMAs skip their operand reads too.
-  constexpr int kFull = 0, kFirst = 1, kLast = 2, kDrain = 4;
+  // block-1 GEMM1 and no GEMM2.  kLast (the wave's last tile, j = nw - 1):
+  // there is no tile after it, so even slots 8-14 run GEMM2 of tile j's
+  // first 32 keys (their P is done by slot 7), and the last 32 keys'
+  // GEMM2 follows slot 15 (kLastTail MFMAs): the pipeline drains inside
+  // the iteration, with no iteration of its own.  Skipped MFMAs skip their
+  // operand reads too.
+  constexpr int kFull = 0, kFirst = 1, kLast = 2;
+  constexpr int kLastTail = 4;
   constexpr auto runs = [](int kind, int L) {
     if (L & 1) return (kind & kFirst) == 0;
-    if (kind & kDrain) return false;
-    return L < 8 ? (kind & kFirst) == 0 : (kind & kLast) == 0;
+    return L < 8 ? (kind & kFirst) == 0 : true;
   };
+  // kLast: the GEMM2 step (head-dim block, key step) of even slot L >= 8,
+  // and of tail MFMA i.
+  constexpr auto fold_db = [](int L) { return ((L - 8) >> 1) & 1; };
+  constexpr auto fold_t = [](int L) { return (L - 8) >> 2; };
   // Iteration j at unrolled position I (ring slots static): fetch K(j+FK)
   // and V(j+FV); 16 slots; the range check of tile j's sum; on MASKED
   // iterations, mask block 1 of tile j (after slot 7, before its
@@ -253,10 +265,11 @@ fa2_fwd_slot_kernel(const T* Q, const T* __restrict__ K, const T* __restrict__ V
     constexpr int I = decltype(i)::value;
     constexpr bool kMasked = decltype(masked)::value;
     constexpr int Kd = decltype(kind)::value;
-    constexpr bool kSoftmax = (Kd & kDrain) == 0;
+    constexpr bool kFold = (Kd & kLast) != 0;
     fetch_tile_z<kSegs>(rk, rings.kslot(Ic<I + FK>{}), tbeg + j + FK, tzero, rw, fk);
     fetch_tile_z<kSegs>(rv, rings.vslot(Ic<I + FV>{}), tbeg + j + FV, tzero, rw, fv);
     V8 op[16];
+    V8 top[kLastTail];  // kLast: the tail MFMAs' operands
     if constexpr ((Kd & kFirst) == 0) {
 #pragma unroll
       for (int a = 0; a < kAhead; ++a) op[a] = ahead[a];
@@ -270,35 +283,43 @@ fa2_fwd_slot_kernel(const T* Q, const T* __restrict__ K, const T* __restrict__ V
       constexpr int L = decltype(sl)::value;
       // The MFMA goes first (fenced): its operand's wait then never covers
       // the read issued in the same slot.
-      if constexpr (runs(Kd, L)) rows.template mfma_slot<L, kMfmaSum>(op[L], S, Pp);
+      if constexpr (runs(Kd, L)) {
+        if constexpr (kFold && L % 2 == 0 && L >= 8)
+          rows.template gemm2_step<fold_db(L), fold_t(L), kMfmaSum>(op[L], P);
+        else
+          rows.template mfma_slot<L, kMfmaSum>(op[L], S, Pp);
+      }
       __builtin_amdgcn_sched_barrier(0);
       if constexpr (L + kAhead < 16) {
-        if constexpr (runs(Kd, L + kAhead))
-          op[L + kAhead] = rows.template read_slot<L + kAhead>(
-              rings.kslot(Ic<I>{}), rings.kslot(Ic<I + 1>{}), rings.vslot(Ic<I - 1>{}));
-      } else if constexpr (kSoftmax && (Kd & kLast) == 0) {
+        constexpr int La = L + kAhead;
+        if constexpr (runs(Kd, La)) {
+          if constexpr (kFold && La % 2 == 0 && La >= 8)
+            op[La] = rows.read_v_op(rings.vslot(Ic<I>{}), fold_db(La), fold_t(La));
+          else
+            op[La] = rows.template read_slot<La>(rings.kslot(Ic<I>{}), rings.kslot(Ic<I + 1>{}),
+                                                 rings.vslot(Ic<I - 1>{}));
+        }
+      } else if constexpr (!kFold) {
         ahead[L + kAhead - 16] = rows.template read_slot<L + kAhead - 16>(
             rings.kslot(Ic<I + 1>{}), rings.kslot(Ic<I + 2>{}), rings.vslot(Ic<I>{}));
-      } else if constexpr (kSoftmax && (L + kAhead - 16) % 2 == 1) {
-        // the wave's last tile: its drain needs only V (odd slots)
-        ahead[L + kAhead - 16] = rows.template read_slot<L + kAhead - 16>(
-            rings.kslot(Ic<I + 1>{}), rings.kslot(Ic<I + 2>{}), rings.vslot(Ic<I>{}));
+      } else if constexpr (L + kAhead - 16 < kLastTail) {
+        // V(j) key steps 2 and 3 for the tail MFMAs
+        constexpr int ti = L + kAhead - 16;
+        top[ti] = rows.read_v_op(rings.vslot(Ic<I>{}), ti & 1, 2 + (ti >> 1));
       }
-      if constexpr (kSoftmax) {
-        if constexpr (L == 0) rows.template scale_pair<0>(S, xs[0]);
-        const float epair = rows.template exp_pair<L>(xs[L & 1], P);
-        if constexpr (kMfmaSum)
-          ;
-        else if constexpr (kTree && !kMasked)
-          RowsT::template sum_slot<L>(P, tree);
-        else
-          RowsT::template sum_pair_f32<L>(epair, sum);
-        if constexpr (kMasked && L == 7) rows.template mask_block<1>(tbeg + j, S[1]);
-        if constexpr (L < 15) rows.template scale_pair<L + 1>(S, xs[(L + 1) & 1]);
-      }
+      if constexpr (L == 0) rows.template scale_pair<0>(S, xs[0]);
+      const float epair = rows.template exp_pair<L>(xs[L & 1], P);
+      if constexpr (kMfmaSum)
+        ;
+      else if constexpr (kTree && !kMasked)
+        RowsT::template sum_slot<L>(P, tree);
+      else
+        RowsT::template sum_pair_f32<L>(epair, sum);
+      if constexpr (kMasked && L == 7) rows.template mask_block<1>(tbeg + j, S[1]);
+      if constexpr (L < 15) rows.template scale_pair<L + 1>(S, xs[(L + 1) & 1]);
       __builtin_amdgcn_sched_barrier(0);
     });
-    if constexpr (!kMfmaSum && kSoftmax) {
+    if constexpr (!kMfmaSum) {
       float tot;
       if constexpr (kTree && !kMasked)
         tot = RowsT::sum_root(tree);
@@ -307,12 +328,15 @@ fa2_fwd_slot_kernel(const T* Q, const T* __restrict__ K, const T* __restrict__ V
       rows.l += tot;
       out_of_range |= __builtin_amdgcn_ballot_w64(!(tot <= kSumLimit));
     }
-    if constexpr (kMasked && (Kd & (kLast | kDrain)) == 0)
-      rows.template mask_block<0>(tbeg + j + 1, S[0]);
-    if constexpr (kSoftmax)
-      sync_ring_ahead<(FV - 1) * kDmaPerIter, kTailReads - ((Kd & kLast) ? kAhead / 2 : 0)>();
-    else
-      sync_ring_ahead<(FV - 1) * kDmaPerIter, 0>();
+    if constexpr (kFold) {
+      // GEMM2 of tile j's last 32 keys (P complete since slot 15)
+      static_for(std::make_integer_sequence<int, kLastTail>{}, [&](auto t) __attribute__((always_inline)) {
+        constexpr int ti = decltype(t)::value;
+        rows.template gemm2_step<ti & 1, 2 + (ti >> 1), kMfmaSum>(top[ti], P);
+      });
+    }
+    if constexpr (kMasked && !kFold) rows.template mask_block<0>(tbeg + j + 1, S[0]);
+    sync_ring_ahead<(FV - 1) * kDmaPerIter, kFold ? 0 : kTailReads>();
   };
   auto group = [&](int j0, auto masked, auto first) __attribute__((always_inline)) {
     static_for(std::make_integer_sequence<int, kUnroll>{}, [&](auto i) __attribute__((always_inline)) {
@@ -326,7 +350,7 @@ fa2_fwd_slot_kernel(const T* Q, const T* __restrict__ K, const T* __restrict__ V
         iteration(i, j, P, Pp, masked, Ic<kFull>{});
     });
   };
-  // The wave's last tile (j = nw - 1, at unrolled position I) and its drain.
+  // The wave's last tile (j = nw - 1, at unrolled position I).
   auto tail = [&](auto i) __attribute__((always_inline)) {
     constexpr int I = decltype(i)::value;
     auto& P = I % 2 == 0 ? P0 : P1;
@@ -339,13 +363,12 @@ fa2_fwd_slot_kernel(const T* Q, const T* __restrict__ K, const T* __restrict__ V
     } else {
       iteration(i, nw - 1, P, Pp, Ic<true>{}, Ic<kLast>{});
     }
-    iteration(Ic<I + 1>{}, nw, Pp, P, Ic<true>{}, Ic<kDrain>{});
   };
   FL_TL_STAMP(tl_loop);
   {
     // iterations 0 .. nw - 2 in unrolled groups: unmasked while every tile
     // is below the diagonal and the range end (j < jm <= nw - 1), then
-    // masked; then the wave's last tile and its drain
+    // masked; then the wave's last tile, whose iteration drains GEMM2
     if (nw >= 2) {
       int j0 = kUnroll;
       if (kUnroll <= jm) {
@@ -359,10 +382,10 @@ fa2_fwd_slot_kernel(const T* Q, const T* __restrict__ K, const T* __restrict__ V
     static_for(std::make_integer_sequence<int, kUnroll>{}, [&](auto i) __attribute__((always_inline)) {
       if ((nw - 1) % kUnroll == decltype(i)::value) tail(i);
     });
-    // Past its drain (iterations nw + 1 .. t0, when other waves of the
+    // Past its last tile (iterations nw .. t0 - 1, when other waves of the
     // work-group need more tiles) a wave only fetches its share of the
     // tiles and meets the barrier.
-    for (int j = nw + 1; j <= t0; ++j) {
+    for (int j = nw; j < t0; ++j) {
       fetch_tile_z<kSegs>(rk, rings.k + kTileBytes * ((j + FK) % kSlots), tbeg + j + FK, tzero, rw,
                           fk);
       fetch_tile_z<kSegs>(rv, rings.v + kTileBytes * ((j + FV) % kSlots), tbeg + j + FV, tzero, rw,
@@ -382,10 +405,10 @@ fa2_fwd_slot_kernel(const T* Q, const T* __restrict__ K, const T* __restrict__ V
 
   // ---- checked pass, when any wave saw a tile sum out of range ----
   // The work-group's flag lives in the last 16 bytes of the V rings, which
-  // neither the checked pass (slot 0) nor the streams' exchange (the first
-  // 35 KiB) touches (the rings are idle here: every wave has drained its
-  // fetches and reads before the first barrier).  No extra LDS, so two
-  // 4-wave work-groups still fit one CU.  Both streams read the one flag,
+  // neither the checked pass (slot 0) nor the streams' exchange touches
+  // (the rings are idle here: every wave has drained its fetches and reads
+  // before the first barrier).  No extra LDS, so two 4-wave work-groups
+  // still fit one CU.  Both streams read the one flag,
   // so every wave takes the same barriers.
   __builtin_amdgcn_s_waitcnt(0);
   int* redo = reinterpret_cast<int*>(vring + SPLIT * kRingBytes - 16);
@@ -422,24 +445,26 @@ fa2_fwd_slot_kernel(const T* Q, const T* __restrict__ K, const T* __restrict__ V
   }
   if (PAIR && bi + 1 < nblk) {
     // Every wave is past its reads of the rings and of its Q block (the
-    // flag's barriers, or the checked pass's last one): the next block's Q
-    // and first two K tiles go out now, to land during the merge and store.
+    // flag's barriers, or the checked pass's last one): the next block's Q,
+    // K(0), K(1) and V(0) go out now, to land during the merge and store.
     const Walk nx = walk_of(bi + 1);
     fetch_q_block(hp.q, geom.q_sr, nx.q0 + 32 * rw, seq, qblk, lane);
     fetch_tile_z<kSegs>(nx.rk, rings.kslot(Ic<0>{}), nx.tbeg, nx.tend, rw, fk);
     fetch_tile_z<kSegs>(nx.rk, rings.kslot(Ic<1>{}), nx.tbeg + 1, nx.tend, rw, fk);
+    fetch_tile_z<kSegs>(nx.rv, rings.vslot(Ic<0>{}), nx.tbeg, nx.tend, rw, fv);
     prefetched = true;
   }
   if constexpr (SPLIT == 2) {
     // Stream 1 hands its O, m, l to stream 0 through the (idle) V rings.
     // (Only LDS needs to settle: the fetches still in flight, the next
-    // block's, write the K rings and Q blocks.)
+    // block's, write the K rings, V slot 0 and the Q blocks.)
     asm volatile("s_waitcnt lgkmcnt(0)" : : : "memory");
     __syncthreads();
-    float* xchg = reinterpret_cast<float*>(vring) + rw * (34 * 64);
-    if (stream == 1) rows.save_partial(xchg, lane);
+    float4* const xchg = reinterpret_cast<float4*>(
+        vring + (rw / kXchgPerRing) * kRingBytes + kTileBytes + (rw % kXchgPerRing) * kXchgBytes);
+    if (stream == 1) rows.save_partial4(xchg, lane);
     __syncthreads();
-    if (stream == 0) rows.merge_partial(xchg, lane);
+    if (stream == 0) rows.merge_partial4(xchg, lane);
   }
   FL_TL_STAMP(tl_store);
   if (SPLIT == 1 || stream == 0) {
@@ -447,7 +472,7 @@ fa2_fwd_slot_kernel(const T* Q, const T* __restrict__ K, const T* __restrict__ V
     rows.store(hp.o, geom.o_sr, hp.lse);
   }
   // (a pair records each block: wave + 8 bi of 16 records per work-group)
-  FL_TL_RECORD(PAIR ? 2 * W * SPLIT : W * SPLIT, wave + bi * W * SPLIT, lane, t0 + 1,
+  FL_TL_RECORD(PAIR ? 2 * W * SPLIT : W * SPLIT, wave + bi * W * SPLIT, lane, t0,
                (bi == 0 ? tl_entry : tl_block), tl_first, tl_loop, tl_loop_end, tl_store);
   // PAIR: every wave past its reads of the rings (the merge's included)
   // before the next block's prologue fetches into them.
