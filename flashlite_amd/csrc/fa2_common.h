@@ -808,6 +808,24 @@ struct Rows {
     sub(s, m0);
     set_m(m0);
   }
+  // The slot schedule's first pass: GEMM1 of key block 0 of tile kt only,
+  // and m = that block's exact row max (a row with no key there has none in
+  // the tile: masks keep key prefixes), so the tile's block 1 can follow
+  // against the same stabiliser inside the first iteration.
+  __device__ __forceinline__ void gemm1_block0(const uint8_t* kt, float16_t (&s)[2]) const {
+#pragma unroll
+    for (int st = 0; st < 4; ++st) s[0] = E::mfma(read_k_op(kt, 0, st), qf[st], st == 0 ? bias : s[0]);
+  }
+  __device__ __forceinline__ void first_block(float16_t& s0) {
+    float mx = ninf();
+#pragma unroll
+    for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s0[r]);
+    mx = pair_max(mx);
+    mx = mx == ninf() ? 0.0f : mx;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) s0[r] -= mx;
+    set_m(mx);
+  }
   // p = 2^(t - m) (times cr when SCALED) packed to fp16 B-operands; returns
   // this lane's sum of p, taken in fp32 over four chains.  (The row sum uses
   // v_add_f32 rather than v_dot2_f32_f16 on the packed p: on gfx950 the dot2

@@ -219,28 +219,31 @@ fa2_fwd_slot_kernel(const T* Q, const T* __restrict__ K, const T* __restrict__ V
   const int jm = max(0, tm - tbeg - 1);
   float16_t S[2];
   V8 P0[2][2], P1[2][2];
-  {
-    // S(tbeg) with the exact row max; iteration 0 exponentiates it.
-    V8 ka[2][4];
-    rows.read_k(rings.kslot(Ic<0>{}), ka);
-    rows.gemm1(ka, S);
-  }
+  // Operands of the next iteration's first kAhead slots.
+  V8 ahead[kAhead];
+  // Key block 0 of S(tbeg), with its exact row max as the stabiliser;
+  // iteration 0 computes block 1 in its even slots 0-6 and exponentiates
+  // both.
+  rows.gemm1_block0(rings.kslot(Ic<0>{}), S);
   static_for(std::make_integer_sequence<int, FK - 2>{}, [&](auto i) __attribute__((always_inline)) {
     prologue_group(Ic<decltype(i)::value + 2>{});
   });
-  rows.mask(tbeg, S);
-  rows.first_tile(S);
-  sync_ring_ahead<(FV - 1) * kDmaPerIter, 0>();  // K(1), V(0)
-  // Operands of the next iteration's first kAhead slots (iteration 0 reads
-  // its own: its first slots carry no MFMA).
-  V8 ahead[kAhead];
+  rows.template mask_block<0>(tbeg, S[0]);
+  rows.first_block(S[0]);
+  // iteration 0's slots 0, 2 and 4: K(tbeg) block 1, steps 0-2
+  static_for(std::make_integer_sequence<int, kAhead / 2>{}, [&](auto i) __attribute__((always_inline)) {
+    constexpr int a = 2 * decltype(i)::value;
+    ahead[a] = rows.template read_slot<a>(rings.kslot(Ic<0>{}), rings.kslot(Ic<1>{}),
+                                          rings.vslot(Ic<-1>{}));
+  });
+  sync_ring_ahead<(FV - 1) * kDmaPerIter, kAhead / 2>();  // K(1), V(0)
 
   uint64_t out_of_range = 0;
   // Iteration kinds (bits): a full iteration j runs GEMM1 of tile j block 1
   // (even slots 0-6) and of tile j+1 block 0 (even slots 8-14), GEMM2 of
-  // tile j-1 (odd slots) and the softmax of tile j.  kFirst (j = 0): tile
-  // 0's scores come from the first pass and there is no tile -1, so no
-  // block-1 GEMM1 and no GEMM2.  kLast (the wave's last tile, j = nw - 1):
+  // tile j-1 (odd slots) and the softmax of tile j.  kFirst (j = 0): block
+  // 0 of tile 0 comes from the first pass and there is no tile -1, so no
+  // GEMM2.  kLast (the wave's last tile, j = nw - 1):
   // there is no tile after it, so even slots 8-14 run GEMM2 of tile j's
   // first 32 keys (their P is done by slot 7), and the last 32 keys'
   // GEMM2 follows slot 15 (kLastTail MFMAs): the pipeline drains inside
@@ -248,10 +251,7 @@ fa2_fwd_slot_kernel(const T* Q, const T* __restrict__ K, const T* __restrict__ V
   // operand reads too.
   constexpr int kFull = 0, kFirst = 1, kLast = 2;
   constexpr int kLastTail = 4;
-  constexpr auto runs = [](int kind, int L) {
-    if (L & 1) return (kind & kFirst) == 0;
-    return L < 8 ? (kind & kFirst) == 0 : true;
-  };
+  constexpr auto runs = [](int kind, int L) { return (L & 1) == 0 || (kind & kFirst) == 0; };
   // kLast: the GEMM2 step (head-dim block, key step) of even slot L >= 8,
   // and of tail MFMA i.
   constexpr auto fold_db = [](int L) { return ((L - 8) >> 1) & 1; };
@@ -270,10 +270,9 @@ fa2_fwd_slot_kernel(const T* Q, const T* __restrict__ K, const T* __restrict__ V
     fetch_tile_z<kSegs>(rv, rings.vslot(Ic<I + FV>{}), tbeg + j + FV, tzero, rw, fv);
     V8 op[16];
     V8 top[kLastTail];  // kLast: the tail MFMAs' operands
-    if constexpr ((Kd & kFirst) == 0) {
 #pragma unroll
-      for (int a = 0; a < kAhead; ++a) op[a] = ahead[a];
-    }
+    for (int a = 0; a < kAhead; ++a)
+      if (runs(Kd, a)) op[a] = ahead[a];
     half2_t tree[14];
     float sum[4];
     // SCALED: each slot scales the next slot's pair, so a slot's
