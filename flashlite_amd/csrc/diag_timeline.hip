@@ -94,22 +94,24 @@ extern "C" {
 
 // Contiguous fp16 [B, H, N, 64] q, k, v, o; sm_scale 1/8.  mode 8 / 4: the
 // br256_bc64_w8_slot / br128_bc64_w4_slot configurations; 2: the key-range
-// split br128_bc64_w4x2_slot; 9: the block pairs br128_bc64_w4x2_pair.
+// split br128_bc64_w4x2_slot; 7: the split on 64-row groups
+// br64_bc64_w2x2_slot; 9: the block pairs br128_bc64_w4x2_pair.
 // `out` holds `out_entries` uint64, at least 8 per wave record of the grid
 // (B*H*ceil(N/256) groups of 8 waves for mode 8, B*H*ceil(N/128) groups of
-// 4 or 8 waves for modes 4 and 2, B*H*ceil(ceil(N/128)/2) groups of 8 waves
+// 4 or 8 waves for modes 4 and 2, B*H*ceil(N/64) groups of 4 waves for mode
+// 7, B*H*ceil(ceil(N/128)/2) groups of 8 waves
 // with one record per wave and block, 16 per group, for mode 9).  Returns a
 // hipError_t.
 int fl_diag_slot_timeline(int mode, int causal, const void* q, const void* k, const void* v,
                           void* o, int B, int H, int N, void* out, long long out_entries,
                           void* stream) {
-  if ((mode != 8 && mode != 4 && mode != 2 && mode != 9) || B < 1 || H < 1 || N < 1 ||
-      out == nullptr)
+  if ((mode != 8 && mode != 4 && mode != 2 && mode != 7 && mode != 9) || B < 1 || H < 1 ||
+      N < 1 || out == nullptr)
     return (int)hipErrorInvalidValue;
-  const long long rows = mode == 8 ? 256 : 128;
+  const long long rows = mode == 8 ? 256 : mode == 7 ? 64 : 128;
   const long long blocks = (N + rows - 1) / rows;
   const long long groups = (long long)B * H * (mode == 9 ? (blocks + 1) / 2 : blocks);
-  const long long records = mode == 4 ? 4 : mode == 9 ? 16 : 8;
+  const long long records = mode == 4 || mode == 7 ? 4 : mode == 9 ? 16 : 8;
   if (out_entries < 8 * records * groups) return (int)hipErrorInvalidValue;
   hipError_t e = hipMemcpyToSymbol(HIP_SYMBOL(g_fl_timeline), &out, sizeof(out));
   if (e != hipSuccess) return (int)e;
@@ -133,6 +135,7 @@ int fl_diag_slot_timeline(int mode, int causal, const void* q, const void* k, co
   a.q_sb = a.k_sb = a.v_sb = a.o_sb = (int64_t)H * N * 64;
   const auto st = static_cast<hipStream_t>(stream);
   e = mode == 2   ? fl::diag_timeline_launch_slot_split(a, 4, st)
+      : mode == 7 ? fl::diag_timeline_launch_slot_split(a, 2, st)
       : mode == 9 ? fl::diag_timeline_launch_slot_pair(a, st)
                   : fl::diag_timeline_launch_slot(a, mode, st);
   return (int)e;

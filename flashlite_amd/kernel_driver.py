@@ -25,8 +25,8 @@ buffer before every launch, evicting the inputs from the L2 caches and the
 256 MiB Infinity Cache (M > 256), and times each launch alone with its own
 HIP event pair; the mean over ``--iters`` launches is printed.
 
-``--timeline MODE`` (MODE 8, 4, 2 or 9: br256_bc64_w8_slot, br128_bc64_w4_slot,
-br128_bc64_w4x2_slot or br128_bc64_w4x2_pair; fp16 D = 64 workloads or
+``--timeline MODE`` (MODE 8, 4, 2, 7 or 9: br256_bc64_w8_slot, br128_bc64_w4_slot,
+br128_bc64_w4x2_slot, br64_bc64_w2x2_slot or br128_bc64_w4x2_pair; fp16 D = 64 workloads or
 ``--shape``, ``--causal``)
 runs the diagnostic build of the slot kernels whose waves stamp their entry,
 loop start and end, and exit (``fl_diag_slot_timeline``), launched
@@ -290,7 +290,7 @@ def _timeline(args, torch):
     q, k, v = (torch.from_numpy(x).to(dev) for x in workload_inputs(w))
     o = torch.empty_like(q)
     mode = args.timeline
-    rows, wpg = (256, 8) if mode == 8 else (128, 4 if mode == 4 else 8)
+    rows, wpg = {8: (256, 8), 4: (128, 4), 7: (64, 4)}.get(mode, (128, 8))
     blocks = (w.seq + rows - 1) // rows
     groups = w.batch * w.heads * blocks
     if mode == 9:  # one group per block pair, one record per wave and block
@@ -318,7 +318,7 @@ def _timeline(args, torch):
     loop = t[:, 3] - t[:, 2]
     clk = d[:, 6] / np.maximum(loop, 1e-9) / 1e3  # GHz
     names = {8: "br256_bc64_w8_slot", 4: "br128_bc64_w4_slot", 2: "br128_bc64_w4x2_slot",
-             9: "br128_bc64_w4x2_pair"}
+             7: "br64_bc64_w2x2_slot", 9: "br128_bc64_w4x2_pair"}
     print(f"timeline {w.name} causal={args.causal} {names[mode]}: {us:.2f} us/launch over "
           f"{args.iters} launches (events); last launch: {len(d)} wave records, span "
           f"{t[:, 5].max():.2f} us (first entry to last exit), start skew {t[:, 0].max():.2f} us",
