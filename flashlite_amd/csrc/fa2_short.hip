@@ -65,8 +65,10 @@ fa2_fwd_quarter_kernel(const T* Q, const T* __restrict__ K, const T* __restrict_
   static_assert(RB * (9 * 64) * 16 <= kQuarterWaveBytes, "partials fit a quarter's LDS");
   constexpr int kSegs = 8 / RB;  // 1 KiB segments of a tile each wave of a quarter fetches
   __shared__ __attribute__((aligned(16))) uint8_t buf[NW][kQuarterWaveBytes];
-  // each wave's 32 query rows (4 KiB)
-  __shared__ __attribute__((aligned(16))) uint8_t qbuf[NW * RB][32 * kRowBytes];
+  // each row block's 32 query rows (4 KiB), fetched a quarter by each of
+  // its NW waves
+  __shared__ __attribute__((aligned(16))) uint8_t qbuf[RB][32 * kRowBytes];
+  static_assert(NW == 4, "one 1 KiB Q segment per wave of a row block");
 
   FL_ST_DECL();
   FL_ST_MARK(0);
@@ -102,21 +104,23 @@ fa2_fwd_quarter_kernel(const T* Q, const T* __restrict__ K, const T* __restrict_
   const int t1 = min(t0 + kQuarterTiles, cend);
   uint8_t* const kb = buf[kq];
   uint8_t* const vb = buf[kq] + kQuarterTiles * kTileBytes;
-  uint8_t* const qblk = qbuf[w];
+  uint8_t* const qblk = qbuf[rb];
 
-  // This wave's 32 query rows come by DMA like a K half-tile (rows >= N_q
-  // read as zeros through the resource's bound), then its quarter's tiles
-  // in the order they are used: K, K, V, V.  Each wave waits for one piece
-  // at a time (the DMA is invisible to the compiler's own counting, so the
-  // waits are explicit) and starts computing as soon as K of the first tile
-  // has landed.  Tiles past the quarter land as zeros with no traffic.
+  // The row block's 32 query rows come by DMA like a K half-tile (rows >=
+  // N_q read as zeros through the resource's bound), 8 rows by each of its
+  // four waves, then each wave's quarter's tiles in the order they are used:
+  // K, K, V, V.  Each wave waits for one piece at a time (the DMA is
+  // invisible to the compiler's own counting, so the waits are explicit);
+  // one barrier publishes the Q rows, and a wave starts computing as soon as
+  // K of its first tile has landed.  Tiles past the quarter land as zeros
+  // with no traffic.
   const int qr = q0 + 32 * rb;  // this wave's rows
   {
     const int qrows = min(32, seq - qr);
     const i32x4_t rq = buffer_rsrc(hp.q + (long long)(qrows > 0 ? qr : 0) * geom.q_sr,
                                    qrows > 0 ? (qrows - 1) * (2 * geom.q_sr) + kRowBytes : 0);
-    const FetchOff<4> fq = fetch_offsets<4, false>(0, lane, 2 * geom.q_sr);
-    fetch_tile_z<4>(rq, qblk, 0, 1, 0, fq);
+    const FetchOff<1> fq = fetch_offsets<1, false>(kq, lane, 2 * geom.q_sr);
+    fetch_tile_z<1>(rq, qblk, 0, 1, kq, fq);
   }
   i32x4_t rk, rv;
   kv_rsrc_rows(geom, bh, K, V, t1 * kBc, rk, rv);
@@ -137,8 +141,9 @@ fa2_fwd_quarter_kernel(const T* Q, const T* __restrict__ K, const T* __restrict_
   // DMA instruction waits at issue while the CU's memory pipeline is backed
   // up, so issuing V before any compute would hold every wave behind all
   // of its CU's loads.  Outstanding fetches of the wave, oldest first:
-  // Q (4), K(t0), K(t0+1), then V(t0), V(t0+1) (kSegs each).  RB = 2 issues
-  // everything at once: a barrier publishes the tiles either way.
+  // its Q segment (1), K(t0), K(t0+1), then V(t0), V(t0+1) (kSegs each).
+  // RB = 2 issues everything at once: a barrier publishes the tiles either
+  // way.
   static_assert(kQuarterTiles == 2, "two tiles per wave");
   constexpr int kT = kSegs;
   if (any) fetch_k();
@@ -146,20 +151,22 @@ fa2_fwd_quarter_kernel(const T* Q, const T* __restrict__ K, const T* __restrict_
   RowsT rows;
   rows.place(lane, qr, seq, geom.seq_k, geom.coff, cr);
   rows.reset();
-  if (any && RB == 1)
-    asm volatile("s_waitcnt vmcnt(%0)" : : "n"(2 * kT) : "memory");
-  else if (any)
-    asm volatile("s_waitcnt vmcnt(%0)" : : "n"(4 * kT) : "memory");
-  else
-    asm volatile("s_waitcnt vmcnt(0)" : : : "memory");
-  rows.set_q_lds(qblk, cq);
-  FL_ST_MARK(1);
-  if constexpr (RB > 1) {
-    // the other wave of each quarter fetched half of every tile: one
-    // barrier publishes them all (taken by every wave)
+  if constexpr (RB == 1) {
+    // this wave's Q segment; one barrier publishes the block's four
+    if (any)
+      asm volatile("s_waitcnt vmcnt(%0)" : : "n"(2 * kT) : "memory");
+    else
+      asm volatile("s_waitcnt vmcnt(0)" : : : "memory");
+    __syncthreads();
+  } else {
+    // the other wave of each quarter fetched half of every tile, and the
+    // row block's other waves the rest of its Q: one barrier publishes
+    // them all (taken by every wave)
     asm volatile("s_waitcnt vmcnt(0)" : : : "memory");
     __syncthreads();
   }
+  rows.set_q_lds(qblk, cq);
+  FL_ST_MARK(1);
   if (any) {
     FL_ST_MARK(2);
     // Both tiles' scores against one stabiliser, the exact row max over
