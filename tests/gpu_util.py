@@ -99,7 +99,9 @@ def redo_expected(q16, k16, sm_scale, causal):
     """True when the kernel's branch-free first pass must hand the block to
     its checked pass: some row has, in a 64-key tile after its first, a lane
     half (32 of the 64 keys) whose sum of 2^(s - m0) exceeds 2^15, m0 being
-    the row's max over the first tile and s its base-2 logits."""
+    the row's max over the first tile and s its base-2 logits.  (The
+    slot-scheduled kernels take m0 over the first tile's first 32 keys
+    only, which can only make the hand-over more likely.)"""
     import numpy as np
 
     log2e = float(np.float32(1.4426950408889634))

@@ -181,6 +181,37 @@ def test_peaked_every_config(cuda, config, scale, causal):
     assert_close_oracle(out, q, k, v, scale, causal, peaked=True)
 
 
+def _second_block_dominates(gap, seed):
+    """B1 H4 N1024 inputs whose keys 32-63 of every 64-key tile score `gap`
+    base-2 logits above keys 0-31 for every row: the slot-scheduled kernels
+    take their stabiliser from keys 0-31 of a walk's first tile, so p of the
+    other half reaches 2^gap in the first pass."""
+    rs = np.random.RandomState(seed)
+    n, d = 1024, 64
+    q = (rs.standard_normal((1, 4, n, d)) * 0.3).astype(np.float32)
+    k = (rs.standard_normal((1, 4, n, d)) * 0.3).astype(np.float32)
+    v = rs.standard_normal((1, 4, n, d)).astype(np.float32)
+    # score gap = a * b * sm_scale * log2 e with sm_scale 1/8
+    ab = gap / (0.125 * 1.4426950408889634)
+    q[..., 0] = np.sqrt(ab)
+    k[..., 0] = np.where((np.arange(n) % 64) >= 32, np.sqrt(ab), 0.0)
+    return q.astype(np.float16), k.astype(np.float16), v.astype(np.float16)
+
+
+@pytest.mark.parametrize("config", range(NCFG))
+@pytest.mark.parametrize("gap", [8.0, 24.0])
+@pytest.mark.parametrize("causal", [False, True])
+def test_first_tile_second_half_dominates(cuda, config, gap, causal):
+    # gap 8: p up to 2^8 beside the stabiliser, no checked pass; gap 24: p
+    # past fp16's range (2^24), which the range check sends to the checked
+    # pass.  Either way the result is the oracle's.
+    q, k, v = _second_block_dominates(gap, seed=71)
+    if not config_fits(config, k.shape[2]):
+        q, k, v = q[:, :, :256], k[:, :, :256], v[:, :, :256]
+    out = run_capi(q, k, v, 0.125, causal, cuda, config=config)
+    assert_close_oracle(out, q, k, v, 0.125, causal, peaked=True)
+
+
 def test_deterministic(cuda):
     q, k, v = make_qkv(2, 8, 1000, 64, seed=51)
     for causal in (False, True):
