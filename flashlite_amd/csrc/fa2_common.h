@@ -638,23 +638,9 @@ struct Rows {
     const float a0 = __shfl(lacc[0], src), a1 = __shfl(lacc[1], src);
     return g == 0 ? (col < 16 ? a0 : a1) : 0.0f;
   }
-  // Softmax share of slot I: scores 2(I%8), 2(I%8)+1 of key block I/8 ->
-  // two exponentials and one fp16 pack into dword I of the tile's P operand
-  // (exponentiate() spread over 16 slots).
-  template <int I>
-  __device__ __forceinline__ void exp_slot(const float16_t (&s)[2], V8 (&pn)[2][2]) const {
-    constexpr int kb = I >> 3, r = 2 * (I & 7), h = r >> 3, e = r & 7;
-    float x0 = s[kb][r], x1 = s[kb][r + 1];
-    if (SCALED) {
-      x0 *= cr;
-      x1 *= cr;
-    }
-    const float e0 = __builtin_amdgcn_exp2f(x0), e1 = __builtin_amdgcn_exp2f(x1);
-    pn[kb][h][e] = (T)e0;
-    pn[kb][h][e + 1] = (T)e1;
-  }
-  // The same split in two steps, for schedules that scale one slot ahead:
-  // the scaled scores of slot I's pair (times cr when SCALED) ...
+  // Softmax share of slot I, in two steps for schedules that scale one slot
+  // ahead: the scaled scores of slot I's pair (scores 2(I%8), 2(I%8)+1 of key
+  // block I/8, times cr when SCALED) ...
   template <int I>
   __device__ __forceinline__ void scale_pair(const float16_t (&s)[2], float (&x)[2]) const {
     constexpr int kb = I >> 3, r = 2 * (I & 7);
@@ -696,24 +682,6 @@ struct Rows {
     if constexpr (I & 1) t[I >> 1] = p_pair(pn, I - 1) + p_pair(pn, I);
     if constexpr ((I & 3) == 3) t[8 + (I >> 2)] = t[(I >> 1) - 1] + t[I >> 1];
     if constexpr ((I & 7) == 7) t[12 + (I >> 3)] = t[8 + (I >> 2) - 1] + t[8 + (I >> 2)];
-  }
-  // fp32 row-sum share of slot I: the slot's two p, recomputed from the
-  // scores (the exponentials of exp_slot, which the compiler shares), in
-  // four partial chains.
-  template <int I>
-  __device__ __forceinline__ static void sum_slot_f32(const float16_t (&s)[2], float (&sum)[4],
-                                                      float crr) {
-    constexpr int kb = I >> 3, r = 2 * (I & 7);
-    float x0 = s[kb][r], x1 = s[kb][r + 1];
-    if (SCALED) {
-      x0 *= crr;
-      x1 *= crr;
-    }
-    const float e = __builtin_amdgcn_exp2f(x0) + __builtin_amdgcn_exp2f(x1);
-    if constexpr (I < 4)
-      sum[I] = e;
-    else
-      sum[I & 3] += e;
   }
   // This lane's tile sum in fp32 from the two level-3 nodes (each half of
   // the root sums 16 of the lane's 32 values).  A tile whose sum leaves the
@@ -931,34 +899,7 @@ struct Rows {
     l += exponentiate(s);
   }
   // Split key range: the partner wave holds the same rows over a disjoint
-  // key range.  Its O, m and l go through LDS as part[k * 64 + lane]
-  // (k < 32: O, 32: m, 33: l) and are combined at the larger m.
-  __device__ __forceinline__ void save_partial(float* part, int lane) const {
-#pragma unroll
-    for (int db = 0; db < 2; ++db)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) part[(16 * db + r) * 64 + lane] = o[db][r];
-    part[32 * 64 + lane] = m;
-    part[33 * 64 + lane] = l;
-  }
-  // Symmetric in the two ranges: a row with no key in one range (l == 0
-  // across the lane pair) takes the other's values.
-  __device__ __forceinline__ void merge_partial(const float* part, int lane) {
-    const float m1 = part[32 * 64 + lane], l1 = part[33 * 64 + lane];
-    const bool has0 = pair_sum(l) > 0.0f;
-    const bool has1 = pair_sum(l1) > 0.0f;
-    const float mm = has0 ? (has1 ? fmaxf(m, m1) : m) : m1;
-    const float k = SCALED ? cr : 1.0f;
-    const float a0 = has0 ? __builtin_amdgcn_exp2f(k * (m - mm)) : 0.0f;
-    const float a1 = has1 ? __builtin_amdgcn_exp2f(k * (m1 - mm)) : 0.0f;
-    l = a0 * l + a1 * l1;
-#pragma unroll
-    for (int db = 0; db < 2; ++db)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) o[db][r] = a0 * o[db][r] + a1 * part[(16 * db + r) * 64 + lane];
-    m = mm;
-  }
-  // The same exchange through LDS in 16-byte chunks, chunk-major
+  // key range.  Its O, m and l go through LDS in 16-byte chunks, chunk-major
   // (part4[c * 64 + lane]: c < 8 O[c/4][4(c%4) .. +3], c = 8 {m, l}): nine
   // 128-bit accesses per lane instead of 34 32-bit ones, each chunk 1 KiB
   // contiguous over the wave.
@@ -970,6 +911,8 @@ struct Rows {
     }
     part4[8 * 64 + lane] = make_float4(m, l, 0.0f, 0.0f);
   }
+  // Symmetric in the two ranges: a row with no key in one range (l == 0
+  // across the lane pair) takes the other's values.
   __device__ __forceinline__ void merge_partial4(const float4* part4, int lane) {
     const float4 ml = part4[8 * 64 + lane];
     const float m1 = ml.x, l1 = ml.y;
