@@ -105,9 +105,9 @@ fa2_fwd_slot_kernel(const T* Q, const T* __restrict__ K, const T* __restrict__ V
   // Slot fences: with two waves per SIMD the even spread of each slot's
   // work keeps the matrix cores busy; a lone wave per SIMD (2 x 2 waves, one
   // group per CU) runs 2-3% faster left to the compiler's own order, and so
-  // do causal 4-wave groups (0.5-4%), whose heavy blocks end their walks
-  // alone on their CU.
-  constexpr bool kFence = W * SPLIT * kWgPerCu > 4 && !(CAUSAL && kWgPerCu == 2);
+  // do causal fp16 4-wave groups (0.5-4%), whose heavy blocks end their walks
+  // alone on their CU (bf16 ones lost 2.5% at B1 H16 N16384 without them).
+  constexpr bool kFence = W * SPLIT * kWgPerCu > 4 && !(CAUSAL && kWgPerCu == 2 && kFp16);
   static_assert(kSegs * W == 8, "tile split");
   static_assert(FV >= 2 && FV <= 6, "fetch distance");
   static_assert(kAhead % 2 == 0 && kAhead < 16, "read-ahead");
