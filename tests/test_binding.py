@@ -172,6 +172,39 @@ def test_c4_out_buffer_reused_100_times(cuda):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("shape,causal", [((2, 8, 4096), False), ((2, 8, 4096), True),
+                                          ((2, 8, 1024), True), ((32, 32, 256), True)])
+def test_flash2_out_buffer_under_graph_capture(cuda, shape, causal):
+    # forward_flash2 with out= allocates nothing, so a HIP graph can capture
+    # it: three replays, with eager work and synchronisations between them,
+    # each equal bit for bit to the eager call on the same inputs
+    from flashlite_amd.workloads import make_qkv
+
+    b, h, n = shape
+    q16, k16, v16 = make_qkv(b, h, n, 64, seed=83)
+    q, k, v = (torch.from_numpy(x).to(cuda) for x in (q16, k16, v16))
+    eager = flash_attn_wmma.forward_flash2(q, k, v, 0.125, causal)
+    torch.cuda.synchronize(cuda)
+    out = torch.full_like(q, float("nan"))
+    graph = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream(cuda)
+    side.wait_stream(torch.cuda.current_stream(cuda))
+    with torch.cuda.stream(side):
+        flash_attn_wmma.forward_flash2(q, k, v, 0.125, causal, out=out)  # warm-up
+    torch.cuda.current_stream(cuda).wait_stream(side)
+    torch.cuda.synchronize(cuda)
+    with torch.cuda.graph(graph):
+        flash_attn_wmma.forward_flash2(q, k, v, 0.125, causal, out=out)
+    for _ in range(3):
+        out.fill_(float("nan"))
+        torch.cuda.synchronize(cuda)
+        graph.replay()
+        torch.cuda.synchronize(cuda)
+        assert torch.equal(out, eager)
+    del graph
+
+
+@pytest.mark.gpu
 def test_naive_via_binding(cuda):
     from oracle import attention_fp32, error_stats
     from flashlite_amd.workloads import make_qkv
