@@ -23,7 +23,8 @@ namespace {
 //
 // Same work per iteration j as fa2_fwd_kernel (GEMM1, GEMM2 of tile j-1
 // with P(j-1), softmax of tile j), laid out as 16 MFMA slots separated by
-// scheduling fences (slot map: Rows::read_slot / mfma_slot).  Each slot
+// scheduling fences where two waves share a SIMD (kFence; slot map:
+// Rows::read_slot / mfma_slot).  Each slot
 // carries two exponentials of the softmax with their fp16 pack and row-sum
 // share, and the LDS read of the A operand of slot +kAhead.  Measured on
 // gfx950: two exponentials and two simple VALU ops issue free under one
