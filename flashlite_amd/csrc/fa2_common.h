@@ -367,15 +367,18 @@ __device__ __forceinline__ void fetch_tile_z(const i32x4_t& rs, const uint8_t* s
 
 // DMA of the 32 query rows [q, q + 32) of a head (rows >= N_q read as
 // zeros) into `qblk`, laid out as the first half of a K tile (Rows::
-// set_q_lds reads it): 4 fetches of 1 KiB per wave, counted by vmcnt.
-template <class T>
+// set_q_lds reads it): 4 fetches of 1 KiB, counted by vmcnt, or with kParts
+// waves sharing the block, the 4 / kParts of them of part `part`.
+template <int kParts = 1, class T>
 __device__ __forceinline__ void fetch_q_block(const T* Qh, int q_sr, int q, int seq,
-                                              uint8_t* qblk, int lane) {
+                                              uint8_t* qblk, int lane, int part = 0) {
+  static_assert(kParts == 1 || kParts == 2 || kParts == 4, "Q block parts");
+  constexpr int kSegs = 4 / kParts;
   const int rows = min(32, seq - q);
   const i32x4_t rq = buffer_rsrc(Qh + (long long)(rows > 0 ? q : 0) * q_sr,
                                  rows > 0 ? (rows - 1) * (2 * q_sr) + kRowBytes : 0);
-  const FetchOff<4> fq = fetch_offsets<4, false>(0, lane, 2 * q_sr);
-  fetch_tile_z<4>(rq, qblk, 0, 1, 0, fq);
+  const FetchOff<kSegs> fq = fetch_offsets<kSegs, false>(part, lane, 2 * q_sr);
+  fetch_tile_z<kSegs>(rq, qblk, 0, 1, part, fq);
 }
 
 template <int kSegs>

@@ -98,7 +98,9 @@ fa2_fwd_slot_kernel(const T* Q, const T* __restrict__ K, const T* __restrict__ V
   // LDS reads of the first kAhead slots (K slots: 1, V slots: 2).
   constexpr int kTailReads = kAhead + kAhead / 2;
   constexpr int kRingBytes = kSlots * kTileBytes;
-  constexpr int kQBytes = W * SPLIT * 32 * kRowBytes;  // each wave's 32 query rows
+  // Each row block's 32 query rows; with SPLIT the two streams' waves of a
+  // row block share them, each fetching half.
+  constexpr int kQBytes = W * 32 * kRowBytes;
   // Two work-groups share a CU when both rings and Q blocks fit its 160 KiB
   // and the waves fit two per SIMD (<= 4 waves each).
   constexpr int kWgPerCu =
@@ -166,7 +168,7 @@ fa2_fwd_slot_kernel(const T* Q, const T* __restrict__ K, const T* __restrict__ V
     kv_rsrc_rows(geom, bh, K, V, w.tend * kBc, w.rk, w.rv);
     return w;
   };
-  uint8_t* const qblk = qbuf + wave * 32 * kRowBytes;
+  uint8_t* const qblk = qbuf + rw * 32 * kRowBytes;
   // PAIR: the next block's Q and first two K tiles, fetched during this
   // block's merge and store.
   bool prefetched = false;
@@ -208,7 +210,7 @@ fa2_fwd_slot_kernel(const T* Q, const T* __restrict__ K, const T* __restrict__ V
   // V(0)) fetched during the first block's merge, in the same order, so
   // the waits below count the same fetches.)
   if (!PAIR || !prefetched) {
-    fetch_q_block(hp.q, geom.q_sr, q0 + 32 * rw, seq, qblk, lane);
+    fetch_q_block<SPLIT>(hp.q, geom.q_sr, q0 + 32 * rw, seq, qblk, lane, stream);
     prologue_group(Ic<0>{});
     prologue_group(Ic<1>{});
   }
@@ -454,7 +456,7 @@ fa2_fwd_slot_kernel(const T* Q, const T* __restrict__ K, const T* __restrict__ V
     // flag's barriers, or the checked pass's last one): the next block's Q,
     // K(0), K(1) and V(0) go out now, to land during the merge and store.
     const Walk nx = walk_of(bi + 1);
-    fetch_q_block(hp.q, geom.q_sr, nx.q0 + 32 * rw, seq, qblk, lane);
+    fetch_q_block<SPLIT>(hp.q, geom.q_sr, nx.q0 + 32 * rw, seq, qblk, lane, stream);
     fetch_tile_z<kSegs>(nx.rk, rings.kslot(Ic<0>{}), nx.tbeg, nx.tend, rw, fk);
     fetch_tile_z<kSegs>(nx.rk, rings.kslot(Ic<1>{}), nx.tbeg + 1, nx.tend, rw, fk);
     fetch_tile_z<kSegs>(nx.rv, rings.vslot(Ic<0>{}), nx.tbeg, nx.tend, rw, fv);
