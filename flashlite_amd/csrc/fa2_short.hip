@@ -23,16 +23,17 @@ namespace {
 // the CUs).  Here a work-group of 4 waves owns one 32-row query block and
 // wave w the key tiles [2w, 2w+2): a quarter of at most 512 keys.  Each wave
 // fetches its own two K and two V tiles into its own 32 KiB of LDS by DMA
-// and reads nothing another wave wrote, so no barrier precedes the compute;
-// Q comes through 4 KiB of LDS by the same DMA, issued first.  Each wave
+// and reads no K or V another wave wrote; the block's Q comes through one
+// shared 4 KiB of LDS by the same DMA, issued first, a quarter by each
+// wave, and one barrier publishes it.  Each wave
 // computes both tiles' scores, takes their exact row max as the one
 // stabiliser (every p <= 1, so no range check and no second pass), then
 // exponentiates and multiplies tile by tile; the quarters' O, m and l
 // merge through LDS in 16-byte chunks at their larger m: 1, 2 and 3 into
 // 0, which stores.  C1 then runs 1024
 // waves of 2 tiles instead of 256 waves of 8.  LDS: 4 x 32 KiB, one
-// work-group per CU, plus 4 KiB of Q per wave.  (Eight waves of one tile
-// each, two per SIMD, measured 7% slower on C1.)
+// work-group per CU, plus 4 KiB of Q.  (Eight waves of one tile each, two
+// per SIMD, measured 7% slower on C1.)
 //
 // RB = 2 (more than 256 blocks of 32 rows, up to 512): a work-group of 8
 // waves owns two 32-row blocks, wave 4 rb + q taking row block rb and key
