@@ -287,7 +287,9 @@ def main():
                    "tile_config": capi.config_name(cfg)},
         "frac_mfma_peak": round(value / MFMA_PEAK_TFLOPS, 4),
         "latency_ms": {"noncausal_median": round(nc["med"], 5), "noncausal_min": round(nc["mn"], 5),
-                       "causal_median": round(ca["med"], 5), "causal_min": round(ca["mn"], 5)},
+                       "noncausal_mean": round(nc["mean"], 5),
+                       "causal_median": round(ca["med"], 5), "causal_min": round(ca["mn"], 5),
+                       "causal_mean": round(ca["mean"], 5)},
         "causal": {
             "value": round(ca["flops"] / (ca["wall_ms"] * 1e-3) / 1e12, 2),
             "ms_per_step": round(ca["wall_ms"], 5),
