@@ -37,6 +37,7 @@ from __future__ import annotations
 import argparse
 import json
 import math
+import os
 import sys
 from typing import Callable, Optional
 
@@ -291,6 +292,7 @@ def main(argv=None) -> int:
             return 1
         results["causal" if causal else "noncausal"] = r
     if args.json:
+        os.makedirs(os.path.dirname(os.path.abspath(args.json)), exist_ok=True)
         with open(args.json, "w") as f:
             json.dump(results, f, indent=1)
     return 0
