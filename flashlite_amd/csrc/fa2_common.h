@@ -98,7 +98,6 @@ namespace {
 
 typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
 typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
-typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
 typedef short short4_t __attribute__((ext_vector_type(4)));
 typedef float float16_t __attribute__((ext_vector_type(16)));
 typedef float float4_t __attribute__((ext_vector_type(4)));
@@ -650,49 +649,14 @@ struct Rows {
     x[0] = SCALED ? s[kb][r] * cr : s[kb][r];
     x[1] = SCALED ? s[kb][r + 1] * cr : s[kb][r + 1];
   }
-  // ... and their exponentials, packed into dword I of the P operand
-  // (returned for an fp32 row sum).
+  // ... and their exponentials, packed into dword I of the P operand (the
+  // row sums come from the matrix core, init_msum).
   template <int I>
-  __device__ __forceinline__ float exp_pair(const float (&x)[2], V8 (&pn)[2][2]) const {
+  __device__ __forceinline__ void exp_pair(const float (&x)[2], V8 (&pn)[2][2]) const {
     constexpr int kb = I >> 3, r = 2 * (I & 7), h = r >> 3, e = r & 7;
     const float e0 = __builtin_amdgcn_exp2f(x[0]), e1 = __builtin_amdgcn_exp2f(x[1]);
     pn[kb][h][e] = (T)e0;
     pn[kb][h][e + 1] = (T)e1;
-    return e0 + e1;
-  }
-  // fp32 row-sum share of slot I from its pair's sum, in four chains.
-  template <int I>
-  __device__ __forceinline__ static void sum_pair_f32(float e, float (&sum)[4]) {
-    if constexpr (I < 4)
-      sum[I] = e;
-    else
-      sum[I & 3] += e;
-  }
-  // Dword i (0-15) of a tile's P operand: the fp16 pair of slot i.
-  __device__ __forceinline__ static half2_t p_pair(const half8_t (&pn)[2][2], int i) {
-    const half8_t& v = pn[i >> 3][(i >> 2) & 1];
-    const int e = 2 * (i & 3);
-    return (half2_t){v[e], v[e + 1]};
-  }
-  // Row-sum share of slot I: a pairwise tree of packed fp16 additions over
-  // the tile's P, i.e. the fp16-rounded p that GEMM2 multiplies (level 1
-  // at odd slots, level 2 every 4th, level 3 every 8th; sum_root finishes
-  // it).  One v_pk_add_f16 per slot instead of two fp32 adds keeps a slot's
-  // VALU work within what issues under one MFMA.  t[0..7] level 1, t[8..11]
-  // level 2, t[12..13] level 3.
-  template <int I>
-  __device__ __forceinline__ static void sum_slot(const half8_t (&pn)[2][2], half2_t (&t)[14]) {
-    if constexpr (I & 1) t[I >> 1] = p_pair(pn, I - 1) + p_pair(pn, I);
-    if constexpr ((I & 3) == 3) t[8 + (I >> 2)] = t[(I >> 1) - 1] + t[I >> 1];
-    if constexpr ((I & 7) == 7) t[12 + (I >> 3)] = t[8 + (I >> 2) - 1] + t[8 + (I >> 2)];
-  }
-  // This lane's tile sum in fp32 from the two level-3 nodes (each half of
-  // the root sums 16 of the lane's 32 values).  A tile whose sum leaves the
-  // fp16-safe range overflows to inf here or exceeds kSumLimit; either way
-  // the caller's range check sends the block to the checked pass.
-  __device__ __forceinline__ static float sum_root(const half2_t (&t)[14]) {
-    const half2_t r = t[12] + t[13];
-    return (float)r[0] + (float)r[1];
   }
   // Masks keys >= kv_lim and, when causal, keys past the lane's diagonal
   // (tile t).  Score r of block kb is key k0 + 4g + c with the constant

@@ -43,10 +43,14 @@ namespace {
 // last read in iteration X-FV-2 and fetched in iteration X-FV-1; V(X) in
 // that of V(X-FV-2), last read in iteration X-FV-1 and fetched in X-FV.
 //
-// Row sums: a packed-fp16 tree (Rows::sum_slot) on tiles that need no mask,
-// fp32 adds on the masked ones (diagonal / tail), where a short causal row
-// sums a few p.  Blocks whose first pass saw a tile sum out of the
-// fp16-safe range are recomputed by a plain one-tile-per-step checked pass.
+// Row sums on the matrix core (Rows::init_msum): each key step's GEMM2 slot
+// carries a 16x16x32 MFMA that sums the fp16- (bf16-) rounded p of that
+// step, the weights GEMM2 multiplies, in fp32, four per tile in place of
+// a VALU sum.  A packed-fp16 tree of the same p (15 adds per tile) ran as
+// fast but rounded its partial sums to fp16: up to about 1e-3 of l, which
+// moved moderately peaked rows (sm_scale -0.3) past the 2e-3 bound.  Blocks
+// whose row sums leave the safe range (above 2^40, inf or NaN) are
+// recomputed by a plain one-tile-per-step checked pass.
 //
 // SPLIT = 2 (configurations br128_bc64_w4x2_slot, W = 4, and
 // br64_bc64_w2x2_slot, W = 2): 2W waves hold the same 32W query rows (W = 4:
@@ -78,16 +82,7 @@ fa2_fwd_slot_kernel(const T* Q, const T* __restrict__ K, const T* __restrict__ V
                     const Geom geom, int nqb, float cq, float cr) {
   using RowsT = Rows<CAUSAL, SCALED, T>;
   using V8 = typename RowsT::V8;
-  // fp16: unmasked tiles sum P with the packed-fp16 tree; bf16 P keeps
-  // fp32 sums throughout (an 8-bit mantissa tree would cost accuracy).
   constexpr bool kFp16 = __is_same(T, _Float16);
-  // The packed-fp16 row-sum tree on unmasked tiles (fp16).
-  constexpr bool kTree = kFp16;
-  // bf16: row sums on the matrix core (Rows::init_msum), four 16x16x32 MFMAs
-  // per tile in place of 32 fp32 adds, measured 4-7% faster on B2 H8 N4096.
-  // For fp16 the packed tree's 15 adds cost less than the MFMAs (3% the
-  // other way), so it keeps the tree.
-  constexpr bool kMfmaSum = !kFp16;
   constexpr int FK = FV + 1;
   constexpr int kSlots = FV + 2;  // per ring
   constexpr int kUnroll = (kSlots % 2 == 0) ? kSlots : 2 * kSlots;
@@ -220,7 +215,7 @@ fa2_fwd_slot_kernel(const T* Q, const T* __restrict__ K, const T* __restrict__ V
   FL_TL_STAMP(tl_first);
   sync_ring_ahead<kDmaPerIter, 0>();  // Q, K(0)
   rows.init_lds(qblk, lane, q0 + 32 * rw, seq, geom.seq_k, geom.coff, cq, cr);
-  if constexpr (kMfmaSum) rows.init_msum(lane);
+  rows.init_msum(lane);
   if (SPLIT == 2 && stream == 0) rows.kv_lim = min(rows.kv_lim, tend * kBc);
   // Iterations j < jm need no mask on tiles tbeg + j and tbeg + j + 1.
   int tm = rows.kv_lim >> 6;
@@ -247,7 +242,6 @@ fa2_fwd_slot_kernel(const T* Q, const T* __restrict__ K, const T* __restrict__ V
   });
   sync_ring_ahead<(FV - 1) * kDmaPerIter, kAhead / 2>();  // K(1), V(0)
 
-  uint64_t out_of_range = 0;
   // Iteration kinds (bits): a full iteration j runs GEMM1 of tile j block 1
   // (even slots 0-6) and of tile j+1 block 0 (even slots 8-14), GEMM2 of
   // tile j-1 (odd slots) and the softmax of tile j.  kFirst (j = 0): block
@@ -282,8 +276,6 @@ fa2_fwd_slot_kernel(const T* Q, const T* __restrict__ K, const T* __restrict__ V
 #pragma unroll
     for (int a = 0; a < kAhead; ++a)
       if (runs(Kd, a)) op[a] = ahead[a];
-    half2_t tree[14];
-    float sum[4];
     // SCALED: each slot scales the next slot's pair, so a slot's
     // exponentials never wait on its own multiplies.
     float xs[2][2];
@@ -293,9 +285,9 @@ fa2_fwd_slot_kernel(const T* Q, const T* __restrict__ K, const T* __restrict__ V
       // the read issued in the same slot.
       if constexpr (runs(Kd, L)) {
         if constexpr (kFold && L % 2 == 0 && L >= 8)
-          rows.template gemm2_step<fold_db(L), fold_t(L), kMfmaSum>(op[L], P);
+          rows.template gemm2_step<fold_db(L), fold_t(L), true>(op[L], P);
         else
-          rows.template mfma_slot<L, kMfmaSum>(op[L], S, Pp);
+          rows.template mfma_slot<L, true>(op[L], S, Pp);
       }
       if constexpr (kFence) __builtin_amdgcn_sched_barrier(0);
       if constexpr (L + kAhead < 16) {
@@ -316,31 +308,16 @@ fa2_fwd_slot_kernel(const T* Q, const T* __restrict__ K, const T* __restrict__ V
         top[ti] = rows.read_v_op(rings.vslot(Ic<I>{}), ti & 1, 2 + (ti >> 1));
       }
       if constexpr (L == 0) rows.template scale_pair<0>(S, xs[0]);
-      const float epair = rows.template exp_pair<L>(xs[L & 1], P);
-      if constexpr (kMfmaSum)
-        ;
-      else if constexpr (kTree && !kMasked)
-        RowsT::template sum_slot<L>(P, tree);
-      else
-        RowsT::template sum_pair_f32<L>(epair, sum);
+      rows.template exp_pair<L>(xs[L & 1], P);
       if constexpr (kMasked && L == 7) rows.template mask_block<1>(tbeg + j, S[1]);
       if constexpr (L < 15) rows.template scale_pair<L + 1>(S, xs[(L + 1) & 1]);
       if constexpr (kFence) __builtin_amdgcn_sched_barrier(0);
     });
-    if constexpr (!kMfmaSum) {
-      float tot;
-      if constexpr (kTree && !kMasked)
-        tot = RowsT::sum_root(tree);
-      else
-        tot = (sum[0] + sum[1]) + (sum[2] + sum[3]);
-      rows.l += tot;
-      out_of_range |= __builtin_amdgcn_ballot_w64(!(tot <= kSumLimit));
-    }
     if constexpr (kFold) {
       // GEMM2 of tile j's last 32 keys (P complete since slot 15)
       static_for(std::make_integer_sequence<int, kLastTail>{}, [&](auto t) __attribute__((always_inline)) {
         constexpr int ti = decltype(t)::value;
-        rows.template gemm2_step<ti & 1, 2 + (ti >> 1), kMfmaSum>(top[ti], P);
+        rows.template gemm2_step<ti & 1, 2 + (ti >> 1), true>(top[ti], P);
       });
     }
     if constexpr (kMasked && !kFold) rows.template mask_block<0>(tbeg + j + 1, S[0]);
@@ -402,16 +379,14 @@ fa2_fwd_slot_kernel(const T* Q, const T* __restrict__ K, const T* __restrict__ V
     }
   }
   FL_TL_STAMP(tl_loop_end);
-  if constexpr (kMfmaSum) {
-    // Every p of the first pass is in its row's sum, so a sum within 2^40
-    // bounds every p by 2^40 (finite O terms for any |V| below 2^88); a
-    // larger sum, inf or NaN (a row max far above the first tile's) sends
-    // the block to the checked pass.
-    rows.l = rows.msum_share();
-    out_of_range = __builtin_amdgcn_ballot_w64(!(rows.l <= kMsumLimit));
-  }
+  // Every p of the first pass is in its row's sum, so a sum within 2^40
+  // bounds every p by 2^40 (finite O terms for any |V| below 2^88); a
+  // larger sum, inf or NaN (a row max far above the first tile's, or an
+  // fp16 p past 65504) sends the block to the checked pass.
+  rows.l = rows.msum_share();
+  const uint64_t out_of_range = __builtin_amdgcn_ballot_w64(!(rows.l <= kMsumLimit));
 
-  // ---- checked pass, when any wave saw a tile sum out of range ----
+  // ---- checked pass, when any wave saw a row sum out of range ----
   // The work-group's flag lives in the last 16 bytes of the V rings, which
   // neither the checked pass (slot 0) nor the streams' exchange touches
   // (the rings are idle here: every wave has drained its fetches and reads

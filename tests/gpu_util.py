@@ -96,12 +96,15 @@ def assert_close_oracle(out, q16, k16, v16, sm_scale, causal, rows=None, max_abs
 
 
 def redo_expected(q16, k16, sm_scale, causal):
-    """True when the kernel's branch-free first pass must hand the block to
+    """True when a branch-free first pass with a per-tile range check (the
+    pipelined, streaming and head_dim-128 kernels) must hand the block to
     its checked pass: some row has, in a 64-key tile after its first, a lane
     half (32 of the 64 keys) whose sum of 2^(s - m0) exceeds 2^15, m0 being
     the row's max over the first tile and s its base-2 logits.  (The
-    slot-scheduled kernels take m0 over the first tile's first 32 keys
-    only, which can only make the hand-over more likely.)"""
+    slot-scheduled kernels take m0 over the first tile's first 32 keys and
+    check once, at the end: a p past fp16's range (2^16) or a row sum past
+    2^40 hands the block over.  The peaked inputs of the tests reach gaps
+    of 2^30 and more, which does both.)"""
     import numpy as np
 
     log2e = float(np.float32(1.4426950408889634))

@@ -5,8 +5,9 @@ has them), every output row is compared with the fp32 oracle for:
 
 * the library's choice (``config=-1``): the reference's score arithmetic --
   Q unscaled, each fp32 score multiplied by ``sm_scale * log2 e``
-  (``kernel_flash2.cu:188-195``, ``:529-536``) -- with the packed-fp16
-  row-sum tree of the fp16-rounded p on unmasked tiles;
+  (``kernel_flash2.cu:188-195``, ``:529-536``) -- with row sums of the
+  fp16-rounded p taken on the matrix core in fp32 (the slot-scheduled
+  configurations);
 * ``br64_bc64_w2`` (the pipelined schedule): the same scores with fp32 sums
   of the unrounded p (``kernel_flash2.cu:268-276``, ``:339``), i.e. the
   reference's row sums;
@@ -16,7 +17,8 @@ has them), every output row is compared with the fp32 oracle for:
 Each row of the printed table is ``workload mask variant max-abs mean-abs``
 (run with ``-s`` to see it).  Every variant must meet the north_star bound
 (max-abs 2e-3, mean-abs 2e-4), and the library's choice must stay within
-10% (mean-abs) of the fp32-sum variant: the tree may not cost accuracy.
+10% (mean-abs) of the fp32-sum variant: summing the rounded p may not cost
+accuracy.
 """
 
 import numpy as np
@@ -55,4 +57,4 @@ def test_full_output_error_table(cuda, name, causal):
     print()
     for label, (mx, mean) in rows:
         print(f"| {name} | {'causal' if causal else 'non-causal'} | {label} | {mx:.3e} | {mean:.3e} |")
-    assert rows[1][1][1] <= 1.1 * rows[2][1][1], "the fp16 row-sum tree costs accuracy"
+    assert rows[1][1][1] <= 1.1 * rows[2][1][1], "the row sums of the rounded p cost accuracy"
