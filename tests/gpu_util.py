@@ -9,6 +9,14 @@ from oracle import attention_fp32, error_stats
 # north_star tolerance for fp16 outputs against the fp32 oracle
 MAX_ABS = 2e-3
 MEAN_ABS = 2e-4
+# bf16: 8x that (unit roundoff 2^-8 against fp16's 2^-11).  The log-sum-exp
+# in natural-log units: l sums the rounded p that weight V, so a row whose
+# sum one p dominates moves ln l by up to that p's rounding, 2^-11 (fp16)
+# or 2^-8 = 3.9e-3 (bf16).
+BF16_MAX_ABS = 8 * MAX_ABS
+BF16_MEAN_ABS = 8 * MEAN_ABS
+LSE_MAX_ABS = {"fp16": 2e-3, "bf16": 4e-3}
+LSE_MEAN_ABS = {"fp16": 3e-4, "bf16": 1e-3}
 
 # Tile configurations by name.  The streaming configuration takes key ranges
 # of at most 256 keys only.
@@ -47,6 +55,43 @@ def run_capi(q16, k16, v16, sm_scale, causal, dev, config=-1, naive=False, out_f
     capi.check(rc)
     torch.cuda.synchronize(dev)
     return o.cpu().numpy()
+
+
+def wide_tol(kind):
+    """(max-abs, mean-abs) bound of an output of element type `kind`."""
+    return (BF16_MAX_ABS, BF16_MEAN_ABS) if kind == "bf16" else (MAX_ABS, MEAN_ABS)
+
+
+def wide_inputs(kind, b, h, nq, nk, d, seed, qk_scale=1.0):
+    """Seeded inputs (float32 arrays of the element type's values)."""
+    rs = np.random.RandomState(seed)
+    mk = lambda n, c: (rs.standard_normal((b, h, n, d)) * c).astype(np.float32)  # noqa: E731
+    q, k, v = mk(nq, qk_scale), mk(nk, qk_scale), mk(nk, 1.0)
+    if kind == "bf16":
+        from flashlite_amd.workloads import round_bf16
+
+        return tuple(round_bf16(x) for x in (q, k, v))
+    return tuple(x.astype(np.float16).astype(np.float32) for x in (q, k, v))
+
+
+def run_wide(kind, q, k, v, sm_scale, causal, dev, config=-1, lse=False, views=None):
+    """fp16 or bf16 (`kind`) at any head dim through fl_attn_fwd_{f16,bf16}_ex;
+    `views` maps the contiguous tensors to the strided ones to pass (default:
+    the contiguous tensors).  Returns (O, log-sum-exp or None) as float32."""
+    import torch
+
+    dt = torch.bfloat16 if kind == "bf16" else torch.float16
+    tq, tk, tv = (torch.from_numpy(np.ascontiguousarray(x)).to(dev).to(dt) for x in (q, k, v))
+    o = torch.full_like(tq, float("nan"))
+    if views is not None:
+        tq, tk, tv, o = views(tq, tk, tv, o)
+    ls = torch.full(tq.shape[:3], float("nan"), dtype=torch.float32, device=dev) if lse else None
+    p = capi.tensor_params_ex(tq, tk, tv, o, sm_scale, causal, lse=ls)
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    fn = capi.fwd_bf16_ex if kind == "bf16" else capi.fwd_ex
+    capi.check(fn(p, stream, config))
+    torch.cuda.synchronize(dev)
+    return o.float().cpu().numpy(), (ls.cpu().numpy() if lse else None)
 
 
 def sample_rows(n, count=256, seed=0):

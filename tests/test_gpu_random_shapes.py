@@ -4,14 +4,18 @@ same inputs.  A broad sweep beside the targeted tests: batch and head counts,
 query and key lengths drawn independently (N_k != N_q both ways, so causal
 rows with no visible key occur), both masks, and the scale sentinel (0.0),
 negative, small and peaked (1.0) scales.  Inputs are N(0,1) in fp16, as the
-reference's tests draw them (tests/test_correctness.py:38-41)."""
+reference's tests draw them (tests/test_correctness.py:38-41).  The second
+test does the same for the wider types (fp16 at head_dim 128, bf16 at 64 and
+128) through fl_attn_fwd_{f16,bf16}_ex, on contiguous or [B, N, H, D]
+layouts, with the log-sum-exp."""
 
 import numpy as np
 import pytest
 
 from flashlite_amd import capi
-from gpu_util import assert_close_oracle, config_fits, run_capi
-from oracle import attention_fp32
+from gpu_util import (LSE_MAX_ABS, LSE_MEAN_ABS, assert_close_oracle, config_fits, run_capi,
+                      run_wide, wide_inputs, wide_tol)
+from oracle import attention_fp32, attention_lse, error_stats
 
 NCFG = capi.num_configs()
 SCALES = (0.0, 0.125, -0.3, 0.05, 1.0)
@@ -53,3 +57,66 @@ def test_random_shape_every_config(cuda, case):
         print(f"random shape {_case_id(case)} config={config}", flush=True)
         out = run_capi(q, k, v, scale, causal, cuda, config=config)
         assert_close_oracle(out, q, k, v, scale, causal, ref=ref, peaked=peaked)
+
+
+# configurations built for each wider type (the others answer FL_ERR_BAD_CONFIG)
+_SLOT = ("br256_bc64_w8_slot", "br128_bc64_w4_slot")
+_BF16_D64 = _SLOT + ("br128_bc64_w4x2_slot", "br64_bc64_w2x2_slot", "br128_bc64_w4x2_pair",
+                     "br256_kv256_w8_stream", "br32_kv512_w4_quarters")
+WIDE_CONFIGS = {("fp16", 128): _SLOT, ("bf16", 128): _SLOT, ("bf16", 64): _BF16_D64}
+
+
+def _wide_cases(n=24, seed=20261203):
+    rs = np.random.RandomState(seed)
+    kinds = sorted(WIDE_CONFIGS)
+    out = []
+    for i in range(n):
+        kind, d = kinds[rs.randint(len(kinds))]
+        b = int(rs.randint(1, 3))
+        h = int(rs.randint(1, 4))
+        nq = int(rs.randint(1, 1100))
+        nk = nq if rs.rand() < 0.5 else int(rs.randint(1, 1100))
+        causal = bool(rs.rand() < 0.5)
+        scale = float(SCALES[rs.randint(len(SCALES))])
+        strided = bool(rs.rand() < 0.5)
+        out.append((i, kind, d, b, h, nq, nk, causal, scale, strided))
+    return out
+
+
+def _wide_id(c):
+    i, kind, d, b, h, nq, nk, causal, scale, strided = c
+    return (f"{i}-{kind}-D{d}-B{b}H{h}-q{nq}-k{nk}-{'causal' if causal else 'full'}-s{scale}"
+            f"{'-bnhd' if strided else ''}")
+
+
+def _bnhd(*ts):
+    """The same values in [B, N, H, D] memory, passed as [B, H, N, D] views."""
+    return tuple(t.transpose(1, 2).contiguous().transpose(1, 2) for t in ts)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("case", _wide_cases(), ids=_wide_id)
+def test_random_shape_wide(cuda, case):
+    i, kind, d, b, h, nq, nk, causal, scale, strided = case
+    q = wide_inputs(kind, b, h, nq, nq, d, seed=3000 + i)[0]
+    _, k, v = wide_inputs(kind, b, h, nk, nk, d, seed=4000 + i)
+    ref = attention_fp32(q, k, v, scale, causal)
+    peaked = abs(scale) >= 1.0
+    ref_lse = None if peaked else attention_lse(q, k, scale, causal)
+    max_abs, mean_abs = wide_tol(kind)
+    names = [n for n in WIDE_CONFIGS[(kind, d)]
+             if config_fits(capi.config_id(n), nk)]
+    for config in [-1] + [capi.config_id(n) for n in names]:
+        print(f"random wide {_wide_id(case)} config={config}", flush=True)
+        out, lse = run_wide(kind, q, k, v, scale, causal, cuda, config=config, lse=not peaked,
+                            views=_bnhd if strided else None)
+        assert_close_oracle(out, q, k, v, scale, causal, ref=ref, max_abs=max_abs,
+                            mean_abs=mean_abs, peaked=peaked,
+                            mant_bits=7 if kind == "bf16" else 10)
+        if ref_lse is not None:
+            fin = np.isfinite(ref_lse)
+            assert np.array_equal(fin, np.isfinite(lse)), "lse -inf pattern"
+            if fin.any():
+                mx, mean = error_stats(lse[fin], ref_lse[fin])
+                assert mx <= LSE_MAX_ABS[kind] and mean <= LSE_MEAN_ABS[kind], (
+                    f"lse max-abs {mx:.3e} mean-abs {mean:.3e}")

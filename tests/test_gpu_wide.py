@@ -11,12 +11,14 @@ Tolerances against the fp32 oracle on the same inputs:
   fp16's (2^-11); the output rounding alone reaches 2^-9 |O| and P is
   rounded to bf16 before the PV product.  The inputs are bf16-exact values
   (``workloads.round_bf16``), so the oracle sees exactly what the kernel reads.
-* log-sum-exp (natural-log units): max-abs <= 2e-3 for both types; mean-abs
-  <= 3e-4 for fp16 and 1e-3 for bf16.  Every path keeps Q unscaled and
-  scales the fp32 scores, as the reference does; but at D = 64 the bf16 row
-  sum l is taken on the matrix core over the bf16-rounded p that weight V (relative
-  error up to 2^-9 = 1.95e-3 each, about 2^-10 on average), so ln l carries
-  about 1e-3 on rows that see few keys.
+* log-sum-exp (natural-log units): max-abs <= 2e-3 for fp16 and 4e-3 for
+  bf16; mean-abs <= 3e-4 for fp16 and 1e-3 for bf16.  Every path keeps Q
+  unscaled and scales the fp32 scores, as the reference does; but at D = 64
+  the row sum l is taken on the matrix core over the rounded p that weight V,
+  so that O is normalised by exactly its weights.  A bf16 p carries a
+  relative rounding error of up to 2^-8 = 3.9e-3 (about 2^-10 on average),
+  and on a row whose sum one p dominates ln l moves by up to that much
+  (2.9e-3 measured on a seeded random shape at sm_scale -0.3).
 A strided launch equals the contiguous launch of the same data bit for bit.
 """
 
@@ -24,60 +26,21 @@ import numpy as np
 import pytest
 
 from flashlite_amd import capi
-from gpu_util import (MAX_ABS, MEAN_ABS, PAIR_CFG, QUARTER_CFG, SLOT_W4_CFG, SLOT_W8_CFG,
-                      SPLIT2_CFG, SPLIT2W2_CFG, STREAM_CFG, half_ulp, sample_rows)
+from gpu_util import (BF16_MAX_ABS, BF16_MEAN_ABS, LSE_MAX_ABS, LSE_MEAN_ABS, MAX_ABS, MEAN_ABS,
+                      PAIR_CFG, QUARTER_CFG, SLOT_W4_CFG, SLOT_W8_CFG, SPLIT2_CFG, SPLIT2W2_CFG,
+                      STREAM_CFG, half_ulp, sample_rows)
+from gpu_util import run_wide as _run
+from gpu_util import wide_inputs as _inputs
+from gpu_util import wide_tol as _tol
 from oracle import attention_fp32, attention_lse, error_stats
 
 pytestmark = pytest.mark.gpu
 
-BF16_MAX_ABS = 8 * MAX_ABS
-BF16_MEAN_ABS = 8 * MEAN_ABS
-LSE_MAX_ABS = 2e-3
-LSE_MEAN_ABS = {"fp16": 3e-4, "bf16": 1e-3}
 SLOT_CFGS = [-1, SLOT_W8_CFG, SLOT_W4_CFG]
 KINDS = [("fp16", 64), ("fp16", 128), ("bf16", 64), ("bf16", 128)]
 WIDE = [k for k in KINDS if k != ("fp16", 64)]
 
 
-def _tol(kind):
-    return (BF16_MAX_ABS, BF16_MEAN_ABS) if kind == "bf16" else (MAX_ABS, MEAN_ABS)
-
-
-def _inputs(kind, b, h, nq, nk, d, seed, qk_scale=1.0):
-    """Seeded inputs (float32 arrays of the element type's values)."""
-    rs = np.random.RandomState(seed)
-    mk = lambda n, c: (rs.standard_normal((b, h, n, d)) * c).astype(np.float32)  # noqa: E731
-    q, k, v = mk(nq, qk_scale), mk(nk, qk_scale), mk(nk, 1.0)
-    if kind == "bf16":
-        from flashlite_amd.workloads import round_bf16
-
-        return tuple(round_bf16(x) for x in (q, k, v))
-    return tuple(x.astype(np.float16).astype(np.float32) for x in (q, k, v))
-
-
-def _torch_dtype(kind):
-    import torch
-
-    return torch.bfloat16 if kind == "bf16" else torch.float16
-
-
-def _run(kind, q, k, v, sm_scale, causal, dev, config=-1, lse=False, views=None):
-    """Launch through the C ABI; `views` maps the contiguous tensors to the
-    strided ones to pass (default: the contiguous tensors)."""
-    import torch
-
-    dt = _torch_dtype(kind)
-    tq, tk, tv = (torch.from_numpy(np.ascontiguousarray(x)).to(dev).to(dt) for x in (q, k, v))
-    o = torch.full_like(tq, float("nan"))
-    if views is not None:
-        tq, tk, tv, o = views(tq, tk, tv, o)
-    ls = torch.full(tq.shape[:3], float("nan"), dtype=torch.float32, device=dev) if lse else None
-    p = capi.tensor_params_ex(tq, tk, tv, o, sm_scale, causal, lse=ls)
-    stream = torch.cuda.current_stream(dev).cuda_stream
-    fn = capi.fwd_bf16_ex if kind == "bf16" else capi.fwd_ex
-    capi.check(fn(p, stream, config))
-    torch.cuda.synchronize(dev)
-    return o.float().cpu().numpy(), (ls.cpu().numpy() if lse else None)
 
 
 def _check(kind, out, ref, what):
@@ -118,7 +81,7 @@ def test_rectangular_with_lse(cuda, kind, d, config, causal):
         fin = np.isfinite(ref_lse)
         assert np.array_equal(fin, np.isfinite(lse)), f"{nq}x{nk}: lse -inf pattern"
         mx, mean = error_stats(lse[fin], ref_lse[fin]) if fin.any() else (0.0, 0.0)
-        assert mx <= LSE_MAX_ABS and mean <= LSE_MEAN_ABS[kind], (
+        assert mx <= LSE_MAX_ABS[kind] and mean <= LSE_MEAN_ABS[kind], (
             f"{nq}x{nk}: lse max-abs {mx:.3e} mean-abs {mean:.3e}")
 
 
@@ -226,7 +189,7 @@ def test_bf16_short_key_kernels(cuda, config, causal):
         fin = np.isfinite(ref_lse)
         assert np.array_equal(fin, np.isfinite(lse)), f"{nq}x{nk}: lse -inf pattern"
         mx, mean = error_stats(lse[fin], ref_lse[fin]) if fin.any() else (0.0, 0.0)
-        assert mx <= LSE_MAX_ABS and mean <= LSE_MEAN_ABS["bf16"], f"{nq}x{nk}: lse {mx:.3e}"
+        assert mx <= LSE_MAX_ABS["bf16"] and mean <= LSE_MEAN_ABS["bf16"], f"{nq}x{nk}: lse {mx:.3e}"
     b, h, n = (32, 32, 256) if config == STREAM_CFG else (4, 8, 512)
     q, k, v = _inputs("bf16", b, h, n, n, 64, seed=7)
     out, _ = _run("bf16", q, k, v, 0.125, causal, cuda, config=config)
@@ -258,7 +221,7 @@ def test_binding_wide(cuda):
 
     for kind, d in WIDE:
         q, k, v = _inputs(kind, 1, 4, 257, 300, d, seed=3)
-        dt = _torch_dtype(kind)
+        dt = torch.bfloat16 if kind == "bf16" else torch.float16
         tq, tk, tv = (torch.from_numpy(x).to(cuda).to(dt) for x in (q, k, v))
         for causal in (False, True):
             out, lse = flashlite_amd.forward_flash2_ex(tq, tk, tv, 0.0, causal, return_lse=True)
