@@ -94,6 +94,25 @@ def run_wide(kind, q, k, v, sm_scale, causal, dev, config=-1, lse=False, views=N
     return o.float().cpu().numpy(), (ls.cpu().numpy() if lse else None)
 
 
+def run_splitkv(tq, tk, tv, sm_scale, causal, splits, lse=True, o_fill=float("nan")):
+    """Split-KV through fl_attn_fwd_f16_splitkv with a NaN-filled workspace of
+    exactly the size the library asks for; returns (O, log-sum-exp or None,
+    workspace bytes) as device tensors."""
+    import torch
+
+    dev = tq.device
+    o = torch.full_like(tq, o_fill)
+    ls = torch.full(tq.shape[:3], float("nan"), dtype=torch.float32, device=dev) if lse else None
+    p = capi.tensor_params_ex(tq, tk, tv, o, sm_scale, causal, lse=ls)
+    need = capi.splitkv_workspace_bytes(p, splits)
+    assert need >= 0, capi.last_error()
+    ws = torch.full((max(need, 4) // 4,), float("nan"), dtype=torch.float32, device=dev)
+    capi.check(capi.fwd_splitkv(p, ws.data_ptr() if need else 0, need,
+                                torch.cuda.current_stream(dev).cuda_stream, splits))
+    torch.cuda.synchronize(dev)
+    return o, ls, need
+
+
 def sample_rows(n, count=256, seed=0):
     """Query rows to check on big shapes: both ends, block edges, random."""
     rs = np.random.RandomState(seed)

@@ -7,14 +7,15 @@ negative, small and peaked (1.0) scales.  Inputs are N(0,1) in fp16, as the
 reference's tests draw them (tests/test_correctness.py:38-41).  The second
 test does the same for the wider types (fp16 at head_dim 128, bf16 at 64 and
 128) through fl_attn_fwd_{f16,bf16}_ex, on contiguous or [B, N, H, D]
-layouts, with the log-sum-exp."""
+layouts, with the log-sum-exp; the third for split-KV decode (few query rows
+over up to 20000 keys, automatic, single and forced chunk counts)."""
 
 import numpy as np
 import pytest
 
 from flashlite_amd import capi
 from gpu_util import (LSE_MAX_ABS, LSE_MEAN_ABS, assert_close_oracle, config_fits, run_capi,
-                      run_wide, wide_inputs, wide_tol)
+                      run_splitkv, run_wide, to_dev, wide_inputs, wide_tol)
 from oracle import attention_fp32, attention_lse, error_stats
 
 NCFG = capi.num_configs()
@@ -120,3 +121,48 @@ def test_random_shape_wide(cuda, case):
                 mx, mean = error_stats(lse[fin], ref_lse[fin])
                 assert mx <= LSE_MAX_ABS[kind] and mean <= LSE_MEAN_ABS[kind], (
                     f"lse max-abs {mx:.3e} mean-abs {mean:.3e}")
+
+
+def _split_cases(n=24, seed=20261204):
+    rs = np.random.RandomState(seed)
+    out = []
+    for i in range(n):
+        b = int(rs.randint(1, 4))
+        h = int(rs.randint(1, 5))
+        lo, hi = ((1, 2), (2, 9), (9, 33), (33, 129))[rs.randint(4)]
+        nq = int(rs.randint(lo, hi))
+        nk = int(rs.randint(1, 20000))
+        causal = bool(rs.rand() < 0.5)
+        scale = float(SCALES[rs.randint(len(SCALES))])
+        splits = int((0, 1, int(rs.randint(2, 300)))[rs.randint(3)])
+        out.append((i, b, h, nq, nk, causal, scale, splits))
+    return out
+
+
+def _split_id(c):
+    i, b, h, nq, nk, causal, scale, splits = c
+    return f"{i}-B{b}H{h}-q{nq}-k{nk}-{'causal' if causal else 'full'}-s{scale}-x{splits}"
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("case", _split_cases(), ids=_split_id)
+def test_random_shape_splitkv(cuda, case):
+    i, b, h, nq, nk, causal, scale, splits = case
+    rs = np.random.RandomState(5000 + i)
+    q = rs.standard_normal((b, h, nq, 64)).astype(np.float32).astype(np.float16)
+    k = rs.standard_normal((b, h, nk, 64)).astype(np.float32).astype(np.float16)
+    v = rs.standard_normal((b, h, nk, 64)).astype(np.float32).astype(np.float16)
+    print(f"random split-KV {_split_id(case)}", flush=True)
+    tq, tk, tv = (to_dev(x, cuda) for x in (q, k, v))
+    peaked = abs(scale) >= 1.0
+    o, ls, _ = run_splitkv(tq, tk, tv, scale, causal, splits)
+    assert_close_oracle(o.float().cpu().numpy(), q, k, v, scale, causal, peaked=peaked)
+    if not peaked:
+        ref = attention_lse(q, k, scale, causal)
+        lse = ls.cpu().numpy()
+        assert np.array_equal(np.isneginf(lse), np.isneginf(ref)), "lse -inf pattern"
+        fin = np.isfinite(ref)
+        if fin.any():
+            mx, mean = error_stats(lse[fin], ref[fin])
+            assert mx <= LSE_MAX_ABS["fp16"] and mean <= LSE_MEAN_ABS["fp16"], (
+                f"lse max-abs {mx:.3e} mean-abs {mean:.3e}")

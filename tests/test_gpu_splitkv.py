@@ -10,6 +10,7 @@ import pytest
 
 from flashlite_amd import capi
 from gpu_util import assert_close_oracle, to_dev
+from gpu_util import run_splitkv as _run_split
 from oracle import attention_fp32, attention_lse, error_stats
 
 pytestmark = pytest.mark.gpu
@@ -22,22 +23,6 @@ def _qkv(b, h, nq, nk, seed):
     rs = np.random.RandomState(seed)
     mk = lambda n: rs.standard_normal((b, h, n, 64)).astype(np.float32).astype(np.float16)
     return mk(nq), mk(nk), mk(nk)
-
-
-def _run_split(tq, tk, tv, sm_scale, causal, splits, lse=True, o_fill=float("nan")):
-    import torch
-
-    dev = tq.device
-    o = torch.full_like(tq, o_fill)
-    ls = torch.full(tq.shape[:3], float("nan"), dtype=torch.float32, device=dev) if lse else None
-    p = capi.tensor_params_ex(tq, tk, tv, o, sm_scale, causal, lse=ls)
-    need = capi.splitkv_workspace_bytes(p, splits)
-    assert need >= 0, capi.last_error()
-    ws = torch.full((max(need, 4) // 4,), float("nan"), dtype=torch.float32, device=dev)
-    capi.check(capi.fwd_splitkv(p, ws.data_ptr() if need else 0, need,
-                                torch.cuda.current_stream(dev).cuda_stream, splits))
-    torch.cuda.synchronize(dev)
-    return o, ls, need
 
 
 # (2, 9000) with 1000 requested: 141 chunks, more than one wave's 64 lanes
