@@ -19,7 +19,8 @@ the rounded p on the matrix core and land about 3x closer).  The second
 test does the same for the wider types (fp16 at head_dim 128, bf16 at 64 and
 128) through fl_attn_fwd_{f16,bf16}_ex, on contiguous or [B, N, H, D]
 layouts, with the log-sum-exp; the third for split-KV decode (few query rows
-over up to 20000 keys, automatic, single and forced chunk counts)."""
+over up to 20000 keys, automatic, single and forced chunk counts); the
+fourth for the naive kernel (forward_naive) at head dims 1-200."""
 
 import numpy as np
 import pytest
@@ -176,3 +177,36 @@ def test_random_shape_splitkv(cuda, case):
             mx, mean = error_stats(lse[fin], ref[fin])
             assert mx <= LSE_MAX_ABS["fp16"] and mean <= LSE_MEAN_ABS["fp16"], (
                 f"lse max-abs {mx:.3e} mean-abs {mean:.3e}")
+
+
+def _naive_cases(n=16, seed=20261205):
+    rs = np.random.RandomState(seed)
+    out = []
+    for i in range(n):
+        b = int(rs.randint(1, 3))
+        h = int(rs.randint(1, 4))
+        d = int(rs.randint(1, 201))
+        nq = int(rs.randint(1, 1500))
+        nk = nq if rs.rand() < 0.5 else int(rs.randint(1, 1500))
+        causal = bool(rs.rand() < 0.5)
+        scale = float(SCALES[rs.randint(len(SCALES))])
+        out.append((i, b, h, d, nq, nk, causal, scale))
+    return out
+
+
+def _naive_id(c):
+    i, b, h, d, nq, nk, causal, scale = c
+    return f"{i}-B{b}H{h}-D{d}-q{nq}-k{nk}-{'causal' if causal else 'full'}-s{scale}"
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("case", _naive_cases(), ids=_naive_id)
+def test_random_shape_naive(cuda, case):
+    i, b, h, d, nq, nk, causal, scale = case
+    rs = np.random.RandomState(6000 + i)
+    q = rs.standard_normal((b, h, nq, d)).astype(np.float32).astype(np.float16)
+    k = rs.standard_normal((b, h, nk, d)).astype(np.float32).astype(np.float16)
+    v = rs.standard_normal((b, h, nk, d)).astype(np.float32).astype(np.float16)
+    print(f"random naive {_naive_id(case)}", flush=True)
+    out = run_capi(q, k, v, scale, causal, cuda, naive=True)
+    assert_close_oracle(out, q, k, v, scale, causal, peaked=True)
