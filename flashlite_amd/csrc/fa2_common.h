@@ -49,12 +49,10 @@
 // exact math since softmax is shift invariant; m never exceeds the running
 // max, so the row sum stays >= 1).  p is packed to fp16 for GEMM2.  Row
 // sums: the reference sums the unrounded fp32 p (kernel_flash2.cu:268-276,
-// :339); the fp16 slot schedules sum the fp16-rounded p that GEMM2
-// multiplies, with a packed-fp16 tree per tile and fp32 across tiles (the
-// same full-output errors as fp32 sums of the unrounded p, to three
-// digits), and bf16 tiles on the matrix core (Rows::init_msum).  Each lane
-// sums its own keys and the two halves of a row meet once, in the
-// epilogue.
+// :339), as the pipelined, streaming, key-quarter and head_dim-128 kernels
+// here do (each lane sums its own keys and the two halves of a row meet
+// once, in the epilogue); the slot schedules sum the rounded p that GEMM2
+// multiplies, in fp32 on the matrix core (Rows::init_msum).
 //
 // K/V staging.  Tiles are fetched straight into LDS with buffer_load ... lds
 // (no VGPRs, no LDS-store instructions; rows past N read as zeros through

@@ -423,7 +423,7 @@ def _stream_timeline(args, torch):
 
 def _quarter_timeline(args, torch):
     """Where the key-quarter kernel's time goes: per wave, its loads' issue
-    and landing, its two tiles, the merge tree and the store."""
+    and landing, its two tiles, the merge and the store."""
     import ctypes
 
     import numpy as np
