@@ -141,6 +141,17 @@ int select_fa2(const fl::FwdArgs& a) {
   // Past 576 keys, at most one group of 64 rows per CU: the key-range split
   // on 64-row groups (2 x 2 waves) in a single round.
   if (a.seq_k > 576 && wgs(64) <= cus) return fl::kCfgSplit2W2;
+  // Square causal problems over at least 4096 keys with at most one pair of
+  // 64-row blocks per CU (so more than half the CUs busy, the rule above
+  // having taken the rest): the 64-row block pairs, every work-group
+  // carrying the same tiles in one round at one wave per SIMD.  Measured
+  // 0-19% faster than the rules below would choose (B1 H2 N16384 109.2
+  // against 124.6 us for the 128-row pairs and 133.8 for the one-block
+  // split, B1 H1 N32768 223.7 against 239.9 and 268.6, B1 H3 N8192 55.4
+  // against 60.9, B1 H8 N4096 34.8 against 35.3); slower at N 2048 (B2 H8:
+  // 21.9 against 20.7) and when the pairs take a second round.
+  const int64_t pairs64 = (((int64_t)a.seq + 63) / 64 + 1) / 2 * a.batch_heads;
+  if (a.causal && a.seq == a.seq_k && a.seq_k >= 4096 && pairs64 <= cus) return fl::kCfgPairW2;
   const bool one_round = a.seq_k >= 2048 && wgs(128) <= cus;
   if (one_round && (!a.causal || wgs(128) >= cus / 4)) return fl::kCfgSplit2;
   // Causal over at least 4096 keys with more than one 128-row block but at
@@ -345,8 +356,8 @@ int select_any(const fl::FwdArgs& a) {
   if (!narrow_configs(a)) return select_fa2(a);
   if (a.head_dim == 64) {
     const int c = select_fa2(a);
-    if (c == fl::kCfgSplit2 || c == fl::kCfgSplit2W2 || c == fl::kCfgPair || c == fl::kStreamConfig ||
-        c == fl::kQuarterConfig)
+    if (c == fl::kCfgSplit2 || c == fl::kCfgSplit2W2 || c == fl::kCfgPair || c == fl::kCfgPairW2 ||
+        c == fl::kStreamConfig || c == fl::kQuarterConfig)
       return c;
   }
   const int64_t cus = fl::device_cus();
@@ -368,7 +379,7 @@ int fwd_ex(const fl_attn_params_ex* p, int32_t config, void* stream, int dtype, 
                 "%s: config %d is not built for %s at head_dim %d (use -1, %d or %d%s)", who,
                 (int)config, dtype == fl::kDtypeBF16 ? "bf16" : "fp16", a.head_dim,
                 fl::kSlotW8Config, fl::kSlotW4Config,
-                a.head_dim == 64 ? ", 2, 5, 6, 7 or 8" : "");
+                a.head_dim == 64 ? ", 2, 5, 6, 7, 8 or 9" : "");
   if (config == fl::kStreamConfig && !fl::stream_config_fits(a))
     return fail(FL_ERR_BAD_CONFIG, "%s: config %d needs N_k <= %d and row strides below 2^22 "
                 "(got N_k %d)", who, (int)config, fl::kStreamMaxKeys, a.seq_k);

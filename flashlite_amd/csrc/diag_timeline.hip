@@ -136,7 +136,7 @@ int fl_diag_slot_timeline(int mode, int causal, const void* q, const void* k, co
   const auto st = static_cast<hipStream_t>(stream);
   e = mode == 2   ? fl::diag_timeline_launch_slot_split(a, 4, st)
       : mode == 7 ? fl::diag_timeline_launch_slot_split(a, 2, st)
-      : mode == 9 ? fl::diag_timeline_launch_slot_pair(a, st)
+      : mode == 9 ? fl::diag_timeline_launch_slot_pair(a, 4, st)
                   : fl::diag_timeline_launch_slot(a, mode, st);
   return (int)e;
 }

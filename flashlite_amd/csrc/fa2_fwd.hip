@@ -17,6 +17,7 @@ const Fa2Config kFa2Configs[kNumFa2Configs] = {
     {4, "br32_kv512_w4_quarters"},
     {4, "br64_bc64_w2x2_slot"},
     {8, "br128_bc64_w4x2_pair"},
+    {4, "br64_bc64_w2x2_pair"},
 };
 
 bool stream_config_fits(const FwdArgs& a) {
@@ -36,7 +37,8 @@ hipError_t launch_fa2(const FwdArgs& a, int cfg, hipStream_t stream) {
     if (cfg == kSlotW4Config) return launch_slot(a, 4, stream);
     if (cfg == kCfgSplit2) return launch_slot_split(a, 4, stream);
     if (cfg == kCfgSplit2W2) return launch_slot_split(a, 2, stream);
-    if (cfg == kCfgPair) return launch_slot_pair(a, stream);
+    if (cfg == kCfgPair) return launch_slot_pair(a, 4, stream);
+    if (cfg == kCfgPairW2) return launch_slot_pair(a, 2, stream);
     if (cfg == kStreamConfig) return launch_stream(a, stream);
     if (cfg == kQuarterConfig) return launch_quarter(a, stream);
     return hipErrorInvalidValue;
@@ -46,7 +48,8 @@ hipError_t launch_fa2(const FwdArgs& a, int cfg, hipStream_t stream) {
     case kCfgW2: return launch_pipe(a, cfg, stream);
     case kCfgSplit2: return launch_slot_split(a, 4, stream);
     case kCfgSplit2W2: return launch_slot_split(a, 2, stream);
-    case kCfgPair: return launch_slot_pair(a, stream);
+    case kCfgPair: return launch_slot_pair(a, 4, stream);
+    case kCfgPairW2: return launch_slot_pair(a, 2, stream);
     case kSlotW8Config: return launch_slot(a, 8, stream);
     case kSlotW4Config: return launch_slot(a, 4, stream);
     case kStreamConfig: return launch_stream(a, stream);

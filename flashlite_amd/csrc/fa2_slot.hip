@@ -65,13 +65,14 @@ namespace {
 // its tiles, and heaviest-first dispatch of one work-group per CU then
 // balances the CUs.
 //
-// PAIR (SPLIT = 2, configuration br128_bc64_w4x2_pair): a work-group walks
-// two 128-row blocks of a head one after the other, p and nqb-1-p (the
-// heavier first), each with its key range split between the streams.
-// Under the causal mask the two need about the same tiles as any other pair
-// (2 nqb + 2 at N_q = N_k), so one round of work-groups, one per CU,
-// carries equal work: no lone heavy block at the end (the 4-wave groups'
-// tail) and no second round of start-ups (the one-block split's).
+// PAIR (SPLIT = 2, configurations br128_bc64_w4x2_pair, W = 4, and
+// br64_bc64_w2x2_pair, W = 2): a work-group walks two blocks of 32W rows of
+// a head one after the other, p and nqb-1-p (the heavier first), each with
+// its key range split between the streams.  Under the causal mask the two
+// need about the same tiles as any other pair (2 nqb + 2 at N_q = N_k), so
+// one round of work-groups, one per CU, carries equal work: no lone heavy
+// block at the end (the 4-wave groups' tail) and no second round of
+// start-ups (the one-block split's).
 template <int W, int FV, bool CAUSAL, bool SCALED, class T = _Float16, int SPLIT = 1,
           bool PAIR = false>
 // Register budget for 2 waves per SIMD (<= 256 VGPRs).  W = 2 with SPLIT
@@ -506,13 +507,18 @@ hipError_t launch_slot(const FwdArgs& a, int waves, hipStream_t stream) {
 // matters more than the deeper pipeline.
 constexpr int kSplitFv = 2;
 
-// fp16 or bf16 by a.dtype: groups of 2 x 4 waves walking a pair of 128-row
-// blocks of a head, p and nqb-1-p, each with its key range halved between
-// the streams (grid B*H*ceil(nqb/2)).
-hipError_t launch_slot_pair(const FwdArgs& a, hipStream_t stream) {
+// fp16 or bf16 by a.dtype: groups of 2 x `waves` waves (4: 128-row blocks,
+// 2: 64-row blocks) walking a pair of blocks of a head, p and nqb-1-p, each
+// with its key range halved between the streams (grid B*H*ceil(nqb/2)).
+hipError_t launch_slot_pair(const FwdArgs& a, int waves, hipStream_t stream) {
   const bool bf = a.dtype == kDtypeBF16;
-  return bf ? dispatch<SlotLaunch<4, kSplitFv, __bf16, 2, true>::L>(a, stream, 128)
-            : dispatch<SlotLaunch<4, kSplitFv, _Float16, 2, true>::L>(a, stream, 128);
+  if (waves == 4)
+    return bf ? dispatch<SlotLaunch<4, kSplitFv, __bf16, 2, true>::L>(a, stream, 128)
+              : dispatch<SlotLaunch<4, kSplitFv, _Float16, 2, true>::L>(a, stream, 128);
+  if (waves == 2)
+    return bf ? dispatch<SlotLaunch<2, kSplitFv, __bf16, 2, true>::L>(a, stream, 64)
+              : dispatch<SlotLaunch<2, kSplitFv, _Float16, 2, true>::L>(a, stream, 64);
+  return hipErrorInvalidValue;
 }
 
 // fp16 or bf16 by a.dtype: groups of 2 x `waves` waves (4: 128 rows, 2: 64

@@ -58,7 +58,9 @@ constexpr int kCfgSplit2W2 = 7;     // br64_bc64_w2x2_slot: 2 x 2 waves, key ran
 // Two 128-row blocks of a head per work-group (p and nqb-1-p, one after the
 // other), each with its key range halved between 2 x 4 waves.
 constexpr int kCfgPair = 8;         // br128_bc64_w4x2_pair
-constexpr int kNumFa2Configs = 9;
+// The same with two 64-row blocks per work-group, 2 x 2 waves.
+constexpr int kCfgPairW2 = 9;       // br64_bc64_w2x2_pair
+constexpr int kNumFa2Configs = 10;
 extern const Fa2Config kFa2Configs[kNumFa2Configs];
 
 // Launches the FA2 kernel for configuration `cfg` on `stream`.  fp16 at
@@ -116,7 +118,7 @@ inline bool quarter_config_fits(const FwdArgs& a) { return a.seq_k <= kQuarterMa
 hipError_t launch_pipe(const FwdArgs& a, int cfg, hipStream_t stream);     // fa2_pipe.hip
 hipError_t launch_slot(const FwdArgs& a, int waves, hipStream_t stream);   // fa2_slot.hip
 hipError_t launch_slot_split(const FwdArgs& a, int waves, hipStream_t stream);  // fa2_slot.hip
-hipError_t launch_slot_pair(const FwdArgs& a, hipStream_t stream);              // fa2_slot.hip
+hipError_t launch_slot_pair(const FwdArgs& a, int waves, hipStream_t stream);   // fa2_slot.hip
 hipError_t launch_stream(const FwdArgs& a, hipStream_t stream);            // fa2_stream.hip
 hipError_t launch_quarter(const FwdArgs& a, hipStream_t stream);           // fa2_short.hip
 hipError_t launch_d128(const FwdArgs& a, int waves, hipStream_t stream);   // fa2_d128.hip

@@ -25,6 +25,7 @@ SLOT_W4_CFG = capi.config_id("br128_bc64_w4_slot")
 SPLIT2_CFG = capi.config_id("br128_bc64_w4x2_slot")
 SPLIT2W2_CFG = capi.config_id("br64_bc64_w2x2_slot")
 PAIR_CFG = capi.config_id("br128_bc64_w4x2_pair")
+PAIR64_CFG = capi.config_id("br64_bc64_w2x2_pair")
 STREAM_CFG = capi.config_id("br256_kv256_w8_stream")
 STREAM_MAX_KEYS = 256
 QUARTER_CFG = capi.config_id("br32_kv512_w4_quarters")

@@ -29,13 +29,13 @@ def test_library_loads_and_exports_header_symbols():
 
 
 def test_config_table():
-    assert capi.num_configs() == 9
-    names = [capi.config_name(i) for i in range(9)]
+    assert capi.num_configs() == 10
+    names = [capi.config_name(i) for i in range(10)]
     # ids are stable: a new configuration is appended, never inserted
     assert names == ["br32_bc64_w1", "br64_bc64_w2", "br128_bc64_w4x2_slot", "br256_bc64_w8_slot",
                      "br128_bc64_w4_slot", "br256_kv256_w8_stream", "br32_kv512_w4_quarters",
-                     "br64_bc64_w2x2_slot", "br128_bc64_w4x2_pair"]
-    assert capi.config_name(9) is None and capi.config_name(-1) is None
+                     "br64_bc64_w2x2_slot", "br128_bc64_w4x2_pair", "br64_bc64_w2x2_pair"]
+    assert capi.config_name(10) is None and capi.config_name(-1) is None
     assert capi.config_id("br256_bc64_w8_slot") == 3
 
 
@@ -174,7 +174,7 @@ def test_dispatcher_choices():
     W8, W4, SPLIT, STRM = ("br256_bc64_w8_slot", "br128_bc64_w4_slot", "br128_bc64_w4x2_slot",
                            "br256_kv256_w8_stream")
     W1, W2, QTR = "br32_bc64_w1", "br64_bc64_w2", "br32_kv512_w4_quarters"
-    PAIR = "br128_bc64_w4x2_pair"
+    PAIR, PAIR64 = "br128_bc64_w4x2_pair", "br64_bc64_w2x2_pair"
     SPLIT64 = "br64_bc64_w2x2_slot"
     # non-causal: 8-wave 256-row slot-scheduled groups when there are more
     # than 128 and the key range is long
@@ -193,7 +193,7 @@ def test_dispatcher_choices():
     assert sel(batch=2, heads=8, seq_q=2048, causal=True) == SPLIT
     assert sel(batch=1, heads=8, seq_q=4096) == SPLIT
     assert sel(batch=1, heads=1, seq_q=2048) == SPLIT64    # 32 groups of 64 rows
-    assert sel(batch=1, heads=8, seq_q=4096, causal=True) == SPLIT
+    assert sel(batch=1, heads=8, seq_q=4096, causal=True) == PAIR64   # 256 pairs of 64 rows
     assert sel(batch=1, heads=1, seq_q=1024, seq_k=4096) == SPLIT64
     assert sel(batch=1, heads=1, seq_q=2048, seq_k=8192) == SPLIT64
     assert sel(batch=1, heads=1, seq_q=1000, seq_k=4096) == SPLIT64
@@ -220,6 +220,16 @@ def test_dispatcher_choices():
     assert sel(batch=2, heads=8, seq_q=4096) == W8
     assert sel(batch=1, heads=16, seq_q=16384, causal=True) == W4
     assert sel(batch=3, heads=8, seq_q=2048, causal=True) == W4   # 384 groups
+    # square causal from N 4096 with 129-256 pairs of 64-row blocks: the
+    # 64-row block pairs (one round)
+    assert sel(batch=1, heads=2, seq_q=16384, causal=True) == PAIR64
+    assert sel(batch=1, heads=1, seq_q=32768, causal=True) == PAIR64
+    assert sel(batch=1, heads=3, seq_q=8192, causal=True) == PAIR64   # 192 pairs
+    assert sel(batch=4, heads=2, seq_q=4096, causal=True) == PAIR64
+    assert sel(batch=1, heads=4, seq_q=16384, causal=True) == PAIR    # 512 pairs
+    assert sel(batch=1, heads=2, seq_q=16384) == SPLIT                # non-causal
+    assert sel(batch=1, heads=2, seq_q=16000, seq_k=16384, causal=True) == SPLIT  # N_q != N_k
+    assert sel(batch=2, heads=8, seq_q=2048, causal=True) == SPLIT    # N 2048
     assert sel(batch=32, heads=32, seq_q=256, causal=True) == STRM   # streaming, any count
     assert sel(batch=1, heads=1, seq_q=128, causal=True) == STRM
     # 256 < N_k <= 512 with at most 512 blocks of 32 rows: key quarters

@@ -12,7 +12,7 @@ import pytest
 
 from flashlite_amd import capi
 from flashlite_amd.workloads import WORKLOADS, make_qkv, workload_inputs
-from gpu_util import (PAIR_CFG, SLOT_W4_CFG, SLOT_W8_CFG, SPLIT2_CFG, SPLIT2W2_CFG,
+from gpu_util import (PAIR64_CFG, PAIR_CFG, SLOT_W4_CFG, SLOT_W8_CFG, SPLIT2_CFG, SPLIT2W2_CFG,
                       assert_close_oracle,
                       config_fits, redo_expected, run_capi, to_dev)
 from oracle import attention_fp32, error_stats
@@ -20,8 +20,9 @@ from oracle import attention_fp32, error_stats
 pytestmark = pytest.mark.gpu
 
 GOLDEN = os.path.join(os.path.dirname(__file__), "golden")
-NCFG = 9  # tile configurations exported by the library
-SPLIT_CFGS = [SPLIT2_CFG, SPLIT2W2_CFG, PAIR_CFG]  # the key-range-split configurations
+NCFG = 10  # tile configurations exported by the library
+# the key-range-split configurations
+SPLIT_CFGS = [SPLIT2_CFG, SPLIT2W2_CFG, PAIR_CFG, PAIR64_CFG]
 
 
 def test_num_configs():
@@ -29,7 +30,7 @@ def test_num_configs():
     assert [capi.config_name(i) for i in range(NCFG)] == [
         "br32_bc64_w1", "br64_bc64_w2", "br128_bc64_w4x2_slot", "br256_bc64_w8_slot",
         "br128_bc64_w4_slot", "br256_kv256_w8_stream", "br32_kv512_w4_quarters",
-        "br64_bc64_w2x2_slot", "br128_bc64_w4x2_pair"]
+        "br64_bc64_w2x2_slot", "br128_bc64_w4x2_pair", "br64_bc64_w2x2_pair"]
 
 
 @pytest.mark.parametrize("config", list(range(NCFG)))
@@ -94,6 +95,19 @@ def test_c3_long_causal(cuda):
     mx, mean = assert_close_oracle(out, q, k, v, w.sm_scale, True)  # all 16384 rows
     print(f"C3 all rows: max-abs {mx:.2e} mean-abs {mean:.2e}")
     # causal row 0 sees only key 0: the output is V[0] exactly
+    assert np.array_equal(out[:, :, 0], v[:, :, 0])
+
+
+def test_pairs64_dispatch(cuda):
+    # a square causal problem the dispatcher gives the 64-row block pairs
+    # (192 pairs: an odd head count, heads split across work-groups' XCDs);
+    # every output row
+    q, k, v = make_qkv(1, 3, 8192, 64, seed=97)
+    tq, tk, tv = (to_dev(x, cuda) for x in (q, k, v))
+    assert capi.select_config(capi.tensor_params(tq, tk, tv, tq, 0.125, True)) == PAIR64_CFG
+    out = run_capi(q, k, v, 0.125, True, cuda)
+    mx, mean = assert_close_oracle(out, q, k, v, 0.125, True)
+    print(f"B1 H3 N8192 causal, 64-row pairs, every row: max-abs {mx:.2e} mean-abs {mean:.2e}")
     assert np.array_equal(out[:, :, 0], v[:, :, 0])
 
 

@@ -74,7 +74,7 @@ def test_random_shape_every_config(cuda, case):
 # configurations built for each wider type (the others answer FL_ERR_BAD_CONFIG)
 _SLOT = ("br256_bc64_w8_slot", "br128_bc64_w4_slot")
 _BF16_D64 = _SLOT + ("br128_bc64_w4x2_slot", "br64_bc64_w2x2_slot", "br128_bc64_w4x2_pair",
-                     "br256_kv256_w8_stream", "br32_kv512_w4_quarters")
+                     "br64_bc64_w2x2_pair", "br256_kv256_w8_stream", "br32_kv512_w4_quarters")
 WIDE_CONFIGS = {("fp16", 128): _SLOT, ("bf16", 128): _SLOT, ("bf16", 64): _BF16_D64}
 
 

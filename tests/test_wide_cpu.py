@@ -61,10 +61,10 @@ def test_wide_config_checks():
             slots = (capi.config_id("br256_bc64_w8_slot"), capi.config_id("br128_bc64_w4_slot"))
             stream_cfg = capi.config_id("br256_kv256_w8_stream")
             quarter_cfg = capi.config_id("br32_kv512_w4_quarters")
-            # bf16 at D = 64 also has both key-range splits (and the streaming and
-            # key-quarter kernels, checked below)
+            # bf16 at D = 64 also has both key-range splits and both block pairs
+            # (and the streaming and key-quarter kernels, checked below)
             splits = (capi.config_id("br128_bc64_w4x2_slot"), capi.config_id("br64_bc64_w2x2_slot"),
-                      capi.config_id("br128_bc64_w4x2_pair"))
+                      capi.config_id("br128_bc64_w4x2_pair"), capi.config_id("br64_bc64_w2x2_pair"))
             for cfg in range(capi.num_configs()):
                 if cfg in slots or cfg in (stream_cfg, quarter_cfg):
                     continue
