@@ -899,6 +899,59 @@ struct Rows {
     }
     m = mm;
   }
+  // Merge of NW partials in save_partial4's layout, one of the four
+  // 8-column chunks of each lane's row (chunk c = 2 db + hh: o[db][8 hh ..
+  // 8 hh + 7], head dims 32 db + 16 hh + 8 g ..), normalised and stored as
+  // 16 bytes per lane; the wave of chunk 0 also writes the log-sum-exp.  The
+  // partials meet at their largest m; one with l = 0 across the lane pair
+  // (no visible key) is skipped.  The object's own o, m, l are not used.
+  template <int NW>
+  __device__ __forceinline__ void merge_store_chunk(const float4* const (&parts)[NW], int c,
+                                                    int lane, T* Oh, int o_sr,
+                                                    float* lse) const {
+    float mj[NW], lj[NW];
+    bool has[NW];
+    float mm = ninf();
+#pragma unroll
+    for (int j = 0; j < NW; ++j) {
+      const float4 ml = parts[j][8 * 64 + lane];
+      mj[j] = ml.x;
+      lj[j] = ml.y;
+      has[j] = pair_sum(lj[j]) > 0.0f;
+      if (has[j]) mm = fmaxf(mm, mj[j]);
+    }
+    const float k = SCALED ? cr : 1.0f;
+    float lt = 0.0f;
+    float acc[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int j = 0; j < NW; ++j) {
+      const float a = has[j] ? __builtin_amdgcn_exp2f(k * (mj[j] - mm)) : 0.0f;
+      lt += a * lj[j];
+      const float4 x0 = parts[j][(2 * c) * 64 + lane];
+      const float4 x1 = parts[j][(2 * c + 1) * 64 + lane];
+      acc[0] += a * x0.x;
+      acc[1] += a * x0.y;
+      acc[2] += a * x0.z;
+      acc[3] += a * x0.w;
+      acc[4] += a * x1.x;
+      acc[5] += a * x1.y;
+      acc[6] += a * x1.z;
+      acc[7] += a * x1.w;
+    }
+    const float l_tot = pair_sum(lt);
+    const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
+    if (lse != nullptr && c == 0 && g == 0 && my_q < seq) {
+      const float lg = mm * k + __builtin_amdgcn_logf(l_tot);
+      lse[my_q] = l_tot > 0.0f ? 0.693147180559945309f * lg : ninf();
+    }
+    if (my_q < seq) {
+      V8 out;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) out[e] = (T)(acc[e] * inv);
+      *reinterpret_cast<V8*>(Oh + (long long)my_q * o_sr + 32 * (c >> 1) + 16 * (c & 1) + 8 * g) =
+          out;
+    }
+  }
   // Split-KV partial of the rows over one key chunk: O unnormalised
   // (relative to the stabiliser), the stabiliser in base-2 logit units
   // (m * cr) and the row sum, kPartStride floats per row.  A row with no key

@@ -29,8 +29,8 @@ namespace {
 // computes both tiles' scores, takes their exact row max as the one
 // stabiliser (every p <= 1, so no range check and no second pass), then
 // exponentiates and multiplies tile by tile; the quarters' O, m and l
-// merge through LDS in 16-byte chunks at their larger m: 1, 2 and 3 into
-// 0, which stores.  C1 then runs 1024
+// merge through LDS in 16-byte chunks at their largest m, each wave merging
+// and storing a quarter of the head dims of every row.  C1 then runs 1024
 // waves of 2 tiles instead of 256 waves of 8.  LDS: 4 x 32 KiB, one
 // work-group per CU, plus 4 KiB of Q.  (Eight waves of one tile each, two
 // per SIMD, measured 7% slower on C1.)
@@ -40,8 +40,8 @@ namespace {
 // quarter q.  The two waves of a quarter fetch half of its tiles each into
 // the quarter's 32 KiB and read all of it, so a barrier publishes the tiles;
 // two more order the merge (every quarter's K/V read before any partial
-// overwrites it; partials written before wave 0 of each row block folds
-// them in).  Up to 512 blocks then still run in one round, two waves per
+// overwrites it; partials written before the row block's waves fold them
+// in).  Up to 512 blocks then still run in one round, two waves per
 // SIMD.
 //
 // KVSPLIT (split-KV chunks of at most 8 tiles, RB = 1): work-group i takes
@@ -228,35 +228,42 @@ fa2_fwd_quarter_kernel(const T* Q, const T* __restrict__ K, const T* __restrict_
     }
   }
   FL_ST_MARK(3);
-  // Merge through each quarter's (now idle) LDS: quarters 1..NW-1 store
-  // their partials at once and, after one barrier, quarter 0 merges them in
-  // order (measured 5% faster on C1 than a two-step tree, which took a
-  // second barrier).  Row block rb's partials start rb x 9 KiB into the
-  // quarter's buffer.  A range with no visible key holds l = 0 and is
-  // skipped by the merge.
+  // Merge through each quarter's (now idle) LDS.  Row block rb's partials
+  // start rb x 9 KiB into the quarter's buffer; a range with no visible key
+  // holds l = 0 and is skipped by the merge.  Every quarter stores its
+  // partial and, after one barrier, wave kq of the row block merges and
+  // stores the kq-th 8-column chunk of every row (Rows::merge_store_chunk:
+  // 12 of the partials' 36 float4s per lane, and a quarter of the stores).
+  // Split-KV chunks keep one merging wave (quarters 1..NW-1 into 0), which
+  // writes the fp32 partial.
   float4* const part = reinterpret_cast<float4*>(buf[kq]) + rb * (9 * 64);
   // own LDS reads done, and every fetch landed (a one-tile quarter's zero
   // tiles too: nothing may still write this LDS once the group ends)
   asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" : : : "memory");
   if constexpr (RB > 1) __syncthreads();  // and the other row block's
-  if (kq != 0) rows.save_partial4(part, lane);
-  __syncthreads();
-  if (kq == 0) {
+  if constexpr (!KVSPLIT) {
+    rows.save_partial4(part, lane);
+    __syncthreads();
+    const float4* parts[NW];
 #pragma unroll
-    for (int s = 1; s < NW; ++s)
-      rows.merge_partial4(reinterpret_cast<const float4*>(buf[s]) + rb * (9 * 64), lane);
-  }
-  FL_ST_MARK(4);
-  if (kq != 0) {
+    for (int j = 0; j < NW; ++j) parts[j] = reinterpret_cast<const float4*>(buf[j]) + rb * (9 * 64);
+    rows.template merge_store_chunk<NW>(parts, kq, lane, hp.o, geom.o_sr, hp.lse);
+    FL_ST_MARK(4);
     FL_ST_FLUSH(w, lane, 5);
-    return;
+  } else {
+    if (kq != 0) rows.save_partial4(part, lane);
+    __syncthreads();
+    if (kq == 0) {
+#pragma unroll
+      for (int s = 1; s < NW; ++s)
+        rows.merge_partial4(reinterpret_cast<const float4*>(buf[s]) + rb * (9 * 64), lane);
+      rows.launder();
+      rows.store_partial(geom.part +
+                         (long long)(chunk * geom.batch_heads + bh) * seq * kPartStride);
+    }
+    FL_ST_MARK(4);
+    FL_ST_FLUSH(w, lane, 5);
   }
-  rows.launder();
-  if constexpr (KVSPLIT)
-    rows.store_partial(geom.part + (long long)(chunk * geom.batch_heads + bh) * seq * kPartStride);
-  else
-    rows.store(hp.o, geom.o_sr, hp.lse);
-  FL_ST_FLUSH(w, lane, 5);
 }
 
 template <int RB, class T>

@@ -423,7 +423,8 @@ def _stream_timeline(args, torch):
 
 def _quarter_timeline(args, torch):
     """Where the key-quarter kernel's time goes: per wave, its loads' issue
-    and landing, its two tiles, the merge and the store."""
+    and landing, its two tiles, the merge with its chunk's stores, and the
+    wait for them to land."""
     import ctypes
 
     import numpy as np
@@ -469,9 +470,10 @@ def _quarter_timeline(args, torch):
     print(f"  entry -> loads issued, Q loaded  {pct((t[:, :, 1] - t[:, :, 0]).ravel())}")
     print(f"  -> loads landed                  {pct((t[:, :, 2] - t[:, :, 1])[busy])}")
     print(f"  -> tiles done                    {pct((t[:, :, 3] - t[:, :, 2])[busy])}")
-    print(f"  -> merged                        {pct((t[:, :, 4] - t[:, :, 3]).ravel())}")
-    print(f"  -> exit (wave 0: the store)      {pct(t[:, 0, 63] - t[:, 0, 4])}")
-    print(f"  group span (first entry -> wave 0 exit) {pct(t[:, 0, 63] - t[:, :, 0].min(axis=1))}")
+    print(f"  -> merged, own chunk's stores issued {pct((t[:, :, 4] - t[:, :, 3]).ravel())}")
+    print(f"  -> exit (stores landed)          {pct((t[:, :, 63] - t[:, :, 4]).ravel())}")
+    print(f"  group span (first entry -> last exit) "
+          f"{pct(t[:, :, 63].max(axis=1) - t[:, :, 0].min(axis=1))}")
     return 0
 
 
