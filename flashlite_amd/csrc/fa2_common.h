@@ -909,9 +909,49 @@ struct Rows {
   __device__ __forceinline__ void merge_store_chunk(const float4* const (&parts)[NW], int c,
                                                     int lane, T* Oh, int o_sr,
                                                     float* lse) const {
+    float acc[8], mm, l_tot;
+    merge_chunk<NW>(parts, c, lane, acc, mm, l_tot);
+    const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
+    if (lse != nullptr && c == 0 && g == 0 && my_q < seq) {
+      const float lg = mm * (SCALED ? cr : 1.0f) + __builtin_amdgcn_logf(l_tot);
+      lse[my_q] = l_tot > 0.0f ? 0.693147180559945309f * lg : ninf();
+    }
+    if (my_q < seq) {
+      V8 out;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) out[e] = (T)(acc[e] * inv);
+      *reinterpret_cast<V8*>(Oh + (long long)my_q * o_sr + 32 * (c >> 1) + 16 * (c & 1) + 8 * g) =
+          out;
+    }
+  }
+  // As merge_store_chunk, for a split-KV chunk: chunk c of the merged
+  // partial in store_partial's layout (O unnormalised, relative to the
+  // merged stabiliser; 8 floats per lane), and with chunk 0 the stabiliser in
+  // base-2 logit units and the row sum.
+  template <int NW>
+  __device__ __forceinline__ void merge_store_partial_chunk(const float4* const (&parts)[NW],
+                                                            int c, int lane, float* part) const {
+    float acc[8], mm, l_tot;
+    merge_chunk<NW>(parts, c, lane, acc, mm, l_tot);
+    if (my_q < seq) {
+      float* r = part + (long long)my_q * kPartStride;
+      float* dst = r + 32 * (c >> 1) + 16 * (c & 1) + 8 * g;
+      *reinterpret_cast<float4*>(dst) = make_float4(acc[0], acc[1], acc[2], acc[3]);
+      *reinterpret_cast<float4*>(dst + 4) = make_float4(acc[4], acc[5], acc[6], acc[7]);
+      if (c == 0 && g == 0) {
+        r[64] = l_tot > 0.0f ? mm * (SCALED ? cr : 1.0f) : ninf();
+        r[65] = l_tot;
+      }
+    }
+  }
+  // The merge itself: acc = chunk c of sum_j a_j O_j, mm = the largest m of
+  // a partial with keys (-inf if none), l_tot = the row's sum_j a_j l_j.
+  template <int NW>
+  __device__ __forceinline__ void merge_chunk(const float4* const (&parts)[NW], int c, int lane,
+                                              float (&acc)[8], float& mm, float& l_tot) const {
     float mj[NW], lj[NW];
     bool has[NW];
-    float mm = ninf();
+    mm = ninf();
 #pragma unroll
     for (int j = 0; j < NW; ++j) {
       const float4 ml = parts[j][8 * 64 + lane];
@@ -922,7 +962,8 @@ struct Rows {
     }
     const float k = SCALED ? cr : 1.0f;
     float lt = 0.0f;
-    float acc[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[e] = 0.0f;
 #pragma unroll
     for (int j = 0; j < NW; ++j) {
       const float a = has[j] ? __builtin_amdgcn_exp2f(k * (mj[j] - mm)) : 0.0f;
@@ -938,19 +979,7 @@ struct Rows {
       acc[6] += a * x1.z;
       acc[7] += a * x1.w;
     }
-    const float l_tot = pair_sum(lt);
-    const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
-    if (lse != nullptr && c == 0 && g == 0 && my_q < seq) {
-      const float lg = mm * k + __builtin_amdgcn_logf(l_tot);
-      lse[my_q] = l_tot > 0.0f ? 0.693147180559945309f * lg : ninf();
-    }
-    if (my_q < seq) {
-      V8 out;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) out[e] = (T)(acc[e] * inv);
-      *reinterpret_cast<V8*>(Oh + (long long)my_q * o_sr + 32 * (c >> 1) + 16 * (c & 1) + 8 * g) =
-          out;
-    }
+    l_tot = pair_sum(lt);
   }
   // Split-KV partial of the rows over one key chunk: O unnormalised
   // (relative to the stabiliser), the stabiliser in base-2 logit units

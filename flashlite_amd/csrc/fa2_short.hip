@@ -46,9 +46,10 @@ namespace {
 //
 // KVSPLIT (split-KV chunks of at most 8 tiles, RB = 1): work-group i takes
 // key chunk i % nsplit of its query block, the waves a quarter of the
-// chunk each, and wave 0 writes the merged partial (O unnormalised, m, l)
-// that splitkv_combine_kernel folds together, as the one-wave chunks of
-// the pipelined kernel do.  A decode step's chunk is then a 2-tile chain
+// chunk each, and the merged partial (O unnormalised, m, l) that
+// splitkv_combine_kernel folds together is written as the one-wave chunks
+// of the pipelined kernel write theirs, a quarter of the head dims by each
+// wave.  A decode step's chunk is then a 2-tile chain
 // per wave instead of an up-to-8-tile one.
 constexpr int kQuarterWaves = 4;
 
@@ -232,38 +233,27 @@ fa2_fwd_quarter_kernel(const T* Q, const T* __restrict__ K, const T* __restrict_
   // start rb x 9 KiB into the quarter's buffer; a range with no visible key
   // holds l = 0 and is skipped by the merge.  Every quarter stores its
   // partial and, after one barrier, wave kq of the row block merges and
-  // stores the kq-th 8-column chunk of every row (Rows::merge_store_chunk:
-  // 12 of the partials' 36 float4s per lane, and a quarter of the stores).
-  // Split-KV chunks keep one merging wave (quarters 1..NW-1 into 0), which
-  // writes the fp32 partial.
+  // stores the kq-th 8-column chunk of every row (Rows::merge_store_chunk,
+  // or for a split-KV chunk the fp32 partial, merge_store_partial_chunk):
+  // 12 of the partials' 36 float4s per lane and a quarter of the stores
+  // each.
   float4* const part = reinterpret_cast<float4*>(buf[kq]) + rb * (9 * 64);
   // own LDS reads done, and every fetch landed (a one-tile quarter's zero
   // tiles too: nothing may still write this LDS once the group ends)
   asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" : : : "memory");
   if constexpr (RB > 1) __syncthreads();  // and the other row block's
-  if constexpr (!KVSPLIT) {
-    rows.save_partial4(part, lane);
-    __syncthreads();
-    const float4* parts[NW];
+  rows.save_partial4(part, lane);
+  __syncthreads();
+  const float4* parts[NW];
 #pragma unroll
-    for (int j = 0; j < NW; ++j) parts[j] = reinterpret_cast<const float4*>(buf[j]) + rb * (9 * 64);
+  for (int j = 0; j < NW; ++j) parts[j] = reinterpret_cast<const float4*>(buf[j]) + rb * (9 * 64);
+  if constexpr (KVSPLIT)
+    rows.template merge_store_partial_chunk<NW>(
+        parts, kq, lane, geom.part + (long long)(chunk * geom.batch_heads + bh) * seq * kPartStride);
+  else
     rows.template merge_store_chunk<NW>(parts, kq, lane, hp.o, geom.o_sr, hp.lse);
-    FL_ST_MARK(4);
-    FL_ST_FLUSH(w, lane, 5);
-  } else {
-    if (kq != 0) rows.save_partial4(part, lane);
-    __syncthreads();
-    if (kq == 0) {
-#pragma unroll
-      for (int s = 1; s < NW; ++s)
-        rows.merge_partial4(reinterpret_cast<const float4*>(buf[s]) + rb * (9 * 64), lane);
-      rows.launder();
-      rows.store_partial(geom.part +
-                         (long long)(chunk * geom.batch_heads + bh) * seq * kPartStride);
-    }
-    FL_ST_MARK(4);
-    FL_ST_FLUSH(w, lane, 5);
-  }
+  FL_ST_MARK(4);
+  FL_ST_FLUSH(w, lane, 5);
 }
 
 template <int RB, class T>
