@@ -244,18 +244,22 @@ int check_ex(const fl_attn_params_ex* p, fl::FwdArgs* a, const char* who, bool w
 // Split-KV plan: waves per work-group by N_q (32 query rows each), number
 // of key chunks, workspace bytes.  nsplit == 0 means "do not split".
 // The library's choice (requested <= 0), from decode sweeps on MI355X
-// (B2 H8 and B1 H16 with N_q 1-16 over 4k-64k keys, B32 H32 over 4k): with
-// at most 128 query rows and fewer query-row groups than CUs, cut each key
-// range so that the groups times chunks cover the CUs twice with
-// single-wave groups (N_q <= 32; 2-11% faster than once, measured) and once
-// with 2- and 4-wave groups (twice: +1% and +25%), keeping at least 4 key
-// tiles per chunk (shorter chunks measured slower: per-work-group start-up);
-// with more single-wave groups, chunks of 8 tiles up to 8 chunks when the
-// range is long (>= 32 tiles).  Otherwise one pass.  The partials grow with
-// B*H: with at least as many groups as CUs the 8-chunk rule alone needs
-// 8 x B*H x 32 rows (71 MB at B32 H32), so the allocation-free entry point
+// (B2 H8 and B1 H16 with N_q 1-16 over 4k-64k keys; B2-B32 with H16-H64 and
+// N_q 1-16 over 2k-32k keys): with at most 128 query rows and fewer
+// query-row groups than CUs (single-wave groups, N_q <= 32: fewer than half
+// as many), cut each key range so that the groups times chunks cover the
+// CUs twice with single-wave groups (2-11% faster than once, measured) and
+// once with 2- and 4-wave groups (twice: +1% and +25%), keeping at least 4
+// key tiles per chunk (shorter chunks measured slower: per-work-group
+// start-up).  Otherwise one pass: from 128 to 1024 single-wave groups the
+// one-pass kernels ran 2-12% faster than 2, 4 or 8 chunks (B4 H32 N_k 8192
+// 41.2 against 46.2 us, B8 H32 N_k 4096 42.4 against 47.6, B32 H32 N_k 4096
+// 186.6 against 196.6, B32 H32 N_q 4 189.5 against 207.3), and at 64 groups
+// the chunks still won (B2 H32 N_k 8192 27.9 against 39.0).  The partials
+// of a plan with 4-wave groups can pass the allocation-free entry point's
+// static scratch (2 x 128 groups x 128 rows: 8.9 MB), so that entry point
 // plans with plan_kvsplit_capped, which lowers the library's chunk count to
-// what its static scratch holds.
+// what its scratch holds.
 //
 // Single-wave groups whose chunks fit the key-quarter kernel (at most 8
 // tiles) in one round of its 4-wave work-groups (at most 256) run there
@@ -282,11 +286,11 @@ KvPlan plan_kvsplit(const fl::FwdArgs& a, int32_t requested) {
     n = std::min<int64_t>({(int64_t)requested, tiles, kMaxSplits});
   } else if (a.seq > 128) {
     n = 0;  // long query ranges: the one-pass kernel's groups fill the GPU
-  } else if (groups < cus) {
+  } else if (groups < (p.waves == 1 ? cus / 2 : cus)) {
     const int64_t cover = (p.waves == 1 ? 2 : 1) * cus;
     n = std::min<int64_t>({(cover + groups - 1) / groups, tiles / 4, kMaxSplits});
   } else {
-    n = (a.seq <= 32 && tiles >= 32) ? std::min<int64_t>(8, tiles / 8) : 0;
+    n = 0;  // enough groups for the one-pass kernels
   }
   if (p.waves == 1 && requested <= 0 && groups < cus) {
     const int64_t nq = (tiles + 7) / 8;  // chunks of at most 8 tiles

@@ -285,11 +285,15 @@ def test_splitkv_plan():
     # fewer than 8 tiles: at most tiles / 4 chunks, and no split below 2
     assert bytes_for(1, 512, 0) == 2 * 16 * 1 * 68 * 4
     assert bytes_for(1, 192, 0) == 0
-    # many groups (B32 H32): chunks of 8 tiles, at most 8, on long ranges only
-    assert bytes_for(1, 4096, 0, batch=32, heads=32) == 8 * 1024 * 68 * 4
+    # at least half as many one-wave groups as CUs (128 and more): one pass;
+    # 64 groups still cut their ranges (8 one-wave chunks: 16 would not fit
+    # one round of key-quarter groups)
+    assert bytes_for(1, 4096, 0, batch=32, heads=32) == 0
     assert bytes_for(1, 1024, 0, batch=32, heads=32) == 0
-    assert bytes_for(16, 4096, 0, batch=32, heads=32) == 8 * 1024 * 16 * 68 * 4
+    assert bytes_for(16, 4096, 0, batch=32, heads=32) == 0
     assert bytes_for(64, 4096, 0, batch=32, heads=32) == 0
+    assert bytes_for(1, 8192, 0, batch=4, heads=32) == 0
+    assert bytes_for(1, 8192, 0, batch=2, heads=32) == 8 * 64 * 1 * 68 * 4
     # long query ranges (the headline shape): one pass
     assert bytes_for(4096, 4096, 0) == 0
     assert bytes_for(129, 1 << 16, 0) == 0
@@ -357,25 +361,21 @@ def test_noalloc_plan_of_reported_shapes():
     p = _ex_shape(8, 16, 128, 65536)
     assert capi.splitkv_workspace_bytes(p, 0) == 8912896
     assert capi.splitkv_noalloc_bytes(p, 0) == 0
-    # B32 H32, 32 query rows over 4096 keys: 8 chunks (71 MB) with a
-    # workspace; one 8.9 MB chunk does not fit either, so one pass
-    p = _ex_shape(32, 32, 32, 4096)
-    assert capi.splitkv_workspace_bytes(p, 0) == 8 * 1024 * 32 * 68 * 4
-    assert capi.splitkv_noalloc_bytes(p, 0) == 0
-    # B32 H32 decode (one query row): 8 chunks of 1024 rows fit
-    p = _ex_shape(32, 32, 1, 4096)
-    assert capi.splitkv_noalloc_bytes(p, 0) == capi.splitkv_workspace_bytes(p, 0) == 8 * 1024 * 272
-    # B16 H64, 16 rows over 65536 keys: 8 chunks (35.7 MB) with a workspace;
-    # one 4.5 MB chunk fits, two do not, so one pass
-    p = _ex_shape(16, 64, 16, 65536)
-    ws = capi.splitkv_workspace_bytes(p, 0)
-    assert ws == 8 * 1024 * 16 * 272 and ws > capi.SCRATCH_BYTES
-    assert capi.splitkv_noalloc_bytes(p, 0) == 0
-    # B4 H64, 16 rows over 65536 keys: 8 chunks of 256 x 16 rows (8.9 MB),
-    # lowered to the 7 that fit
-    p = _ex_shape(4, 64, 16, 65536)
-    assert capi.splitkv_workspace_bytes(p, 0) == 8 * 256 * 16 * 272
-    assert capi.splitkv_noalloc_bytes(p, 0) == 7 * 256 * 16 * 272
+    # B32 H32, 32 query rows over 4096 keys (1024 one-wave groups): one pass
+    # with or without a workspace; so too the B32 H32 decode step and 16 rows
+    # of B16 H64 over 65536 keys
+    for shape in ((32, 32, 32, 4096), (32, 32, 1, 4096), (16, 64, 16, 65536)):
+        p = _ex_shape(*shape)
+        assert capi.splitkv_workspace_bytes(p, 0) == capi.splitkv_noalloc_bytes(p, 0) == 0
+    # B4 H16, 128 rows over 1024 keys: 4 chunks of 64 x 128 rows (8.9 MB),
+    # lowered to the 3 that fit; B2 H16, 128 rows over 4096 keys: 8 chunks of
+    # 32 x 128 rows, lowered to 7
+    p = _ex_shape(4, 16, 128, 1024)
+    assert capi.splitkv_workspace_bytes(p, 0) == 4 * 64 * 128 * 272
+    assert capi.splitkv_noalloc_bytes(p, 0) == 3 * 64 * 128 * 272
+    p = _ex_shape(2, 16, 128, 4096)
+    assert capi.splitkv_workspace_bytes(p, 0) == 8 * 32 * 128 * 272
+    assert capi.splitkv_noalloc_bytes(p, 0) == 7 * 32 * 128 * 272
     # a requested count is kept as asked, even when it will be refused
     p = _ex_shape(4, 16, 256, 4096)
     assert capi.splitkv_noalloc_bytes(p, 16) == capi.splitkv_workspace_bytes(p, 16) \
