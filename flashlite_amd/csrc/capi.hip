@@ -244,22 +244,23 @@ int check_ex(const fl_attn_params_ex* p, fl::FwdArgs* a, const char* who, bool w
 // Split-KV plan: waves per work-group by N_q (32 query rows each), number
 // of key chunks, workspace bytes.  nsplit == 0 means "do not split".
 // The library's choice (requested <= 0), from decode sweeps on MI355X
-// (B2 H8 and B1 H16 with N_q 1-16 over 4k-64k keys; B2-B32 with H16-H64 and
-// N_q 1-16 over 2k-32k keys): with at most 128 query rows and fewer
-// query-row groups than CUs (single-wave groups, N_q <= 32: fewer than half
-// as many), cut each key range so that the groups times chunks cover the
-// CUs twice with single-wave groups (2-11% faster than once, measured) and
-// once with 2- and 4-wave groups (twice: +1% and +25%), keeping at least 4
-// key tiles per chunk (shorter chunks measured slower: per-work-group
-// start-up).  Otherwise one pass: from 128 to 1024 single-wave groups the
-// one-pass kernels ran 2-12% faster than 2, 4 or 8 chunks (B4 H32 N_k 8192
-// 41.2 against 46.2 us, B8 H32 N_k 4096 42.4 against 47.6, B32 H32 N_k 4096
-// 186.6 against 196.6, B32 H32 N_q 4 189.5 against 207.3), and at 64 groups
-// the chunks still won (B2 H32 N_k 8192 27.9 against 39.0).  The partials
-// of a plan with 4-wave groups can pass the allocation-free entry point's
-// static scratch (2 x 128 groups x 128 rows: 8.9 MB), so that entry point
-// plans with plan_kvsplit_capped, which lowers the library's chunk count to
-// what its scratch holds.
+// (B2 H8 and B1 H16 with N_q 1-16 over 4k-64k keys; B1-B32 with H16-H64 and
+// N_q 1-128 over 2k-32k keys): with at most 128 query rows and fewer than
+// half as many query-row groups as CUs, cut each key range so that the
+// groups times chunks cover the CUs twice with single-wave groups (N_q <=
+// 32; 2-11% faster than once, measured) and once with 2- and 4-wave groups
+// (twice: +1% and +25%), keeping at least 4 key tiles per chunk (shorter
+// chunks measured slower: per-work-group start-up).  Otherwise one pass:
+// from 128 to 1024 groups the one-pass kernels ran 2-17% faster than 2, 4
+// or 8 chunks (B4 H32 N_q 1 N_k 8192 41.2 against 46.2 us, B32 H32 N_q 1
+// N_k 4096 186.6 against 196.6, B4 H32 N_q 64 N_k 8192 48.3 against 53.2,
+// B8 H16 N_q 64 N_k 4096 26.0 against 31.5), while at 32-64 groups the
+// chunks still won or tied (B2 H32 N_q 1 N_k 8192 27.9 against 39.0, N_q
+// 64 31.2 against 43.3).  The partials of a plan with 4-wave groups can
+// pass the allocation-free entry point's static scratch (4 chunks x 64
+// groups x 128 rows: 8.9 MB), so that entry point plans with
+// plan_kvsplit_capped, which lowers the library's chunk count to what its
+// scratch holds.
 //
 // Single-wave groups whose chunks fit the key-quarter kernel (at most 8
 // tiles) in one round of its 4-wave work-groups (at most 256) run there
@@ -286,7 +287,7 @@ KvPlan plan_kvsplit(const fl::FwdArgs& a, int32_t requested) {
     n = std::min<int64_t>({(int64_t)requested, tiles, kMaxSplits});
   } else if (a.seq > 128) {
     n = 0;  // long query ranges: the one-pass kernel's groups fill the GPU
-  } else if (groups < (p.waves == 1 ? cus / 2 : cus)) {
+  } else if (2 * groups < cus) {
     const int64_t cover = (p.waves == 1 ? 2 : 1) * cus;
     n = std::min<int64_t>({(cover + groups - 1) / groups, tiles / 4, kMaxSplits});
   } else {

@@ -356,10 +356,13 @@ def test_noalloc_plan_fits_the_scratch_array():
 
 
 def test_noalloc_plan_of_reported_shapes():
-    # B8 H16, 128 query rows over 65536 keys: 2 chunks of 128 x 128 rows need
-    # 8,912,896 bytes, above the 8 MiB array, and one chunk is no split
+    # B8 H16, 128 query rows over 65536 keys (128 groups): one pass, with or
+    # without a workspace; B4 H31 (124 groups): 3 chunks of 124 x 128 rows
+    # (12.9 MB) with a workspace, and one 4.3 MB chunk is no split
     p = _ex_shape(8, 16, 128, 65536)
-    assert capi.splitkv_workspace_bytes(p, 0) == 8912896
+    assert capi.splitkv_workspace_bytes(p, 0) == capi.splitkv_noalloc_bytes(p, 0) == 0
+    p = _ex_shape(4, 31, 128, 65536)
+    assert capi.splitkv_workspace_bytes(p, 0) == 3 * 124 * 128 * 272
     assert capi.splitkv_noalloc_bytes(p, 0) == 0
     # B32 H32, 32 query rows over 4096 keys (1024 one-wave groups): one pass
     # with or without a workspace; so too the B32 H32 decode step and 16 rows

@@ -85,10 +85,10 @@ def test_noalloc_rejects_oversized_plan(cuda):
 
 # The library's own plan (num_splits = 0) lowered to fit the array:
 # (B, H, N_q, N_k, chunks with a workspace, chunks without). B4 H16 N_q 128
-# over 1024 keys plans 4 chunks of 64 groups (8.9 MB) and runs 3; B8 H16
-# N_q 128 over 4096 keys plans 2 chunks (8.9 MB) and runs one pass; B2 H16
+# over 1024 keys plans 4 chunks of 64 groups (8.9 MB) and runs 3; B4 H31
+# N_q 128 over 4096 keys plans 3 chunks (12.9 MB) and runs one pass; B2 H16
 # N_q 128 over 4096 keys plans 8 chunks of 32 groups (8.9 MB) and runs 7.
-CAPPED = [(4, 16, 128, 1024, 4, 3), (8, 16, 128, 4096, 2, 0), (2, 16, 128, 4096, 8, 7)]
+CAPPED = [(4, 16, 128, 1024, 4, 3), (4, 31, 128, 4096, 3, 0), (2, 16, 128, 4096, 8, 7)]
 
 
 @pytest.mark.parametrize("b,h,nq,nk,ws_chunks,na_chunks", CAPPED)
