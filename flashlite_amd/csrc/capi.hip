@@ -138,6 +138,13 @@ int select_fa2(const fl::FwdArgs& a) {
   // N_k <= 512 with few query blocks: quarter the key range (4-wave groups
   // of 32 rows, or 8-wave groups of 64 past 256 blocks; a single round).
   if (fl::quarter_config_fits(a) && wgs(32) <= 2 * cus) return fl::kQuarterConfig;
+  // At most 32 query rows per head (decode-like) over at least as many
+  // heads as CUs: HBM-bound; the 4-wave groups, two per CU, were 0.6-6.8%
+  // faster than the 256-row groups or the 64-row split (B64 H32 N_q 1 N_k
+  // 2048 181.8 against 195.1 us, B32 H32 N_k 4096 178.2 against 183.1, B8
+  // H32 N_k 8192 93.4 against 94.0; within 2% of the best at B16 H32 N_k
+  // 16384).
+  if (a.seq <= 32 && a.batch_heads >= cus) return fl::kSlotW4Config;
   // Past 576 keys, at most one group of 64 rows per CU: the key-range split
   // on 64-row groups (2 x 2 waves) in a single round.
   if (a.seq_k > 576 && wgs(64) <= cus) return fl::kCfgSplit2W2;

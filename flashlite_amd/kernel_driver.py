@@ -45,7 +45,8 @@ workloads do not name.
 
 ``--decode B H NQ NK`` runs a decode-shaped call (NQ query rows over NK
 keys, seeded N(0,1) inputs) through ``fl_attn_fwd_f16_splitkv`` with
-``--splits S`` (1 = one pass, 0 = the library's choice, n = n key chunks)
+``--splits S`` (1 = one pass, 0 = the library's choice, n = n key chunks;
+a one pass runs ``--config``'s configuration, by default the dispatcher's)
 and reports the K/V read rate against 8 TB/s: bytes = 2 * B*H*NK*64*2
 (K and V once) + Q and O.
 
@@ -194,16 +195,20 @@ def _decode(args, torch):
     need = 0 if args.splits == 1 else capi.splitkv_workspace_bytes(p, args.splits)
     ws = torch.empty(max(need, 16) // 4, dtype=torch.float32, device=dev)
 
+    # one pass (no chunks): the dispatcher's configuration, or --config's
+    cfg = args.config if need == 0 else -1
+
     def launch():
         if need == 0:
-            capi.check(capi.fwd_ex(p, stream, -1))
+            capi.check(capi.fwd_ex(p, stream, cfg))
         else:
             capi.check(capi.fwd_splitkv(p, ws.data_ptr(), need, stream, args.splits))
 
     us = _time_launches(launch, args, torch)
     nbytes = 2 * b * h * nk * 64 * 2 + 2 * b * h * nq * 64 * 2
     chunks = need // (b * h * nq * 68 * 4) if need else 1
-    print(f"decode B{b} H{h} NQ{nq} NK{nk} causal={args.causal_decode} chunks={chunks}"
+    name = f" {capi.config_name(cfg)}" if need == 0 and cfg >= 0 else ""
+    print(f"decode B{b} H{h} NQ{nq} NK{nk} causal={args.causal_decode} chunks={chunks}{name}"
           f"{' cold' if args.cold_mib else ''}: "
           f"{us:.2f} us/call, {nbytes / us / 1e3:.1f} GB/s ({nbytes / us / 1e3 / 8000:.1%} of 8 TB/s)",
           flush=True)

@@ -220,6 +220,12 @@ def test_dispatcher_choices():
     assert sel(batch=2, heads=8, seq_q=4096) == W8
     assert sel(batch=1, heads=16, seq_q=16384, causal=True) == W4
     assert sel(batch=3, heads=8, seq_q=2048, causal=True) == W4   # 384 groups
+    # at most 32 query rows over at least 256 heads: 4-wave groups
+    assert sel(batch=32, heads=32, seq_q=1, seq_k=4096) == W4
+    assert sel(batch=8, heads=32, seq_q=1, seq_k=8192) == W4
+    assert sel(batch=8, heads=32, seq_q=32, seq_k=8192, causal=True) == W4
+    assert sel(batch=4, heads=32, seq_q=1, seq_k=8192) == SPLIT64  # 128 heads
+    assert sel(batch=8, heads=32, seq_q=33, seq_k=8192) == SPLIT64  # 33 rows: not this rule
     # square causal from N 4096 with 129-256 pairs of 64-row blocks: the
     # 64-row block pairs (one round)
     assert sel(batch=1, heads=2, seq_q=16384, causal=True) == PAIR64
