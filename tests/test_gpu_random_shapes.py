@@ -19,8 +19,9 @@ the rounded p on the matrix core and land about 3x closer).  The second
 test does the same for the wider types (fp16 at head_dim 128, bf16 at 64 and
 128) through fl_attn_fwd_{f16,bf16}_ex, on contiguous or [B, N, H, D]
 layouts, with the log-sum-exp; the third for split-KV decode (few query rows
-over up to 20000 keys, automatic, single and forced chunk counts); the
-fourth for the naive kernel (forward_naive) at head dims 1-200."""
+over up to 20000 keys, automatic, single and forced chunk counts), the
+fourth for the library's own decode plan over 64-512 heads; the fifth for
+the naive kernel (forward_naive) at head dims 1-200."""
 
 import numpy as np
 import pytest
@@ -155,6 +156,17 @@ def _split_id(c):
     return f"{i}-B{b}H{h}-q{nq}-k{nk}-{'causal' if causal else 'full'}-s{scale}-x{splits}"
 
 
+def _split_id_many(c):
+    i, b, h, nq, nk, causal, scale = c
+    return f"{i}-B{b}H{h}-q{nq}-k{nk}-{'causal' if causal else 'full'}-s{scale}"
+
+
+def torch_cus(dev):
+    import torch
+
+    return torch.cuda.get_device_properties(dev).multi_processor_count
+
+
 @pytest.mark.gpu
 @pytest.mark.parametrize("case", _split_cases(), ids=_split_id)
 def test_random_shape_splitkv(cuda, case):
@@ -177,6 +189,48 @@ def test_random_shape_splitkv(cuda, case):
             mx, mean = error_stats(lse[fin], ref[fin])
             assert mx <= LSE_MAX_ABS["fp16"] and mean <= LSE_MEAN_ABS["fp16"], (
                 f"lse max-abs {mx:.3e} mean-abs {mean:.3e}")
+
+
+def _many_head_cases(n=8, seed=20261209):
+    rs = np.random.RandomState(seed)
+    out = []
+    for i in range(n):
+        b = int(rs.choice([4, 8, 16]))
+        h = int(rs.choice([16, 32]))
+        nq = int(rs.choice([1, 4, 16, 32, 64]))
+        nk = int(rs.randint(600, 4097))
+        causal = bool(rs.rand() < 0.5)
+        scale = float(SCALES[rs.randint(3)])
+        out.append((i, b, h, nq, nk, causal, scale))
+    return out
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("case", _many_head_cases(), ids=_split_id_many)
+def test_random_shape_splitkv_many_heads(cuda, case):
+    """The library's own plan over 64-512 heads: one pass from half as many
+    query-row groups as CUs (the 4-wave groups for at most 32 rows over at
+    least as many heads as CUs), key chunks below; up to 1024 keys, single-
+    wave groups that fit one round of 2-chunk key-quarter groups still take
+    them."""
+    i, b, h, nq, nk, causal, scale = case
+    rs = np.random.RandomState(7000 + i)
+    q = rs.standard_normal((b, h, nq, 64)).astype(np.float32).astype(np.float16)
+    k = rs.standard_normal((b, h, nk, 64)).astype(np.float32).astype(np.float16)
+    v = rs.standard_normal((b, h, nk, 64)).astype(np.float32).astype(np.float16)
+    print(f"random split-KV many heads {_split_id_many(case)}", flush=True)
+    tq, tk, tv = (to_dev(x, cuda) for x in (q, k, v))
+    o, ls, need = run_splitkv(tq, tk, tv, scale, causal, 0)
+    waves = 1 if nq <= 32 else (2 if nq <= 64 else 4)
+    groups = b * h * -(-nq // (32 * waves))
+    if 2 * groups >= torch_cus(cuda) and nk > 1024:
+        assert need == 0, "one pass expected"
+    assert_close_oracle(o.float().cpu().numpy(), q, k, v, scale, causal, peaked=True)
+    ref = attention_lse(q, k, scale, causal)
+    fin = np.isfinite(ref)
+    mx, mean = error_stats(ls.cpu().numpy()[fin], ref[fin])
+    assert mx <= LSE_MAX_ABS["fp16"] and mean <= LSE_MEAN_ABS["fp16"], (
+        f"lse max-abs {mx:.3e} mean-abs {mean:.3e}")
 
 
 def _naive_cases(n=16, seed=20261205):
