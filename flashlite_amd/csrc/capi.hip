@@ -272,7 +272,10 @@ int check_ex(const fl_attn_params_ex* p, fl::FwdArgs* a, const char* who, bool w
 // Single-wave groups whose chunks fit the key-quarter kernel (at most 8
 // tiles) in one round of its 4-wave work-groups (at most 256) run there
 // (`quarter`): the library's choice cuts such ranges into chunks of 8 tiles
-// when that fits, and a requested chunk count takes it when it does.
+// when that fits (below half as many groups as CUs: from 128 groups its 2
+// chunks measured level with one pass or 9-14% slower, B8 H16 N_q 1 N_k 692
+// 8.92 against 8.09 us, B2 H64 N_q 16 N_k 1000 10.96 against 9.47), and a
+// requested chunk count takes it when it does.
 struct KvPlan {
   int waves, nsplit;
   bool quarter;
@@ -300,7 +303,7 @@ KvPlan plan_kvsplit(const fl::FwdArgs& a, int32_t requested) {
   } else {
     n = 0;  // enough groups for the one-pass kernels
   }
-  if (p.waves == 1 && requested <= 0 && groups < cus) {
+  if (p.waves == 1 && requested <= 0 && 2 * groups < cus) {
     const int64_t nq = (tiles + 7) / 8;  // chunks of at most 8 tiles
     if (nq >= 2 && groups * nq <= cus) {
       n = nq;

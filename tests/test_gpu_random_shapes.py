@@ -210,9 +210,7 @@ def _many_head_cases(n=8, seed=20261209):
 def test_random_shape_splitkv_many_heads(cuda, case):
     """The library's own plan over 64-512 heads: one pass from half as many
     query-row groups as CUs (the 4-wave groups for at most 32 rows over at
-    least as many heads as CUs), key chunks below; up to 1024 keys, single-
-    wave groups that fit one round of 2-chunk key-quarter groups still take
-    them."""
+    least as many heads as CUs), key chunks below."""
     i, b, h, nq, nk, causal, scale = case
     rs = np.random.RandomState(7000 + i)
     q = rs.standard_normal((b, h, nq, 64)).astype(np.float32).astype(np.float16)
@@ -223,7 +221,7 @@ def test_random_shape_splitkv_many_heads(cuda, case):
     o, ls, need = run_splitkv(tq, tk, tv, scale, causal, 0)
     waves = 1 if nq <= 32 else (2 if nq <= 64 else 4)
     groups = b * h * -(-nq // (32 * waves))
-    if 2 * groups >= torch_cus(cuda) and nk > 1024:
+    if 2 * groups >= torch_cus(cuda):
         assert need == 0, "one pass expected"
     assert_close_oracle(o.float().cpu().numpy(), q, k, v, scale, causal, peaked=True)
     ref = attention_lse(q, k, scale, causal)
