@@ -161,6 +161,16 @@ int select_fa2(const fl::FwdArgs& a) {
   if (a.causal && a.seq == a.seq_k && a.seq_k >= 4096 && pairs64 <= cus) return fl::kCfgPairW2;
   const bool one_round = a.seq_k >= 2048 && wgs(128) <= cus;
   if (one_round && (!a.causal || wgs(128) >= cus / 4)) return fl::kCfgSplit2;
+  // Square causal problems over 2048-4095 keys with one to two rounds of
+  // 128-row groups: the one-block split up to one and a half rounds (2-8%
+  // faster than the 4-wave groups: B2 H8 N3072 31.8 against 34.9 us, B1 H16
+  // N3072 32.2 against 34.5, B2 H8 N2560 26.7 against 28.4), and from 2560
+  // keys the block pairs beyond (B2 H10 N2560 30.8 against 34.7, B2 H8
+  // N3584 42.6 against 43.8).
+  if (a.causal && a.seq == a.seq_k && a.seq_k >= 2048 && a.seq_k < 4096 && wgs(128) > cus) {
+    if (wgs(128) <= cus + cus / 2) return fl::kCfgSplit2;
+    if (a.seq_k >= 2560 && wgs(128) <= 2 * cus) return fl::kCfgPair;
+  }
   // Causal over at least 4096 keys with more than one 128-row block but at
   // most one block pair per CU: the block pairs (one round of equal
   // work-groups, each key range halved), 2-10% faster than the 4-wave

@@ -210,16 +210,23 @@ def test_dispatcher_choices():
     assert sel(batch=1, heads=1, seq_q=2048, causal=True) == SPLIT64
     assert sel(batch=3, heads=8, seq_q=1024) == W4         # 384 groups of 64 rows
     assert sel(batch=4, heads=4, seq_q=1536, causal=True) == W4
-    # causal from N_k 4096 with 257-512 groups of 128 rows: the split in two
-    # rounds; beyond, and at N_k 2048, 128-row slot-scheduled groups
-    # balanced by dispatch order
+    # causal from N_k 4096 with 257-512 groups of 128 rows: the block pairs;
+    # square causal over 2048-4095 keys: the one-block split up to 384
+    # groups, the block pairs to 512 from 2560 keys; beyond, 128-row
+    # slot-scheduled groups balanced by dispatch order
     assert sel(batch=2, heads=8, seq_q=4096, causal=True) == PAIR
     assert sel(batch=1, heads=8, seq_q=8192, causal=True) == PAIR
     assert sel(batch=4, heads=8, seq_q=4096, causal=True) == W4
     assert sel(batch=2, heads=16, seq_q=2048, causal=True) == W4
     assert sel(batch=2, heads=8, seq_q=4096) == W8
     assert sel(batch=1, heads=16, seq_q=16384, causal=True) == W4
-    assert sel(batch=3, heads=8, seq_q=2048, causal=True) == W4   # 384 groups
+    assert sel(batch=3, heads=8, seq_q=2048, causal=True) == SPLIT   # 384 groups, 2 rounds
+    assert sel(batch=2, heads=8, seq_q=3072, causal=True) == SPLIT   # 384 groups
+    assert sel(batch=2, heads=10, seq_q=2560, causal=True) == PAIR   # 400 groups
+    assert sel(batch=2, heads=8, seq_q=3584, causal=True) == PAIR    # 448 groups
+    assert sel(batch=5, heads=8, seq_q=2048, causal=True) == W4      # 640 groups
+    assert sel(batch=4, heads=8, seq_q=2048, causal=True) == W4      # 512 groups, N 2048
+    assert sel(batch=2, heads=8, seq_q=3072) == W8                   # non-causal
     # at most 32 query rows over at least 256 heads: 4-wave groups
     assert sel(batch=32, heads=32, seq_q=1, seq_k=4096) == W4
     assert sel(batch=8, heads=32, seq_q=1, seq_k=8192) == W4
