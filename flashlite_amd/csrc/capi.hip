@@ -162,7 +162,7 @@ int select_fa2(const fl::FwdArgs& a) {
   const bool one_round = a.seq_k >= 2048 && wgs(128) <= cus;
   if (one_round && (!a.causal || wgs(128) >= cus / 4)) return fl::kCfgSplit2;
   // Square causal problems over 2048-4095 keys with one to two rounds of
-  // 128-row groups: the one-block split up to one and a half rounds (2-8%
+  // 128-row groups: the one-block split up to one and a half rounds (1-9%
   // faster than the 4-wave groups: B2 H8 N3072 31.8 against 34.9 us, B1 H16
   // N3072 32.2 against 34.5, B2 H8 N2560 26.7 against 28.4), and from 2560
   // keys the block pairs beyond (B2 H10 N2560 30.8 against 34.7, B2 H8
