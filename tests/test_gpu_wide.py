@@ -27,8 +27,8 @@ import pytest
 
 from flashlite_amd import capi
 from gpu_util import (BF16_MAX_ABS, BF16_MEAN_ABS, LSE_MAX_ABS, LSE_MEAN_ABS, MAX_ABS, MEAN_ABS,
-                      PAIR_CFG, QUARTER_CFG, SLOT_W4_CFG, SLOT_W8_CFG, SPLIT2_CFG, SPLIT2W2_CFG,
-                      STREAM_CFG, half_ulp, sample_rows)
+                      PAIR64_CFG, PAIR_CFG, QUARTER_CFG, SLOT_W4_CFG, SLOT_W8_CFG, SPLIT2_CFG,
+                      SPLIT2W2_CFG, STREAM_CFG, half_ulp, sample_rows)
 from gpu_util import run_wide as _run
 from gpu_util import wide_inputs as _inputs
 from gpu_util import wide_tol as _tol
@@ -146,11 +146,11 @@ def test_strided_bit_exact(cuda, kind, d, causal):
         assert np.array_equal(out, base), views.__name__
 
 
-@pytest.mark.parametrize("config", [SPLIT2_CFG, SPLIT2W2_CFG, PAIR_CFG])
+@pytest.mark.parametrize("config", [SPLIT2_CFG, SPLIT2W2_CFG, PAIR_CFG, PAIR64_CFG])
 @pytest.mark.parametrize("causal", [False, True])
 def test_bf16_key_range_splits(cuda, config, causal):
     """bf16 at D = 64 on the key-range splits (128- and 64-row groups, and
-    the 128-row block pairs):
+    the 128- and 64-row block pairs):
     ragged lengths, every output row of B1 H4 N1024, and a peaked scale whose
     row sums leave the first pass's range (the checked pass)."""
     for n in RAGGED:
