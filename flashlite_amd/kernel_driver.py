@@ -46,7 +46,8 @@ workloads do not name.
 ``--decode B H NQ NK`` runs a decode-shaped call (NQ query rows over NK
 keys, seeded N(0,1) inputs) through ``fl_attn_fwd_f16_splitkv`` with
 ``--splits S`` (1 = one pass, 0 = the library's choice, n = n key chunks;
-a one pass runs ``--config``'s configuration, by default the dispatcher's)
+a one pass runs ``--config``'s configuration, by default the dispatcher's;
+``--dtype bf16`` runs one pass only)
 and reports the K/V read rate against 8 TB/s: bytes = 2 * B*H*NK*64*2
 (K and V once) + Q and O.
 
@@ -184,10 +185,14 @@ def _decode(args, torch):
     from flashlite_amd import capi
 
     b, h, nq, nk = args.decode
+    bf16 = args.dtype == "bf16"
+    if bf16 and args.splits != 1:
+        raise SystemExit("--decode with --dtype bf16 runs one pass only (--splits 1)")
     dev = torch.device("cuda:0")
     rs = np.random.RandomState(7)
-    mk = lambda n: torch.from_numpy(
-        rs.standard_normal((b, h, n, 64)).astype(np.float32).astype(np.float16)).to(dev)
+    dt = torch.bfloat16 if bf16 else torch.float16
+    mk = lambda n: torch.from_numpy(  # noqa: E731
+        rs.standard_normal((b, h, n, 64)).astype(np.float32)).to(dev).to(dt)
     q, k, v = mk(nq), mk(nk), mk(nk)
     o = torch.empty_like(q)
     stream = torch.cuda.current_stream().cuda_stream
@@ -200,7 +205,7 @@ def _decode(args, torch):
 
     def launch():
         if need == 0:
-            capi.check(capi.fwd_ex(p, stream, cfg))
+            capi.check((capi.fwd_bf16_ex if bf16 else capi.fwd_ex)(p, stream, cfg))
         else:
             capi.check(capi.fwd_splitkv(p, ws.data_ptr(), need, stream, args.splits))
 
@@ -208,7 +213,8 @@ def _decode(args, torch):
     nbytes = 2 * b * h * nk * 64 * 2 + 2 * b * h * nq * 64 * 2
     chunks = need // (b * h * nq * 68 * 4) if need else 1
     name = f" {capi.config_name(cfg)}" if need == 0 and cfg >= 0 else ""
-    print(f"decode B{b} H{h} NQ{nq} NK{nk} causal={args.causal_decode} chunks={chunks}{name}"
+    print(f"decode B{b} H{h} NQ{nq} NK{nk}{' bf16' if bf16 else ''} causal={args.causal_decode} "
+          f"chunks={chunks}{name}"
           f"{' cold' if args.cold_mib else ''}: "
           f"{us:.2f} us/call, {nbytes / us / 1e3:.1f} GB/s ({nbytes / us / 1e3 / 8000:.1%} of 8 TB/s)",
           flush=True)
